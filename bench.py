@@ -1,0 +1,325 @@
+"""Benchmark of the DSQG offset-gather path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline workload (the training microbatch): one DSQG layer forward+backward,
+bf16, B=15, H=8, T=2048, head_dim=64, the 96-offset lattice, synthetic seeded
+inputs resident in HBM.  A step is dwarf_dsqg_fwd + dwarf_dsqg_bwd_dq +
+dwarf_dsqg_bwd_dkdv on the current stream.  value = tokens (B*T) per second.
+
+Also reported under "extra": the q6 decode step (256 sequences x 9 layers,
+cache length 2048), the q6 prefill forward (B=20) and the long-context
+DSQG fwd+bwd + EMA fwd+bwd (B=4, T=8192).  cpu_baseline times the CPU
+restatement of the reference's eager path (oracle/) on a bounded sample.
+
+Prints one JSON line.  Runs on one GPU only.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
+TABLE_BYTES = 47_872         # pos_bias + scale_embed + phase tables per layer (J=96, H=8, hd=64)
+FWD_BYTES_PER_TH = 548       # q,k,v (3x128) + y,z (2x16) + out (128) + lse (4)
+BWD_BYTES_PER_TH = 1092      # read q,k,v,o,dO + lse + y,z; write dq,dk,dv + dy,dz
+DQ_BYTES_PER_TH = 820        # dq launch: read q,k,v,o,dO,lse,y,z; write dq,dy
+DKDV_BYTES_PER_TH = 820      # dkdv launch: read k,v,q,dO,lse,y,z; write dk,dv,dz
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def synth(pkg, B, H, N, seed, device, dtype=torch.bfloat16, plane_shift=0):
+    """Seeded synthetic DSQG inputs (draw order fixed; CPU generator, then copied)."""
+    offsets = list(pkg.ALL_OFFSETS)
+    J, js = len(offsets), 17
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    k = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    v = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    dout = torch.randn(B, H, N, 64, generator=g).to(dtype)
+    pb = 0.02 * torch.randn(J, H, generator=g)
+    se = 0.01 * torch.randn(J, 64, generator=g)
+    se = se - se.mean(0, keepdim=True)
+    pbase = 0.5 * 0.01 * torch.randn(J - js, H, 4, generator=g)
+    pgain = 0.5 * 1.28 * torch.randn(J - js, H, 4, generator=g)
+    qp, kp = pkg._orthogonal_phase_probes(4, 64, plane_shift)
+
+    def feat(x, p):
+        xf = x.float()
+        inv = torch.rsqrt(xf.square().sum(-1, keepdim=True) + 64e-6)
+        return (torch.einsum("bhnd,rd->bhnr", xf, torch.nn.functional.normalize(p, dim=-1)) * inv).contiguous()
+
+    t = dict(q=q, k=k, v=v, dout=dout, pos_bias=pb, scale_embed=se, phase_base=pbase, phase_gain=pgain,
+             y_pre=feat(q, qp), z_pre=feat(k, kp))
+    t = {n: x.to(device) for n, x in t.items()}
+    t["offsets"] = torch.tensor(offsets, dtype=torch.int32, device=device)
+    t["qp"], t["kp"] = qp, kp
+    return t, js, J - js
+
+
+def time_dsqg_step(pkg, t, js, jl, steps, warmup, flush=None):
+    """Returns (ms_per_step, per-launch average ms dict)."""
+    ops = pkg.dsqg if hasattr(pkg, "dsqg") else importlib.import_module("dwarf-v2_amd.dsqg")
+    args = (t["q"], t["k"], t["v"], t["pos_bias"], t["scale_embed"], t["phase_base"], t["phase_gain"],
+            t["y_pre"], t["z_pre"], t["offsets"])
+
+    def step(ev_f=None, ev_b=None):
+        out, lse = ops.dsqg_forward(*args, js, jl, 0, 1, events=ev_f)
+        ops.dsqg_backward(t["dout"], *args, out, lse, js, jl, 0, 1, events=ev_b)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [([torch.cuda.Event(enable_timing=True) for _ in range(2)],
+            [torch.cuda.Event(enable_timing=True) for _ in range(3)]) for _ in range(steps)]
+    total_ms = 0.0
+    if flush is None:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for ef, eb in evs:
+            step(ef, eb)
+        end.record()
+        torch.cuda.synchronize()
+        total_ms = start.elapsed_time(end)
+    else:
+        for ef, eb in evs:
+            flush()
+            step(ef, eb)
+        torch.cuda.synchronize()
+        total_ms = sum(ef[0].elapsed_time(eb[2]) for ef, eb in evs)
+    per = {
+        "fwd": sum(ef[0].elapsed_time(ef[1]) for ef, _ in evs) / steps,
+        "bwd_dq": sum(eb[0].elapsed_time(eb[1]) for _, eb in evs) / steps,
+        "bwd_dkdv": sum(eb[1].elapsed_time(eb[2]) for _, eb in evs) / steps,
+    }
+    return total_ms / steps, per
+
+
+def cpu_baseline(pkg):
+    """The CPU restatement of the reference eager path (oracle/), fp32 fwd+bwd on
+    batch row 0 of the training microbatch (B=1 of 15: 2,048 of 30,720 tokens)."""
+    from oracle import dsqg_ref
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    t, js, jl = synth(pkg, 1, 8, 2048, 0, torch.device("cpu"), dtype=torch.float32)
+    names = ("q", "k", "v", "pos_bias", "scale_embed", "phase_base", "phase_gain", "y_pre", "z_pre")
+    inputs = {n: t[n] for n in names}
+    offsets = t["offsets"].tolist()
+    t0 = time.perf_counter()
+    dsqg_ref.dsqg_forward_backward(inputs, offsets, js, t["dout"], query_start=1)
+    dt = time.perf_counter() - t0
+    cpu = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": 2048 / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle/dsqg_ref fp32 fwd+bwd of batch row 0 (B=1,H=8,T=2048,J=96): {dt:.2f} s; {cpu}"}
+
+
+def q6_decode_extra(pkg, device, steps, warmup):
+    S, L, H, N = 256, 9, 8, 2048
+    offsets = list(pkg.ALL_OFFSETS)
+    J, js = len(offsets), 17
+    g = torch.Generator().manual_seed(0)
+    pos = torch.randint(96, N, (S,), generator=g, dtype=torch.int32)
+    qdec = torch.randn(S, L, H, 64, generator=g).to(torch.bfloat16).to(device)
+    pb = (0.02 * torch.randn(L, J, H, generator=g)).to(device)
+    se = (0.01 * torch.randn(L, J, 64, generator=g)).to(device)
+    pbase = (0.005 * torch.randn(L, J - js, H, 4, generator=g)).to(device)
+    pgain = (0.64 * torch.randn(L, J - js, H, 4, generator=g)).to(device)
+    qp, kp = pkg._orthogonal_phase_probes(4, 64, 0)
+    qpn = torch.nn.functional.normalize(qp, dim=-1)
+    kpn = torch.nn.functional.normalize(kp, dim=-1).to(device)
+    caches = torch.empty((L, S, H, N, 128), dtype=torch.uint8, device=device)
+    gd = torch.Generator(device=device).manual_seed(1)
+    for l in range(L):
+        k = torch.randn(S, H, N, 64, generator=gd, device=device, dtype=torch.bfloat16)
+        v = torch.randn(S, H, N, 64, generator=gd, device=device, dtype=torch.bfloat16)
+        caches[l] = pkg.q6.pack_kv(k, v, kpn)
+        del k, v
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    posd = pos.to(device)
+    qps = torch.stack([qpn] * L).to(device)
+
+    def run():
+        return pkg.q6.q6_decode(qdec, posd, caches, pb, se, pbase, pgain, qps, off, js, J - js, 0)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    nv = [sum(1 for d in offsets if int(t) - d >= 0) for t in pos]
+    nf = [sum(1 for d in offsets[js:] if int(t) - d >= 0) for t in pos]
+    bytes_ = sum(L * H * (256 + 104 * a_ + 16 * b_) for a_, b_ in zip(nv, nf)) + L * TABLE_BYTES
+    del caches
+    torch.cuda.empty_cache()
+    return {"tokens_per_s": S / (ms * 1e-3), "ms_per_step": ms, "algorithmic_bytes": bytes_,
+            "achieved_GBps": bytes_ / (ms * 1e-3) / 1e9, "hbm_frac": bytes_ / (ms * 1e-3) / HBM_PEAK,
+            "config": "S=256 seqs x L=9 layers x H=8, cache 2048, positions U{96..2047} seed 0; "
+                      "bytes count 104 B q6 K+V per valid row + 16 B stored z per valid far row"}
+
+
+def q6_prefill_extra(pkg, device, steps, warmup):
+    B, H, N = 20, 8, 2048
+    t, js, jl = synth(pkg, B, H, N, 3, device)
+    kpn = torch.nn.functional.normalize(t["kp"], dim=-1).to(device)
+    qpn = torch.nn.functional.normalize(t["qp"], dim=-1).to(device)
+    cache = pkg.q6.pack_kv(t["k"], t["v"], kpn)
+
+    def run():
+        return pkg.q6.q6_prefill(t["q"], cache, t["pos_bias"], t["scale_embed"], t["phase_base"],
+                                 t["phase_gain"], qpn, t["offsets"], js, jl, 0, 1)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    bytes_ = B * H * N * (128 + 104 + 16 + 128) + TABLE_BYTES
+    return {"tokens_per_s": B * N / (ms * 1e-3), "ms_per_step": ms, "algorithmic_bytes": bytes_,
+            "hbm_frac": bytes_ / (ms * 1e-3) / HBM_PEAK,
+            "config": "B=20 H=8 T=2048 q6 K/V (+16 B stored z per row), y in-kernel"}
+
+
+def long_context_extra(pkg, device, steps, warmup):
+    B, H, N = 4, 8, 8192
+    t, js, jl = synth(pkg, B, H, N, 4, device)
+    ms_dsqg, _ = time_dsqg_step(pkg, t, js, jl, steps, warmup)
+    del t
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B, N, 512, generator=g).to(torch.bfloat16).to(device)
+    dy = torch.randn(B, N, 512, generator=g).to(torch.bfloat16).to(device)
+    alpha = (1.0 - (0.90 + 0.099 * torch.rand(512, generator=g))).to(device)
+    ema = importlib.import_module("dwarf-v2_amd.ema")
+
+    def run():
+        y = ema.ema_forward(x, alpha, 1e-5, 0.5)
+        ema.ema_backward(x, y, dy, alpha, 1e-5, 0.5, True)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    ms_ema = a.elapsed_time(b) / steps
+    dsqg_bytes = B * H * N * (FWD_BYTES_PER_TH + BWD_BYTES_PER_TH) + 2 * TABLE_BYTES
+    ema_bytes = 12 * B * N * 512
+    total = ms_dsqg + ms_ema
+    return {"tokens_per_s": B * N / (total * 1e-3), "ms_per_step": total, "ms_dsqg": ms_dsqg, "ms_ema": ms_ema,
+            "ema_hbm_frac": ema_bytes / (ms_ema * 1e-3) / HBM_PEAK,
+            "hbm_frac": (dsqg_bytes + ema_bytes) / (total * 1e-3) / HBM_PEAK,
+            "config": "B=4 H=8 T=8192 bf16 DSQG fwd+bwd + EMA fwd+bwd x[4,8192,512], per-channel alpha"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the DSQG op shards over batch/heads with no exchange; no multi-GPU figure is produced)",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    pkg = importlib.import_module("dwarf-v2_amd")
+    pkg._lib.load()
+    device = torch.device("cuda", 0)
+    B, H, N = 15, 8, 2048
+    log("training microbatch: DSQG fwd+bwd B15 H8 T2048 bf16")
+    t, js, jl = synth(pkg, B, H, N, 0, device)
+    ms, per = time_dsqg_step(pkg, t, js, jl, args.steps, args.warmup)
+    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+    ms_cold, per_cold = time_dsqg_step(pkg, t, js, jl, max(5, args.steps // 2), 1,
+                                       flush=lambda: flush_buf.fill_(1))
+    del flush_buf
+    th = B * H * N
+    bytes_launch = {"fwd": th * FWD_BYTES_PER_TH + TABLE_BYTES,
+                    "bwd_dq": th * DQ_BYTES_PER_TH + 2 * TABLE_BYTES,
+                    "bwd_dkdv": th * DKDV_BYTES_PER_TH + TABLE_BYTES}
+    dominant = max(per, key=per.get)
+    achieved = bytes_launch[dominant] / (per[dominant] * 1e-3)
+    path_bytes = th * (FWD_BYTES_PER_TH + BWD_BYTES_PER_TH) + 2 * TABLE_BYTES
+    del t
+    torch.cuda.empty_cache()
+
+    extra = {"per_launch_ms": per, "per_launch_ms_cold": per_cold, "ms_per_step_cold": ms_cold,
+             "path_roofline": {"bytes": path_bytes, "achieved_GBps": path_bytes / (ms * 1e-3) / 1e9,
+                               "frac": path_bytes / (ms * 1e-3) / HBM_PEAK}}
+    if not args.no_extra:
+        log("q6 decode step: 256 seqs x 9 layers")
+        extra["q6_decode"] = q6_decode_extra(pkg, device, args.steps, args.warmup)
+        log("q6 prefill: B20 H8 T2048")
+        extra["q6_prefill"] = q6_prefill_extra(pkg, device, args.steps, args.warmup)
+        log("long context: B4 T8192 DSQG fwd+bwd + EMA fwd+bwd")
+        extra["long_context"] = long_context_extra(pkg, device, max(3, args.steps // 4), 2)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dominant)
+    line = {
+        "metric": "DSQG fwd+bwd tokens/s (B15 T2048 bf16) + % HBM roofline; q6 decode tok/s",
+        "value": B * N / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v/dO, reference-calibrated parameter tables)",
+        "config": {"workload": "dsqg_fwd_bwd_training_microbatch", "batch": B, "heads": H, "seq_len": N,
+                   "head_dim": 64, "offsets": 96, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": traffic},
+        "extra": extra,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline: oracle fp32 fwd+bwd, B=1 sample")
+        line["cpu_baseline"] = cpu_baseline(pkg)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

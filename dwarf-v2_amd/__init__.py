@@ -1,0 +1,50 @@
+"""dwarf-v2_amd: MI355X (gfx950) kernels for DWARF-v2's DSQG offset-gather path.
+
+The directory name is not a Python identifier; import it with
+``importlib.import_module("dwarf-v2_amd")``.
+
+Public surface (reference names, Lanerra/dwarf-v2):
+  dsqg_attention_v18_grouped, _DSQGV18GroupedFn      kernels/dsqg_attention_v22.py
+  ALL_OFFSETS, R_PLANES and the lattice helpers      kernels/dsqg_attention_v22.py
+  causal_ema_scan, bounded_ema_factor,
+  inverse_bounded_ema_factor                         kernels/causal_ema_scan.py
+  q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
+"""
+
+from . import _lib, lattice, q6
+from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
+from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
+from .lattice import (
+    ALL_OFFSETS,
+    GROUPED_MODE_IDS,
+    R_PLANES,
+    _canonicalize_offsets,
+    _normalize_plane_shift,
+    _orthogonal_phase_probes,
+    _phase_plane_channels,
+    build_offset_groups,
+)
+
+__all__ = [
+    "ALL_OFFSETS",
+    "GROUPED_MODE_IDS",
+    "R_PLANES",
+    "_DSQGV18GroupedFn",
+    "_canonicalize_offsets",
+    "_normalize_plane_shift",
+    "_orthogonal_phase_probes",
+    "_phase_plane_channels",
+    "bounded_ema_factor",
+    "build_offset_groups",
+    "causal_ema_scan",
+    "dsqg_attention_v18_grouped",
+    "dsqg_backward",
+    "dsqg_forward",
+    "inverse_bounded_ema_factor",
+    "q6",
+]
+
+
+def native_library_path() -> str:
+    """Path of the HIP library every op in this package calls."""
+    return _lib.library_path()

@@ -1,0 +1,232 @@
+"""ctypes binding of libdwarf_dsqg.so (declarations: include/dwarf_dsqg.h).
+
+The structures below mirror the C structs field for field.  Loading never
+builds anything: a missing library raises, so no code path silently falls
+back to a CPU implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint8, c_void_p
+
+LIB_NAME = "libdwarf_dsqg.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+DWARF_OK = 0
+DWARF_ERR_INVALID_ARGUMENT = 1
+DWARF_ERR_UNSUPPORTED = 2
+DWARF_ERR_HIP = 3
+DWARF_ERR_WORKSPACE = 4
+
+DWARF_BF16 = 0
+DWARF_F32 = 1
+
+EXPORTED_SYMBOLS = (
+    "dwarf_abi_version",
+    "dwarf_last_error",
+    "dwarf_dsqg_fwd",
+    "dwarf_dsqg_bwd_workspace_bytes",
+    "dwarf_dsqg_bwd",
+    "dwarf_dsqg_bwd_dq",
+    "dwarf_dsqg_bwd_dkdv",
+    "dwarf_ema_fwd_workspace_bytes",
+    "dwarf_ema_fwd",
+    "dwarf_ema_bwd_workspace_bytes",
+    "dwarf_ema_bwd",
+    "dwarf_q6_pack_kv",
+    "dwarf_q6_unpack_kv",
+    "dwarf_dsqg_q6_prefill_fwd",
+    "dwarf_dsqg_q6_decode",
+)
+
+
+def _i64(n):
+    return c_int64 * n
+
+
+class DsqgFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int32), ("H", c_int32), ("H_kv", c_int32), ("N", c_int32), ("head_dim", c_int32),
+        ("J", c_int32), ("J_small", c_int32), ("J_large", c_int32),
+        ("plane_shift", c_int32), ("query_start", c_int32),
+        ("dtype", c_int32), ("se_round_bf16", c_int32),
+        ("q", c_void_p), ("q_stride", _i64(4)),
+        ("k", c_void_p), ("k_stride", _i64(4)),
+        ("v", c_void_p), ("v_stride", _i64(4)),
+        ("pos_bias", c_void_p), ("pb_stride", _i64(2)),
+        ("scale_embed", c_void_p), ("se_stride", _i64(2)),
+        ("phase_base", c_void_p), ("pbase_stride", _i64(2)),
+        ("phase_gain", c_void_p), ("pgain_stride", _i64(2)),
+        ("y_pre", c_void_p), ("y_stride", _i64(3)),
+        ("z_pre", c_void_p), ("z_stride", _i64(3)),
+        ("offsets", c_void_p),
+        ("out", c_void_p), ("out_stride", _i64(4)),
+        ("lse", c_void_p), ("lse_stride", _i64(3)),
+    ]
+
+
+class DsqgBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", DsqgFwdArgs),
+        ("dout", c_void_p), ("dout_stride", _i64(4)),
+        ("dq", c_void_p), ("dq_stride", _i64(4)),
+        ("dk", c_void_p), ("dk_stride", _i64(4)),
+        ("dv", c_void_p), ("dv_stride", _i64(4)),
+        ("dpos_bias", c_void_p),
+        ("dscale_embed", c_void_p),
+        ("dphase_base", c_void_p),
+        ("dphase_gain", c_void_p),
+        ("dy_pre", c_void_p),
+        ("dz_pre", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class EmaFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int32), ("N", c_int32), ("D", c_int32),
+        ("dtype", c_int32), ("alpha_per_channel", c_int32),
+        ("floor_", c_float), ("ceiling", c_float),
+        ("x", c_void_p), ("x_stride", _i64(3)),
+        ("alpha", c_void_p),
+        ("y", c_void_p), ("y_stride", _i64(3)),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class EmaBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int32), ("N", c_int32), ("D", c_int32),
+        ("dtype", c_int32), ("alpha_per_channel", c_int32),
+        ("floor_", c_float), ("ceiling", c_float),
+        ("x", c_void_p), ("x_stride", _i64(3)),
+        ("y", c_void_p), ("y_stride", _i64(3)),
+        ("dy", c_void_p), ("dy_stride", _i64(3)),
+        ("alpha", c_void_p),
+        ("dx", c_void_p), ("dx_stride", _i64(3)),
+        ("dalpha", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class Q6PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int32), ("H", c_int32), ("H_kv", c_int32), ("N", c_int32), ("head_dim", c_int32),
+        ("J", c_int32), ("J_small", c_int32), ("J_large", c_int32),
+        ("plane_shift", c_int32), ("query_start", c_int32),
+        ("se_round_bf16", c_int32),
+        ("q", c_void_p), ("q_stride", _i64(4)),
+        ("cache", c_void_p), ("cache_stride", _i64(3)),
+        ("pos_bias", c_void_p), ("pb_stride", _i64(2)),
+        ("scale_embed", c_void_p), ("se_stride", _i64(2)),
+        ("phase_base", c_void_p), ("pbase_stride", _i64(2)),
+        ("phase_gain", c_void_p), ("pgain_stride", _i64(2)),
+        ("query_probes", c_void_p),
+        ("offsets", c_void_p),
+        ("out", c_void_p), ("out_stride", _i64(4)),
+        ("lse", c_void_p), ("lse_stride", _i64(3)),
+    ]
+
+
+class Q6DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("S", c_int32), ("L", c_int32), ("H", c_int32), ("H_kv", c_int32), ("Ncache", c_int32),
+        ("head_dim", c_int32),
+        ("J", c_int32), ("J_small", c_int32), ("J_large", c_int32),
+        ("plane_shift", c_int32),
+        ("se_round_bf16", c_int32),
+        ("q", c_void_p), ("q_stride", _i64(4)),
+        ("pos", c_void_p),
+        ("cache", c_void_p), ("cache_stride", _i64(4)),
+        ("pos_bias", c_void_p), ("pb_stride", _i64(3)),
+        ("scale_embed", c_void_p), ("se_stride", _i64(3)),
+        ("phase_base", c_void_p), ("pbase_stride", _i64(3)),
+        ("phase_gain", c_void_p), ("pgain_stride", _i64(3)),
+        ("query_probes", c_void_p), ("qprobe_layer_stride", c_int64),
+        ("offsets", c_void_p),
+        ("out", c_void_p), ("out_stride", _i64(4)),
+    ]
+
+
+_LIB = None
+
+
+class NativeLibraryError(RuntimeError):
+    """The HIP library is missing, stale or failed a call."""
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load libdwarf_dsqg.so once, declaring every entry point's signature."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise NativeLibraryError(
+            f"{LIB_NAME} is not built at {LIB_PATH}; build it with "
+            "`make -C dwarf-v2_amd/csrc` or __graft_entry__.build()"
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.dwarf_abi_version.restype = c_int
+    lib.dwarf_abi_version.argtypes = []
+    lib.dwarf_last_error.restype = c_char_p
+    lib.dwarf_last_error.argtypes = []
+    lib.dwarf_dsqg_fwd.restype = c_int
+    lib.dwarf_dsqg_fwd.argtypes = [POINTER(DsqgFwdArgs), c_void_p]
+    lib.dwarf_dsqg_bwd_workspace_bytes.restype = c_size_t
+    lib.dwarf_dsqg_bwd_workspace_bytes.argtypes = [POINTER(DsqgBwdArgs)]
+    lib.dwarf_dsqg_bwd.restype = c_int
+    lib.dwarf_dsqg_bwd.argtypes = [POINTER(DsqgBwdArgs), c_void_p]
+    for name in ("dwarf_dsqg_bwd_dq", "dwarf_dsqg_bwd_dkdv"):
+        getattr(lib, name).restype = c_int
+        getattr(lib, name).argtypes = [POINTER(DsqgBwdArgs), c_void_p]
+    lib.dwarf_ema_fwd_workspace_bytes.restype = c_size_t
+    lib.dwarf_ema_fwd_workspace_bytes.argtypes = [POINTER(EmaFwdArgs)]
+    lib.dwarf_ema_fwd.restype = c_int
+    lib.dwarf_ema_fwd.argtypes = [POINTER(EmaFwdArgs), c_void_p]
+    lib.dwarf_ema_bwd_workspace_bytes.restype = c_size_t
+    lib.dwarf_ema_bwd_workspace_bytes.argtypes = [POINTER(EmaBwdArgs)]
+    lib.dwarf_ema_bwd.restype = c_int
+    lib.dwarf_ema_bwd.argtypes = [POINTER(EmaBwdArgs), c_void_p]
+    lib.dwarf_q6_pack_kv.restype = c_int
+    lib.dwarf_q6_pack_kv.argtypes = [
+        c_int32, c_int32, c_int32, c_int32, c_int32,
+        c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64),
+        POINTER(c_uint8), POINTER(c_int64), c_void_p, c_void_p,
+    ]
+    lib.dwarf_q6_unpack_kv.restype = c_int
+    lib.dwarf_q6_unpack_kv.argtypes = [
+        c_int32, c_int32, c_int32, c_int32,
+        POINTER(c_uint8), POINTER(c_int64), c_void_p, c_void_p, c_void_p,
+    ]
+    lib.dwarf_dsqg_q6_prefill_fwd.restype = c_int
+    lib.dwarf_dsqg_q6_prefill_fwd.argtypes = [POINTER(Q6PrefillArgs), c_void_p]
+    lib.dwarf_dsqg_q6_decode.restype = c_int
+    lib.dwarf_dsqg_q6_decode.argtypes = [POINTER(Q6DecodeArgs), c_void_p]
+    version = lib.dwarf_abi_version()
+    if version != ABI_VERSION:
+        raise NativeLibraryError(f"{LIB_NAME} ABI {version} does not match the binding's ABI {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    """Map a dwarf_status to the exception type the reference raises."""
+    if status == DWARF_OK:
+        return
+    message = (load().dwarf_last_error() or b"").decode(errors="replace")
+    text = f"{what}: {message}"
+    if status == DWARF_ERR_INVALID_ARGUMENT:
+        raise ValueError(text)
+    raise NativeLibraryError(text)
+
+
+def i64_array(values):
+    values = [int(v) for v in values]
+    return (c_int64 * len(values))(*values)

@@ -1,0 +1,309 @@
+// extern "C" entry points of libdwarf_dsqg.so (declared in dwarf_dsqg.h).
+// Every argument is validated on the host before a kernel is launched, so a
+// malformed call returns a status instead of reaching the GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "dsqg_internal.h"
+#include "dwarf_dsqg.h"
+
+namespace dwarf {
+size_t ema_fwd_workspace(int B, int N, int D);
+size_t ema_bwd_workspace(int B, int N, int D);
+hipError_t launch_ema_fwd(const dwarf_ema_fwd_args& a, hipStream_t stream);
+hipError_t launch_ema_bwd(const dwarf_ema_bwd_args& a, hipStream_t stream);
+hipError_t launch_q6_pack(int B, int Hkv, int N, int dtype, const void* k, const int64_t* ks, const void* v,
+                          const int64_t* vs, uint8_t* cache, const int64_t* cs, const float* kprobe,
+                          hipStream_t stream);
+hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const int64_t* cs, float* kout,
+                            float* vout, hipStream_t stream);
+hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream);
+hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream);
+int q6_max_decode_offsets();
+}  // namespace dwarf
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_error[0] = '\0';
+  return DWARF_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(DWARF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int kMaxOffsets = 256;  // LDS tables of the DSQG kernels
+
+size_t elem_size(int dtype) { return dtype == DWARF_BF16 ? 2 : 4; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// A [.., rows, hd] tensor read/written with 16-byte vectors along hd.
+int check_rows(const char* name, const void* p, const int64_t* stride, int ndim_outer, int dtype) {
+  if (!p) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (stride[ndim_outer] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s needs unit stride on head_dim", name);
+  if (!aligned16(p)) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s must be 16-byte aligned", name);
+  const int64_t per16 = 16 / static_cast<int64_t>(elem_size(dtype));
+  for (int i = 0; i < ndim_outer; ++i)
+    if (stride[i] % per16 != 0)
+      return fail(DWARF_ERR_INVALID_ARGUMENT, "%s stride[%d]=%lld breaks 16-byte row alignment", name, i,
+                  static_cast<long long>(stride[i]));
+  return DWARF_OK;
+}
+
+// [B,H,N,4] fp32 plane features read as float4.
+int check_planes(const char* name, const float* p, const int64_t* stride) {
+  if (!p) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (!aligned16(p)) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s must be 16-byte aligned", name);
+  for (int i = 0; i < 3; ++i)
+    if (stride[i] % 4 != 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s stride[%d] must be a multiple of 4", name, i);
+  return DWARF_OK;
+}
+
+int check_lattice(int H, int H_kv, int N, int hd, int J, int J_small, int J_large, int plane_shift, int query_start) {
+  if (H <= 0 || H_kv <= 0 || N < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes H=%d H_kv=%d N=%d", H, H_kv, N);
+  if (H % H_kv != 0)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "num query heads H=%d must be divisible by KV heads H_kv=%d", H, H_kv);
+  if (hd != dwarf::kHeadDim) return fail(DWARF_ERR_UNSUPPORTED, "head_dim=%d is not built (head_dim 64 only)", hd);
+  if (J < 1 || J_small < 0 || J_large < 0 || J_small + J_large != J)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "J=%d must equal J_small=%d + J_large=%d and be >= 1", J, J_small, J_large);
+  if (J > kMaxOffsets) return fail(DWARF_ERR_UNSUPPORTED, "J=%d exceeds the %d offsets the kernels stage", J, kMaxOffsets);
+  const int segment = hd / DWARF_R_PLANES;
+  if (plane_shift < 0 || plane_shift > segment - 2)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "plane_shift=%d outside [0, %d]", plane_shift, segment - 2);
+  if (query_start < 0 || query_start > N)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "query_start=%d outside [0, N=%d]", query_start, N);
+  return DWARF_OK;
+}
+
+int check_fwd(const dwarf_dsqg_fwd_args& a) {
+  if (a.B < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "B=%d", a.B);
+  int rc = check_lattice(a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, a.query_start);
+  if (rc) return rc;
+  if (a.dtype != DWARF_BF16 && a.dtype != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", a.dtype);
+  if ((rc = check_rows("q", a.q, a.q_stride, 3, a.dtype))) return rc;
+  if ((rc = check_rows("k", a.k, a.k_stride, 3, a.dtype))) return rc;
+  if ((rc = check_rows("v", a.v, a.v_stride, 3, a.dtype))) return rc;
+  if ((rc = check_rows("out", a.out, a.out_stride, 3, a.dtype))) return rc;
+  if ((rc = check_planes("y_pre", a.y_pre, a.y_stride))) return rc;
+  if ((rc = check_planes("z_pre", a.z_pre, a.z_stride))) return rc;
+  if (!a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.lse)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter table, offsets or lse is NULL");
+  return DWARF_OK;
+}
+
+int check_contig_rows(const char* name, const void* p, const int64_t* stride, int dtype) {
+  return check_rows(name, p, stride, 3, dtype);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dwarf_abi_version(void) { return DWARF_ABI_VERSION; }
+
+const char* dwarf_last_error(void) { return g_error; }
+
+int dwarf_dsqg_fwd(const dwarf_dsqg_fwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  int rc = check_fwd(*args);
+  if (rc) return rc;
+  if (args->B == 0 || args->N == 0) return ok();
+  return hip_status(dwarf::launch_dsqg_fwd(*args, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_fwd");
+}
+
+size_t dwarf_dsqg_bwd_workspace_bytes(const dwarf_dsqg_bwd_args* args) {
+  if (!args) return 0;
+  return dwarf::bwd_workspace_layout(*args).total;
+}
+
+static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, bool do_dq, bool do_dkdv,
+                     const char* name) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_dsqg_bwd_args& a = *args;
+  int rc = check_fwd(a.fwd);
+  if (rc) return rc;
+  const int dt = a.fwd.dtype;
+  if ((rc = check_contig_rows("dout", a.dout, a.dout_stride, dt))) return rc;
+  if (do_dq) {
+    if ((rc = check_contig_rows("dq", a.dq, a.dq_stride, dt))) return rc;
+    if (!a.dpos_bias || !a.dscale_embed || !a.dphase_base || !a.dphase_gain || !a.dy_pre)
+      return fail(DWARF_ERR_INVALID_ARGUMENT, "a gradient output is NULL");
+    if (!aligned16(a.dy_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dy_pre must be 16-byte aligned");
+  }
+  if (do_dkdv) {
+    if ((rc = check_contig_rows("dk", a.dk, a.dk_stride, dt))) return rc;
+    if ((rc = check_contig_rows("dv", a.dv, a.dv_stride, dt))) return rc;
+    if (!a.dz_pre) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre is NULL");
+    if (!aligned16(a.dz_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre must be 16-byte aligned");
+  }
+  if (a.fwd.B == 0 || a.fwd.N == 0) return ok();
+  const dwarf::BwdWorkspace ws = dwarf::bwd_workspace_layout(a);
+  if (!a.workspace || a.workspace_bytes < ws.total)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", ws.total, a.workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(a.workspace) & 255u) != 0)
+    return fail(DWARF_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return hip_status(dwarf::launch_dsqg_bwd(a, ws, reinterpret_cast<hipStream_t>(stream), do_dq, do_dkdv), name);
+}
+
+int dwarf_dsqg_bwd(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
+  return bwd_stage(args, stream, true, true, "dwarf_dsqg_bwd");
+}
+
+int dwarf_dsqg_bwd_dq(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
+  return bwd_stage(args, stream, true, false, "dwarf_dsqg_bwd_dq");
+}
+
+int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
+  return bwd_stage(args, stream, false, true, "dwarf_dsqg_bwd_dkdv");
+}
+
+// ---- EMA --------------------------------------------------------------------
+static int check_ema_common(int B, int N, int D, int dtype, int per_channel, float lo, float hi, const float* alpha) {
+  if (B < 0 || N < 0 || D < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes B=%d N=%d D=%d", B, N, D);
+  if (dtype != DWARF_BF16 && dtype != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);
+  if (!(lo > 0.f && lo < hi && hi < 1.f))
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "EMA bounds must satisfy 0 < floor < ceiling < 1");
+  if (per_channel != 0 && per_channel != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "alpha_per_channel=%d", per_channel);
+  if (!alpha) return fail(DWARF_ERR_INVALID_ARGUMENT, "alpha is NULL");
+  return DWARF_OK;
+}
+
+static int check_btd(const char* name, const void* p, const int64_t* s, int dtype, int D) {
+  if (!p) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (s[2] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "%s needs unit stride on D", name);
+  if (D % 4 == 0) {
+    const uintptr_t align = dtype == DWARF_BF16 ? 8 : 16;
+    if ((reinterpret_cast<uintptr_t>(p) % align) || s[0] % 4 || s[1] % 4)
+      return fail(DWARF_ERR_INVALID_ARGUMENT, "%s: with D %% 4 == 0 rows must be %zu-byte aligned", name,
+                  static_cast<size_t>(align));
+  }
+  return DWARF_OK;
+}
+
+size_t dwarf_ema_fwd_workspace_bytes(const dwarf_ema_fwd_args* a) {
+  return a ? dwarf::ema_fwd_workspace(a->B, a->N, a->D) : 0;
+}
+size_t dwarf_ema_bwd_workspace_bytes(const dwarf_ema_bwd_args* a) {
+  return a ? dwarf::ema_bwd_workspace(a->B, a->N, a->D) : 0;
+}
+
+int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_ema_fwd_args& a = *args;
+  int rc = check_ema_common(a.B, a.N, a.D, a.dtype, a.alpha_per_channel, a.floor_, a.ceiling, a.alpha);
+  if (rc) return rc;
+  if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
+  if ((rc = check_btd("y", a.y, a.y_stride, a.dtype, a.D))) return rc;
+  if (a.B == 0 || a.N == 0 || a.D == 0) return ok();
+  const size_t need = dwarf::ema_fwd_workspace(a.B, a.N, a.D);
+  if (!a.workspace || a.workspace_bytes < need)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  return hip_status(dwarf::launch_ema_fwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_ema_fwd");
+}
+
+int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_ema_bwd_args& a = *args;
+  int rc = check_ema_common(a.B, a.N, a.D, a.dtype, a.alpha_per_channel, a.floor_, a.ceiling, a.alpha);
+  if (rc) return rc;
+  if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
+  if ((rc = check_btd("y", a.y, a.y_stride, a.dtype, a.D))) return rc;
+  if ((rc = check_btd("dy", a.dy, a.dy_stride, a.dtype, a.D))) return rc;
+  if ((rc = check_btd("dx", a.dx, a.dx_stride, a.dtype, a.D))) return rc;
+  if (a.B == 0 || a.N == 0 || a.D == 0) return ok();
+  const size_t need = dwarf::ema_bwd_workspace(a.B, a.N, a.D);
+  if (!a.workspace || a.workspace_bytes < need)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  return hip_status(dwarf::launch_ema_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_ema_bwd");
+}
+
+// ---- q6 ---------------------------------------------------------------------
+static int check_cache(const uint8_t* cache, const int64_t* cs, int n_outer) {
+  if (!cache) return fail(DWARF_ERR_INVALID_ARGUMENT, "cache is NULL");
+  if (!aligned16(cache)) return fail(DWARF_ERR_INVALID_ARGUMENT, "cache must be 16-byte aligned");
+  if (cs[n_outer] != DWARF_Q6_SLOT_BYTES)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "cache slot stride must be %d bytes", DWARF_Q6_SLOT_BYTES);
+  for (int i = 0; i < n_outer; ++i)
+    if (cs[i] % 16) return fail(DWARF_ERR_INVALID_ARGUMENT, "cache stride[%d] must be a multiple of 16", i);
+  return DWARF_OK;
+}
+
+int dwarf_q6_pack_kv(int32_t B, int32_t H_kv, int32_t N, int32_t head_dim, int32_t dtype, const void* k,
+                     const int64_t k_stride[4], const void* v, const int64_t v_stride[4], uint8_t* cache,
+                     const int64_t cache_stride[3], const float* key_probes, dwarf_stream_t stream) {
+  if (B < 0 || H_kv < 0 || N < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (head_dim != dwarf::kHeadDim) return fail(DWARF_ERR_UNSUPPORTED, "head_dim=%d is not built (64 only)", head_dim);
+  if (dtype != DWARF_BF16 && dtype != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", dtype);
+  int rc;
+  if ((rc = check_rows("k", k, k_stride, 3, dtype))) return rc;
+  if ((rc = check_rows("v", v, v_stride, 3, dtype))) return rc;
+  if ((rc = check_cache(cache, cache_stride, 2))) return rc;
+  if (static_cast<int64_t>(B) * H_kv * N == 0) return ok();
+  return hip_status(dwarf::launch_q6_pack(B, H_kv, N, dtype, k, k_stride, v, v_stride, cache, cache_stride,
+                                          key_probes, reinterpret_cast<hipStream_t>(stream)),
+                    "dwarf_q6_pack_kv");
+}
+
+int dwarf_q6_unpack_kv(int32_t B, int32_t H_kv, int32_t N, int32_t head_dim, const uint8_t* cache,
+                       const int64_t cache_stride[3], float* k_out, float* v_out, dwarf_stream_t stream) {
+  if (B < 0 || H_kv < 0 || N < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (head_dim != dwarf::kHeadDim) return fail(DWARF_ERR_UNSUPPORTED, "head_dim=%d is not built (64 only)", head_dim);
+  int rc;
+  if ((rc = check_cache(cache, cache_stride, 2))) return rc;
+  if (!k_out || !v_out) return fail(DWARF_ERR_INVALID_ARGUMENT, "output is NULL");
+  if (static_cast<int64_t>(B) * H_kv * N == 0) return ok();
+  return hip_status(dwarf::launch_q6_unpack(B, H_kv, N, cache, cache_stride, k_out, v_out,
+                                            reinterpret_cast<hipStream_t>(stream)),
+                    "dwarf_q6_unpack_kv");
+}
+
+int dwarf_dsqg_q6_prefill_fwd(const dwarf_dsqg_q6_prefill_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_dsqg_q6_prefill_args& a = *args;
+  if (a.B < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "B=%d", a.B);
+  int rc = check_lattice(a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, a.query_start);
+  if (rc) return rc;
+  if ((rc = check_rows("q", a.q, a.q_stride, 3, DWARF_BF16))) return rc;
+  if ((rc = check_rows("out", a.out, a.out_stride, 3, DWARF_BF16))) return rc;
+  if ((rc = check_cache(a.cache, a.cache_stride, 2))) return rc;
+  if (!a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter table, probe table or offsets is NULL");
+  if (a.B == 0 || a.N == 0) return ok();
+  return hip_status(dwarf::launch_q6_prefill(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_q6_prefill_fwd");
+}
+
+int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_dsqg_q6_decode_args& a = *args;
+  if (a.S < 0 || a.L < 0 || a.Ncache < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes");
+  int rc = check_lattice(a.H, a.H_kv, a.Ncache, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, 0);
+  if (rc) return rc;
+  if (a.J > dwarf::q6_max_decode_offsets())
+    return fail(DWARF_ERR_UNSUPPORTED, "decode supports at most %d offsets", dwarf::q6_max_decode_offsets());
+  if ((rc = check_rows("q", a.q, a.q_stride, 3, DWARF_BF16))) return rc;
+  if (!a.out || a.out_stride[3] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "out is NULL or not unit-stride");
+  if ((rc = check_cache(a.cache, a.cache_stride, 3))) return rc;
+  if (!a.pos || !a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "positions, a parameter table, probes or offsets is NULL");
+  if (a.se_stride[2] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "scale_embed needs unit stride on head_dim");
+  if (a.S == 0 || a.L == 0) return ok();
+  return hip_status(dwarf::launch_q6_decode(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_q6_decode");
+}
+
+}  // extern "C"

@@ -1,0 +1,50 @@
+// Internal launch interface between the C-ABI layer (capi.hip) and the
+// kernel translation units.  Nothing here is exported.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "dwarf_dsqg.h"
+
+namespace dwarf {
+
+constexpr int kHeadDim = 64;
+constexpr int kBlock = 256;  // threads per workgroup for the DSQG kernels
+
+// Workgroup index -> work item, so that consecutive work items (the query
+// tiles of one (b, h), which share K/V rows) land on the same XCD and share
+// its L2.  Workgroups are dealt round-robin over the 8 XCDs of an MI355X.
+__device__ __forceinline__ int xcd_remap(int block_linear, int total) {
+  constexpr int kXcd = 8;
+  const int per = total / kXcd, rem = total % kXcd;
+  const int xcd = block_linear % kXcd, idx = block_linear / kXcd;
+  return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Geometry shared by the DSQG kernels.
+struct DsqgGeom {
+  int queries_per_block;
+  int tiles;   // query tiles per (b, h)
+  int blocks;  // tiles * B * H
+};
+
+hipError_t launch_dsqg_fwd(const dwarf_dsqg_fwd_args& a, hipStream_t stream);
+
+// Backward workspace layout (bytes, 256-byte aligned sections).
+struct BwdWorkspace {
+  size_t delta_off, delta_bytes;        // [B,H,N] fp32
+  size_t part_se_off, part_se_bytes;    // [blocks_q][J][64] fp32
+  size_t part_pb_off, part_pb_bytes;    // [blocks_q][J] fp32
+  size_t part_ph_off, part_ph_bytes;    // [blocks_q][J_L][4][2] fp32
+  size_t total;
+  int blocks_q;                         // query-centric workgroups
+};
+BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a);
+// do_dq: delta + dQ/dY + parameter-gradient partials and their reduction;
+// do_dkdv: dK/dV/dZ (reads the delta written by the dq stage).
+hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
+                           bool do_dkdv);
+
+}  // namespace dwarf

@@ -1,0 +1,482 @@
+// q6 K/V cache: codec, prefill forward and decode step.
+//
+// Format (no counterpart in the reference repository):
+// a head-dim row of 64 values is two groups of 32.  Per group
+//   scale = fp16_rne(absmax / 31)   (fp32 division; +inf saturates to 65504)
+//   code  = clamp(rint(x / float(scale)), -31, 31), 0 when scale == 0
+// Codes are packed 4 per 24-bit little-endian word, w = sum (c_i & 63) << 6i,
+// so element e of a group sits at bits [6e, 6e+6) of the group's 24 bytes.
+// dequant(e) = float(sign_extend6(code)) * float(scale), exact in fp32.
+//
+// Cache slot, one per (b, kv head, t), 128 bytes:
+//   [0,48) K codes   [48,52) K scales   [52,100) V codes   [100,104) V scales
+//   [104,120) z[4] fp32 (key-probe features of the dequantised K row)
+//   [120,128) zero
+// A gathered offset therefore reads exactly one 128-byte line.
+#include "common.h"
+#include "dsqg_internal.h"
+
+namespace dwarf {
+namespace {
+
+constexpr int kSlot = DWARF_Q6_SLOT_BYTES;
+constexpr int kGroup = DWARF_Q6_GROUP;
+constexpr int kKCodes = 0, kKScales = 48, kVCodes = 52, kVScales = 100, kZ = 104;
+
+__device__ __forceinline__ float half_bits_to_f32(uint16_t hbits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, hbits));
+}
+
+// Quantise one group of 32 fp32 values; returns the fp16 scale bits.
+__device__ __forceinline__ uint16_t q6_quantize_group(const float* x, uint8_t* codes24) {
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < kGroup; ++e) amax = fmaxf(amax, fabsf(x[e]));
+  const _Float16 hs = static_cast<_Float16>(__fdiv_rn(amax, 31.f));  // round to nearest even
+  uint16_t sbits = __builtin_bit_cast(uint16_t, hs);
+  if ((sbits & 0x7fffu) == 0x7c00u) sbits = (sbits & 0x8000u) | 0x7bffu;  // saturate +inf
+  const float sc = half_bits_to_f32(sbits);
+  uint32_t w = 0;
+#pragma unroll
+  for (int e = 0; e < kGroup; ++e) {
+    int c = 0;
+    if (sc != 0.f) {
+      const float r = rintf(__fdiv_rn(x[e], sc));
+      c = static_cast<int>(fminf(fmaxf(r, -31.f), 31.f));
+    }
+    w |= (static_cast<uint32_t>(c) & 63u) << (6 * (e & 3));
+    if ((e & 3) == 3) {
+      const int k = e >> 2;
+      codes24[3 * k + 0] = static_cast<uint8_t>(w);
+      codes24[3 * k + 1] = static_cast<uint8_t>(w >> 8);
+      codes24[3 * k + 2] = static_cast<uint8_t>(w >> 16);
+      w = 0;
+    }
+  }
+  return sbits;
+}
+
+// 32 signed codes of one group from its 24 bytes (6 dwords, 4-byte aligned).
+__device__ __forceinline__ void q6_codes(const uint8_t* p, float* c) {
+  uint32_t dw[7];
+  const uint32_t* p32 = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) dw[i] = p32[i];
+  dw[6] = 0;
+#pragma unroll
+  for (int e = 0; e < kGroup; ++e) {
+    const int bit = 6 * e;
+    const int i = bit >> 5, sh = bit & 31;
+    const uint64_t pair = (static_cast<uint64_t>(dw[i + 1]) << 32) | dw[i];
+    const int v = static_cast<int>(static_cast<uint32_t>(pair >> sh) << 26) >> 26;
+    c[e] = static_cast<float>(v);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void q6_pack_kernel(int B, int Hkv, int N, const T* __restrict__ k,
+                                                         const int64_t* ks, const T* __restrict__ v,
+                                                         const int64_t* vs, uint8_t* __restrict__ cache,
+                                                         const int64_t* cs, const float* __restrict__ kprobe,
+                                                         int64_t ks0, int64_t ks1, int64_t ks2, int64_t vs0,
+                                                         int64_t vs1, int64_t vs2, int64_t cs0, int64_t cs1,
+                                                         int64_t cs2) {
+  (void)ks; (void)vs; (void)cs;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (idx >= static_cast<int64_t>(B) * Hkv * N) return;
+  const int t = idx % N;
+  const int hk = (idx / N) % Hkv;
+  const int b = idx / (static_cast<int64_t>(N) * Hkv);
+  float kr[kHeadDim], vr[kHeadDim];
+  load_f32<T, kHeadDim>(k + b * ks0 + hk * ks1 + static_cast<int64_t>(t) * ks2, kr);
+  load_f32<T, kHeadDim>(v + b * vs0 + hk * vs1 + static_cast<int64_t>(t) * vs2, vr);
+  alignas(16) uint8_t slot[kSlot];
+#pragma unroll
+  for (int i = 0; i < kSlot; ++i) slot[i] = 0;
+  uint16_t sk0 = q6_quantize_group(kr, slot + kKCodes);
+  uint16_t sk1 = q6_quantize_group(kr + kGroup, slot + kKCodes + 24);
+  uint16_t sv0 = q6_quantize_group(vr, slot + kVCodes);
+  uint16_t sv1 = q6_quantize_group(vr + kGroup, slot + kVCodes + 24);
+  slot[kKScales + 0] = sk0 & 0xff; slot[kKScales + 1] = sk0 >> 8;
+  slot[kKScales + 2] = sk1 & 0xff; slot[kKScales + 3] = sk1 >> 8;
+  slot[kVScales + 0] = sv0 & 0xff; slot[kVScales + 1] = sv0 >> 8;
+  slot[kVScales + 2] = sv1 & 0xff; slot[kVScales + 3] = sv1 >> 8;
+  if (kprobe) {
+    // z from the dequantised K row, as the prefill/decode kernels see it.
+    float kq[kHeadDim];
+    q6_codes(slot + kKCodes, kq);
+    q6_codes(slot + kKCodes + 24, kq + kGroup);
+    const float s0 = half_bits_to_f32(sk0), s1 = half_bits_to_f32(sk1);
+    float ss = 0.f;
+#pragma unroll
+    for (int d = 0; d < kHeadDim; ++d) {
+      kq[d] *= d < kGroup ? s0 : s1;
+      ss = fmaf(kq[d], kq[d], ss);
+    }
+    const float inv = rsqrtf(ss + 1e-6f * kHeadDim);
+    float z[4];
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) {
+      float acc = 0.f;
+      for (int d = 0; d < kHeadDim; ++d) acc = fmaf(kq[d], kprobe[r * kHeadDim + d], acc);
+      z[r] = acc * inv;
+    }
+    float* zp = reinterpret_cast<float*>(slot + kZ);
+    zp[0] = z[0]; zp[1] = z[1]; zp[2] = z[2]; zp[3] = z[3];
+  }
+  uint4* dst = reinterpret_cast<uint4*>(cache + b * cs0 + hk * cs1 + static_cast<int64_t>(t) * cs2);
+  const uint4* src = reinterpret_cast<const uint4*>(slot);
+#pragma unroll
+  for (int i = 0; i < kSlot / 16; ++i) dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(kBlock) void q6_unpack_kernel(int B, int Hkv, int N, const uint8_t* __restrict__ cache,
+                                                           int64_t cs0, int64_t cs1, int64_t cs2,
+                                                           float* __restrict__ kout, float* __restrict__ vout) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t rows = static_cast<int64_t>(B) * Hkv * N;
+  if (idx >= rows * 4) return;
+  const int part = idx % 4;  // K g0, K g1, V g0, V g1
+  const int64_t row = idx / 4;
+  const int t = row % N;
+  const int hk = (row / N) % Hkv;
+  const int b = row / (static_cast<int64_t>(N) * Hkv);
+  const uint8_t* slot = cache + b * cs0 + hk * cs1 + static_cast<int64_t>(t) * cs2;
+  const int grp = part & 1;
+  const bool is_v = part >= 2;
+  const uint8_t* codes = slot + (is_v ? kVCodes : kKCodes) + 24 * grp;
+  const uint16_t sb = *reinterpret_cast<const uint16_t*>(slot + (is_v ? kVScales : kKScales) + 2 * grp);
+  const float sc = half_bits_to_f32(sb);
+  float c[kGroup];
+  q6_codes(codes, c);
+  float* dst = (is_v ? vout : kout) + row * kHeadDim + grp * kGroup;
+#pragma unroll
+  for (int e = 0; e < kGroup; ++e) dst[e] = c[e] * sc;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill forward.  Two lanes per query, each owning one 32-wide group, so a
+// lane dequantises exactly the K and V groups it multiplies.  q.k is formed
+// on the integer codes and scaled once per group.
+// ---------------------------------------------------------------------------
+constexpr float kRescaleSlack = 8.0f;
+
+template <int SHIFT>
+__global__ __launch_bounds__(kBlock) void q6_prefill_kernel(const dwarf_dsqg_q6_prefill_args a, int tiles, int total) {
+  constexpr int L = 2, DPL = 32, QPB = kBlock / L, HD = kHeadDim, SEG = HD / kPlanes;
+  extern __shared__ float smem[];
+  float* s_se = smem;                       // [J][64]
+  float* s_pb = s_se + a.J * HD;            // [J]
+  float* s_qp = s_pb + a.J;                 // [4][64] query probes
+  int* s_off = reinterpret_cast<int*>(s_qp + kPlanes * HD);
+
+  const int work = xcd_remap(blockIdx.x, total);
+  const int bh = work / tiles;
+  const int tile = work - bh * tiles;
+  const int b = bh / a.H;
+  const int h = bh - b * a.H;
+  const int hk = h / (a.H / a.H_kv);
+  for (int i = threadIdx.x; i < a.J * HD; i += kBlock) {
+    const int j = i / HD, d = i - j * HD;
+    const float e = a.scale_embed[j * a.se_stride[0] + d * a.se_stride[1]];
+    s_se[i] = a.se_round_bf16 ? round_bf16(e) : e;
+  }
+  for (int j = threadIdx.x; j < a.J; j += kBlock) {
+    s_pb[j] = a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]];
+    s_off[j] = a.offsets[j];
+  }
+  for (int i = threadIdx.x; i < kPlanes * HD; i += kBlock) s_qp[i] = a.query_probes[i];
+  __syncthreads();
+
+  const int lane = threadIdx.x;
+  const int g = lane % L;
+  const int n = tile * QPB + lane / L;
+  const int wave_n_last = uniform(tile * QPB + (lane / kWave) * (kWave / L)) + kWave / L - 1;
+  if (n >= a.N) return;
+  bf16* orow = reinterpret_cast<bf16*>(a.out) + b * a.out_stride[0] + h * a.out_stride[1] +
+               static_cast<int64_t>(n) * a.out_stride[2] + g * DPL;
+
+  float acc[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
+  float m = -INFINITY, l = 0.f;
+
+  if (n >= a.query_start) {
+    float q[DPL];
+    load_f32<bf16, DPL>(reinterpret_cast<const bf16*>(a.q) + b * a.q_stride[0] + h * a.q_stride[1] +
+                            static_cast<int64_t>(n) * a.q_stride[2] + g * DPL, q);
+    // y[r] = <q, probe_r> / sqrt(|q|^2 + 1e-6 hd)  (dsqg:3234-3249)
+    float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) {
+      ss = fmaf(q[d], q[d], ss);
+#pragma unroll
+      for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(q[d], s_qp[r * HD + g * DPL + d], yp[r]);
+    }
+    ss = group_sum<L>(ss);
+    const float qinv = rsqrtf(ss + 1e-6f * HD);
+    float ys[4];
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) ys[r] = group_sum<L>(yp[r]) * qinv;
+
+    const uint8_t* cbase = a.cache + b * a.cache_stride[0] + hk * a.cache_stride[1];
+    constexpr float scale = 0.125f;
+    for (int j = 0; j < a.J; ++j) {
+      const int delta = s_off[j];
+      if (wave_n_last < delta) continue;
+      const int s = n - delta;
+      if (s < 0 || s >= a.N) continue;
+      const uint8_t* slot = cbase + static_cast<int64_t>(s) * a.cache_stride[2];
+      float c[DPL];
+      q6_codes(slot + kKCodes + 24 * g, c);
+      const float ksc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kKScales + 2 * g));
+      const float* e = s_se + j * HD + g * DPL;
+      float dk = 0.f, de = 0.f;
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) { dk = fmaf(q[d], c[d], dk); de = fmaf(q[d], e[d], de); }
+      const float dot = group_sum<L>(fmaf(dk, ksc, de));
+      const float score = fmaf(dot, scale, s_pb[j]);
+
+      q6_codes(slot + kVCodes + 24 * g, c);
+      const float vsc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kVScales + 2 * g));
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) c[d] *= vsc;
+      if (j >= a.J_small) {
+        const int i = j - a.J_small;
+        const float4 zk = *reinterpret_cast<const float4*>(slot + kZ);
+        const float zs[4] = {zk.x, zk.y, zk.z, zk.w};
+#pragma unroll
+        for (int r = 0; r < kPlanes; ++r) {
+          const int ch = r * SEG + SHIFT;
+          if (ch / DPL != g) continue;
+          const int la = ch % DPL;
+          const float theta = a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r] +
+                              a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r] * ys[r] * zs[r];
+          float sn, cs;
+          dsincos<true>(theta, &sn, &cs);
+          const float va = c[la], vb = c[la + 1];
+          c[la] = cs * va - sn * vb;
+          c[la + 1] = sn * va + cs * vb;
+        }
+      }
+      if (score > m + kRescaleSlack) {
+        const float cc = __expf(m - score);
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) acc[d] *= cc;
+        l *= cc;
+        m = score;
+      }
+      const float p = __expf(score - m);
+      l += p;
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) acc[d] = fmaf(p, c[d], acc[d]);
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) acc[d] *= inv;
+  store_from_f32<bf16, DPL>(orow, acc);
+  if (a.lse && g == 0)
+    a.lse[b * a.lse_stride[0] + h * a.lse_stride[1] + static_cast<int64_t>(n) * a.lse_stride[2]] =
+        l > 0.f ? m + __logf(l) : -INFINITY;
+}
+
+// ---------------------------------------------------------------------------
+// Decode.  One wave per (sequence, layer, head).  Lane pair (jl, g): offset
+// jl of each 32-offset round, group g of the head dims.  Scores of all
+// offsets are kept in registers, the softmax is reduced over the wave, and
+// the weighted V rows are summed through LDS.
+// ---------------------------------------------------------------------------
+constexpr int kDecRounds = 4;  // up to 128 offsets
+
+template <int SHIFT>
+__global__ __launch_bounds__(kBlock) void q6_decode_kernel(const dwarf_dsqg_q6_decode_args a, int items) {
+  constexpr int L = 2, DPL = 32, HD = kHeadDim, SEG = HD / kPlanes, OPR = kWave / L;
+  __shared__ float s_red[kBlock / kWave][OPR][HD + 1];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int item = blockIdx.x * (kBlock / kWave) + wave;  // (s, l, h)
+  if (item >= items) return;  // whole wave leaves together; no block barriers
+  const int h = item % a.H;
+  const int ly = (item / a.H) % a.L;
+  const int sq = item / (a.H * a.L);
+  const int hk = h / (a.H / a.H_kv);
+  const int g = lane % L;
+  const int jl = lane / L;
+  const int t = a.pos[sq];
+
+  float q[DPL];
+  load_f32<bf16, DPL>(reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1] +
+                          h * a.q_stride[2] + g * DPL, q);
+  const float* qp = a.query_probes + ly * a.qprobe_layer_stride;
+  float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) {
+    ss = fmaf(q[d], q[d], ss);
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(q[d], qp[r * HD + g * DPL + d], yp[r]);
+  }
+  ss = group_sum<L>(ss);
+  const float qinv = rsqrtf(ss + 1e-6f * HD);
+  float ys[4];
+#pragma unroll
+  for (int r = 0; r < kPlanes; ++r) ys[r] = group_sum<L>(yp[r]) * qinv;
+
+  const float* pb = a.pos_bias + ly * a.pb_stride[0];
+  const float* se = a.scale_embed + ly * a.se_stride[0];
+  const float* pbase = a.phase_base + ly * a.pbase_stride[0];
+  const float* pgain = a.phase_gain + ly * a.pgain_stride[0];
+  const uint8_t* cbase = a.cache + ly * a.cache_stride[0] + sq * a.cache_stride[1] + hk * a.cache_stride[2];
+  constexpr float scale = 0.125f;
+
+  float sc[kDecRounds];
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int rd = 0; rd < kDecRounds; ++rd) {
+    sc[rd] = -INFINITY;
+    if (rd * OPR >= a.J) continue;  // uniform
+    const int j = rd * OPR + jl;
+    const int jc = j < a.J ? j : a.J - 1;
+    const int s = t - a.offsets[jc];
+    const bool ok = j < a.J && s >= 0 && s < a.Ncache;  // identical for both lanes of a pair
+    float part = 0.f;
+    if (ok) {
+      const uint8_t* slot = cbase + static_cast<int64_t>(s) * a.cache_stride[3];
+      float c[DPL];
+      q6_codes(slot + kKCodes + 24 * g, c);
+      const float ksc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kKScales + 2 * g));
+      const float* e = se + jc * a.se_stride[1] + g * DPL;
+      float dk = 0.f, de = 0.f;
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) {
+        const float ev = a.se_round_bf16 ? round_bf16(e[d]) : e[d];
+        dk = fmaf(q[d], c[d], dk);
+        de = fmaf(q[d], ev, de);
+      }
+      part = fmaf(dk, ksc, de);
+    }
+    part = group_sum<L>(part);
+    if (ok) sc[rd] = fmaf(part, scale, pb[jc * a.pb_stride[1] + h * a.pb_stride[2]]);
+    mloc = fmaxf(mloc, sc[rd]);
+  }
+  // wave max
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o));
+  float acc[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
+  float lsum = 0.f;
+#pragma unroll
+  for (int rd = 0; rd < kDecRounds; ++rd) {
+    if (rd * OPR >= a.J) continue;
+    const int j = rd * OPR + jl;
+    if (sc[rd] == -INFINITY) continue;
+    const float p = __expf(sc[rd] - mloc);
+    lsum += p;
+    const int s = t - a.offsets[j];
+    const uint8_t* slot = cbase + static_cast<int64_t>(s) * a.cache_stride[3];
+    float c[DPL];
+    q6_codes(slot + kVCodes + 24 * g, c);
+    const float vsc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kVScales + 2 * g));
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) c[d] *= vsc;
+    if (j >= a.J_small) {
+      const int i = j - a.J_small;
+      const float4 zk = *reinterpret_cast<const float4*>(slot + kZ);
+      const float zs[4] = {zk.x, zk.y, zk.z, zk.w};
+#pragma unroll
+      for (int r = 0; r < kPlanes; ++r) {
+        const int ch = r * SEG + SHIFT;
+        if (ch / DPL != g) continue;
+        const int la = ch % DPL;
+        const float theta = pbase[i * a.pbase_stride[1] + h * a.pbase_stride[2] + r] +
+                            pgain[i * a.pgain_stride[1] + h * a.pgain_stride[2] + r] * ys[r] * zs[r];
+        float sn, cs;
+        dsincos<true>(theta, &sn, &cs);
+        const float va = c[la], vb = c[la + 1];
+        c[la] = cs * va - sn * vb;
+        c[la + 1] = sn * va + cs * vb;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DPL; ++d) acc[d] = fmaf(p, c[d], acc[d]);
+  }
+  // lsum counts each offset twice (both lanes of a pair).
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) lsum += __shfl_xor(lsum, o);
+  lsum *= 0.5f;
+  // Sum acc over the 32 offset slots of each group through LDS.
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) s_red[wave][jl][g * DPL + d] = acc[d];
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float o = 0.f;
+  for (int k = 0; k < OPR; ++k) o += s_red[wave][k][lane];
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  reinterpret_cast<uint16_t*>(a.out)[sq * a.out_stride[0] + ly * a.out_stride[1] + h * a.out_stride[2] + lane] =
+      f32_to_bf16_bits(o * inv);
+}
+
+}  // namespace
+
+hipError_t launch_q6_pack(int B, int Hkv, int N, int dtype, const void* k, const int64_t* ks, const void* v,
+                          const int64_t* vs, uint8_t* cache, const int64_t* cs, const float* kprobe,
+                          hipStream_t stream) {
+  const int64_t rows = static_cast<int64_t>(B) * Hkv * N;
+  const int blocks = static_cast<int>((rows + kBlock - 1) / kBlock);
+  if (dtype == DWARF_BF16)
+    hipLaunchKernelGGL(q6_pack_kernel<bf16>, dim3(blocks), dim3(kBlock), 0, stream, B, Hkv, N,
+                       static_cast<const bf16*>(k), nullptr, static_cast<const bf16*>(v), nullptr, cache, nullptr,
+                       kprobe, ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], cs[0], cs[1], cs[2]);
+  else
+    hipLaunchKernelGGL(q6_pack_kernel<float>, dim3(blocks), dim3(kBlock), 0, stream, B, Hkv, N,
+                       static_cast<const float*>(k), nullptr, static_cast<const float*>(v), nullptr, cache, nullptr,
+                       kprobe, ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], cs[0], cs[1], cs[2]);
+  return hipGetLastError();
+}
+
+hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const int64_t* cs, float* kout,
+                            float* vout, hipStream_t stream) {
+  const int64_t parts = static_cast<int64_t>(B) * Hkv * N * 4;
+  const int blocks = static_cast<int>((parts + kBlock - 1) / kBlock);
+  hipLaunchKernelGGL(q6_unpack_kernel, dim3(blocks), dim3(kBlock), 0, stream, B, Hkv, N, cache, cs[0], cs[1], cs[2],
+                     kout, vout);
+  return hipGetLastError();
+}
+
+hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream) {
+  constexpr int QPB = kBlock / 2;
+  const int tiles = (a.N + QPB - 1) / QPB;
+  const int total = tiles * a.B * a.H;
+  const size_t lds = (static_cast<size_t>(a.J) * (kHeadDim + 2) + kPlanes * kHeadDim) * sizeof(float);
+#define DWARF_Q6P_CASE(S) \
+  case S: hipLaunchKernelGGL(q6_prefill_kernel<S>, dim3(total), dim3(kBlock), lds, stream, a, tiles, total); break;
+  switch (a.plane_shift) {
+    DWARF_Q6P_CASE(0) DWARF_Q6P_CASE(1) DWARF_Q6P_CASE(2) DWARF_Q6P_CASE(3) DWARF_Q6P_CASE(4)
+    DWARF_Q6P_CASE(5) DWARF_Q6P_CASE(6) DWARF_Q6P_CASE(7) DWARF_Q6P_CASE(8) DWARF_Q6P_CASE(9)
+    DWARF_Q6P_CASE(10) DWARF_Q6P_CASE(11) DWARF_Q6P_CASE(12) DWARF_Q6P_CASE(13) DWARF_Q6P_CASE(14)
+    default: return hipErrorInvalidValue;
+  }
+#undef DWARF_Q6P_CASE
+  return hipGetLastError();
+}
+
+hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream) {
+  const int items = a.S * a.L * a.H;
+  const int blocks = (items + kBlock / kWave - 1) / (kBlock / kWave);
+#define DWARF_Q6D_CASE(S) \
+  case S: hipLaunchKernelGGL(q6_decode_kernel<S>, dim3(blocks), dim3(kBlock), 0, stream, a, items); break;
+  switch (a.plane_shift) {
+    DWARF_Q6D_CASE(0) DWARF_Q6D_CASE(1) DWARF_Q6D_CASE(2) DWARF_Q6D_CASE(3) DWARF_Q6D_CASE(4)
+    DWARF_Q6D_CASE(5) DWARF_Q6D_CASE(6) DWARF_Q6D_CASE(7) DWARF_Q6D_CASE(8) DWARF_Q6D_CASE(9)
+    DWARF_Q6D_CASE(10) DWARF_Q6D_CASE(11) DWARF_Q6D_CASE(12) DWARF_Q6D_CASE(13) DWARF_Q6D_CASE(14)
+    default: return hipErrorInvalidValue;
+  }
+#undef DWARF_Q6D_CASE
+  return hipGetLastError();
+}
+
+int q6_max_decode_offsets() { return kDecRounds * (kWave / 2); }
+
+}  // namespace dwarf

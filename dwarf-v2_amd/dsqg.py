@@ -1,0 +1,254 @@
+"""DSQG offset-gather attention on MI355X: the drop-in for the reference op.
+
+``dsqg_attention_v18_grouped`` keeps the reference signature
+(kernels/dsqg_attention_v22.py:2691-2719) and ``_DSQGV18GroupedFn`` keeps the
+25-argument autograd contract (dsqg:2194-2552).  Both run the HIP kernels of
+libdwarf_dsqg.so through its C ABI; there is no CPU path.  A caller patches
+the reference module's global::
+
+    import importlib
+    dsqg_amd = importlib.import_module("dwarf-v2_amd.dsqg")
+    dsqg_attention_v22.dsqg_attention_v18_grouped = dsqg_amd.dsqg_attention_v18_grouped
+
+Precision: bf16 inputs run the bf16 kernels with the reference GPU path's
+numerics (scale embeddings rounded to bf16, dsqg:760-763; fp32 softmax and
+accumulation; bf16 outputs and dQ/dK/dV).  fp32 inputs run fp32 kernels with
+the eager oracle's numerics (unrounded scale embeddings, dsqg:2660); the
+reference GPU path would round them to bf16 first (dsqg:2746-2749).  Any other
+dtype is cast to bf16, as the reference does.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .lattice import GROUPED_MODE_IDS, R_PLANES
+
+HEAD_DIM = 64
+_SLAB_MODES = (GROUPED_MODE_IDS["overlap_slab"], GROUPED_MODE_IDS["overlap_slab_bwd"])
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _rows_ok(t: torch.Tensor) -> bool:
+    """Unit head-dim stride and 16-byte aligned rows, as the kernels load them."""
+    per16 = 16 // t.element_size()
+    return (
+        t.stride(-1) == 1
+        and t.data_ptr() % 16 == 0
+        and all(s % per16 == 0 for s in t.stride()[:-1])
+    )
+
+
+def _kernel_rows(t: torch.Tensor) -> torch.Tensor:
+    return t if _rows_ok(t) else t.contiguous()
+
+
+def _planes(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _fill_fwd(a: _lib.DsqgFwdArgs, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
+              offsets, j_small, j_large, plane_shift, query_start, out, lse, se_round) -> None:
+    B, H, N, HD = q.shape
+    a.B, a.H, a.H_kv, a.N, a.head_dim = B, H, k.shape[1], N, HD
+    a.J, a.J_small, a.J_large = int(j_small) + int(j_large), int(j_small), int(j_large)
+    a.plane_shift, a.query_start = int(plane_shift), int(query_start)
+    a.dtype = _lib.DWARF_F32 if q.dtype == torch.float32 else _lib.DWARF_BF16
+    a.se_round_bf16 = int(se_round)
+    a.q, a.q_stride = q.data_ptr(), _lib.i64_array(q.stride())
+    a.k, a.k_stride = k.data_ptr(), _lib.i64_array(k.stride())
+    a.v, a.v_stride = v.data_ptr(), _lib.i64_array(v.stride())
+    a.pos_bias, a.pb_stride = pos_bias.data_ptr(), _lib.i64_array(pos_bias.stride())
+    a.scale_embed, a.se_stride = scale_embed.data_ptr(), _lib.i64_array(scale_embed.stride())
+    a.phase_base, a.pbase_stride = phase_base.data_ptr(), _lib.i64_array(phase_base.stride()[:2])
+    a.phase_gain, a.pgain_stride = phase_gain.data_ptr(), _lib.i64_array(phase_gain.stride()[:2])
+    a.y_pre, a.y_stride = y_pre.data_ptr(), _lib.i64_array(y_pre.stride()[:3])
+    a.z_pre, a.z_stride = z_pre.data_ptr(), _lib.i64_array(z_pre.stride()[:3])
+    a.offsets = offsets.data_ptr()
+    a.out, a.out_stride = out.data_ptr(), _lib.i64_array(out.stride())
+    a.lse, a.lse_stride = lse.data_ptr(), _lib.i64_array(lse.stride())
+
+
+def _device_offsets(offsets_dev: torch.Tensor, device: torch.device, j_val: int) -> torch.Tensor:
+    off = offsets_dev
+    if off.device != device or off.dtype != torch.int32:
+        off = off.to(device=device, dtype=torch.int32)
+    off = off.contiguous()
+    if off.numel() != j_val:
+        raise ValueError(f"offsets_dev has {off.numel()} entries, expected j_val={j_val}")
+    return off
+
+
+def dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
+                 j_small, j_large, plane_shift=0, query_start=0, *, events=None):
+    """Raw forward launch: returns (out, lse).  q/k/v share one dtype (bf16 or fp32).
+
+    ``events``: optional (start, end) torch.cuda.Event pair recorded around the
+    launch on the current stream.
+    """
+    lib = _lib.load()
+    B, H, N, _ = q.shape
+    out = torch.empty((B, H, N, q.shape[3]), device=q.device, dtype=q.dtype)
+    lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
+    args = _lib.DsqgFwdArgs()
+    _fill_fwd(args, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
+              j_small, j_large, plane_shift, query_start, out, lse, se_round=q.dtype != torch.float32)
+    if events:
+        events[0].record()
+    _lib.check(lib.dwarf_dsqg_fwd(ctypes.byref(args), _stream(q.device)), "dwarf_dsqg_fwd")
+    if events:
+        events[1].record()
+    return out, lse
+
+
+def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
+                  out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None):
+    """Raw backward: the dq launch then the dkdv launch on the current stream.
+
+    Returns (dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz).  ``events``:
+    optional three torch.cuda.Events recorded before dq, between, and after dkdv.
+    """
+    lib = _lib.load()
+    dev = q.device
+    dout = _kernel_rows(dout.to(q.dtype))
+    dq = torch.empty(q.shape, device=dev, dtype=q.dtype)
+    dk = torch.empty(k.shape, device=dev, dtype=k.dtype)
+    dv = torch.empty(v.shape, device=dev, dtype=v.dtype)
+    dpb = torch.empty(pos_bias.shape, device=dev, dtype=torch.float32)
+    dse = torch.empty(scale_embed.shape, device=dev, dtype=torch.float32)
+    dpbase = torch.zeros(phase_base.shape, device=dev, dtype=torch.float32)
+    dpgain = torch.zeros(phase_gain.shape, device=dev, dtype=torch.float32)
+    dy = torch.empty(y_pre.shape, device=dev, dtype=torch.float32)
+    dz = torch.empty(z_pre.shape, device=dev, dtype=torch.float32)
+    args = _lib.DsqgBwdArgs()
+    _fill_fwd(args.fwd, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
+              j_small, j_large, plane_shift, query_start, out, lse, se_round=q.dtype != torch.float32)
+    args.dout, args.dout_stride = dout.data_ptr(), _lib.i64_array(dout.stride())
+    args.dq, args.dq_stride = dq.data_ptr(), _lib.i64_array(dq.stride())
+    args.dk, args.dk_stride = dk.data_ptr(), _lib.i64_array(dk.stride())
+    args.dv, args.dv_stride = dv.data_ptr(), _lib.i64_array(dv.stride())
+    args.dpos_bias, args.dscale_embed = dpb.data_ptr(), dse.data_ptr()
+    args.dphase_base, args.dphase_gain = dpbase.data_ptr(), dpgain.data_ptr()
+    args.dy_pre, args.dz_pre = dy.data_ptr(), dz.data_ptr()
+    nbytes = lib.dwarf_dsqg_bwd_workspace_bytes(ctypes.byref(args))
+    workspace = torch.empty(max(int(nbytes), 256), device=dev, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    stream = _stream(dev)
+    if events:
+        events[0].record()
+    _lib.check(lib.dwarf_dsqg_bwd_dq(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dq")
+    if events:
+        events[1].record()
+    _lib.check(lib.dwarf_dsqg_bwd_dkdv(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dkdv")
+    if events:
+        events[2].record()
+    return dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz
+
+
+class _DSQGV18GroupedFn(torch.autograd.Function):
+    """Autograd wrapper with the reference's 25 positional arguments (dsqg:2197-2203)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
+                j_val, j_small, j_large, offsets_dev, sparse_order_dev,
+                group_start_dev, group_len_dev, group_dmin_dev, group_dmax_dev,
+                k_group_size, grouped_mode_id, verify_mode, max_group_spread_observed,
+                plane_shift, query_start, online_softmax):
+        B, H, N, HD = q.shape
+        query_start = max(0, min(int(query_start), N))
+        Bk, H_KV, Nk, HDk = k.shape
+        if v.shape != k.shape:
+            raise ValueError(f"k/v shape mismatch: k={tuple(k.shape)} v={tuple(v.shape)}")
+        if Bk != B or Nk != N or HDk != HD:
+            raise ValueError(f"native GQA requires q/k/v to share B,N,HD: q={tuple(q.shape)} k={tuple(k.shape)}")
+        if H % H_KV != 0:
+            raise ValueError(f"num query heads H={H} must be divisible by KV heads H_KV={H_KV}")
+        if H != H_KV and int(grouped_mode_id) in _SLAB_MODES:
+            raise NotImplementedError("native GQA is currently implemented for grouped_mode='baseline' only")
+        if tuple(y_pre.shape[:3]) != (B, H, N):
+            raise ValueError(f"y_pre must have shape [B,Hq,N,R]; got {tuple(y_pre.shape)} for q={tuple(q.shape)}")
+        if tuple(z_pre.shape[:3]) != (B, H_KV, N):
+            raise ValueError(f"z_pre must have shape [B,Hkv,N,R]; got {tuple(z_pre.shape)} for k={tuple(k.shape)}")
+        assert q.dtype in (torch.bfloat16, torch.float32)
+        if not q.is_cuda:
+            raise RuntimeError("DSQG HIP kernels require device tensors")
+        if HD != HEAD_DIM or y_pre.shape[3] != R_PLANES:
+            raise RuntimeError(f"Unsupported DSQG launch shape: head_dim={HD}, planes={y_pre.shape[3]} "
+                               f"(built for head_dim={HEAD_DIM}, {R_PLANES} planes)")
+        if int(j_small) + int(j_large) != int(j_val):
+            raise ValueError(f"j_val={j_val} != j_small={j_small} + j_large={j_large}")
+        q, k, v = _kernel_rows(q), _kernel_rows(k.to(q.dtype)), _kernel_rows(v.to(q.dtype))
+        pos_bias = pos_bias.float().contiguous()
+        scale_embed = scale_embed.float().contiguous()
+        phase_base = phase_base.float().contiguous()
+        phase_gain = phase_gain.float().contiguous()
+        y_pre, z_pre = _planes(y_pre.float()), _planes(z_pre.float())
+        offsets = _device_offsets(offsets_dev, q.device, int(j_val))
+        out, lse = dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets,
+                                int(j_small), int(j_large), int(plane_shift), query_start)
+        ctx.save_for_backward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
+                              out, lse, offsets)
+        ctx.j_small, ctx.j_large = int(j_small), int(j_large)
+        ctx.plane_shift, ctx.query_start = int(plane_shift), query_start
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
+         out, lse, offsets) = ctx.saved_tensors
+        grads = dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
+                              offsets, out, lse, ctx.j_small, ctx.j_large, ctx.plane_shift, ctx.query_start)
+        return grads + (None,) * 16
+
+
+def dsqg_attention_v18_grouped(
+    q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
+    j_val, j_small, j_large, offsets_dev, sparse_order_dev, group_start_dev, group_len_dev,
+    group_dmin_dev, group_dmax_dev, k_group_size, grouped_mode_id, verify_mode,
+    max_group_spread_observed, plane_shift=0, query_start=0, *, backend: str = "auto",
+    online_softmax: bool = True,
+):
+    """DSQG attention on the HIP kernels (reference signature: dsqg:2691-2719).
+
+    ``backend`` accepts the reference's values: "auto" and "triton" (both run
+    the HIP kernels here; "hip" is an alias) and "eager", which the reference
+    maps to its CPU oracle.  This library ships no CPU path, so "eager" and
+    non-device tensors raise instead of falling back.  ``online_softmax`` and
+    the overlap-slab ``grouped_mode_id`` values select schedules of the same
+    mathematics in the reference; they are accepted and run the one HIP
+    schedule.  The five sparse-plan buffers are unused, as in the baseline mode.
+    """
+    del verify_mode, sparse_order_dev, group_start_dev, group_len_dev, group_dmin_dev, group_dmax_dev
+    del k_group_size, max_group_spread_observed, online_softmax
+    backend = str(backend).lower()
+    if backend not in {"auto", "triton", "hip", "eager"}:
+        raise ValueError("backend must be auto, triton, hip, or eager")
+    if backend == "eager":
+        raise NotImplementedError(
+            "backend='eager' selects the reference's CPU oracle, which is not part of this library"
+        )
+    if not q.is_cuda:
+        raise RuntimeError("DSQG HIP kernels were requested but the tensors are not on a GPU device")
+    original_dtype = q.dtype
+    compute = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
+    output = _DSQGV18GroupedFn.apply(
+        q.to(compute), k.to(compute), v.to(compute),
+        pos_bias.float(), scale_embed.float(), phase_base.float(), phase_gain.float(),
+        y_pre.float(), z_pre.float(),
+        int(j_val), int(j_small), int(j_large), offsets_dev, None, None, None, None, None,
+        0, int(grouped_mode_id), False, 0, int(plane_shift), int(query_start), True,
+    )
+    return output if output.dtype == original_dtype else output.to(original_dtype)

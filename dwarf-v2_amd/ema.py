@@ -1,0 +1,136 @@
+"""Causal EMA scan on MI355X, drop-in for kernels/causal_ema_scan.py.
+
+``causal_ema_scan`` (ema:541-567), ``bounded_ema_factor`` (ema:37-47) and
+``inverse_bounded_ema_factor`` (ema:50-61) keep the reference's names,
+arguments and errors.  The scan runs the HIP kernels of libdwarf_dsqg.so:
+y[t] = a x[t] + (1 - a) y[t-1] with fp32 state, a = clamp(ema_factor, floor,
+ceiling).  ``ema_factor`` may hold one value (the reference contract) or one
+value per channel of x (an extension used by the long-context benchmark).
+The reset-aware variant (``reset_mask``, ema:368-509) is not built here.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+
+def bounded_ema_factor(raw: torch.Tensor, *, floor: float = 1e-5, ceiling: float = 0.5) -> torch.Tensor:
+    """Map an unconstrained value smoothly into (floor, ceiling)."""
+    floor, ceiling = float(floor), float(ceiling)
+    if not (math.isfinite(floor) and math.isfinite(ceiling) and 0 < floor < ceiling < 1):
+        raise ValueError("EMA bounds must satisfy 0 < floor < ceiling < 1")
+    return floor + (ceiling - floor) * torch.sigmoid(raw)
+
+
+def inverse_bounded_ema_factor(alpha: float, *, floor: float = 1e-5, ceiling: float = 0.5) -> float:
+    """Raw value whose bounded_ema_factor is ``alpha``."""
+    alpha, floor, ceiling = float(alpha), float(floor), float(ceiling)
+    if not floor < alpha < ceiling:
+        raise ValueError(f"alpha must be strictly inside ({floor}, {ceiling})")
+    p = (alpha - floor) / (ceiling - floor)
+    return math.log(p / (1.0 - p))
+
+
+def _btd_ok(t: torch.Tensor) -> bool:
+    if t.stride(-1) != 1:
+        return False
+    if t.shape[-1] % 4:
+        return True
+    align = 8 if t.element_size() == 2 else 16
+    return t.data_ptr() % align == 0 and t.stride(0) % 4 == 0 and t.stride(1) % 4 == 0
+
+
+def _btd(t: torch.Tensor) -> torch.Tensor:
+    return t if _btd_ok(t) else t.contiguous()
+
+
+def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: float) -> torch.Tensor:
+    """Raw launch: y with x's dtype.  alpha fp32 on x's device, numel 1 or D."""
+    lib = _lib.load()
+    B, N, D = x.shape
+    y = torch.empty((B, N, D), device=x.device, dtype=x.dtype)
+    a = _lib.EmaFwdArgs()
+    a.B, a.N, a.D = B, N, D
+    a.dtype = _lib.DWARF_F32 if x.dtype == torch.float32 else _lib.DWARF_BF16
+    a.alpha_per_channel = int(alpha.numel() != 1)
+    a.floor_, a.ceiling = float(floor), float(ceiling)
+    a.x, a.x_stride = x.data_ptr(), _lib.i64_array(x.stride())
+    a.alpha = alpha.data_ptr()
+    a.y, a.y_stride = y.data_ptr(), _lib.i64_array(y.stride())
+    ws = torch.empty(max(int(lib.dwarf_ema_fwd_workspace_bytes(ctypes.byref(a))), 16), device=x.device,
+                     dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(lib.dwarf_ema_fwd(ctypes.byref(a), torch.cuda.current_stream(x.device).cuda_stream), "dwarf_ema_fwd")
+    return y
+
+
+def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool):
+    """Raw launch: (dx, dalpha or None); dalpha already clamp-projected."""
+    lib = _lib.load()
+    B, N, D = x.shape
+    dy = _btd(dy.to(x.dtype))
+    dx = torch.empty((B, N, D), device=x.device, dtype=x.dtype)
+    dalpha = torch.empty(alpha.numel(), device=x.device, dtype=torch.float32) if need_dalpha else None
+    a = _lib.EmaBwdArgs()
+    a.B, a.N, a.D = B, N, D
+    a.dtype = _lib.DWARF_F32 if x.dtype == torch.float32 else _lib.DWARF_BF16
+    a.alpha_per_channel = int(alpha.numel() != 1)
+    a.floor_, a.ceiling = float(floor), float(ceiling)
+    a.x, a.x_stride = x.data_ptr(), _lib.i64_array(x.stride())
+    a.y, a.y_stride = y.data_ptr(), _lib.i64_array(y.stride())
+    a.dy, a.dy_stride = dy.data_ptr(), _lib.i64_array(dy.stride())
+    a.alpha = alpha.data_ptr()
+    a.dx, a.dx_stride = dx.data_ptr(), _lib.i64_array(dx.stride())
+    a.dalpha = dalpha.data_ptr() if dalpha is not None else None
+    ws = torch.empty(max(int(lib.dwarf_ema_bwd_workspace_bytes(ctypes.byref(a))), 16), device=x.device,
+                     dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(lib.dwarf_ema_bwd(ctypes.byref(a), torch.cuda.current_stream(x.device).cuda_stream), "dwarf_ema_bwd")
+    return dx, dalpha
+
+
+class _CausalEMAFn(torch.autograd.Function):
+    """Autograd wrapper (reference: ema:263-364)."""
+
+    @staticmethod
+    def forward(ctx, x, alpha_input, floor, ceiling):
+        x = _btd(x)
+        alpha = alpha_input.detach().to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
+        y = ema_forward(x, alpha, floor, ceiling)
+        ctx.save_for_backward(x, y, alpha)
+        ctx.floor, ctx.ceiling = float(floor), float(ceiling)
+        ctx.alpha_shape, ctx.alpha_dtype = alpha_input.shape, alpha_input.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, y, alpha = ctx.saved_tensors
+        need = bool(ctx.needs_input_grad[1])
+        dx, dalpha = ema_backward(x, y, dy, alpha, ctx.floor, ctx.ceiling, need)
+        if not need:
+            return dx, None, None, None
+        return dx, dalpha.reshape(ctx.alpha_shape).to(ctx.alpha_dtype), None, None
+
+
+def causal_ema_scan(x: torch.Tensor, ema_factor: torch.Tensor, floor: float = 1e-5, ceiling: float = 0.5, *,
+                    reset_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal EMA of x[B,N,D] on the HIP kernels (reference signature: ema:541-567)."""
+    if x.ndim != 3:
+        raise ValueError(f"x must be [B,N,D], got {tuple(x.shape)}")
+    if ema_factor.numel() not in (1, x.shape[2]):
+        raise ValueError("ema_factor must contain one scalar or one value per channel")
+    if not (0 < float(floor) < float(ceiling) < 1):
+        raise ValueError("EMA bounds must satisfy 0 < floor < ceiling < 1")
+    if reset_mask is not None:
+        raise NotImplementedError("the reset-aware EMA scan is not built in this library")
+    if not x.is_cuda:
+        raise RuntimeError("the EMA HIP kernels require device tensors")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        out = _CausalEMAFn.apply(x.to(torch.bfloat16), ema_factor, float(floor), float(ceiling))
+        return out.to(x.dtype)
+    return _CausalEMAFn.apply(x, ema_factor, float(floor), float(ceiling))

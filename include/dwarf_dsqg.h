@@ -1,0 +1,271 @@
+/*
+ * dwarf_dsqg.h -- C ABI of the MI355X (gfx950) DSQG offset-gather library.
+ *
+ * One shared library, libdwarf_dsqg.so, exports every entry point below.
+ * The ABI carries plain device pointers, element strides and a hipStream_t;
+ * no framework types cross it.  The caller owns every buffer: outputs,
+ * gradients and the workspaces whose sizes the *_workspace_bytes queries
+ * report.  Every entry point is stateless and re-entrant, launches on the
+ * stream it is given, never allocates device memory and never throws.  It
+ * returns a dwarf_status; dwarf_last_error() describes the most recent
+ * failure on the calling thread.
+ *
+ * Reference interfaces replaced (Lanerra/dwarf-v2):
+ *   dsqg = kernels/dsqg_attention_v22.py, ema = kernels/causal_ema_scan.py
+ */
+#ifndef DWARF_DSQG_H
+#define DWARF_DSQG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DWARF_ABI_VERSION 1
+#define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
+#define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
+#define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
+
+typedef struct ihipStream_t* dwarf_stream_t; /* == hipStream_t */
+
+typedef enum {
+  DWARF_OK = 0,
+  DWARF_ERR_INVALID_ARGUMENT = 1, /* shapes, strides, offsets (ValueError)      */
+  DWARF_ERR_UNSUPPORTED = 2,      /* legal but not built here (RuntimeError)     */
+  DWARF_ERR_HIP = 3,              /* a HIP runtime call failed                   */
+  DWARF_ERR_WORKSPACE = 4         /* workspace pointer missing or too small      */
+} dwarf_status;
+
+typedef enum { DWARF_BF16 = 0, DWARF_F32 = 1 } dwarf_dtype;
+
+/* Library version (DWARF_ABI_VERSION) and last-error text for this thread. */
+int dwarf_abi_version(void);
+const char* dwarf_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* DSQG offset-gather attention                                              */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Forward inputs.  Shapes: q [B,H,N,hd]; k, v [B,H_kv,N,hd]; pos_bias [J,H];
+ * scale_embed [J,hd]; phase_base, phase_gain [max(J_large,1),H,4];
+ * y_pre [B,H,N,4]; z_pre [B,H_kv,N,4]; offsets [J] int32 on the device, in the
+ * canonical order [small <= 28 ascending | large >= 48 ascending]; out like q;
+ * lse [B,H,N] fp32.  Strides are in elements.  q/k/v/out need unit stride on
+ * the last dimension and 16-byte aligned rows; the 4-plane tables need unit
+ * stride on the plane dimension.  hd must be 64.
+ *
+ * se_round_bf16 = 1 rounds scale_embed to bf16 before use, as the reference's
+ * GPU kernels do (dsqg:760-763); 0 uses it unrounded, as the eager oracle does
+ * (dsqg:2660).  Rows n < query_start are written as out = 0, lse = -inf
+ * (dsqg:2265-2268).
+ */
+typedef struct {
+  int32_t B, H, H_kv, N, head_dim;
+  int32_t J, J_small, J_large;
+  int32_t plane_shift, query_start;
+  int32_t dtype;          /* dwarf_dtype of q, k, v, out */
+  int32_t se_round_bf16;
+  const void* q;  int64_t q_stride[4];
+  const void* k;  int64_t k_stride[4];
+  const void* v;  int64_t v_stride[4];
+  const float* pos_bias;    int64_t pb_stride[2];
+  const float* scale_embed; int64_t se_stride[2];
+  const float* phase_base;  int64_t pbase_stride[2];
+  const float* phase_gain;  int64_t pgain_stride[2];
+  const float* y_pre; int64_t y_stride[3];
+  const float* z_pre; int64_t z_stride[3];
+  const int32_t* offsets;
+  void* out;  int64_t out_stride[4];
+  float* lse; int64_t lse_stride[3];
+} dwarf_dsqg_fwd_args;
+
+/*
+ * Replaces the forward launch of _DSQGV18GroupedFn.forward (dsqg:2300-2314,
+ * kernel _fwd_v22_online dsqg:698-860) together with the out/lse
+ * initialisation it relies on (dsqg:2267-2268).
+ */
+int dwarf_dsqg_fwd(const dwarf_dsqg_fwd_args* args, dwarf_stream_t stream);
+
+/*
+ * Backward.  `fwd` holds the forward inputs plus the saved out and lse.
+ * Gradient outputs: dq like q, dk/dv like k (all of `dtype`, written, not
+ * accumulated); dpos_bias [J,H], dscale_embed [J,hd], dphase_base and
+ * dphase_gain [max(J_large,1),H,4], dy_pre [B,H,N,4], dz_pre [B,H_kv,N,4],
+ * all fp32 and contiguous.  Parameter gradients are reduced in a fixed order,
+ * so results are bitwise reproducible run to run.
+ */
+typedef struct {
+  dwarf_dsqg_fwd_args fwd;
+  const void* dout; int64_t dout_stride[4];
+  void* dq; int64_t dq_stride[4];
+  void* dk; int64_t dk_stride[4];
+  void* dv; int64_t dv_stride[4];
+  float* dpos_bias;
+  float* dscale_embed;
+  float* dphase_base;
+  float* dphase_gain;
+  float* dy_pre;
+  float* dz_pre;
+  void* workspace; size_t workspace_bytes;
+} dwarf_dsqg_bwd_args;
+
+/* Bytes of device workspace dwarf_dsqg_bwd needs for these shapes. */
+size_t dwarf_dsqg_bwd_workspace_bytes(const dwarf_dsqg_bwd_args* args);
+
+/*
+ * Replaces _DSQGV18GroupedFn.backward's launches (dsqg:2354-2552): the delta
+ * pass _compute_D_v18_grouped (dsqg:1263-1289), the query-centric
+ * _bwd_dq_v18_grouped (dsqg:1296-1488) and the key-centric
+ * _bwd_dkdv_v18_grouped (dsqg:1734-1955), including native GQA.
+ */
+int dwarf_dsqg_bwd(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
+
+/*
+ * The same backward as two launches on one stream, in this order, sharing the
+ * workspace.  dwarf_dsqg_bwd_dq replaces _compute_D_v18_grouped plus
+ * _bwd_dq_v18_grouped (dsqg:2378-2454): it writes delta into the workspace,
+ * dq, dy_pre and the four parameter gradients.  dwarf_dsqg_bwd_dkdv replaces
+ * _bwd_dkdv_v18_grouped (dsqg:2456-2544): it reads that delta and writes dk,
+ * dv and dz_pre.  Fields a stage does not write may be NULL.
+ */
+int dwarf_dsqg_bwd_dq(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
+int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Causal EMA scan  y[t] = a*x[t] + (1-a)*y[t-1],  a = clamp(alpha, fl, ce)  */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * x, y [B,N,D] of `dtype` (unit stride on D); alpha fp32 on the device, one
+ * value (alpha_per_channel = 0, the reference's contract, ema:557-558) or D
+ * values (alpha_per_channel = 1).  State is fp32.
+ */
+typedef struct {
+  int32_t B, N, D;
+  int32_t dtype;
+  int32_t alpha_per_channel;
+  float floor_, ceiling;
+  const void* x; int64_t x_stride[3];
+  const float* alpha;
+  void* y; int64_t y_stride[3];
+  void* workspace; size_t workspace_bytes;
+} dwarf_ema_fwd_args;
+
+size_t dwarf_ema_fwd_workspace_bytes(const dwarf_ema_fwd_args* args);
+
+/* Replaces _CausalEMAFn.forward's three launches (ema:265-313). */
+int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream);
+
+/*
+ * dx [B,N,D] of `dtype`; dalpha fp32 with alpha's length, written (not
+ * accumulated), already projected for the clamp as ema:357-364 does.
+ * Pass dalpha = NULL when alpha needs no gradient.
+ */
+typedef struct {
+  int32_t B, N, D;
+  int32_t dtype;
+  int32_t alpha_per_channel;
+  float floor_, ceiling;
+  const void* x;  int64_t x_stride[3];
+  const void* y;  int64_t y_stride[3];
+  const void* dy; int64_t dy_stride[3];
+  const float* alpha;
+  void* dx; int64_t dx_stride[3];
+  float* dalpha;
+  void* workspace; size_t workspace_bytes;
+} dwarf_ema_bwd_args;
+
+size_t dwarf_ema_bwd_workspace_bytes(const dwarf_ema_bwd_args* args);
+
+/* Replaces _CausalEMAFn.backward's three launches (ema:315-364). */
+int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* q6 K/V cache (no reference counterpart in the reference repository;      */
+/* signed 6-bit codes, 4 codes per 3 bytes, group 32, fp16 absmax scale)     */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Quantise K and V rows into q6 cache slots.  k, v [B,H_kv,N,hd] of `dtype`;
+ * cache [B,H_kv,N] slots of DWARF_Q6_SLOT_BYTES with byte strides
+ * cache_stride[3] (slot stride must be 128).  Slot layout for hd = 64:
+ * bytes 0-47 K codes, 48-51 K fp16 scales, 52-99 V codes, 100-103 V scales,
+ * 104-119 z[4] fp32, 120-127 zero.  z is the key-probe feature of the
+ * dequantised K row, z_r = <k, p_r> / sqrt(|k|^2 + 1e-6 hd) with the
+ * normalised key_probes [4,hd] fp32 (dsqg:3242-3254); key_probes = NULL
+ * stores z = 0.  Codes and scales are bit-exact with the CPU codec.
+ */
+int dwarf_q6_pack_kv(int32_t B, int32_t H_kv, int32_t N, int32_t head_dim,
+                     int32_t dtype,
+                     const void* k, const int64_t k_stride[4],
+                     const void* v, const int64_t v_stride[4],
+                     uint8_t* cache, const int64_t cache_stride[3],
+                     const float* key_probes,
+                     dwarf_stream_t stream);
+
+/* Dequantise cache slots back to fp32 K and V [B,H_kv,N,hd] (contiguous). */
+int dwarf_q6_unpack_kv(int32_t B, int32_t H_kv, int32_t N, int32_t head_dim,
+                       const uint8_t* cache, const int64_t cache_stride[3],
+                       float* k_out, float* v_out, dwarf_stream_t stream);
+
+/*
+ * q6 prefill forward: the DSQG forward with K and V dequantised on read from
+ * the cache slots.  y is computed in-kernel from q with the normalised
+ * query_probes [4,hd] fp32 (dsqg:3234-3249); z is read from the slot (written
+ * by dwarf_q6_pack_kv from the dequantised K).  q [B,H,N,hd] bf16; out like q;
+ * lse may be NULL.
+ */
+typedef struct {
+  int32_t B, H, H_kv, N, head_dim;
+  int32_t J, J_small, J_large;
+  int32_t plane_shift, query_start;
+  int32_t se_round_bf16;
+  const void* q; int64_t q_stride[4];
+  const uint8_t* cache; int64_t cache_stride[3];
+  const float* pos_bias;    int64_t pb_stride[2];
+  const float* scale_embed; int64_t se_stride[2];
+  const float* phase_base;  int64_t pbase_stride[2];
+  const float* phase_gain;  int64_t pgain_stride[2];
+  const float* query_probes;
+  const int32_t* offsets;
+  void* out; int64_t out_stride[4];
+  float* lse; int64_t lse_stride[3];
+} dwarf_dsqg_q6_prefill_args;
+
+int dwarf_dsqg_q6_prefill_fwd(const dwarf_dsqg_q6_prefill_args* args,
+                              dwarf_stream_t stream);
+
+/*
+ * q6 decode step: S sequences x L layers, one new query per (sequence, layer)
+ * at position pos[s] (int32, device).  q [S,L,H,hd] bf16; caches
+ * [L,S,H_kv,Ncache] slots (byte strides cache_stride[4]); per-layer tables
+ * with a leading layer stride (elements); out [S,L,H,hd] bf16.
+ */
+typedef struct {
+  int32_t S, L, H, H_kv, Ncache, head_dim;
+  int32_t J, J_small, J_large;
+  int32_t plane_shift;
+  int32_t se_round_bf16;
+  const void* q; int64_t q_stride[4];
+  const int32_t* pos;
+  const uint8_t* cache; int64_t cache_stride[4];
+  const float* pos_bias;    int64_t pb_stride[3];
+  const float* scale_embed; int64_t se_stride[3];
+  const float* phase_base;  int64_t pbase_stride[3];
+  const float* phase_gain;  int64_t pgain_stride[3];
+  const float* query_probes; int64_t qprobe_layer_stride; /* [L,4,hd] */
+  const int32_t* offsets;    /* [J], shared by all layers */
+  void* out; int64_t out_stride[4];
+} dwarf_dsqg_q6_decode_args;
+
+int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args,
+                         dwarf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DWARF_DSQG_H */

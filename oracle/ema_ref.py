@@ -1,0 +1,65 @@
+"""CPU restatement of the causal EMA scan -- test infrastructure, not the product.
+
+Follows the reference recurrence (kernels/causal_ema_scan.py:3-11) and its
+eager ``_reference`` (ema:511-538): a = clamp(alpha, floor, ceiling),
+y[t] = a x[t] + (1 - a) y[t-1], y[-1] = 0, with float64 state for float64
+inputs and float32 state otherwise.  alpha may be one value or one per
+channel ([D]); ``_reference`` broadcasts a [D] alpha the same way.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def ema_scan(x: torch.Tensor, alpha: torch.Tensor, floor: float = 1e-5, ceiling: float = 0.5) -> torch.Tensor:
+    acc = torch.float64 if x.dtype == torch.float64 else torch.float32
+    a = alpha.to(acc).clamp(floor, ceiling).reshape(-1)
+    decay = 1.0 - a
+    xf = x.to(acc)
+    state = torch.zeros(x.shape[0], x.shape[2], dtype=acc)
+    rows = []
+    for t in range(x.shape[1]):
+        state = a * xf[:, t] + decay * state
+        rows.append(state)
+    if not rows:
+        return torch.empty_like(x)
+    return torch.stack(rows, dim=1).to(x.dtype)
+
+
+def ema_closed_form(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
+    """y[t] = sum_{s<=t} a (1-a)^(t-s) x[s], evaluated directly in float64 (alpha unclamped)."""
+    x64 = x.to(torch.float64)
+    a = alpha.to(torch.float64).reshape(-1)
+    N = x.shape[1]
+    t = torch.arange(N, dtype=torch.float64)
+    lag = (t[:, None] - t[None, :])                      # [t, s]
+    mask = lag >= 0
+    w = torch.where(mask[..., None], a * (1 - a) ** lag.clamp(min=0)[..., None], torch.zeros((), dtype=torch.float64))
+    return torch.einsum("tsd,bsd->btd", w, x64)
+
+
+def ema_adjoint(x: torch.Tensor, y: torch.Tensor, dy: torch.Tensor, alpha: torch.Tensor,
+                floor: float = 1e-5, ceiling: float = 0.5):
+    """Reverse adjoint (ema:3-11): lambda[t] = dy[t] + (1-a) lambda[t+1], dx = a lambda,
+    dalpha = sum lambda[t] (x[t] - y[t-1]); dalpha per channel summed over batch and time,
+    then zeroed where the clamp blocks it (ema:357-364)."""
+    acc = torch.float64 if x.dtype == torch.float64 else torch.float32
+    a_in = alpha.to(acc).reshape(-1)
+    a = a_in.clamp(floor, ceiling)
+    xf, yf, g = x.to(acc), y.to(acc), dy.to(acc)
+    B, N, D = x.shape
+    lam = torch.zeros(B, D, dtype=acc)
+    dx = torch.zeros(B, N, D, dtype=acc)
+    da = torch.zeros(B, D, dtype=acc)
+    for t in range(N - 1, -1, -1):
+        lam = g[:, t] + (1 - a) * lam
+        dx[:, t] = a * lam
+        prev = yf[:, t - 1] if t > 0 else torch.zeros(B, D, dtype=acc)
+        da += lam * (xf[:, t] - prev)
+    da = da.sum(0)
+    if a_in.numel() == 1:
+        da = da.sum().reshape(1)
+    blocked = ((a_in <= floor) & (da > 0)) | ((a_in >= ceiling) & (da < 0))
+    da = torch.where(blocked, torch.zeros_like(da), da)
+    return dx, da

@@ -1,0 +1,97 @@
+"""The C-ABI library: exports, struct layout and host-side validation (no GPU).
+
+No kernel is launched here: every call below fails validation on the host,
+which the library does before touching the HIP runtime.
+"""
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "dwarf_dsqg.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(dwarf_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg._lib.load()
+
+
+def test_exports_every_declared_symbol(pkg, lib):
+    names = declared_functions()
+    assert len(names) == 15
+    assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.dwarf_abi_version() == pkg._lib.ABI_VERSION
+
+
+STRUCTS = {
+    "dwarf_dsqg_fwd_args": "DsqgFwdArgs",
+    "dwarf_dsqg_bwd_args": "DsqgBwdArgs",
+    "dwarf_ema_fwd_args": "EmaFwdArgs",
+    "dwarf_ema_bwd_args": "EmaBwdArgs",
+    "dwarf_dsqg_q6_prefill_args": "Q6PrefillArgs",
+    "dwarf_dsqg_q6_decode_args": "Q6DecodeArgs",
+}
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_ctypes_layout_matches_header(pkg, tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "dwarf_dsqg.h"', "int main(void) {"]
+    for cname, pyname in STRUCTS.items():
+        struct = getattr(pkg._lib, pyname)
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for field, _ in struct._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    for line in filter(None, out):
+        cname, field, value = line.split()
+        struct = getattr(pkg._lib, STRUCTS[cname])
+        got = ctypes.sizeof(struct) if field == "sizeof" else getattr(struct, field).offset
+        assert got == int(value), (cname, field, got, value)
+
+
+def test_validation_errors_without_gpu(pkg, lib):
+    L = pkg._lib
+    assert lib.dwarf_dsqg_fwd(None, None) == L.DWARF_ERR_INVALID_ARGUMENT
+    assert b"NULL" in lib.dwarf_last_error()
+    a = L.DsqgFwdArgs()
+    a.B, a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large = 1, 3, 2, 16, 64, 2, 1, 1
+    assert lib.dwarf_dsqg_fwd(ctypes.byref(a), None) == L.DWARF_ERR_INVALID_ARGUMENT
+    assert b"divisible" in lib.dwarf_last_error()
+    a.H_kv, a.head_dim = 1, 128
+    assert lib.dwarf_dsqg_fwd(ctypes.byref(a), None) == L.DWARF_ERR_UNSUPPORTED
+    a.head_dim, a.plane_shift = 64, 15
+    assert lib.dwarf_dsqg_fwd(ctypes.byref(a), None) == L.DWARF_ERR_INVALID_ARGUMENT
+    assert b"plane_shift" in lib.dwarf_last_error()
+    a.plane_shift, a.J = 0, 5
+    assert lib.dwarf_dsqg_fwd(ctypes.byref(a), None) == L.DWARF_ERR_INVALID_ARGUMENT
+    a.J, a.query_start = 2, 17
+    assert lib.dwarf_dsqg_fwd(ctypes.byref(a), None) == L.DWARF_ERR_INVALID_ARGUMENT
+    a.query_start = 0
+    assert lib.dwarf_dsqg_fwd(ctypes.byref(a), None) == L.DWARF_ERR_INVALID_ARGUMENT  # q is NULL
+    assert b"q is NULL" in lib.dwarf_last_error()
+    e = L.EmaFwdArgs()
+    e.B, e.N, e.D, e.floor_, e.ceiling = 1, 4, 4, 0.6, 0.5
+    assert lib.dwarf_ema_fwd(ctypes.byref(e), None) == L.DWARF_ERR_INVALID_ARGUMENT
+    with pytest.raises(ValueError):
+        L.check(lib.dwarf_ema_fwd(ctypes.byref(e), None), "dwarf_ema_fwd")
+    d = L.Q6DecodeArgs()
+    d.S, d.L, d.H, d.H_kv, d.Ncache, d.head_dim, d.J, d.J_small, d.J_large = 1, 1, 1, 1, 64, 64, 200, 100, 100
+    assert lib.dwarf_dsqg_q6_decode(ctypes.byref(d), None) == L.DWARF_ERR_UNSUPPORTED

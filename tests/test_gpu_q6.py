@@ -1,0 +1,95 @@
+"""GPU q6 path against the CPU codec and oracle (runs on an MI355X).
+
+Codec: GPU-packed slots byte-identical to the CPU codec, GPU dequant equal to
+the CPU dequant (both exact).  Prefill/decode: within 2e-2 max-abs of the DSQG
+oracle evaluated on the dequantised K/V, with y from q and z from the
+dequantised K, and bf16-rounded scale embeddings.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsqg_ref, q6_ref
+from tests.dsqg_cases import NAMES, features, make_inputs, max_abs, orthogonal_probes
+
+pytestmark = pytest.mark.gpu
+
+
+def edge_rows(shape, g):
+    x = torch.randn(*shape, generator=g)
+    x[..., 0, :] = 0.0                          # all-zero row -> zero scales
+    x[..., 1, :32] = 1e-7                       # fp16-subnormal scale
+    x[..., 2, 5] = 4.0e6                        # saturating scale
+    x[..., 3, :] = torch.arange(64) - 31.5      # half-way codes
+    return x
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_pack_matches_cpu_codec_bit_exact(pkg, device, dtype):
+    g = torch.Generator().manual_seed(1)
+    k = edge_rows((2, 3, 37, 64), g).to(dtype)
+    v = (3.0 * torch.randn(2, 3, 37, 64, generator=g)).to(dtype)
+    _, kp = orthogonal_probes(64, 4)
+    kpn = torch.nn.functional.normalize(kp, dim=-1)
+    cache = pkg.q6.pack_kv(k.to(device), v.to(device), kpn.to(device)).cpu().numpy()
+    ref = q6_ref.pack_slots(k.float().numpy(), v.float().numpy(), None)
+    assert np.array_equal(cache[..., :104], ref[..., :104])
+    assert not cache[..., 120:].any()
+    kd, vd = pkg.q6.unpack_kv(torch.from_numpy(cache).to(device))
+    rk, rv, _ = q6_ref.unpack_slots(cache)
+    assert np.array_equal(kd.cpu().numpy(), rk) and np.array_equal(vd.cpu().numpy(), rv)
+    z = np.ascontiguousarray(cache[..., 104:120]).view(np.float32).reshape(2, 3, 37, 4)
+    rz = features(torch.from_numpy(rk), kpn).numpy()
+    assert np.allclose(z, rz, rtol=1e-5, atol=1e-6)
+
+
+def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs):
+    kd, vd, _ = q6_ref.unpack_slots(cache_np)
+    inp = dict(x)
+    inp["k"] = torch.from_numpy(kd).double()
+    inp["v"] = torch.from_numpy(vd).double()
+    inp["y_pre"] = features(x["q"].double(), qp).double()
+    inp["z_pre"] = features(torch.from_numpy(kd).double(), kp).double()
+    return dsqg_ref.dsqg_forward(*(inp[n].double() for n in NAMES), offsets, js, plane_shift=shift,
+                                 query_start=qs, round_se=True)
+
+
+def test_prefill_matches_oracle(pkg, device):
+    offsets = list(pkg.ALL_OFFSETS)
+    shift = 2
+    x = make_inputs(2, 4, 2, 300, offsets, 17, seed=3, dtype=torch.bfloat16, plane_shift=shift, gain_std=6.0)
+    qp, kp = orthogonal_probes(64, shift)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    xd = {n: t.to(device) for n, t in x.items()}
+    cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"],
+                            xd["phase_gain"], qp.to(device), off, 17, 79, shift, 1)
+    ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, shift, qp, kp, 1)
+    assert max_abs(out, ref) < 2e-2
+
+
+def test_decode_matches_oracle(pkg, device):
+    offsets = list(pkg.ALL_OFFSETS)
+    shift = 0
+    S, L, H, Hkv, N = 3, 2, 4, 2, 300
+    g = torch.Generator().manual_seed(7)
+    layers = [make_inputs(S, H, Hkv, N, offsets, 17, seed=50 + l, dtype=torch.bfloat16, plane_shift=shift,
+                          gain_std=6.0) for l in range(L)]
+    pos = torch.tensor([299, 96, 150], dtype=torch.int32)
+    qp, kp = orthogonal_probes(64, shift)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    caches = torch.stack([pkg.q6.pack_kv(x["k"].to(device), x["v"].to(device), kp.to(device)) for x in layers])
+    qdec = torch.stack([torch.stack([layers[l]["q"][s, :, int(pos[s])] for l in range(L)]) for s in range(S)])
+    tables = {n: torch.stack([x[n] for x in layers]).to(device) for n in ("pos_bias", "scale_embed", "phase_base",
+                                                                          "phase_gain")}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_decode(qdec.to(device), pos.to(device), caches, tables["pos_bias"], tables["scale_embed"],
+                           tables["phase_base"], tables["phase_gain"], torch.stack([qp] * L).to(device), off,
+                           17, 79, shift).cpu()
+    for l in range(L):
+        ref = _oracle_on_cache(layers[l], caches[l].cpu().numpy(), offsets, 17, shift, qp, kp, 0)
+        for s in range(S):
+            t = int(pos[s])
+            assert max_abs(out[s, l], ref[s, :, t]) < 2e-2, (s, l)

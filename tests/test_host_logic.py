@@ -1,0 +1,111 @@
+"""Host-side behaviour of the Python mirror of the reference interface (no GPU).
+
+Errors are raised with the reference's exception types before any device
+work: ValueError for shapes/arguments (dsqg:2209-2225), NotImplementedError
+for unsupported modes (dsqg:2217-2221), RuntimeError when no GPU tensors are
+given -- this library has no CPU fallback.
+"""
+
+import importlib
+
+import pytest
+import torch
+
+
+def _args(B=1, H=2, Hkv=2, N=8, hd=64, J=3, js=2):
+    return dict(
+        q=torch.zeros(B, H, N, hd), k=torch.zeros(B, Hkv, N, hd), v=torch.zeros(B, Hkv, N, hd),
+        pos_bias=torch.zeros(J, H), scale_embed=torch.zeros(J, hd),
+        phase_base=torch.zeros(max(J - js, 1), H, 4), phase_gain=torch.zeros(max(J - js, 1), H, 4),
+        y_pre=torch.zeros(B, H, N, 4), z_pre=torch.zeros(B, Hkv, N, 4),
+    )
+
+
+def _call(pkg, a, J=3, js=2, backend="auto", mode=0):
+    return pkg.dsqg_attention_v18_grouped(
+        a["q"], a["k"], a["v"], a["pos_bias"], a["scale_embed"], a["phase_base"], a["phase_gain"],
+        a["y_pre"], a["z_pre"], J, js, J - js, torch.tensor([1, 2, 48], dtype=torch.int32),
+        None, None, None, None, None, 3, mode, False, 0, 0, 1, backend=backend,
+    )
+
+
+def _fn(pkg, a, mode=0):
+    return pkg._DSQGV18GroupedFn.apply(
+        a["q"], a["k"], a["v"], a["pos_bias"], a["scale_embed"], a["phase_base"], a["phase_gain"],
+        a["y_pre"], a["z_pre"], 3, 2, 1, torch.tensor([1, 2, 48], dtype=torch.int32),
+        None, None, None, None, None, 3, mode, False, 0, 0, 1, True,
+    )
+
+
+def test_backend_selection(pkg):
+    a = _args()
+    with pytest.raises(ValueError):
+        _call(pkg, a, backend="cuda")
+    with pytest.raises(NotImplementedError):
+        _call(pkg, a, backend="eager")
+    with pytest.raises(RuntimeError):
+        _call(pkg, a)                 # CPU tensors: no fallback
+    with pytest.raises(RuntimeError):
+        _call(pkg, a, backend="triton")
+
+
+def test_function_shape_errors(pkg):
+    a = _args()
+    a["v"] = torch.zeros(1, 2, 9, 64)
+    with pytest.raises(ValueError, match="k/v shape mismatch"):
+        _fn(pkg, a)
+    a = _args(H=3, Hkv=2)
+    with pytest.raises(ValueError, match="divisible"):
+        _fn(pkg, a)
+    a = _args(H=4, Hkv=2)
+    with pytest.raises(NotImplementedError):
+        _fn(pkg, a, mode=1)
+    a = _args()
+    a["y_pre"] = torch.zeros(1, 2, 7, 4)
+    with pytest.raises(ValueError, match="y_pre"):
+        _fn(pkg, a)
+    a = _args()
+    a["z_pre"] = torch.zeros(1, 1, 8, 4)
+    with pytest.raises(ValueError, match="z_pre"):
+        _fn(pkg, a)
+    a = _args()
+    with pytest.raises(RuntimeError, match="device"):
+        _fn(pkg, a)
+
+
+def test_ema_errors(pkg):
+    x = torch.zeros(2, 5, 3)
+    a = torch.tensor([0.1])
+    with pytest.raises(ValueError):
+        pkg.causal_ema_scan(torch.zeros(5, 3), a)
+    with pytest.raises(ValueError):
+        pkg.causal_ema_scan(x, torch.tensor([0.1, 0.2]))
+    with pytest.raises(ValueError):
+        pkg.causal_ema_scan(x, a, 0.6, 0.5)
+    with pytest.raises(NotImplementedError):
+        pkg.causal_ema_scan(x, a, reset_mask=torch.zeros(2, 5, dtype=torch.bool))
+    with pytest.raises(RuntimeError):
+        pkg.causal_ema_scan(x, a)
+    with pytest.raises(RuntimeError):
+        pkg.causal_ema_scan(x, torch.full((3,), 0.1))   # per-channel accepted, but no CPU path
+
+
+def test_q6_errors(pkg):
+    with pytest.raises(ValueError):
+        pkg.q6.pack_kv(torch.zeros(1, 1, 4, 64), torch.zeros(1, 1, 5, 64))
+    with pytest.raises(RuntimeError):
+        pkg.q6.pack_kv(torch.zeros(1, 1, 4, 64), torch.zeros(1, 1, 4, 64))
+    with pytest.raises(ValueError):
+        pkg.q6.unpack_kv(torch.zeros(1, 1, 4, 100, dtype=torch.uint8))
+
+
+def test_library_is_the_only_path(pkg):
+    """The package loads its HIP library eagerly on use and never imports the oracle."""
+    import sys
+
+    for name in list(sys.modules):
+        if name.startswith("dwarf-v2_amd"):
+            mod = sys.modules[name]
+            src = open(mod.__file__).read() if getattr(mod, "__file__", None) else ""
+            assert "import oracle" not in src and "from oracle" not in src
+    assert pkg.native_library_path().endswith("libdwarf_dsqg.so")
