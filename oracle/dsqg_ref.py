@@ -127,12 +127,24 @@ def dsqg_forward(
     return out, lse
 
 
-def dsqg_forward_backward(inputs: dict, offsets, j_small, dout: torch.Tensor, **kw):
-    """(out, lse, grads) with grads keyed like the reference's 9 gradient slots (dsqg:2546-2547)."""
+def dsqg_forward_backward(inputs: dict, offsets, j_small, dout: torch.Tensor, *, delta_from_bf16_out=False, **kw):
+    """(out, lse, grads) with grads keyed like the reference's 9 gradient slots (dsqg:2546-2547).
+
+    delta_from_bf16_out: the reference GPU backward forms delta = <dO, O> from
+    the bf16 output it stored (dsqg:1263-1289, 2380-2386) rather than the exact
+    O.  With eps[n] = <dO[n], bf16(O[n]) - O[n]> held constant, that backward
+    is exactly the gradient of <dO, out> - sum_n eps[n] * lse[n], because
+    d lse / d score = P; this option evaluates that.
+    """
     names = ("q", "k", "v", "pos_bias", "scale_embed", "phase_base", "phase_gain", "y_pre", "z_pre")
     leaves = {n: inputs[n].detach().clone().requires_grad_(True) for n in names}
     out, lse = dsqg_forward(*(leaves[n] for n in names), offsets, j_small, return_lse=True, **kw)
-    out.backward(dout.to(out.dtype))
+    g = dout.to(out.dtype)
+    loss = (out * g).sum()
+    if delta_from_bf16_out:
+        eps = (g * (out.detach().to(torch.bfloat16).to(out.dtype) - out.detach())).sum(-1)
+        loss = loss - (eps * torch.where(torch.isfinite(lse), lse, torch.zeros_like(lse))).sum()
+    loss.backward()
     grads = {n: leaves[n].grad for n in names}
     return out.detach(), lse.detach(), grads
 

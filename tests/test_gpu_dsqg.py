@@ -3,8 +3,9 @@
 Bars (stated per test): fp32 forward and all nine gradients within 1e-5
 relative (||a-b||_inf / ||b||_inf) of the float64 oracle; bf16 within 2e-2
 max-abs of the oracle evaluated on the same bf16-rounded inputs; index
-selection bit-exact.  The bf16 oracle uses bf16-rounded scale embeddings,
-as the reference GPU path does (dsqg:760-763).
+selection bit-exact.  The bf16 oracle follows the reference GPU path's two
+bf16 conventions: scale embeddings rounded to bf16 (dsqg:760-763) and the
+backward's delta = <dO, O> taken from the stored bf16 output (dsqg:1263-1289).
 """
 
 import os
@@ -36,12 +37,12 @@ def gpu_fwd_bwd(pkg, x, offsets, js, shift, qs, dout, device):
 
 
 def oracle_fwd_bwd(x, offsets, js, shift, qs, dout, round_se):
+    """float64 oracle; for bf16 (round_se) it follows the reference GPU path's
+    conventions: bf16 scale embeddings and delta from the bf16 output."""
     inp = {n: t.double() for n, t in x.items()}
     return dsqg_ref.dsqg_forward_backward(inp, offsets, js, dout.double(), plane_shift=shift,
-                                          query_start=qs, round_se=round_se)
+                                          query_start=qs, round_se=round_se, delta_from_bf16_out=round_se)
 
-
-LATTICE = None
 
 
 def lattice(pkg):

@@ -175,3 +175,32 @@ def test_round_se_is_straight_through():
     _, _, g1 = dsqg_ref.dsqg_forward_backward(x, offsets, 2, dout, round_se=True)
     _, _, g2 = dsqg_ref.dsqg_forward_backward(rounded, offsets, 2, dout)
     assert rel(g1["scale_embed"], g2["scale_embed"]) < 1e-14
+
+
+def test_delta_from_bf16_out_matches_explicit_formula():
+    """The surrogate-loss form of the GPU convention equals the explicit
+    dS = P (g - <dO, bf16(O)>) backward, checked on dpos_bias = sum_n dS."""
+    offsets = [1, 2, 5, 48]
+    x = _random_inputs(1, 2, 2, 40, 8, 4, 3, seed=9, gain=1.0)
+    dout = torch.randn(1, 2, 40, 8, dtype=torch.float64)
+    out, lse, g = dsqg_ref.dsqg_forward_backward(x, offsets, 3, dout, delta_from_bf16_out=True)
+    o16 = out.to(torch.bfloat16).to(torch.float64)
+    delta = (dout * o16).sum(-1)
+    c = 1 / math.sqrt(8)
+    expect = torch.zeros(4, 2, dtype=torch.float64)
+    pairs = dsqg_ref.channel_pairs(8, 0)
+    for j, d in enumerate(offsets):
+        for n in range(d, 40):
+            for h in range(2):
+                s = float((x["q"][0, h, n] * (x["k"][0, h, n - d] + x["scale_embed"][j])).sum() * c + x["pos_bias"][j, h])
+                P = math.exp(s - float(lse[0, h, n]))
+                v = x["v"][0, h, n - d].clone()
+                if j >= 3:
+                    for r, (a, b) in enumerate(pairs):
+                        th = float(x["phase_base"][j - 3, h, r] + x["phase_gain"][j - 3, h, r]
+                                   * x["y_pre"][0, h, n, r] * x["z_pre"][0, h, n - d, r])
+                        va, vb = float(v[a]), float(v[b])
+                        v[a], v[b] = math.cos(th) * va - math.sin(th) * vb, math.sin(th) * va + math.cos(th) * vb
+                gd = float((dout[0, h, n] * v).sum())
+                expect[j, h] += P * (gd - float(delta[0, h, n]))
+    assert rel(g["pos_bias"], expect) < 1e-12
