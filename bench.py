@@ -256,6 +256,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy 10 times (scales HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -265,9 +267,17 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    device = torch.device("cuda", 0)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel(), "launches": 10}))
+        return 0
     pkg = importlib.import_module("dwarf-v2_amd")
     pkg._lib.load()
-    device = torch.device("cuda", 0)
     B, H, N = 15, 8, 2048
     log("training microbatch: DSQG fwd+bwd B15 H8 T2048 bf16")
     t, js, jl = synth(pkg, B, H, N, 0, device)

@@ -1,0 +1,545 @@
+// DSQG backward, query-centric launch: delta, dQ, dY and the per-workgroup
+// partials of dPB, dSE, dPhaseBase, dPhaseGain (reference kernels
+// _compute_D_v18_grouped dsqg:1263-1289 and _bwd_dq_v18_grouped
+// dsqg:1296-1488; the reference sums the parameter gradients with fp32
+// atomics, here they are reduced in a fixed order).
+//
+// Mapping.  A workgroup of 4 waves walks `tpw` consecutive 128-query tiles of
+// one (b, h).  Two lanes share a query (32 head dims each); wave w owns
+// queries 32w..32w+31 of the tile.  Offsets are processed in chunks of 16.
+//
+// Per chunk, the dense sub-products run on MFMA:
+//   QE   = Q E^T          the <q, e_j> term of every score       (wave level)
+//   dQe += dS E            the e_j part of dQ                      (wave level)
+//   dSE  = dS^T Q, dPB = dS^T 1                                    (workgroup level)
+// and the lanes do the gathered work: <q, k_s>, <dO, v_s>, the MOVT rotation
+// of the 8 rotated channels, P, dS and dQ += c dS k_s.  For bf16 inputs the
+// MFMAs are v_mfma_f32_16x16x32_bf16 with dS split into bf16 high and low
+// parts (~2^-17 relative); for fp32 inputs they are v_mfma_f32_16x16x4_f32.
+// dPhase sums are formed every 4 offsets by a padded per-wave LDS transpose.
+// Workgroup partials are accumulated in their own global slots (each entry
+// owned by one wave, so the update order is fixed) and summed by
+// dsqg_bwd_reduce.
+#include "common.h"
+#include "dsqg_internal.h"
+#include "mfma.h"
+
+namespace dwarf {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kQ = 128;       // queries per tile
+constexpr int kCJ = 16;       // offsets per chunk
+constexpr int kDsRow = kQ + 4;    // s_ds[jj][q] row (floats), 16-byte aligned, bank-staggered
+constexpr int kQeRow = 33;        // s_qe[jj][qi]
+constexpr int kDs2Row = 20;       // s_ds2[qi][jj]
+constexpr int kPhRow = 36;        // s_ph[jj4 * 8 + r * 2 + kind][qi]
+constexpr int kStageRow = 68;     // dQe staging [qi][d]
+constexpr int kQeOff = 0;
+constexpr int kDs2Off = kCJ * kQeRow;                 // 528
+constexpr int kPhOff = kDs2Off + 32 * kDs2Row;        // 1168
+constexpr int kWaveRegion = kPhOff + 32 * kPhRow;     // 2320 floats (>= 32 * kStageRow = 2176)
+constexpr int kERowBf16 = 72;     // bf16 E row stride (elements)
+constexpr int kERowF32 = 68;      // fp32 E row stride (floats)
+
+__host__ __device__ constexpr int align4(int x) { return (x + 3) & ~3; }
+
+struct DqLds {
+  int e_words;     // words of the E table (bf16 pairs or fp32)
+  int et_words;    // words of the bf16 E^T table
+  int jp;          // E^T row length (bf16 elements)
+  size_t bytes;
+};
+
+template <typename T>
+__host__ __device__ DqLds dq_lds(int J) {
+  DqLds s;
+  if constexpr (sizeof(T) == 2) {
+    s.e_words = J * kERowBf16 / 2;
+    s.jp = ((J + 7) / 8) * 8 + 8;
+    s.et_words = kHeadDim * s.jp / 2;
+  } else {
+    s.e_words = J * kERowF32;
+    s.jp = 0;
+    s.et_words = 0;
+  }
+  const int words = align4(s.e_words) + align4(s.et_words) + align4(J) * 2 + 2 * kCJ * kDsRow + kWaves * kWaveRegion;
+  s.bytes = static_cast<size_t>(words) * 4;
+  return s;
+}
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+template <typename T, int SHIFT>
+__global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_v2(const dwarf_dsqg_bwd_args a, float* __restrict__ delta_ws,
+                                                            float* __restrict__ part_se, float* __restrict__ part_pb,
+                                                            float* __restrict__ part_ph, int tiles, int tpw, int n_tg,
+                                                            int total) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int HD = kHeadDim, DPL = 32, SEG = HD / kPlanes;
+  constexpr float kScale = 0.125f;
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  const int J = f.J;
+  const DqLds lay = dq_lds<T>(J);
+
+  extern __shared__ float smem[];
+  uint32_t* sE = reinterpret_cast<uint32_t*>(smem);                        // E rows
+  uint32_t* sET = sE + align4(lay.e_words);                                // bf16 E^T rows (bf16 path)
+  float* s_pb = reinterpret_cast<float*>(sET + align4(lay.et_words));      // [J]
+  int* s_off = reinterpret_cast<int*>(s_pb + align4(J));                   // [J]
+  float* s_ds = reinterpret_cast<float*>(s_off + align4(J));               // [2][kCJ][kDsRow]
+  float* s_wave = s_ds + 2 * kCJ * kDsRow;                                 // [kWaves][kWaveRegion]
+
+  const int work = xcd_remap(blockIdx.x, total);
+  const int bh = work / n_tg;
+  const int tg = work - bh * n_tg;
+  const int b = bh / f.H;
+  const int h = bh - b * f.H;
+  const int hk = h / (f.H / f.H_kv);
+  const int slot = (h * f.B + b) * n_tg + tg;   // head-major partial slot
+
+  // ---- stage the offset tables -------------------------------------------
+  for (int i = threadIdx.x; i < J * HD; i += kBlock) {
+    const int j = i / HD, d = i - j * HD;
+    float e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
+    if (f.se_round_bf16) e = round_bf16(e);
+    if constexpr (BF) {
+      uint16_t* e16 = reinterpret_cast<uint16_t*>(sE);
+      e16[j * kERowBf16 + d] = f32_to_bf16_bits(e);
+    } else {
+      reinterpret_cast<float*>(sE)[j * kERowF32 + d] = e;
+    }
+  }
+  if constexpr (BF) {
+    uint16_t* et16 = reinterpret_cast<uint16_t*>(sET);
+    for (int i = threadIdx.x; i < HD * lay.jp; i += kBlock) {
+      const int d = i / lay.jp, j = i - d * lay.jp;
+      float e = 0.f;
+      if (j < J) {
+        e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
+        if (f.se_round_bf16) e = round_bf16(e);
+      }
+      et16[d * lay.jp + j] = f32_to_bf16_bits(e);
+    }
+  }
+  for (int j = threadIdx.x; j < J; j += kBlock) {
+    s_pb[j] = f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]];
+    s_off[j] = f.offsets[j];
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;       // MFMA lane
+  const int g = lane & 1;           // head-dim half
+  const int qi = l >> 1;            // query within the wave
+  const int qw = 32 * w + qi;       // query within the tile
+  const int lr = l & 15, lc = l >> 4;
+  float* wreg = s_wave + w * kWaveRegion;
+  float* s_qe = wreg + kQeOff;
+  float* s_ds2 = wreg + kDs2Off;
+  float* s_ph = wreg + kPhOff;
+  float* s_stage = wreg;
+
+  const T* qb = reinterpret_cast<const T*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1];
+  const T* kb = reinterpret_cast<const T*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1] + g * DPL;
+  const T* vb = reinterpret_cast<const T*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1] + g * DPL;
+  const float* zb = f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1];
+  const float* pbase_h = f.phase_base + h * f.pbase_stride[1];
+  const float* pgain_h = f.phase_gain + h * f.pgain_stride[1];
+
+  const int t_begin = tg * tpw;
+  const int t_end = min(tiles, t_begin + tpw);
+  int chunk_count = 0;  // s_ds buffer parity alternates across tiles too (one barrier per chunk)
+  for (int t = t_begin; t < t_end; ++t) {
+    const bool first = t == t_begin;
+    const int n0 = t * kQ;
+    const int n = n0 + qw;
+    const bool row_ok = n < f.N;
+    const bool row_live = row_ok && n >= f.query_start;
+    const int wave_n_last = n0 + 32 * w + 31;
+    const int64_t nn = n;
+
+    // ---- this lane's query slice, dO slice, delta, lse, y ------------------
+    uint32_t qw16[BF ? 16 : 1], dw16[BF ? 16 : 1];
+    float qf[BF ? 1 : DPL], df[BF ? 1 : DPL];
+    float dlt = 0.f, lse = -INFINITY;
+    float ys[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (BF) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { qw16[i] = 0u; dw16[i] = 0u; }
+    } else {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) { qf[i] = 0.f; df[i] = 0.f; }
+    }
+    if (row_live) {
+      const T* qp = qb + nn * f.q_stride[2] + g * DPL;
+      const T* dp = reinterpret_cast<const T*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1] +
+                    nn * a.dout_stride[2] + g * DPL;
+      const T* op = reinterpret_cast<const T*>(f.out) + b * f.out_stride[0] + h * f.out_stride[1] +
+                    nn * f.out_stride[2] + g * DPL;
+      if constexpr (BF) {
+        const uint4* q4 = reinterpret_cast<const uint4*>(qp);
+        const uint4* d4 = reinterpret_cast<const uint4*>(dp);
+        const uint4* o4 = reinterpret_cast<const uint4*>(op);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint4 x = q4[i], y = d4[i], o = o4[i];
+          qw16[4 * i] = x.x; qw16[4 * i + 1] = x.y; qw16[4 * i + 2] = x.z; qw16[4 * i + 3] = x.w;
+          dw16[4 * i] = y.x; dw16[4 * i + 1] = y.y; dw16[4 * i + 2] = y.z; dw16[4 * i + 3] = y.w;
+          dlt = dot2_bf16(y.x, o.x, dlt); dlt = dot2_bf16(y.y, o.y, dlt);
+          dlt = dot2_bf16(y.z, o.z, dlt); dlt = dot2_bf16(y.w, o.w, dlt);
+        }
+      } else {
+        float o[DPL];
+        load_f32<float, DPL>(reinterpret_cast<const float*>(qp), qf);
+        load_f32<float, DPL>(reinterpret_cast<const float*>(dp), df);
+        load_f32<float, DPL>(reinterpret_cast<const float*>(op), o);
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) dlt = fmaf(df[i], o[i], dlt);
+      }
+      lse = f.lse[b * f.lse_stride[0] + h * f.lse_stride[1] + nn * f.lse_stride[2]];
+      const float4 y4 = *reinterpret_cast<const float4*>(f.y_pre + b * f.y_stride[0] + h * f.y_stride[1] + nn * f.y_stride[2]);
+      ys[0] = y4.x; ys[1] = y4.y; ys[2] = y4.z; ys[3] = y4.w;
+    }
+    dlt = group_sum<2>(dlt);
+    if (row_ok && g == 0) delta_ws[static_cast<int64_t>(bh) * f.N + n] = dlt;
+    const bool has_mass = row_live && lse > -INFINITY;
+
+    // ---- MFMA operands for this tile ----------------------------------------
+    // QE:  A[i = query 16mt + lr][k = dim]   (wave's own queries)
+    // dSE: B[k = query of the tile][j = dim 16w + lr]
+    bf16x8 aq[BF ? 2 : 1][BF ? 2 : 1];
+    bf16x8 bq[BF ? 4 : 1];
+    if constexpr (BF) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int na = n0 + 32 * w + 16 * mt + lr;
+        const bool ok = na < f.N && na >= f.query_start;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          uint4 x = {0u, 0u, 0u, 0u};
+          if (ok) x = *reinterpret_cast<const uint4*>(qb + static_cast<int64_t>(na) * f.q_stride[2] + 32 * ks + 8 * lc);
+          aq[mt][ks] = bf16x8_from_bits(x);
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int nq = n0 + 32 * ks + 8 * lc + e;
+          uint16_t bits = 0;
+          if (nq < f.N && nq >= f.query_start)
+            bits = reinterpret_cast<const uint16_t*>(qb + static_cast<int64_t>(nq) * f.q_stride[2])[16 * w + lr];
+          bq[ks][e] = __builtin_bit_cast(__bf16, bits);
+        }
+      }
+    }
+    // fp32 inputs: the MFMA operands are re-read from global (L1) per chunk.
+    auto qf32_at = [&](int nq, int d) -> float {
+      return (nq < f.N && nq >= f.query_start)
+                 ? reinterpret_cast<const float*>(qb + static_cast<int64_t>(nq) * f.q_stride[2])[d]
+                 : 0.f;
+    };
+
+    float dq[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) dq[i] = 0.f;
+    float dy[4] = {0.f, 0.f, 0.f, 0.f};
+    f32x4 dqe[2][4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) dqe[mt][nt] = zero4();
+
+    for (int j0 = 0; j0 < J; j0 += kCJ) {
+      float* sdsb = s_ds + (chunk_count++ & 1) * kCJ * kDsRow;
+      const int jrow = j0 + lr;  // this MFMA lane's offset row
+
+      // ---- (a) QE for the wave's 32 queries x 16 offsets ---------------------
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        f32x4 c = zero4();
+        if constexpr (BF) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            uint4 x = {0u, 0u, 0u, 0u};
+            if (jrow < J)
+              x = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(sE) + jrow * kERowBf16 + 32 * ks + 8 * lc);
+            c = mfma16_bf16(aq[mt][ks], bf16x8_from_bits(x), c);
+          }
+        } else {
+          const float* er = reinterpret_cast<const float*>(sE) + jrow * kERowF32;
+          const int na = n0 + 32 * w + 16 * mt + lr;
+#pragma unroll
+          for (int st = 0; st < 16; ++st)
+            c = mfma16_f32(qf32_at(na, 4 * st + lc), jrow < J ? er[4 * st + lc] : 0.f, c);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_qe[lr * kQeRow + 16 * mt + 4 * lc + r] = c[r];
+      }
+      __builtin_amdgcn_wave_barrier();
+
+      // ---- (b) gathered pair work --------------------------------------------
+      for (int jj = 0; jj < kCJ; ++jj) {
+        const int j = j0 + jj;
+        float dS = 0.f;
+        float dth[4] = {0.f, 0.f, 0.f, 0.f}, dthyz[4] = {0.f, 0.f, 0.f, 0.f};
+        if (j < J) {
+          const int delta = s_off[j];
+          const int s = n - delta;
+          if (wave_n_last >= delta && has_mass && s >= 0 && s < f.N) {
+            const int64_t ss = s;
+            float dot = 0.f, gd = 0.f;
+            uint32_t kw[BF ? 16 : 1], vw[BF ? 16 : 1];
+            float kf[BF ? 1 : DPL], vf[BF ? 1 : DPL];
+            if constexpr (BF) {
+              const uint4* k4 = reinterpret_cast<const uint4*>(kb + ss * f.k_stride[2]);
+              const uint4* v4 = reinterpret_cast<const uint4*>(vb + ss * f.v_stride[2]);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const uint4 x = k4[i], y = v4[i];
+                kw[4 * i] = x.x; kw[4 * i + 1] = x.y; kw[4 * i + 2] = x.z; kw[4 * i + 3] = x.w;
+                vw[4 * i] = y.x; vw[4 * i + 1] = y.y; vw[4 * i + 2] = y.z; vw[4 * i + 3] = y.w;
+              }
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                dot = dot2_bf16(qw16[i], kw[i], dot);
+                gd = dot2_bf16(dw16[i], vw[i], gd);
+              }
+            } else {
+              load_f32<float, DPL>(reinterpret_cast<const float*>(kb + ss * f.k_stride[2]), kf);
+              load_f32<float, DPL>(reinterpret_cast<const float*>(vb + ss * f.v_stride[2]), vf);
+#pragma unroll
+              for (int i = 0; i < DPL; ++i) {
+                dot = fmaf(qf[i], kf[i], dot);
+                gd = fmaf(df[i], vf[i], gd);
+              }
+            }
+            dot = group_sum<2>(dot) + s_qe[jj * kQeRow + qi];
+            const float P = dexp<BF>(fmaf(dot, kScale, s_pb[j]) - lse);
+            if (j >= f.J_small) {
+              const int i = j - f.J_small;
+              const float4 zk = *reinterpret_cast<const float4*>(zb + ss * f.z_stride[2]);
+              const float zs[4] = {zk.x, zk.y, zk.z, zk.w};
+#pragma unroll
+              for (int r = 0; r < kPlanes; ++r) {
+                const int ch = r * SEG + SHIFT;
+                if (ch / DPL != g) continue;
+                const int la = ch % DPL;
+                float va, vb2, da, db;
+                if constexpr (BF) {
+                  va = (la & 1) ? bf16_hi(vw[la >> 1]) : bf16_lo(vw[la >> 1]);
+                  vb2 = ((la + 1) & 1) ? bf16_hi(vw[(la + 1) >> 1]) : bf16_lo(vw[(la + 1) >> 1]);
+                  da = (la & 1) ? bf16_hi(dw16[la >> 1]) : bf16_lo(dw16[la >> 1]);
+                  db = ((la + 1) & 1) ? bf16_hi(dw16[(la + 1) >> 1]) : bf16_lo(dw16[(la + 1) >> 1]);
+                } else {
+                  va = vf[la]; vb2 = vf[la + 1]; da = df[la]; db = df[la + 1];
+                }
+                const float pg = pgain_h[i * f.pgain_stride[0] + r];
+                const float theta = pbase_h[i * f.pbase_stride[0] + r] + pg * ys[r] * zs[r];
+                float sn, cs;
+                dsincos<BF>(theta, &sn, &cs);
+                gd += da * (cs * va - sn * vb2 - va) + db * (sn * va + cs * vb2 - vb2);
+                const float tq = P * (da * (-va * sn - vb2 * cs) + db * (va * cs - vb2 * sn));
+                dth[r] = tq;
+                dthyz[r] = tq * ys[r] * zs[r];
+                dy[r] = fmaf(tq * pg, zs[r], dy[r]);
+              }
+            }
+            gd = group_sum<2>(gd);
+            dS = P * (gd - dlt);
+            const float cds = kScale * dS;
+            if constexpr (BF) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                dq[2 * i] = fmaf(cds, bf16_lo(kw[i]), dq[2 * i]);
+                dq[2 * i + 1] = fmaf(cds, bf16_hi(kw[i]), dq[2 * i + 1]);
+              }
+            } else {
+#pragma unroll
+              for (int i = 0; i < DPL; ++i) dq[i] = fmaf(cds, kf[i], dq[i]);
+            }
+          }
+        }
+        if (g == 0) {
+          sdsb[jj * kDsRow + qw] = dS;
+          s_ds2[qi * kDs2Row + jj] = dS;
+        }
+#pragma unroll
+        for (int r = 0; r < kPlanes; ++r) {
+          if ((r * SEG + SHIFT) / DPL != g) continue;
+          s_ph[((jj & 3) * 8 + r * 2 + 0) * kPhRow + qi] = dth[r];
+          s_ph[((jj & 3) * 8 + r * 2 + 1) * kPhRow + qi] = dthyz[r];
+        }
+        if ((jj & 3) == 3) {
+          // dPhase sums of these 4 offsets over the wave's 32 queries.
+          __builtin_amdgcn_wave_barrier();
+          const int row = l >> 1;           // (jj4, r, kind)
+          const int half = l & 1;
+          const float* src = s_ph + row * kPhRow + 16 * half;
+          float sum = 0.f;
+#pragma unroll
+          for (int x = 0; x < 16; ++x) sum += src[x];
+          sum = group_sum<2>(sum);
+          const int jq = j0 + (jj & ~3) + (row >> 3);
+          if (half == 0 && jq >= f.J_small && jq < J) {
+            const int i = jq - f.J_small;
+            const int rk = row & 7;
+            float* dst = part_ph + ((static_cast<int64_t>(slot) * kWaves + w) * f.J_large + i) * 8 + rk;
+            *dst = first ? sum : *dst + sum;
+          }
+          __builtin_amdgcn_wave_barrier();
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+
+      // ---- (c) dQe += dS E over this chunk (wave's queries) -----------------
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        if constexpr (BF) {
+          bf16x8 ahi = bf16x8_zero(), alo = bf16x8_zero();
+          if (lc < 2) {
+            float x[8];
+            const float* src = s_ds2 + (16 * mt + lr) * kDs2Row + 8 * lc;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = src[e];
+            split_bf16x8(x, ahi, alo);
+          }
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) {
+            uint4 xb = {0u, 0u, 0u, 0u};
+            if (lc < 2)
+              xb = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(sET) + (16 * nt + lr) * lay.jp + j0 + 8 * lc);
+            const bf16x8 bb = bf16x8_from_bits(xb);
+            dqe[mt][nt] = mfma16_bf16(ahi, bb, dqe[mt][nt]);
+            dqe[mt][nt] = mfma16_bf16(alo, bb, dqe[mt][nt]);
+          }
+        } else {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) {
+            const float av = s_ds2[(16 * mt + lr) * kDs2Row + 4 * st + lc];
+            const int je = j0 + 4 * st + lc;
+            const float* er = reinterpret_cast<const float*>(sE) + je * kERowF32;
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) dqe[mt][nt] = mfma16_f32(av, je < J ? er[16 * nt + lr] : 0.f, dqe[mt][nt]);
+          }
+        }
+      }
+
+      __syncthreads();  // the tile's dS for this chunk is complete in sdsb
+
+      // ---- (e) dSE (dims 16w..16w+15) and dPB (wave 0) over the 128 queries ----
+      {
+        f32x4 c = zero4(), c1 = zero4();
+        if constexpr (BF) {
+          bf16x8 one;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) one[e] = static_cast<__bf16>(lr == 0 ? 1.f : 0.f);
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            float x[8];
+            const float* src = sdsb + lr * kDsRow + 32 * ks + 8 * lc;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = src[e];
+            bf16x8 ahi, alo;
+            split_bf16x8(x, ahi, alo);
+            c = mfma16_bf16(ahi, bq[ks], c);
+            c = mfma16_bf16(alo, bq[ks], c);
+            if (w == 0) {
+              c1 = mfma16_bf16(ahi, one, c1);
+              c1 = mfma16_bf16(alo, one, c1);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int st = 0; st < 32; ++st) {
+            const float av = sdsb[lr * kDsRow + 4 * st + lc];
+            c = mfma16_f32(av, qf32_at(n0 + 4 * st + lc, 16 * w + lr), c);
+            if (w == 0) c1 = mfma16_f32(av, lr == 0 ? 1.f : 0.f, c1);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = j0 + 4 * lc + r;
+          if (j < J) {
+            float* dst = part_se + (static_cast<int64_t>(slot) * J + j) * HD + 16 * w + lr;
+            const float v = kScale * c[r];
+            *dst = first ? v : *dst + v;
+            if (w == 0 && lr == 0) {
+              float* dp = part_pb + static_cast<int64_t>(slot) * J + j;
+              *dp = first ? c1[r] : *dp + c1[r];
+            }
+          }
+        }
+      }
+    }
+
+    // ---- end of tile: dQ += c dQe, store dQ and dY ---------------------------
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_stage[(16 * mt + 4 * lc + r) * kStageRow + 16 * nt + lr] = dqe[mt][nt][r];
+    __builtin_amdgcn_wave_barrier();
+    {
+      const float* src = s_stage + qi * kStageRow + g * DPL;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) dq[i] = fmaf(kScale, src[i], dq[i]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (row_ok) {
+      T* dqp = reinterpret_cast<T*>(a.dq) + b * a.dq_stride[0] + h * a.dq_stride[1] + nn * a.dq_stride[2] + g * DPL;
+      store_from_f32<T, DPL>(dqp, dq);
+    }
+    float dyo[4];
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) dyo[r] = group_sum<2>(dy[r]);
+    if (row_ok && g == 0)
+      *reinterpret_cast<float4*>(a.dy_pre + (static_cast<int64_t>(bh) * f.N + n) * kPlanes) =
+          make_float4(dyo[0], dyo[1], dyo[2], dyo[3]);
+  }
+}
+
+template <typename T>
+hipError_t launch_dq_typed(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  char* base = static_cast<char*>(a.workspace);
+  float* delta = reinterpret_cast<float*>(base + ws.delta_off);
+  float* part_se = reinterpret_cast<float*>(base + ws.part_se_off);
+  float* part_pb = reinterpret_cast<float*>(base + ws.part_pb_off);
+  float* part_ph = reinterpret_cast<float*>(base + ws.part_ph_off);
+  const size_t lds = dq_lds<T>(f.J).bytes;
+#define DWARF_DQ_CASE(S)                                                                                        \
+  case S:                                                                                                       \
+    hipLaunchKernelGGL((dsqg_bwd_dq_v2<T, S>), dim3(ws.dq_wgs), dim3(kBlock), lds, stream, a, delta, part_se,   \
+                       part_pb, part_ph, ws.dq_tiles, ws.dq_tpw, ws.dq_ntg, ws.dq_wgs);                          \
+    break;
+  switch (f.plane_shift) {
+    DWARF_DQ_CASE(0) DWARF_DQ_CASE(1) DWARF_DQ_CASE(2) DWARF_DQ_CASE(3) DWARF_DQ_CASE(4)
+    DWARF_DQ_CASE(5) DWARF_DQ_CASE(6) DWARF_DQ_CASE(7) DWARF_DQ_CASE(8) DWARF_DQ_CASE(9)
+    DWARF_DQ_CASE(10) DWARF_DQ_CASE(11) DWARF_DQ_CASE(12) DWARF_DQ_CASE(13) DWARF_DQ_CASE(14)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef DWARF_DQ_CASE
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t dq_lds_bytes(int J, int dtype) {
+  return dtype == DWARF_BF16 ? dq_lds<bf16>(J).bytes : dq_lds<float>(J).bytes;
+}
+
+hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+  if (a.fwd.dtype == DWARF_BF16) return launch_dq_typed<bf16>(a, ws, stream);
+  return launch_dq_typed<float>(a, ws, stream);
+}
+
+}  // namespace dwarf

@@ -32,19 +32,28 @@ struct DsqgGeom {
 
 hipError_t launch_dsqg_fwd(const dwarf_dsqg_fwd_args& a, hipStream_t stream);
 
-// Backward workspace layout (bytes, 256-byte aligned sections).
+// Backward workspace layout (bytes, 256-byte aligned sections).  The dq
+// launch writes one partial slot per workgroup (slot = (h*B + b)*n_tg + tg);
+// the reduce launch sums them in a fixed order.
 struct BwdWorkspace {
   size_t delta_off, delta_bytes;        // [B,H,N] fp32
-  size_t part_se_off, part_se_bytes;    // [blocks_q][J][64] fp32
-  size_t part_pb_off, part_pb_bytes;    // [blocks_q][J] fp32
-  size_t part_ph_off, part_ph_bytes;    // [blocks_q][J_L][4][2] fp32
+  size_t part_se_off, part_se_bytes;    // [W][J][64] fp32
+  size_t part_pb_off, part_pb_bytes;    // [W][J] fp32
+  size_t part_ph_off, part_ph_bytes;    // [W][4 waves][J_L][8] fp32
+  size_t red_off, red_bytes;            // stage-1 sums of the reduction
   size_t total;
-  int blocks_q;                         // query-centric workgroups
+  int dq_tiles;   // 128-query tiles per (b, h)
+  int dq_tpw;     // tiles per workgroup
+  int dq_ntg;     // workgroups per (b, h)
+  int dq_wgs;     // W = B * H * dq_ntg
+  int red_groups_se, red_groups_pb, red_groups_ph;  // stage-1 row groups per segment
 };
 BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a);
 // do_dq: delta + dQ/dY + parameter-gradient partials and their reduction;
 // do_dkdv: dK/dV/dZ (reads the delta written by the dq stage).
 hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
                            bool do_dkdv);
+hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
+size_t dq_lds_bytes(int J, int dtype);
 
 }  // namespace dwarf
