@@ -91,6 +91,15 @@ int check_lattice(int H, int H_kv, int N, int hd, int J, int J_small, int J_larg
   return DWARF_OK;
 }
 
+// The bf16 kernels gather rows with 32-bit buffer offsets (row - offset) * stride
+// that may run to about 2N + 64 rows in either direction.
+int check_gather_span(const char* name, int64_t row_stride, int64_t elem, int N) {
+  if (row_stride <= 0) return fail(DWARF_ERR_UNSUPPORTED, "%s needs a positive row stride", name);
+  if ((2 * static_cast<int64_t>(N) + 64) * row_stride * elem >= (int64_t(1) << 31))
+    return fail(DWARF_ERR_UNSUPPORTED, "%s: (2N+64) rows x stride must stay below 2 GiB for 32-bit gathers", name);
+  return DWARF_OK;
+}
+
 int check_fwd(const dwarf_dsqg_fwd_args& a) {
   if (a.B < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "B=%d", a.B);
   int rc = check_lattice(a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, a.query_start);
@@ -104,6 +113,11 @@ int check_fwd(const dwarf_dsqg_fwd_args& a) {
   if ((rc = check_planes("z_pre", a.z_pre, a.z_stride))) return rc;
   if (!a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.lse)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter table, offsets or lse is NULL");
+  if (a.dtype == DWARF_BF16) {
+    if ((rc = check_gather_span("k", a.k_stride[2], 2, a.N))) return rc;
+    if ((rc = check_gather_span("v", a.v_stride[2], 2, a.N))) return rc;
+    if ((rc = check_gather_span("z_pre", a.z_stride[2], 4, a.N))) return rc;
+  }
   return DWARF_OK;
 }
 

@@ -152,6 +152,185 @@ __global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_kernel(const dwarf_dsqg_
         make_float4(dzo[0], dzo[1], dzo[2], dzo[3]);
 }
 
+// ---- bf16 dkdv: packed rows and v_dot2 ------------------------------------
+// Same mapping as dsqg_bwd_dkdv_kernel (two lanes per key, 32 dims each).
+// <q, k>, <q, e_j> and <dO, v> are v_dot2_f32_bf16 on the packed rows (exact
+// bf16 products, fp32 sums); the rank-1 updates dK += c dS q and dV += P dO
+// stay fp32 FMAs on the widened rows, and the rotated MOVT channels of dV get
+// an fp32 correction term.
+constexpr int kERowDkdv = 72;  // bf16 E row stride (elements)
+
+__device__ __forceinline__ float dot2b(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+template <int SHIFT>
+__global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_bf16_v2(const dwarf_dsqg_bwd_args a,
+                                                                const float* __restrict__ delta_ws, int tiles,
+                                                                int total) {
+  constexpr int HD = kHeadDim, DPL = 32, KPB = kBlock / 2, SEG = HD / kPlanes;
+  constexpr float kScale = 0.125f;
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  extern __shared__ float smem[];
+  int* s_off = reinterpret_cast<int*>(smem);
+  uint16_t* sE = reinterpret_cast<uint16_t*>(smem + ((f.J + 3) & ~3));   // [J][kERowDkdv]
+
+  const int work = xcd_remap(blockIdx.x, total);
+  const int bhk = work / tiles;
+  const int tile = work - bhk * tiles;
+  const int b = bhk / f.H_kv;
+  const int hk = bhk - b * f.H_kv;
+  const int group = f.H / f.H_kv;
+  for (int i = threadIdx.x; i < f.J * HD; i += kBlock) {
+    const int j = i / HD, d = i - j * HD;
+    float e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
+    if (f.se_round_bf16) e = round_bf16(e);
+    sE[j * kERowDkdv + d] = f32_to_bf16_bits(e);
+  }
+  for (int j = threadIdx.x; j < f.J; j += kBlock) s_off[j] = f.offsets[j];
+  __syncthreads();
+
+  const int lane = threadIdx.x;
+  const int g = lane & 1;
+  const int m = tile * KPB + lane / 2;
+  if (m >= f.N) return;  // no barriers below
+  const int wave_m_first = uniform(tile * KPB + (lane / kWave) * (kWave / 2));
+  const int wave_m_last = wave_m_first + kWave / 2 - 1;
+  const int64_t mm = m;
+
+  uint32_t k32[16], v32[16];
+  {
+    const uint4* k4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] +
+                                                     hk * f.k_stride[1] + mm * f.k_stride[2] + g * DPL);
+    const uint4* v4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] +
+                                                     hk * f.v_stride[1] + mm * f.v_stride[2] + g * DPL);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 x = k4[i], y = v4[i];
+      k32[4 * i] = x.x; k32[4 * i + 1] = x.y; k32[4 * i + 2] = x.z; k32[4 * i + 3] = x.w;
+      v32[4 * i] = y.x; v32[4 * i + 1] = y.y; v32[4 * i + 2] = y.z; v32[4 * i + 3] = y.w;
+    }
+  }
+  float dk[DPL], dv[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) { dk[d] = 0.f; dv[d] = 0.f; }
+  const float4 z4 = *reinterpret_cast<const float4*>(f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2]);
+  const float zs[4] = {z4.x, z4.y, z4.z, z4.w};
+  float dz[4] = {0.f, 0.f, 0.f, 0.f};
+
+  for (int hh = 0; hh < group; ++hh) {
+    const int h = hk * group + hh;
+    const int bh = b * f.H + h;
+    const bf16* qbase = reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1] + g * DPL;
+    const bf16* dobase = reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1] + g * DPL;
+    const float* lsebase = f.lse + b * f.lse_stride[0] + h * f.lse_stride[1];
+    const float* dltbase = delta_ws + static_cast<int64_t>(bh) * f.N;
+    const float* ybase = f.y_pre + b * f.y_stride[0] + h * f.y_stride[1];
+    for (int j = 0; j < f.J; ++j) {
+      const int delta = s_off[j];
+      if (wave_m_first + delta >= f.N || wave_m_last + delta < f.query_start) continue;
+      const int n = m + delta;
+      if (n < 0 || n >= f.N) continue;
+      const int64_t nn = n;
+      const float lse = lsebase[nn * f.lse_stride[2]];
+      if (!(lse > -INFINITY)) continue;
+      uint32_t q32[16], o32[16];
+      const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * f.q_stride[2]);
+      const uint4* o4 = reinterpret_cast<const uint4*>(dobase + nn * a.dout_stride[2]);
+      const uint4* e4 = reinterpret_cast<const uint4*>(sE + j * kERowDkdv + g * DPL);
+      float dot = 0.f, gd = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 x = q4[i], e = e4[i], y = o4[i];
+        q32[4 * i] = x.x; q32[4 * i + 1] = x.y; q32[4 * i + 2] = x.z; q32[4 * i + 3] = x.w;
+        o32[4 * i] = y.x; o32[4 * i + 1] = y.y; o32[4 * i + 2] = y.z; o32[4 * i + 3] = y.w;
+        dot = dot2b(x.x, k32[4 * i], dot); dot = dot2b(x.y, k32[4 * i + 1], dot);
+        dot = dot2b(x.z, k32[4 * i + 2], dot); dot = dot2b(x.w, k32[4 * i + 3], dot);
+        dot = dot2b(x.x, e.x, dot); dot = dot2b(x.y, e.y, dot);
+        dot = dot2b(x.z, e.z, dot); dot = dot2b(x.w, e.w, dot);
+        gd = dot2b(y.x, v32[4 * i], gd); gd = dot2b(y.y, v32[4 * i + 1], gd);
+        gd = dot2b(y.z, v32[4 * i + 2], gd); gd = dot2b(y.w, v32[4 * i + 3], gd);
+      }
+      dot = group_sum<2>(dot);
+      const float P = __expf(fmaf(dot, kScale, f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]]) - lse);
+      float corr_a[4] = {0.f, 0.f, 0.f, 0.f}, corr_b[4] = {0.f, 0.f, 0.f, 0.f};
+      const bool far = j >= f.J_small;
+      if (far) {
+        const int i = j - f.J_small;
+        const float4 y4 = *reinterpret_cast<const float4*>(ybase + nn * f.y_stride[2]);
+        const float ys[4] = {y4.x, y4.y, y4.z, y4.w};
+#pragma unroll
+        for (int r = 0; r < kPlanes; ++r) {
+          const int ch = r * SEG + SHIFT;
+          if (ch / DPL != g) continue;
+          const int la = ch % DPL, lb = la + 1;
+          const float va = (la & 1) ? bf16_hi(v32[la >> 1]) : bf16_lo(v32[la >> 1]);
+          const float vb = (lb & 1) ? bf16_hi(v32[lb >> 1]) : bf16_lo(v32[lb >> 1]);
+          const float da = (la & 1) ? bf16_hi(o32[la >> 1]) : bf16_lo(o32[la >> 1]);
+          const float db = (lb & 1) ? bf16_hi(o32[lb >> 1]) : bf16_lo(o32[lb >> 1]);
+          const float pg = f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r];
+          const float theta = f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r] + pg * ys[r] * zs[r];
+          float sn, cs;
+          dsincos<true>(theta, &sn, &cs);
+          gd += da * (cs * va - sn * vb - va) + db * (sn * va + cs * vb - vb);
+          const float t = P * (da * (-va * sn - vb * cs) + db * (va * cs - vb * sn));
+          dz[r] = fmaf(t * pg, ys[r], dz[r]);
+          corr_a[r] = (cs - 1.f) * da + sn * db;   // (R^T dO - dO)_a
+          corr_b[r] = -sn * da + (cs - 1.f) * db;  // (R^T dO - dO)_b
+        }
+      }
+      gd = group_sum<2>(gd);
+      const float dS = P * (gd - dltbase[nn]);
+      const float cdS = kScale * dS;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        dk[2 * i] = fmaf(cdS, bf16_lo(q32[i]), dk[2 * i]);
+        dk[2 * i + 1] = fmaf(cdS, bf16_hi(q32[i]), dk[2 * i + 1]);
+        dv[2 * i] = fmaf(P, bf16_lo(o32[i]), dv[2 * i]);
+        dv[2 * i + 1] = fmaf(P, bf16_hi(o32[i]), dv[2 * i + 1]);
+      }
+      if (far) {
+#pragma unroll
+        for (int r = 0; r < kPlanes; ++r) {
+          const int ch = r * SEG + SHIFT;
+          if (ch / DPL != g) continue;
+          const int la = ch % DPL;
+          dv[la] = fmaf(P, corr_a[r], dv[la]);
+          dv[la + 1] = fmaf(P, corr_b[r], dv[la + 1]);
+        }
+      }
+    }
+  }
+  store_from_f32<bf16, DPL>(reinterpret_cast<bf16*>(a.dk) + b * a.dk_stride[0] + hk * a.dk_stride[1] + mm * a.dk_stride[2] + g * DPL, dk);
+  store_from_f32<bf16, DPL>(reinterpret_cast<bf16*>(a.dv) + b * a.dv_stride[0] + hk * a.dv_stride[1] + mm * a.dv_stride[2] + g * DPL, dv);
+  float dzo[4];
+#pragma unroll
+  for (int r = 0; r < kPlanes; ++r) dzo[r] = group_sum<2>(dz[r]);
+  if (g == 0)
+    *reinterpret_cast<float4*>(a.dz_pre + (static_cast<int64_t>(bhk) * f.N + m) * kPlanes) =
+        make_float4(dzo[0], dzo[1], dzo[2], dzo[3]);
+}
+
+hipError_t launch_dkdv_bf16_v2(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  constexpr int KPB = kBlock / 2;
+  const float* delta = reinterpret_cast<const float*>(static_cast<char*>(a.workspace) + ws.delta_off);
+  const int tiles = (f.N + KPB - 1) / KPB;
+  const int total = tiles * f.B * f.H_kv;
+  const size_t lds = static_cast<size_t>((f.J + 3) & ~3) * sizeof(int) + static_cast<size_t>(f.J) * kERowDkdv * 2;
+#define DWARF_DKDV2_CASE(S) \
+  case S: hipLaunchKernelGGL(dsqg_bwd_dkdv_bf16_v2<S>, dim3(total), dim3(kBlock), lds, stream, a, delta, tiles, total); break;
+  switch (f.plane_shift) {
+    DWARF_DKDV2_CASE(0) DWARF_DKDV2_CASE(1) DWARF_DKDV2_CASE(2) DWARF_DKDV2_CASE(3) DWARF_DKDV2_CASE(4)
+    DWARF_DKDV2_CASE(5) DWARF_DKDV2_CASE(6) DWARF_DKDV2_CASE(7) DWARF_DKDV2_CASE(8) DWARF_DKDV2_CASE(9)
+    DWARF_DKDV2_CASE(10) DWARF_DKDV2_CASE(11) DWARF_DKDV2_CASE(12) DWARF_DKDV2_CASE(13) DWARF_DKDV2_CASE(14)
+    default: return hipErrorInvalidValue;
+  }
+#undef DWARF_DKDV2_CASE
+  return hipGetLastError();
+}
+
 // ---- fixed-order reduction of the dq partials -----------------------------
 constexpr int kRedRows = 16;  // rows summed per stage-1 group
 
@@ -261,7 +440,9 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   constexpr int kTile = 128;
   w.dq_tiles = (f.N + kTile - 1) / kTile;
   const int total_tiles = w.dq_tiles * f.B * f.H;
-  w.dq_tpw = total_tiles / 512;  // aim for about 512 workgroups
+  // Two 4-wave workgroups fit per CU (VGPR/LDS bound): size the tile groups so
+  // every workgroup is resident at once (at most 512 on 256 CUs).
+  w.dq_tpw = (total_tiles + 511) / 512;
   if (w.dq_tpw < 1) w.dq_tpw = 1;
   if (w.dq_tpw > 8) w.dq_tpw = 8;
   if (w.dq_tpw > w.dq_tiles) w.dq_tpw = w.dq_tiles > 0 ? w.dq_tiles : 1;
@@ -308,7 +489,7 @@ hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws,
     if (e != hipSuccess) return e;
   }
   if (do_dkdv) {
-    if (a.fwd.dtype == DWARF_BF16) return launch_dkdv_typed<bf16, kLanesBwd, true>(a, ws, stream);
+    if (a.fwd.dtype == DWARF_BF16) return launch_dkdv_bf16_v2(a, ws, stream);
     return launch_dkdv_typed<float, kLanesBwd, false>(a, ws, stream);
   }
   return hipSuccess;

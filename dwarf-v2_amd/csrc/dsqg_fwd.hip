@@ -15,6 +15,7 @@
 // unchanged mathematically.
 #include "common.h"
 #include "dsqg_internal.h"
+#include "mfma.h"
 
 namespace dwarf {
 namespace {
@@ -135,6 +136,342 @@ __global__ __launch_bounds__(kBlock) void dsqg_fwd_kernel(const dwarf_dsqg_fwd_a
   if (g == 0) *lse_p = l > 0.f ? m + dlog<FAST>(l) : -INFINITY;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 forward, four lanes per query.
+//
+// Lane g of a query holds head dims [16g, 16g+16): its slices of q, of the
+// accumulator and of every gathered K/V row (two 16-byte loads each), so one
+// wave load instruction covers 64 contiguous bytes of 16 consecutive source
+// rows.
+//
+// Each wave first lists the offsets that give at least one of its 16 queries
+// a source row (s_list, padded with a sentinel whose rows are out of range),
+// then walks that list in chunks of CJ with the next chunk's loads already in
+// flight (two register buffers).  The gathers are raw buffer loads with
+// 32-bit offsets: a lane without a source gets an offset past the end of the
+// tensor and reads zeros, so the loop has no per-lane branches.
+//
+// <q, e_j> for the wave's 16 queries and all offsets is one
+// v_mfma_f32_16x16x32_bf16 pass at the start, stored pre-scaled together
+// with pos_bias (s_qe = log2(e) * (<q,e_j>/8 + pb_j)); the softmax runs in
+// base 2.  <q, k> is v_dot2_f32_bf16 on the packed rows summed over the 4
+// lanes with DPP.  P.V stays fp32 (widened bf16 rows times the fp32 weight),
+// as the reference accumulates it (dsqg:993-1013).  With plane_shift <= 14
+// the MOVT pair of plane r (dims 16r+shift, 16r+shift+1) lies in lane r's
+// slice, so each lane rotates exactly one pair of every far V row.
+// ---------------------------------------------------------------------------
+constexpr int kLanesQ = 4;                  // lanes per query
+constexpr int kQPW = kWave / kLanesQ;       // 16 queries per wave
+constexpr int kQPB = kBlock / kLanesQ;      // 64 queries per workgroup
+constexpr int kChunkFwd = 2;                // offsets per prefetch chunk (the launch's choice)
+constexpr int kERowFwd = 72;                // bf16 E row stride (elements)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every tensor (spans are < 2^31)
+
+__device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t row_bytes, int rows, int tail) {
+  const int64_t span = rows > 0 ? (rows - 1) * row_bytes + tail : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(span), 0x00020000);
+}
+
+// LDS: s_pb[JE] f32, s_off[JE] i32, s_ph[JL4][4] float2, s_list[4][list_len] int2,
+// then one region that first holds the bf16 E rows (sE[JE][72]) and, after a
+// barrier, the four waves' s_qe[16][qe_row] tables.
+struct FwdLayout {
+  int JE, JL4, qe_row, list_len, max_blocks;
+  size_t off_ph, off_list, off_big, bytes;
+};
+
+constexpr int kMaxQeBlocks = 17;   // JE / 16 for J <= kMaxOffsets (256) plus the sentinel
+
+// JE >= J + 1 keeps a sentinel slot (index J) with an unreachable offset.
+__host__ __device__ inline FwdLayout fwd_layout(int J, int J_large, int CJ) {
+  FwdLayout L;
+  L.JE = (J + 1 + 15) / 16 * 16;
+  L.JL4 = (J_large + 1) / 2 * 2;                       // keeps the float2 table a multiple of 16 bytes
+  L.qe_row = L.JE + 4;
+  L.list_len = (L.JE + 4 * CJ + 1) / 2 * 2;            // list + padding for the prefetch overrun
+  L.off_ph = static_cast<size_t>(2 * L.JE) * 4;
+  L.off_list = L.off_ph + static_cast<size_t>(L.JL4) * 4 * 8;
+  L.off_big = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;
+  const size_t e_bytes = static_cast<size_t>(L.JE) * kERowFwd * 2;
+  const size_t qe_bytes = static_cast<size_t>(4 * kQPW * L.qe_row) * 4;
+  L.bytes = L.off_big + (e_bytes > qe_bytes ? e_bytes : qe_bytes);
+  return L;
+}
+
+template <int CJ>
+struct FwdChunk {
+  uint4 k[CJ][2], v[CJ][2];
+  float z[CJ];
+  bool ok[CJ];
+  int j[CJ];
+};
+
+template <int SHIFT, int CJ>
+__global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_fwd_args a, int tiles, int total) {
+  constexpr float kC = 0.125f * kLog2e;           // 1/sqrt(64) in base-2 score units
+  constexpr float kSlack2 = 8.0f * kLog2e;        // kRescaleSlack in base 2
+  static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
+  const int J = a.J, N = a.N, J_small = a.J_small;
+  const FwdLayout lay = fwd_layout(J, a.J_large, CJ);
+  extern __shared__ float smem[];
+  char* sm = reinterpret_cast<char*>(smem);
+  float* s_pb = smem;
+  int* s_off = reinterpret_cast<int*>(smem + lay.JE);
+  float2* s_ph = reinterpret_cast<float2*>(sm + lay.off_ph);
+  int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
+  uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_big);
+  float* s_qe_all = reinterpret_cast<float*>(sm + lay.off_big);   // replaces sE after the second barrier
+
+  const int work = xcd_remap(blockIdx.x, total);
+  const int bh = work / tiles;
+  const int tile = work - bh * tiles;
+  const int b = bh / a.H;
+  const int h = bh - b * a.H;
+  const int hk = h / (a.H / a.H_kv);
+
+  for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
+    const int j = i / kHeadDim, d = i - j * kHeadDim;
+    float e = 0.f;
+    if (j < J) {
+      e = a.scale_embed[j * a.se_stride[0] + d * a.se_stride[1]];
+      if (a.se_round_bf16) e = round_bf16(e);
+    }
+    sE[j * kERowFwd + d] = f32_to_bf16_bits(e);
+  }
+  for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
+    s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
+    s_off[j] = j < J ? a.offsets[j] : 0;
+  }
+  for (int t = threadIdx.x; t < a.J_large * kPlanes; t += kBlock) {
+    const int i = t / kPlanes, r = t - i * kPlanes;
+    s_ph[t] = make_float2(a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r],
+                          a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r]);
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int qi = l >> 2;
+  const int n0w = tile * kQPB + w * kQPW;
+  const int n = n0w + qi;
+  const int n_hi = min(n0w + kQPW - 1, N - 1);
+  const bool row_ok = n < N;
+  const bool live = row_ok && n >= a.query_start;
+  const int64_t nn = n;
+  float* s_qe = s_qe_all + w * kQPW * lay.qe_row;
+  int2* s_list = s_list_all + w * lay.list_len;
+
+  const bf16* qbase = reinterpret_cast<const bf16*>(a.q) + b * a.q_stride[0] + h * a.q_stride[1];
+  // s_qe[query][j] = log2(e) * (<q, e_j> / 8 + pb_j) for the wave's 16 queries:
+  // products into registers, a barrier (every wave is done reading sE), then
+  // the tables are written over sE.
+  {
+    const int lr = l & 15, lc = l >> 4;
+    const int nq = n0w + lr;
+    uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (nq < N) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        xa[ks] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(nq) * a.q_stride[2] + 32 * ks + 8 * lc);
+    }
+    f32x4 c[kMaxQeBlocks];
+#pragma unroll
+    for (int bi = 0; bi < kMaxQeBlocks; ++bi) {
+      c[bi] = zero4();
+      if (bi * 16 < lay.JE) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const uint4 xb = *reinterpret_cast<const uint4*>(sE + (bi * 16 + lr) * kERowFwd + 32 * ks + 8 * lc);
+          c[bi] = mfma16_bf16(bf16x8_from_bits(xa[ks]), bf16x8_from_bits(xb), c[bi]);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int bi = 0; bi < kMaxQeBlocks; ++bi) {
+      if (bi * 16 < lay.JE) {
+        const float pb8 = 8.0f * s_pb[bi * 16 + lr];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_qe[(4 * lc + r) * lay.qe_row + bi * 16 + lr] = (c[bi][r] + pb8) * kC;
+      }
+    }
+  }
+  if (n0w >= N) return;                       // whole wave past the end (no block barriers below)
+  // The wave's offset list: offsets giving some query n0w..n_hi a source row in [0, N).
+  // The sentinel (index J) gets the offset n0w - N, out of range for every query.
+  int cnt = 0;
+  for (int base = 0; base < J; base += kWave) {
+    const int j = base + l;
+    const int d = j < J ? s_off[j] : 0;
+    const bool need = j < J && d <= n_hi && d >= n0w - (N - 1);
+    const uint64_t mask = __ballot(need);
+    const int pos = cnt + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+    if (need) s_list[pos] = make_int2(j, d);
+    cnt += __popcll(mask);
+  }
+  cnt = uniform(cnt);
+  const int cntp = (cnt + CJ - 1) / CJ * CJ;
+  for (int t = cnt + l; t < cntp + 2 * CJ; t += kWave) s_list[t] = make_int2(J, n0w - N);
+  __builtin_amdgcn_wave_barrier();
+
+  uint32_t q32[8];
+  float yg = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q32[i] = 0u;
+  if (live) {
+    const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * a.q_stride[2] + 16 * g);
+    const uint4 x0 = q4[0], x1 = q4[1];
+    q32[0] = x0.x; q32[1] = x0.y; q32[2] = x0.z; q32[3] = x0.w;
+    q32[4] = x1.x; q32[5] = x1.y; q32[6] = x1.z; q32[7] = x1.w;
+    yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
+  }
+  // Per-lane byte offsets of row 0 shifted by the lane's query; a lane without
+  // a live query uses n_eff = n0w - 2N, so n_eff - d < 0 for every listed d.
+  const int n_eff = live ? n : n0w - 2 * N;
+  const int ks_b = static_cast<int>(a.k_stride[2]) * 2, vs_b = static_cast<int>(a.v_stride[2]) * 2;
+  const int zs_b = static_cast<int>(a.z_stride[2]) * 4;
+  const __amdgpu_buffer_rsrc_t rk =
+      rows_rsrc(reinterpret_cast<const bf16*>(a.k) + b * a.k_stride[0] + hk * a.k_stride[1], ks_b, N, 128);
+  const __amdgpu_buffer_rsrc_t rv =
+      rows_rsrc(reinterpret_cast<const bf16*>(a.v) + b * a.v_stride[0] + hk * a.v_stride[1], vs_b, N, 128);
+  const __amdgpu_buffer_rsrc_t rz = rows_rsrc(a.z_pre + b * a.z_stride[0] + hk * a.z_stride[1], zs_b, N, 16);
+  const int kb_lane = n_eff * ks_b + 32 * g;
+  const int vb_lane = n_eff * vs_b + 32 * g;
+  const int zb_lane = n_eff * zs_b + 4 * g;
+
+  float acc[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+  float m = -3.0e38f, lsum = 0.f;
+
+  auto fetch = [&](int k0, FwdChunk<CJ>& c) {
+#pragma unroll
+    for (int jj = 0; jj < CJ; ++jj) {
+      const int2 e = s_list[k0 + jj];
+      const int j = uniform(e.x), d = uniform(e.y);
+      c.j[jj] = j;
+      c.ok[jj] = static_cast<uint32_t>(n_eff - d) < static_cast<uint32_t>(N);
+      const uint32_t ko = static_cast<uint32_t>(kb_lane - d * ks_b);
+      const uint32_t vo = static_cast<uint32_t>(vb_lane - d * vs_b);
+      const uint32_t zo = (j >= J_small && j < J) ? static_cast<uint32_t>(zb_lane - d * zs_b) : kOutOfRange;
+      c.k[jj][0] = buf_load16(rk, ko);
+      c.k[jj][1] = buf_load16(rk, ko + 16);
+      c.v[jj][0] = buf_load16(rv, vo);
+      c.v[jj][1] = buf_load16(rv, vo + 16);
+      c.z[jj] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rz, zo, 0, 0));
+    }
+  };
+
+  auto consume = [&](const FwdChunk<CJ>& c) {
+    float sc[CJ];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int jj = 0; jj < CJ; ++jj) {
+      const uint32_t* kw = reinterpret_cast<const uint32_t*>(&c.k[jj][0]);
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dot = dot2bf(q32[i], kw[i], dot);
+      dot = group_sum<4>(dot);
+      const float s2 = fmaf(dot, kC, s_qe[qi * lay.qe_row + c.j[jj]]);
+      sc[jj] = c.ok[jj] ? s2 : -INFINITY;
+      cmax = fmaxf(cmax, sc[jj]);
+    }
+    if (cmax > m + kSlack2) {
+      const float f = __builtin_amdgcn_exp2f(m - cmax);   // 0 on the first valid chunk
+#pragma unroll
+      for (int d = 0; d < 16; ++d) acc[d] *= f;
+      lsum *= f;
+      m = cmax;
+    }
+#pragma unroll
+    for (int jj = 0; jj < CJ; ++jj) {
+      const float p = __builtin_amdgcn_exp2f(sc[jj] - m);  // m is finite: 0 without a source
+      lsum += p;
+      const uint32_t* vw = reinterpret_cast<const uint32_t*>(&c.v[jj][0]);
+      float vf[16];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        vf[2 * i] = bf16_lo(vw[i]);
+        vf[2 * i + 1] = bf16_hi(vw[i]);
+      }
+      const int j = c.j[jj];
+      if (j >= J_small && j < J) {
+        const float2 ph = s_ph[(j - J_small) * kPlanes + g];
+        float sn, cs;
+        dsincos<true>(fmaf(ph.y * yg, c.z[jj], ph.x), &sn, &cs);
+        const float va = vf[SHIFT], vb = vf[SHIFT + 1];
+        vf[SHIFT] = cs * va - sn * vb;
+        vf[SHIFT + 1] = sn * va + cs * vb;
+      }
+#pragma unroll
+      for (int d = 0; d < 16; ++d) acc[d] = fmaf(p, vf[d], acc[d]);
+    }
+  };
+
+  if (cnt > 0) {
+    FwdChunk<CJ> c0, c1;
+    fetch(0, c0);
+    for (int k0 = 0; k0 < cntp; k0 += 2 * CJ) {
+      fetch(k0 + CJ, c1);        // past the list end this reads the sentinel: zeros
+      consume(c0);
+      fetch(k0 + 2 * CJ, c0);
+      consume(c1);
+    }
+  }
+
+  if (!row_ok) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.out) + b * a.out_stride[0] + h * a.out_stride[1] +
+                                       nn * a.out_stride[2] + 16 * g);
+  uint4 x0, x1;
+  x0.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  x0.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  x0.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);
+  x0.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
+  x1.x = pack_bf16x2(acc[8] * inv, acc[9] * inv);
+  x1.y = pack_bf16x2(acc[10] * inv, acc[11] * inv);
+  x1.z = pack_bf16x2(acc[12] * inv, acc[13] * inv);
+  x1.w = pack_bf16x2(acc[14] * inv, acc[15] * inv);
+  o4[0] = x0;
+  o4[1] = x1;
+  if (g == 0)
+    a.lse[b * a.lse_stride[0] + h * a.lse_stride[1] + nn * a.lse_stride[2]] =
+        lsum > 0.f ? (m + __builtin_amdgcn_logf(lsum)) * kLn2 : -INFINITY;
+}
+
+template <int CJ>
+hipError_t launch_fwd_bf16_q4(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
+  const int tiles = (a.N + kQPB - 1) / kQPB;
+  const int total = tiles * a.B * a.H;
+  if (total == 0) return hipSuccess;
+  const size_t lds = fwd_layout(a.J, a.J_large, CJ).bytes;
+#define DWARF_FWDQ4_CASE(S) \
+  case S: hipLaunchKernelGGL((dsqg_fwd_bf16_q4<S, CJ>), dim3(total), dim3(kBlock), lds, stream, a, tiles, total); break;
+  switch (a.plane_shift) {
+    DWARF_FWDQ4_CASE(0) DWARF_FWDQ4_CASE(1) DWARF_FWDQ4_CASE(2) DWARF_FWDQ4_CASE(3) DWARF_FWDQ4_CASE(4)
+    DWARF_FWDQ4_CASE(5) DWARF_FWDQ4_CASE(6) DWARF_FWDQ4_CASE(7) DWARF_FWDQ4_CASE(8) DWARF_FWDQ4_CASE(9)
+    DWARF_FWDQ4_CASE(10) DWARF_FWDQ4_CASE(11) DWARF_FWDQ4_CASE(12) DWARF_FWDQ4_CASE(13) DWARF_FWDQ4_CASE(14)
+    default: return hipErrorInvalidValue;
+  }
+#undef DWARF_FWDQ4_CASE
+  return hipGetLastError();
+}
+
 template <typename T, int L, bool FAST>
 hipError_t launch_shift(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
   constexpr int QPB = kBlock / L;
@@ -160,7 +497,7 @@ hipError_t launch_shift(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_dsqg_fwd(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
-  if (a.dtype == DWARF_BF16) return launch_shift<bf16, 2, true>(a, stream);
+  if (a.dtype == DWARF_BF16) return launch_fwd_bf16_q4<kChunkFwd>(a, stream);
   return launch_shift<float, 2, false>(a, stream);
 }
 
