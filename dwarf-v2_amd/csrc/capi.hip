@@ -91,12 +91,12 @@ int check_lattice(int H, int H_kv, int N, int hd, int J, int J_small, int J_larg
   return DWARF_OK;
 }
 
-// The bf16 kernels gather rows with 32-bit buffer offsets (row - offset) * stride
-// that may run to about 2N + 64 rows in either direction.
+// The bf16 kernels gather rows with 32-bit buffer offsets row * stride where
+// the row index stays within 2N + 128 of zero in either direction.
 int check_gather_span(const char* name, int64_t row_stride, int64_t elem, int N) {
   if (row_stride <= 0) return fail(DWARF_ERR_UNSUPPORTED, "%s needs a positive row stride", name);
-  if ((2 * static_cast<int64_t>(N) + 64) * row_stride * elem >= (int64_t(1) << 31))
-    return fail(DWARF_ERR_UNSUPPORTED, "%s: (2N+64) rows x stride must stay below 2 GiB for 32-bit gathers", name);
+  if ((2 * static_cast<int64_t>(N) + 128) * row_stride * elem >= (int64_t(1) << 31))
+    return fail(DWARF_ERR_UNSUPPORTED, "%s: (2N+128) rows x stride must stay below 2 GiB for 32-bit gathers", name);
   return DWARF_OK;
 }
 
@@ -114,6 +114,9 @@ int check_fwd(const dwarf_dsqg_fwd_args& a) {
   if (!a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.lse)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter table, offsets or lse is NULL");
   if (a.dtype == DWARF_BF16) {
+    if ((rc = check_gather_span("q", a.q_stride[2], 2, a.N))) return rc;
+    if ((rc = check_gather_span("lse", a.lse_stride[2], 4, a.N))) return rc;
+    if ((rc = check_gather_span("y_pre", a.y_stride[2], 4, a.N))) return rc;
     if ((rc = check_gather_span("k", a.k_stride[2], 2, a.N))) return rc;
     if ((rc = check_gather_span("v", a.v_stride[2], 2, a.N))) return rc;
     if ((rc = check_gather_span("z_pre", a.z_stride[2], 4, a.N))) return rc;
@@ -154,6 +157,7 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
   if (rc) return rc;
   const int dt = a.fwd.dtype;
   if ((rc = check_contig_rows("dout", a.dout, a.dout_stride, dt))) return rc;
+  if (dt == DWARF_BF16 && (rc = check_gather_span("dout", a.dout_stride[2], 2, a.fwd.N))) return rc;
   if (do_dq) {
     if ((rc = check_contig_rows("dq", a.dq, a.dq_stride, dt))) return rc;
     if (!a.dpos_bias || !a.dscale_embed || !a.dphase_base || !a.dphase_gain || !a.dy_pre)

@@ -13,6 +13,7 @@
 //     dV and dZ in registers; the GQA head sum happens in-kernel.
 #include "common.h"
 #include "dsqg_internal.h"
+#include "gather.h"
 
 namespace dwarf {
 namespace {
@@ -152,186 +153,286 @@ __global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_kernel(const dwarf_dsqg_
         make_float4(dzo[0], dzo[1], dzo[2], dzo[3]);
 }
 
-// ---- bf16 dkdv: packed rows and v_dot2 ------------------------------------
-// Same mapping as dsqg_bwd_dkdv_kernel (two lanes per key, 32 dims each).
-// <q, k>, <q, e_j> and <dO, v> are v_dot2_f32_bf16 on the packed rows (exact
-// bf16 products, fp32 sums); the rank-1 updates dK += c dS q and dV += P dO
-// stay fp32 FMAs on the widened rows, and the rotated MOVT channels of dV get
-// an fp32 correction term.
-constexpr int kERowDkdv = 72;  // bf16 E row stride (elements)
+// ---- bf16 dK/dV launch: four lanes per key ------------------------------
+// A workgroup of 4 waves owns 64 consecutive keys of one (b, kv head); wave w
+// owns keys 16w..16w+15 and lane g of a key holds head dims [16g, 16g+16) of
+// its K and V rows and of the dK/dV accumulators.  Each wave lists the
+// offsets that give one of its keys a query n = m + delta inside [0, N) and
+// walks that list once per query head of the GQA group, in chunks of CJ with
+// the next chunk's loads in flight: the lane gathers its slices of q_n and
+// dO_n (16-byte buffer loads) plus lse_n, delta_n and y_n[g]; lanes without a
+// query read zeros through an out-of-range offset and get P = 0.  Per pair:
+// <q, k + e_j> and <dO, v> on v_dot2_f32_bf16 (summed over the 4 lanes by
+// DPP), P, dS = P (g - delta), dK += c dS q_n and dV += P R^T dO_n in fp32; the
+// MOVT pair of plane g lies in lane g's slice (plane_shift <= 14), so the
+// lane also forms its dZ term.  Reference kernel: _bwd_dkdv_v18_grouped
+// (dsqg:1734-1955).
+constexpr int kKPW = 16;       // keys per wave
+constexpr int kKPB = 64;       // keys per workgroup
+constexpr int kChunkKv = 2;    // offsets per prefetch chunk
+constexpr int kERowKv = 72;    // bf16 E row stride (elements)
 
-__device__ __forceinline__ float dot2b(uint32_t a, uint32_t b, float c) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+struct KvLayout {
+  int JE, JL4, list_len, group;
+  size_t off_ph, off_list, off_e, bytes;
+};
+
+__host__ __device__ inline KvLayout kv_layout(int J, int J_large, int group, int CJ) {
+  KvLayout L;
+  L.JE = (J + 1 + 15) / 16 * 16;
+  L.JL4 = (J_large + 1) / 2 * 2;
+  L.group = group;
+  L.list_len = (L.JE + 4 * CJ + 1) / 2 * 2;
+  L.off_ph = static_cast<size_t>(group + 1) * L.JE * 4;                  // s_pb2[group][JE], s_off[JE]
+  L.off_list = L.off_ph + static_cast<size_t>(group) * L.JL4 * 4 * 8;    // s_ph[group][JL4][4] float2
+  L.off_e = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;        // s_list[4][list_len] int2
+  L.bytes = L.off_e + static_cast<size_t>(L.JE) * kERowKv * 2;           // sE[JE][72] bf16
+  return L;
 }
 
-template <int SHIFT>
-__global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_bf16_v2(const dwarf_dsqg_bwd_args a,
-                                                                const float* __restrict__ delta_ws, int tiles,
-                                                                int total) {
-  constexpr int HD = kHeadDim, DPL = 32, KPB = kBlock / 2, SEG = HD / kPlanes;
+template <int CJ>
+struct KvChunk {
+  uint4 q[CJ][2], d[CJ][2];
+  float lse[CJ], dl[CJ], y[CJ];
+  bool ok[CJ];
+  int j[CJ];
+};
+
+template <int SHIFT, int CJ>
+__global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
+                                                                   const float* __restrict__ delta_ws, int tiles,
+                                                                   int total) {
+  constexpr float kC = 0.125f * kLog2e;
   constexpr float kScale = 0.125f;
+  static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
   const dwarf_dsqg_fwd_args& f = a.fwd;
+  const int J = f.J, N = f.N, J_small = f.J_small, JL = f.J_large;
+  const int group = f.H / f.H_kv;
+  const KvLayout lay = kv_layout(J, JL, group, CJ);
   extern __shared__ float smem[];
-  int* s_off = reinterpret_cast<int*>(smem);
-  uint16_t* sE = reinterpret_cast<uint16_t*>(smem + ((f.J + 3) & ~3));   // [J][kERowDkdv]
+  char* sm = reinterpret_cast<char*>(smem);
+  float* s_pb2 = smem;                                   // [group][JE] log2(e) * pb
+  int* s_off = reinterpret_cast<int*>(smem + group * lay.JE);
+  float2* s_ph = reinterpret_cast<float2*>(sm + lay.off_ph);
+  int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
+  uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
 
   const int work = xcd_remap(blockIdx.x, total);
   const int bhk = work / tiles;
   const int tile = work - bhk * tiles;
   const int b = bhk / f.H_kv;
   const int hk = bhk - b * f.H_kv;
-  const int group = f.H / f.H_kv;
-  for (int i = threadIdx.x; i < f.J * HD; i += kBlock) {
-    const int j = i / HD, d = i - j * HD;
-    float e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
-    if (f.se_round_bf16) e = round_bf16(e);
-    sE[j * kERowDkdv + d] = f32_to_bf16_bits(e);
+
+  for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
+    const int j = i / kHeadDim, d = i - j * kHeadDim;
+    float e = 0.f;
+    if (j < J) {
+      e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
+      if (f.se_round_bf16) e = round_bf16(e);
+    }
+    sE[j * kERowKv + d] = f32_to_bf16_bits(e);
   }
-  for (int j = threadIdx.x; j < f.J; j += kBlock) s_off[j] = f.offsets[j];
+  for (int t = threadIdx.x; t < group * lay.JE; t += kBlock) {
+    const int hh = t / lay.JE, j = t - hh * lay.JE;
+    const int h = hk * group + hh;
+    s_pb2[t] = j < J ? kLog2e * f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]] : 0.f;
+  }
+  for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
+  for (int t = threadIdx.x; t < group * JL * kPlanes; t += kBlock) {
+    const int hh = t / (JL * kPlanes), rest = t - hh * JL * kPlanes;
+    const int i = rest / kPlanes, r = rest - i * kPlanes;
+    const int h = hk * group + hh;
+    s_ph[hh * lay.JL4 * kPlanes + rest] =
+        make_float2(f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r],
+                    f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r]);
+  }
   __syncthreads();
 
   const int lane = threadIdx.x;
-  const int g = lane & 1;
-  const int m = tile * KPB + lane / 2;
-  if (m >= f.N) return;  // no barriers below
-  const int wave_m_first = uniform(tile * KPB + (lane / kWave) * (kWave / 2));
-  const int wave_m_last = wave_m_first + kWave / 2 - 1;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int ki = l >> 2;
+  const int m0w = tile * kKPB + w * kKPW;
+  if (m0w >= N) return;                       // whole wave past the end (no block barriers below)
+  const int m = m0w + ki;
+  const int m_hi = min(m0w + kKPW - 1, N - 1);
+  const bool key_ok = m < N;
   const int64_t mm = m;
+  int2* s_list = s_list_all + w * lay.list_len;
+  // offsets giving some key m0w..m_hi a query m + delta in [0, N); the
+  // sentinel offset N + 16 - m0w puts every key's query past the end.
+  const int cnt = build_offset_list<CJ>(s_list, s_off, J, m0w, m_hi, N, -1, make_int2(J, N + 16 - m0w));
+  const int cntp = (cnt + CJ - 1) / CJ * CJ;
 
-  uint32_t k32[16], v32[16];
-  {
+  uint32_t k32[8], v32[8];
+  float zg = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { k32[i] = 0u; v32[i] = 0u; }
+  if (key_ok) {
     const uint4* k4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] +
-                                                     hk * f.k_stride[1] + mm * f.k_stride[2] + g * DPL);
+                                                     hk * f.k_stride[1] + mm * f.k_stride[2] + 16 * g);
     const uint4* v4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] +
-                                                     hk * f.v_stride[1] + mm * f.v_stride[2] + g * DPL);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 x = k4[i], y = v4[i];
-      k32[4 * i] = x.x; k32[4 * i + 1] = x.y; k32[4 * i + 2] = x.z; k32[4 * i + 3] = x.w;
-      v32[4 * i] = y.x; v32[4 * i + 1] = y.y; v32[4 * i + 2] = y.z; v32[4 * i + 3] = y.w;
-    }
+                                                     hk * f.v_stride[1] + mm * f.v_stride[2] + 16 * g);
+    const uint4 x0 = k4[0], x1 = k4[1], y0 = v4[0], y1 = v4[1];
+    k32[0] = x0.x; k32[1] = x0.y; k32[2] = x0.z; k32[3] = x0.w;
+    k32[4] = x1.x; k32[5] = x1.y; k32[6] = x1.z; k32[7] = x1.w;
+    v32[0] = y0.x; v32[1] = y0.y; v32[2] = y0.z; v32[3] = y0.w;
+    v32[4] = y1.x; v32[5] = y1.y; v32[6] = y1.z; v32[7] = y1.w;
+    zg = f.z_pre[b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2] + g];
   }
-  float dk[DPL], dv[DPL];
+  // own V pair of plane g (dims 16g + SHIFT, +1)
+  const float va = (SHIFT & 1) ? bf16_hi(v32[SHIFT >> 1]) : bf16_lo(v32[SHIFT >> 1]);
+  const float vb = ((SHIFT + 1) & 1) ? bf16_hi(v32[(SHIFT + 1) >> 1]) : bf16_lo(v32[(SHIFT + 1) >> 1]);
+
+  float dk[16], dv[16];
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) { dk[d] = 0.f; dv[d] = 0.f; }
-  const float4 z4 = *reinterpret_cast<const float4*>(f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2]);
-  const float zs[4] = {z4.x, z4.y, z4.z, z4.w};
-  float dz[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 16; ++i) { dk[i] = 0.f; dv[i] = 0.f; }
+  float dz = 0.f;
+
+  // a key past the end uses m_eff = m0w - 2N - 64: m_eff + delta < 0 for every listed delta
+  const int m_eff = key_ok ? m : m0w - 2 * N - 64;
+  const int qs_b = static_cast<int>(f.q_stride[2]) * 2, ds_b = static_cast<int>(a.dout_stride[2]) * 2;
+  const int ls_b = static_cast<int>(f.lse_stride[2]) * 4, ys_b = static_cast<int>(f.y_stride[2]) * 4;
+  const int qstart = f.query_start;
 
   for (int hh = 0; hh < group; ++hh) {
     const int h = hk * group + hh;
     const int bh = b * f.H + h;
-    const bf16* qbase = reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1] + g * DPL;
-    const bf16* dobase = reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1] + g * DPL;
-    const float* lsebase = f.lse + b * f.lse_stride[0] + h * f.lse_stride[1];
-    const float* dltbase = delta_ws + static_cast<int64_t>(bh) * f.N;
-    const float* ybase = f.y_pre + b * f.y_stride[0] + h * f.y_stride[1];
-    for (int j = 0; j < f.J; ++j) {
-      const int delta = s_off[j];
-      if (wave_m_first + delta >= f.N || wave_m_last + delta < f.query_start) continue;
-      const int n = m + delta;
-      if (n < 0 || n >= f.N) continue;
-      const int64_t nn = n;
-      const float lse = lsebase[nn * f.lse_stride[2]];
-      if (!(lse > -INFINITY)) continue;
-      uint32_t q32[16], o32[16];
-      const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * f.q_stride[2]);
-      const uint4* o4 = reinterpret_cast<const uint4*>(dobase + nn * a.dout_stride[2]);
-      const uint4* e4 = reinterpret_cast<const uint4*>(sE + j * kERowDkdv + g * DPL);
-      float dot = 0.f, gd = 0.f;
+    const __amdgpu_buffer_rsrc_t rq =
+        rows_rsrc(reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1], qs_b, N, 128);
+    const __amdgpu_buffer_rsrc_t rd = rows_rsrc(
+        reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1], ds_b, N, 128);
+    const __amdgpu_buffer_rsrc_t rl = rows_rsrc(f.lse + b * f.lse_stride[0] + h * f.lse_stride[1], ls_b, N, 4);
+    const __amdgpu_buffer_rsrc_t rdl = rows_rsrc(delta_ws + static_cast<int64_t>(bh) * N, 4, N, 4);
+    const __amdgpu_buffer_rsrc_t ry = rows_rsrc(f.y_pre + b * f.y_stride[0] + h * f.y_stride[1], ys_b, N, 16);
+    const float* pb2 = s_pb2 + hh * lay.JE;
+    const float2* ph_h = s_ph + hh * lay.JL4 * kPlanes;
+
+    auto fetch = [&](int k0, KvChunk<CJ>& c) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint4 x = q4[i], e = e4[i], y = o4[i];
-        q32[4 * i] = x.x; q32[4 * i + 1] = x.y; q32[4 * i + 2] = x.z; q32[4 * i + 3] = x.w;
-        o32[4 * i] = y.x; o32[4 * i + 1] = y.y; o32[4 * i + 2] = y.z; o32[4 * i + 3] = y.w;
-        dot = dot2b(x.x, k32[4 * i], dot); dot = dot2b(x.y, k32[4 * i + 1], dot);
-        dot = dot2b(x.z, k32[4 * i + 2], dot); dot = dot2b(x.w, k32[4 * i + 3], dot);
-        dot = dot2b(x.x, e.x, dot); dot = dot2b(x.y, e.y, dot);
-        dot = dot2b(x.z, e.z, dot); dot = dot2b(x.w, e.w, dot);
-        gd = dot2b(y.x, v32[4 * i], gd); gd = dot2b(y.y, v32[4 * i + 1], gd);
-        gd = dot2b(y.z, v32[4 * i + 2], gd); gd = dot2b(y.w, v32[4 * i + 3], gd);
+      for (int jj = 0; jj < CJ; ++jj) {
+        const int2 e = s_list[k0 + jj];
+        const int j = uniform(e.x), d = uniform(e.y);
+        const int n = m_eff + d;
+        c.j[jj] = j;
+        c.ok[jj] = n >= qstart && n < N;
+        const uint32_t qo = static_cast<uint32_t>(n * qs_b + 32 * g);
+        const uint32_t dof = static_cast<uint32_t>(n * ds_b + 32 * g);
+        c.q[jj][0] = buf_load16(rq, qo);
+        c.q[jj][1] = buf_load16(rq, qo + 16);
+        c.d[jj][0] = buf_load16(rd, dof);
+        c.d[jj][1] = buf_load16(rd, dof + 16);
+        c.lse[jj] = buf_load_f32(rl, static_cast<uint32_t>(n * ls_b));
+        c.dl[jj] = buf_load_f32(rdl, static_cast<uint32_t>(n * 4));
+        c.y[jj] = buf_load_f32(ry, (j >= J_small && j < J) ? static_cast<uint32_t>(n * ys_b + 4 * g) : kOutOfRange);
       }
-      dot = group_sum<2>(dot);
-      const float P = __expf(fmaf(dot, kScale, f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]]) - lse);
-      float corr_a[4] = {0.f, 0.f, 0.f, 0.f}, corr_b[4] = {0.f, 0.f, 0.f, 0.f};
-      const bool far = j >= f.J_small;
-      if (far) {
-        const int i = j - f.J_small;
-        const float4 y4 = *reinterpret_cast<const float4*>(ybase + nn * f.y_stride[2]);
-        const float ys[4] = {y4.x, y4.y, y4.z, y4.w};
+    };
+
+    auto consume = [&](const KvChunk<CJ>& c) {
 #pragma unroll
-        for (int r = 0; r < kPlanes; ++r) {
-          const int ch = r * SEG + SHIFT;
-          if (ch / DPL != g) continue;
-          const int la = ch % DPL, lb = la + 1;
-          const float va = (la & 1) ? bf16_hi(v32[la >> 1]) : bf16_lo(v32[la >> 1]);
-          const float vb = (lb & 1) ? bf16_hi(v32[lb >> 1]) : bf16_lo(v32[lb >> 1]);
-          const float da = (la & 1) ? bf16_hi(o32[la >> 1]) : bf16_lo(o32[la >> 1]);
-          const float db = (lb & 1) ? bf16_hi(o32[lb >> 1]) : bf16_lo(o32[lb >> 1]);
-          const float pg = f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r];
-          const float theta = f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r] + pg * ys[r] * zs[r];
-          float sn, cs;
-          dsincos<true>(theta, &sn, &cs);
+      for (int jj = 0; jj < CJ; ++jj) {
+        const int j = c.j[jj];
+        const bool far = j >= J_small && j < J;
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(&c.q[jj][0]);
+        const uint32_t* dw = reinterpret_cast<const uint32_t*>(&c.d[jj][0]);
+        const uint4* e4 = reinterpret_cast<const uint4*>(sE + j * kERowKv + 16 * g);
+        const uint4 e0 = e4[0], e1 = e4[1];
+        const uint32_t ew[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+        float dot = 0.f, gd = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dot = dot2bf(qw[i], k32[i], dot);
+          dot = dot2bf(qw[i], ew[i], dot);
+          gd = dot2bf(dw[i], v32[i], gd);
+        }
+        const float da = (SHIFT & 1) ? bf16_hi(dw[SHIFT >> 1]) : bf16_lo(dw[SHIFT >> 1]);
+        const float db = ((SHIFT + 1) & 1) ? bf16_hi(dw[(SHIFT + 1) >> 1]) : bf16_lo(dw[(SHIFT + 1) >> 1]);
+        float sn = 0.f, cs = 1.f, pg = 0.f;
+        if (far) {
+          const float2 ph = ph_h[(j - J_small) * kPlanes + g];
+          pg = ph.y;
+          dsincos<true>(fmaf(ph.y * c.y[jj], zg, ph.x), &sn, &cs);
           gd += da * (cs * va - sn * vb - va) + db * (sn * va + cs * vb - vb);
-          const float t = P * (da * (-va * sn - vb * cs) + db * (va * cs - vb * sn));
-          dz[r] = fmaf(t * pg, ys[r], dz[r]);
-          corr_a[r] = (cs - 1.f) * da + sn * db;   // (R^T dO - dO)_a
-          corr_b[r] = -sn * da + (cs - 1.f) * db;  // (R^T dO - dO)_b
+        }
+        dot = group_sum<4>(dot);
+        gd = group_sum<4>(gd);
+        const bool live = c.ok[jj] && c.lse[jj] > -INFINITY;
+        const float P = live ? __builtin_amdgcn_exp2f(fmaf(dot, kC, pb2[j]) - c.lse[jj] * kLog2e) : 0.f;
+        const float dS = P * (gd - c.dl[jj]);
+        const float cds = kScale * dS;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dk[2 * i] = fmaf(cds, bf16_lo(qw[i]), dk[2 * i]);
+          dk[2 * i + 1] = fmaf(cds, bf16_hi(qw[i]), dk[2 * i + 1]);
+          dv[2 * i] = fmaf(P, bf16_lo(dw[i]), dv[2 * i]);
+          dv[2 * i + 1] = fmaf(P, bf16_hi(dw[i]), dv[2 * i + 1]);
+        }
+        if (far) {
+          // dV gets R^T dO on the rotated pair; dZ gets d(theta) * gain * y
+          dv[SHIFT] = fmaf(P, (cs - 1.f) * da + sn * db, dv[SHIFT]);
+          dv[SHIFT + 1] = fmaf(P, (cs - 1.f) * db - sn * da, dv[SHIFT + 1]);
+          const float tq = P * (da * (-va * sn - vb * cs) + db * (va * cs - vb * sn));
+          dz = fmaf(tq * pg, c.y[jj], dz);
         }
       }
-      gd = group_sum<2>(gd);
-      const float dS = P * (gd - dltbase[nn]);
-      const float cdS = kScale * dS;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        dk[2 * i] = fmaf(cdS, bf16_lo(q32[i]), dk[2 * i]);
-        dk[2 * i + 1] = fmaf(cdS, bf16_hi(q32[i]), dk[2 * i + 1]);
-        dv[2 * i] = fmaf(P, bf16_lo(o32[i]), dv[2 * i]);
-        dv[2 * i + 1] = fmaf(P, bf16_hi(o32[i]), dv[2 * i + 1]);
-      }
-      if (far) {
-#pragma unroll
-        for (int r = 0; r < kPlanes; ++r) {
-          const int ch = r * SEG + SHIFT;
-          if (ch / DPL != g) continue;
-          const int la = ch % DPL;
-          dv[la] = fmaf(P, corr_a[r], dv[la]);
-          dv[la + 1] = fmaf(P, corr_b[r], dv[la + 1]);
-        }
+    };
+
+    if (cnt > 0) {
+      KvChunk<CJ> c0, c1;
+      fetch(0, c0);
+      for (int k0 = 0; k0 < cntp; k0 += 2 * CJ) {
+        fetch(k0 + CJ, c1);
+        consume(c0);
+        fetch(k0 + 2 * CJ, c0);
+        consume(c1);
       }
     }
   }
-  store_from_f32<bf16, DPL>(reinterpret_cast<bf16*>(a.dk) + b * a.dk_stride[0] + hk * a.dk_stride[1] + mm * a.dk_stride[2] + g * DPL, dk);
-  store_from_f32<bf16, DPL>(reinterpret_cast<bf16*>(a.dv) + b * a.dv_stride[0] + hk * a.dv_stride[1] + mm * a.dv_stride[2] + g * DPL, dv);
-  float dzo[4];
-#pragma unroll
-  for (int r = 0; r < kPlanes; ++r) dzo[r] = group_sum<2>(dz[r]);
-  if (g == 0)
-    *reinterpret_cast<float4*>(a.dz_pre + (static_cast<int64_t>(bhk) * f.N + m) * kPlanes) =
-        make_float4(dzo[0], dzo[1], dzo[2], dzo[3]);
+
+  if (!key_ok) return;
+  uint4* k4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dk) + b * a.dk_stride[0] + hk * a.dk_stride[1] +
+                                       mm * a.dk_stride[2] + 16 * g);
+  uint4* v4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dv) + b * a.dv_stride[0] + hk * a.dv_stride[1] +
+                                       mm * a.dv_stride[2] + 16 * g);
+  uint4 x;
+  x.x = pack_bf16x2(dk[0], dk[1]);   x.y = pack_bf16x2(dk[2], dk[3]);
+  x.z = pack_bf16x2(dk[4], dk[5]);   x.w = pack_bf16x2(dk[6], dk[7]);
+  k4[0] = x;
+  x.x = pack_bf16x2(dk[8], dk[9]);   x.y = pack_bf16x2(dk[10], dk[11]);
+  x.z = pack_bf16x2(dk[12], dk[13]); x.w = pack_bf16x2(dk[14], dk[15]);
+  k4[1] = x;
+  x.x = pack_bf16x2(dv[0], dv[1]);   x.y = pack_bf16x2(dv[2], dv[3]);
+  x.z = pack_bf16x2(dv[4], dv[5]);   x.w = pack_bf16x2(dv[6], dv[7]);
+  v4[0] = x;
+  x.x = pack_bf16x2(dv[8], dv[9]);   x.y = pack_bf16x2(dv[10], dv[11]);
+  x.z = pack_bf16x2(dv[12], dv[13]); x.w = pack_bf16x2(dv[14], dv[15]);
+  v4[1] = x;
+  a.dz_pre[(static_cast<int64_t>(bhk) * N + m) * kPlanes + g] = dz;
 }
 
-hipError_t launch_dkdv_bf16_v2(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
-  constexpr int KPB = kBlock / 2;
   const float* delta = reinterpret_cast<const float*>(static_cast<char*>(a.workspace) + ws.delta_off);
-  const int tiles = (f.N + KPB - 1) / KPB;
+  const int tiles = (f.N + kKPB - 1) / kKPB;
   const int total = tiles * f.B * f.H_kv;
-  const size_t lds = static_cast<size_t>((f.J + 3) & ~3) * sizeof(int) + static_cast<size_t>(f.J) * kERowDkdv * 2;
-#define DWARF_DKDV2_CASE(S) \
-  case S: hipLaunchKernelGGL(dsqg_bwd_dkdv_bf16_v2<S>, dim3(total), dim3(kBlock), lds, stream, a, delta, tiles, total); break;
+  if (total == 0) return hipSuccess;
+  const size_t lds = kv_layout(f.J, f.J_large, f.H / f.H_kv, kChunkKv).bytes;
+#define DWARF_KV4_CASE(S) \
+  case S: hipLaunchKernelGGL((dsqg_bwd_dkdv_bf16_k4<S, kChunkKv>), dim3(total), dim3(kBlock), lds, stream, a, delta, tiles, total); break;
   switch (f.plane_shift) {
-    DWARF_DKDV2_CASE(0) DWARF_DKDV2_CASE(1) DWARF_DKDV2_CASE(2) DWARF_DKDV2_CASE(3) DWARF_DKDV2_CASE(4)
-    DWARF_DKDV2_CASE(5) DWARF_DKDV2_CASE(6) DWARF_DKDV2_CASE(7) DWARF_DKDV2_CASE(8) DWARF_DKDV2_CASE(9)
-    DWARF_DKDV2_CASE(10) DWARF_DKDV2_CASE(11) DWARF_DKDV2_CASE(12) DWARF_DKDV2_CASE(13) DWARF_DKDV2_CASE(14)
+    DWARF_KV4_CASE(0) DWARF_KV4_CASE(1) DWARF_KV4_CASE(2) DWARF_KV4_CASE(3) DWARF_KV4_CASE(4)
+    DWARF_KV4_CASE(5) DWARF_KV4_CASE(6) DWARF_KV4_CASE(7) DWARF_KV4_CASE(8) DWARF_KV4_CASE(9)
+    DWARF_KV4_CASE(10) DWARF_KV4_CASE(11) DWARF_KV4_CASE(12) DWARF_KV4_CASE(13) DWARF_KV4_CASE(14)
     default: return hipErrorInvalidValue;
   }
-#undef DWARF_DKDV2_CASE
+#undef DWARF_KV4_CASE
   return hipGetLastError();
 }
 
-// ---- fixed-order reduction of the dq partials -----------------------------
+// ---------------------------------------------------------------------------
+// Fixed-order reduction of the parameter-gradient partials.
+// ---------------------------------------------------------------------------
 constexpr int kRedRows = 16;  // rows summed per stage-1 group
 
 struct RedArray {
@@ -437,14 +538,14 @@ constexpr int kLanesBwd = 2;
 BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
   BwdWorkspace w{};
-  constexpr int kTile = 128;
+  const int kTile = dq_tile_queries(f.dtype);
   w.dq_tiles = (f.N + kTile - 1) / kTile;
   const int total_tiles = w.dq_tiles * f.B * f.H;
   // Two 4-wave workgroups fit per CU (VGPR/LDS bound): size the tile groups so
   // every workgroup is resident at once (at most 512 on 256 CUs).
   w.dq_tpw = (total_tiles + 511) / 512;
   if (w.dq_tpw < 1) w.dq_tpw = 1;
-  if (w.dq_tpw > 8) w.dq_tpw = 8;
+  if (w.dq_tpw > 16) w.dq_tpw = 16;
   if (w.dq_tpw > w.dq_tiles) w.dq_tpw = w.dq_tiles > 0 ? w.dq_tiles : 1;
   w.dq_ntg = (w.dq_tiles + w.dq_tpw - 1) / w.dq_tpw;
   w.dq_wgs = f.B * f.H * w.dq_ntg;
@@ -489,7 +590,7 @@ hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws,
     if (e != hipSuccess) return e;
   }
   if (do_dkdv) {
-    if (a.fwd.dtype == DWARF_BF16) return launch_dkdv_bf16_v2(a, ws, stream);
+    if (a.fwd.dtype == DWARF_BF16) return launch_dkdv_bf16_k4(a, ws, stream);
     return launch_dkdv_typed<float, kLanesBwd, false>(a, ws, stream);
   }
   return hipSuccess;

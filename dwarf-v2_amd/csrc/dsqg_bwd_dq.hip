@@ -23,6 +23,7 @@
 #include "common.h"
 #include "dsqg_internal.h"
 #include "mfma.h"
+#include "gather.h"
 
 namespace dwarf {
 namespace {
@@ -506,6 +507,409 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_v2(const dwarf_dsqg_bwd
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 dQ launch, four lanes per query (the forward's mapping).
+//
+// A workgroup of 4 waves walks every n_tg-th 64-query tile of one (b, h);
+// wave w owns queries 16w..16w+15 of a tile and lane g of a query holds head
+// dims [16g, 16g+16).  Each wave walks its offset list (offsets that give one
+// of its queries a source row) in chunks of CJ with the next chunk's K/V/z
+// loads in flight; a lane without a source reads zeros (out-of-range buffer
+// offset) and gets P = 0.  Per pair the lanes form <q, k_s> + <q, e_j> and
+// <dO, v_s> with v_dot2_f32_bf16, the MOVT rotation of their one channel pair,
+// P, dS = P (g - delta) and dQ += c dS k_s, and write dS into the tile's
+// s_ds[j][q] matrix.  At the end of the tile, on MFMA (dS split into bf16
+// high and low parts):
+//   dQe^T = E^T dS^T   (added to dQ through an LDS transpose)
+//   dSE   = dS^T Q     (wave w: dims 16w..16w+15), dPB = dS^T 1 (wave 0)
+// accumulated into the workgroup's partial slots.  dPhase sums over the
+// wave's 16 queries are reduced per chunk (DPP + lane shuffles) into a
+// per-wave LDS table written to the partial slot at the end, so every sum has
+// a fixed order.
+// ---------------------------------------------------------------------------
+constexpr int kQT = 64;           // queries per tile
+constexpr int kQPW = 16;          // queries per wave
+constexpr int kChunkDq = 2;       // offsets per prefetch chunk (the launch's choice)
+constexpr int kDsRowT = 68;       // s_ds[j][q] row (floats)
+constexpr int kERowT = 72;        // bf16 E row stride (elements)
+
+struct DqT4Layout {
+  int JE, JK, jt, JL4, list_len;
+  size_t off_ph, off_list, off_dph, off_e, off_et, off_ds, bytes;
+};
+
+// JE >= J + 1 keeps a sentinel row J; the MFMA reduction over j runs to JK
+// (a multiple of 32) and reads zeros for rows JE..JK-1 instead of storing them.
+__host__ __device__ inline DqT4Layout dq_t4_layout(int J, int J_large, int CJ) {
+  DqT4Layout L;
+  L.JE = (J + 1 + 15) / 16 * 16;
+  L.JK = (L.JE + 31) / 32 * 32;
+  L.jt = L.JE + 8;
+  L.JL4 = (J_large + 1) / 2 * 2;
+  L.list_len = (L.JE + 4 * CJ + 1) / 2 * 2;
+  L.off_ph = static_cast<size_t>(2 * L.JE) * 4;                       // s_pb2[JE], s_off[JE]
+  L.off_list = L.off_ph + static_cast<size_t>(L.JL4) * 4 * 8;         // s_ph[JL4][4] float2
+  L.off_dph = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;   // s_list[4][list_len] int2
+  L.off_e = L.off_dph + static_cast<size_t>(4 * L.JL4) * 8 * 4;       // s_dph[4][JL4][8]
+  L.off_et = L.off_e + static_cast<size_t>(L.JE) * kERowT * 2;        // sE[JE][72] bf16
+  L.off_ds = L.off_et + static_cast<size_t>(kHeadDim) * L.jt * 2;     // sEt[64][jt] bf16
+  const int ds_rows = L.JE > kQT ? L.JE : kQT;                       // the dQe staging needs 4 x 16 rows
+  L.bytes = L.off_ds + static_cast<size_t>(ds_rows) * kDsRowT * 4;    // s_ds[JE][68] (also dQe staging)
+  return L;
+}
+
+template <int SHIFT, int CJ>
+struct DqChunk {
+  uint4 k[CJ][2], v[CJ][2];
+  float z[CJ];
+  bool ok[CJ];
+  int j[CJ];
+};
+
+template <int SHIFT, int CJ>
+__global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsqg_bwd_args a, float* __restrict__ delta_ws,
+                                                                 float* __restrict__ part_se, float* __restrict__ part_pb,
+                                                                 float* __restrict__ part_ph, int tiles, int tpw, int n_tg,
+                                                                 int total) {
+  constexpr float kC = 0.125f * kLog2e;
+  constexpr float kScale = 0.125f;
+  static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  const int J = f.J, N = f.N, J_small = f.J_small, JL = f.J_large;
+  const DqT4Layout lay = dq_t4_layout(J, JL, CJ);
+  extern __shared__ float smem[];
+  char* sm = reinterpret_cast<char*>(smem);
+  float* s_pb2 = smem;                                        // log2(e) * pb_j
+  int* s_off = reinterpret_cast<int*>(smem + lay.JE);
+  float2* s_ph = reinterpret_cast<float2*>(sm + lay.off_ph);
+  int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
+  float* s_dph_all = reinterpret_cast<float*>(sm + lay.off_dph);
+  uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
+  uint16_t* sEt = reinterpret_cast<uint16_t*>(sm + lay.off_et);
+  float* s_ds = reinterpret_cast<float*>(sm + lay.off_ds);
+
+  const int work = xcd_remap(blockIdx.x, total);
+  const int bh = work / n_tg;
+  const int tg = work - bh * n_tg;
+  const int b = bh / f.H;
+  const int h = bh - b * f.H;
+  const int hk = h / (f.H / f.H_kv);
+  const int slot = (h * f.B + b) * n_tg + tg;   // head-major partial slot
+
+  for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
+    const int j = i / kHeadDim, d = i - j * kHeadDim;
+    float e = 0.f;
+    if (j < J) {
+      e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
+      if (f.se_round_bf16) e = round_bf16(e);
+    }
+    const uint16_t bits = f32_to_bf16_bits(e);
+    sE[j * kERowT + d] = bits;
+    sEt[d * lay.jt + j] = bits;
+  }
+  for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
+    s_pb2[j] = j < J ? kLog2e * f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]] : 0.f;
+    s_off[j] = j < J ? f.offsets[j] : 0;
+  }
+  for (int t = threadIdx.x; t < JL * kPlanes; t += kBlock) {
+    const int i = t / kPlanes, r = t - i * kPlanes;
+    s_ph[t] = make_float2(f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r],
+                          f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r]);
+  }
+  for (int t = threadIdx.x; t < 4 * lay.JL4 * 8; t += kBlock) s_dph_all[t] = 0.f;
+
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int qi = l >> 2;
+  const int lr = l & 15, lc = l >> 4;
+  int2* s_list = s_list_all + w * lay.list_len;
+  float* s_dph = s_dph_all + w * lay.JL4 * 8;
+
+  const bf16* qb = reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1];
+  const bf16* dob = reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1];
+  const bf16* ob = reinterpret_cast<const bf16*>(f.out) + b * f.out_stride[0] + h * f.out_stride[1];
+  const int ks_b = static_cast<int>(f.k_stride[2]) * 2, vs_b = static_cast<int>(f.v_stride[2]) * 2;
+  const int zs_b = static_cast<int>(f.z_stride[2]) * 4, qs_b = static_cast<int>(f.q_stride[2]) * 2;
+  const __amdgpu_buffer_rsrc_t rk =
+      rows_rsrc(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1], ks_b, N, 128);
+  const __amdgpu_buffer_rsrc_t rv =
+      rows_rsrc(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1], vs_b, N, 128);
+  const __amdgpu_buffer_rsrc_t rz = rows_rsrc(f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1], zs_b, N, 16);
+  const __amdgpu_buffer_rsrc_t rq = rows_rsrc(qb, qs_b, N, 128);
+
+  // Tiles tg, tg + n_tg, tg + 2 n_tg, ...: every workgroup gets early (few
+  // valid offsets) and late tiles of the sequence alike.
+  for (int t = tg; t < tiles; t += n_tg) {
+    const bool first = t == tg;
+    const int n0 = t * kQT;
+    const int n0w = n0 + kQPW * w;
+    const int n = n0w + qi;
+    const int n_hi = min(n0w + kQPW - 1, N - 1);
+    const bool row_ok = n < N;
+    const bool live = row_ok && n >= f.query_start;
+    const int64_t nn = n;
+
+    // ---- this lane's slices of q and dO, delta = <dO, O> (bf16 O), lse, y ----
+    uint32_t q32[8], d32[8];
+    float dlt = 0.f, lse2 = 0.f, yg = 0.f;
+    bool mass = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { q32[i] = 0u; d32[i] = 0u; }
+    if (live) {
+      const uint4* q4 = reinterpret_cast<const uint4*>(qb + nn * f.q_stride[2] + 16 * g);
+      const uint4* d4 = reinterpret_cast<const uint4*>(dob + nn * a.dout_stride[2] + 16 * g);
+      const uint4* o4 = reinterpret_cast<const uint4*>(ob + nn * f.out_stride[2] + 16 * g);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint4 x = q4[i], y = d4[i], o = o4[i];
+        q32[4 * i] = x.x; q32[4 * i + 1] = x.y; q32[4 * i + 2] = x.z; q32[4 * i + 3] = x.w;
+        d32[4 * i] = y.x; d32[4 * i + 1] = y.y; d32[4 * i + 2] = y.z; d32[4 * i + 3] = y.w;
+        dlt = dot2bf(y.x, o.x, dlt); dlt = dot2bf(y.y, o.y, dlt);
+        dlt = dot2bf(y.z, o.z, dlt); dlt = dot2bf(y.w, o.w, dlt);
+      }
+      const float lse = f.lse[b * f.lse_stride[0] + h * f.lse_stride[1] + nn * f.lse_stride[2]];
+      mass = lse > -INFINITY;
+      lse2 = mass ? lse * kLog2e : 0.f;
+      yg = f.y_pre[b * f.y_stride[0] + h * f.y_stride[1] + nn * f.y_stride[2] + g];
+    }
+    dlt = group_sum<4>(dlt);
+    if (row_ok && g == 0) delta_ws[static_cast<int64_t>(bh) * N + n] = dlt;
+    const int n_eff = mass ? n : n0w - 2 * N;   // no source for queries without softmax mass
+    const int kb_lane = n_eff * ks_b + 32 * g;
+    const int vb_lane = n_eff * vs_b + 32 * g;
+    const int zb_lane = n_eff * zs_b + 4 * g;
+
+    __syncthreads();   // the previous tile's dQe staging reads are done
+    for (int i = lane; i < lay.JE * kQT; i += kBlock) s_ds[(i / kQT) * kDsRowT + (i % kQT)] = 0.f;
+    int cnt = 0;
+    if (n0w < N) cnt = build_offset_list<CJ>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
+    const int cntp = (cnt + CJ - 1) / CJ * CJ;
+    __syncthreads();   // s_ds cleared
+
+    float dq[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dq[i] = 0.f;
+    float dy = 0.f;
+
+    auto fetch = [&](int k0, DqChunk<SHIFT, CJ>& c) {
+#pragma unroll
+      for (int jj = 0; jj < CJ; ++jj) {
+        const int2 e = s_list[k0 + jj];
+        const int j = uniform(e.x), d = uniform(e.y);
+        c.j[jj] = j;
+        c.ok[jj] = static_cast<uint32_t>(n_eff - d) < static_cast<uint32_t>(N);
+        const uint32_t ko = static_cast<uint32_t>(kb_lane - d * ks_b);
+        const uint32_t vo = static_cast<uint32_t>(vb_lane - d * vs_b);
+        const uint32_t zo = (j >= J_small && j < J) ? static_cast<uint32_t>(zb_lane - d * zs_b) : kOutOfRange;
+        c.k[jj][0] = buf_load16(rk, ko);
+        c.k[jj][1] = buf_load16(rk, ko + 16);
+        c.v[jj][0] = buf_load16(rv, vo);
+        c.v[jj][1] = buf_load16(rv, vo + 16);
+        c.z[jj] = buf_load_f32(rz, zo);
+      }
+    };
+
+    auto consume = [&](const DqChunk<SHIFT, CJ>& c) {
+      float ph_sum[CJ][2];
+#pragma unroll
+      for (int jj = 0; jj < CJ; ++jj) {
+        const int j = c.j[jj];
+        const bool far = j >= J_small && j < J;
+        const uint32_t* kw = reinterpret_cast<const uint32_t*>(&c.k[jj][0]);
+        const uint32_t* vw = reinterpret_cast<const uint32_t*>(&c.v[jj][0]);
+        const uint4* e4 = reinterpret_cast<const uint4*>(sE + j * kERowT + 16 * g);
+        const uint4 e0 = e4[0], e1 = e4[1];
+        const uint32_t ew[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+        float dot = 0.f, gd = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dot = dot2bf(q32[i], kw[i], dot);
+          dot = dot2bf(q32[i], ew[i], dot);
+          gd = dot2bf(d32[i], vw[i], gd);
+        }
+        float tq_pre = 0.f, pg = 0.f;
+        if (far) {
+          const float2 ph = s_ph[(j - J_small) * kPlanes + g];
+          pg = ph.y;
+          float sn, cs;
+          dsincos<true>(fmaf(ph.y * yg, c.z[jj], ph.x), &sn, &cs);
+          const float va = (SHIFT & 1) ? bf16_hi(vw[SHIFT >> 1]) : bf16_lo(vw[SHIFT >> 1]);
+          const float vb = ((SHIFT + 1) & 1) ? bf16_hi(vw[(SHIFT + 1) >> 1]) : bf16_lo(vw[(SHIFT + 1) >> 1]);
+          const float da = (SHIFT & 1) ? bf16_hi(d32[SHIFT >> 1]) : bf16_lo(d32[SHIFT >> 1]);
+          const float db = ((SHIFT + 1) & 1) ? bf16_hi(d32[(SHIFT + 1) >> 1]) : bf16_lo(d32[(SHIFT + 1) >> 1]);
+          gd += da * (cs * va - sn * vb - va) + db * (sn * va + cs * vb - vb);
+          tq_pre = da * (-va * sn - vb * cs) + db * (va * cs - vb * sn);
+        }
+        dot = group_sum<4>(dot);
+        gd = group_sum<4>(gd);
+        const float P = c.ok[jj] ? __builtin_amdgcn_exp2f(fmaf(dot, kC, s_pb2[j]) - lse2) : 0.f;
+        const float dS = P * (gd - dlt);
+        const float cds = kScale * dS;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dq[2 * i] = fmaf(cds, bf16_lo(kw[i]), dq[2 * i]);
+          dq[2 * i + 1] = fmaf(cds, bf16_hi(kw[i]), dq[2 * i + 1]);
+        }
+        if (g == 0) s_ds[j * kDsRowT + kQPW * w + qi] = dS;
+        const float tq = P * tq_pre;
+        dy = fmaf(tq * pg, c.z[jj], dy);
+        ph_sum[jj][0] = tq;
+        ph_sum[jj][1] = tq * yg * c.z[jj];
+      }
+#pragma unroll
+      for (int jj = 0; jj < CJ; ++jj) {
+        const int j = c.j[jj];
+        if (j >= J_small && j < J) {   // wave-uniform
+          const float s0 = sum_over_queries16(ph_sum[jj][0]);
+          const float s1 = sum_over_queries16(ph_sum[jj][1]);
+          if (l < 4) {
+            float* dst = s_dph + (j - J_small) * 8 + 2 * g;
+            dst[0] += s0;
+            dst[1] += s1;
+          }
+        }
+      }
+    };
+
+    if (cnt > 0) {
+      DqChunk<SHIFT, CJ> c0, c1;
+      fetch(0, c0);
+      for (int k0 = 0; k0 < cntp; k0 += 2 * CJ) {
+        fetch(k0 + CJ, c1);
+        consume(c0);
+        fetch(k0 + 2 * CJ, c0);
+        consume(c1);
+      }
+    }
+    __syncthreads();   // the tile's dS matrix is complete
+
+    // ---- dQe^T = E^T dS^T for the wave's 16 queries (C^T[d][q]) ----------------
+    f32x4 dqe[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) dqe[nb] = zero4();
+    for (int ks = 0; ks < lay.JK / 32; ++ks) {
+      const int jb = 32 * ks + 8 * lc;   // rows jb..jb+7 exist iff jb < JE (JE is a multiple of 16)
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = jb < lay.JE ? s_ds[(jb + e) * kDsRowT + kQPW * w + lr] : 0.f;
+      bf16x8 bhi, blo;
+      split_bf16x8(x, bhi, blo);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        uint4 xe = {0u, 0u, 0u, 0u};
+        if (jb < lay.JE) xe = *reinterpret_cast<const uint4*>(sEt + (16 * nb + lr) * lay.jt + jb);
+        const bf16x8 ae = bf16x8_from_bits(xe);
+        dqe[nb] = mfma16_bf16(ae, bhi, dqe[nb]);
+        dqe[nb] = mfma16_bf16(ae, blo, dqe[nb]);
+      }
+    }
+    // ---- dSE[j][16w + lr] += c sum_q dS[q][j] q[q][16w + lr]; dPB (wave 0) -------
+    {
+      bf16x8 bq[2], one;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int nq = n0 + 32 * ks + 8 * lc + e;
+          const uint32_t off = nq < N ? static_cast<uint32_t>(nq * qs_b + 2 * (16 * w + lr)) : kOutOfRange;
+          bq[ks][e] = __builtin_bit_cast(__bf16, buf_load_u16(rq, off));
+        }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) one[e] = static_cast<__bf16>(lr == 0 ? 1.f : 0.f);
+      for (int mb = 0; mb < lay.JE / 16; ++mb) {
+        f32x4 c = zero4(), c1 = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const float4* src = reinterpret_cast<const float4*>(s_ds + (16 * mb + lr) * kDsRowT + 32 * ks + 8 * lc);
+          const float4 x0 = src[0], x1 = src[1];
+          const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          bf16x8 ahi, alo;
+          split_bf16x8(x, ahi, alo);
+          c = mfma16_bf16(ahi, bq[ks], c);
+          c = mfma16_bf16(alo, bq[ks], c);
+          if (w == 0) {
+            c1 = mfma16_bf16(ahi, one, c1);
+            c1 = mfma16_bf16(alo, one, c1);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * mb + 4 * lc + r;
+          if (j < J) {
+            float* dst = part_se + (static_cast<int64_t>(slot) * J + j) * kHeadDim + 16 * w + lr;
+            const float v = kScale * c[r];
+            *dst = first ? v : *dst + v;
+            if (w == 0 && lr == 0) {
+              float* dp = part_pb + static_cast<int64_t>(slot) * J + j;
+              *dp = first ? c1[r] : *dp + c1[r];
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();   // every wave is done reading s_ds; it now stages dQe
+    float* stage = s_ds + w * kQPW * kDsRowT;   // [16 q][68]
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) stage[lr * kDsRowT + 16 * nb + 4 * lc + r] = dqe[nb][r];
+    __builtin_amdgcn_wave_barrier();
+    if (row_ok) {
+      const float4* src = reinterpret_cast<const float4*>(stage + qi * kDsRowT + 16 * g);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 x = src[i];
+        dq[4 * i] = fmaf(kScale, x.x, dq[4 * i]);
+        dq[4 * i + 1] = fmaf(kScale, x.y, dq[4 * i + 1]);
+        dq[4 * i + 2] = fmaf(kScale, x.z, dq[4 * i + 2]);
+        dq[4 * i + 3] = fmaf(kScale, x.w, dq[4 * i + 3]);
+      }
+      uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dq) + b * a.dq_stride[0] + h * a.dq_stride[1] +
+                                           nn * a.dq_stride[2] + 16 * g);
+      uint4 x0, x1;
+      x0.x = pack_bf16x2(dq[0], dq[1]);   x0.y = pack_bf16x2(dq[2], dq[3]);
+      x0.z = pack_bf16x2(dq[4], dq[5]);   x0.w = pack_bf16x2(dq[6], dq[7]);
+      x1.x = pack_bf16x2(dq[8], dq[9]);   x1.y = pack_bf16x2(dq[10], dq[11]);
+      x1.z = pack_bf16x2(dq[12], dq[13]); x1.w = pack_bf16x2(dq[14], dq[15]);
+      o4[0] = x0;
+      o4[1] = x1;
+      a.dy_pre[(static_cast<int64_t>(bh) * N + n) * kPlanes + g] = dy;
+    }
+  }
+  __syncthreads();
+  for (int t = lane; t < 4 * JL * 8; t += kBlock) {
+    const int ww = t / (JL * 8), rest = t - ww * JL * 8;
+    part_ph[(static_cast<int64_t>(slot) * 4 + ww) * JL * 8 + rest] = s_dph_all[ww * lay.JL4 * 8 + rest];
+  }
+}
+
+template <int CJ>
+hipError_t launch_dq_bf16_t4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  char* base = static_cast<char*>(a.workspace);
+  float* delta = reinterpret_cast<float*>(base + ws.delta_off);
+  float* part_se = reinterpret_cast<float*>(base + ws.part_se_off);
+  float* part_pb = reinterpret_cast<float*>(base + ws.part_pb_off);
+  float* part_ph = reinterpret_cast<float*>(base + ws.part_ph_off);
+  if (ws.dq_wgs == 0) return hipSuccess;
+  const size_t lds = dq_t4_layout(f.J, f.J_large, CJ).bytes;
+#define DWARF_DQT4_CASE(S)                                                                                       \
+  case S:                                                                                                       \
+    hipLaunchKernelGGL((dsqg_bwd_dq_bf16_t4<S, CJ>), dim3(ws.dq_wgs), dim3(kBlock), lds, stream, a, delta,        \
+                       part_se, part_pb, part_ph, ws.dq_tiles, ws.dq_tpw, ws.dq_ntg, ws.dq_wgs);                  \
+    break;
+  switch (f.plane_shift) {
+    DWARF_DQT4_CASE(0) DWARF_DQT4_CASE(1) DWARF_DQT4_CASE(2) DWARF_DQT4_CASE(3) DWARF_DQT4_CASE(4)
+    DWARF_DQT4_CASE(5) DWARF_DQT4_CASE(6) DWARF_DQT4_CASE(7) DWARF_DQT4_CASE(8) DWARF_DQT4_CASE(9)
+    DWARF_DQT4_CASE(10) DWARF_DQT4_CASE(11) DWARF_DQT4_CASE(12) DWARF_DQT4_CASE(13) DWARF_DQT4_CASE(14)
+    default: return hipErrorInvalidValue;
+  }
+#undef DWARF_DQT4_CASE
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_dq_typed(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
@@ -533,12 +937,14 @@ hipError_t launch_dq_typed(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws,
 
 }  // namespace
 
-size_t dq_lds_bytes(int J, int dtype) {
-  return dtype == DWARF_BF16 ? dq_lds<bf16>(J).bytes : dq_lds<float>(J).bytes;
+size_t dq_lds_bytes(int J, int J_large, int dtype) {
+  return dtype == DWARF_BF16 ? dq_t4_layout(J, J_large, kChunkDq).bytes : dq_lds<float>(J).bytes;
 }
 
+int dq_tile_queries(int dtype) { return dtype == DWARF_BF16 ? kQT : kQ; }
+
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
-  if (a.fwd.dtype == DWARF_BF16) return launch_dq_typed<bf16>(a, ws, stream);
+  if (a.fwd.dtype == DWARF_BF16) return launch_dq_bf16_t4<kChunkDq>(a, ws, stream);
   return launch_dq_typed<float>(a, ws, stream);
 }
 

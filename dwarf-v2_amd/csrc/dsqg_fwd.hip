@@ -16,6 +16,7 @@
 #include "common.h"
 #include "dsqg_internal.h"
 #include "mfma.h"
+#include "gather.h"
 
 namespace dwarf {
 namespace {
@@ -165,25 +166,6 @@ constexpr int kQPW = kWave / kLanesQ;       // 16 queries per wave
 constexpr int kQPB = kBlock / kLanesQ;      // 64 queries per workgroup
 constexpr int kChunkFwd = 2;                // offsets per prefetch chunk (the launch's choice)
 constexpr int kERowFwd = 72;                // bf16 E row stride (elements)
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every tensor (spans are < 2^31)
-
-__device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
-}
-
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-  return uint4{v[0], v[1], v[2], v[3]};
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t row_bytes, int rows, int tail) {
-  const int64_t span = rows > 0 ? (rows - 1) * row_bytes + tail : 0;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(span), 0x00020000);
-}
-
 // LDS: s_pb[JE] f32, s_off[JE] i32, s_ph[JL4][4] float2, s_list[4][list_len] int2,
 // then one region that first holds the bf16 E rows (sE[JE][72]) and, after a
 // barrier, the four waves' s_qe[16][qe_row] tables.
@@ -313,21 +295,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
   if (n0w >= N) return;                       // whole wave past the end (no block barriers below)
   // The wave's offset list: offsets giving some query n0w..n_hi a source row in [0, N).
   // The sentinel (index J) gets the offset n0w - N, out of range for every query.
-  int cnt = 0;
-  for (int base = 0; base < J; base += kWave) {
-    const int j = base + l;
-    const int d = j < J ? s_off[j] : 0;
-    const bool need = j < J && d <= n_hi && d >= n0w - (N - 1);
-    const uint64_t mask = __ballot(need);
-    const int pos = cnt + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-    if (need) s_list[pos] = make_int2(j, d);
-    cnt += __popcll(mask);
-  }
-  cnt = uniform(cnt);
+  const int cnt = build_offset_list<CJ>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
   const int cntp = (cnt + CJ - 1) / CJ * CJ;
-  for (int t = cnt + l; t < cntp + 2 * CJ; t += kWave) s_list[t] = make_int2(J, n0w - N);
-  __builtin_amdgcn_wave_barrier();
 
   uint32_t q32[8];
   float yg = 0.f;

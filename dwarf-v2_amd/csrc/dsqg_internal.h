@@ -54,6 +54,7 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a);
 hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
                            bool do_dkdv);
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
-size_t dq_lds_bytes(int J, int dtype);
+size_t dq_lds_bytes(int J, int J_large, int dtype);
+int dq_tile_queries(int dtype);   // queries per tile of the dQ launch
 
 }  // namespace dwarf

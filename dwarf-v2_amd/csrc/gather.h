@@ -1,0 +1,76 @@
+// Shared pieces of the bf16 gather kernels (forward, dQ and dK/dV launches):
+// packed-bf16 dot products, raw buffer loads with 32-bit offsets (an offset
+// past the end of the tensor reads zeros) and the per-wave offset list.
+#pragma once
+
+#include "common.h"
+
+namespace dwarf {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every tensor (spans are < 2^31)
+
+__device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return uint4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+__device__ __forceinline__ uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// Resource over `rows` rows of `row_bytes` stride whose last row is `tail` bytes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int64_t row_bytes, int rows, int tail) {
+  const int64_t span = rows > 0 ? (rows - 1) * row_bytes + tail : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(span), 0x00020000);
+}
+
+// Appends to `list` (wave-private LDS) the (index, offset) pairs of the
+// offsets that give some position in [lo, hi] a partner position inside
+// [0, N): partner = position - dir * offset, dir = +1 for queries looking
+// back at keys, -1 for keys looking forward at queries.  Pads with `pad`
+// up to a multiple of CJ plus two chunks.  Returns the (uniform) count.
+template <int CJ>
+__device__ __forceinline__ int build_offset_list(int2* list, const int* s_off, int J, int lo, int hi, int N, int dir,
+                                                 int2 pad) {
+  const int l = threadIdx.x % kWave;
+  int cnt = 0;
+  for (int base = 0; base < J; base += kWave) {
+    const int j = base + l;
+    const int d = j < J ? s_off[j] : 0;
+    const int sd = dir * d;
+    const bool need = j < J && sd <= hi && sd >= lo - (N - 1);
+    const uint64_t mask = __ballot(need);
+    const int pos = cnt + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+    if (need) list[pos] = make_int2(j, d);
+    cnt += __popcll(mask);
+  }
+  cnt = uniform(cnt);
+  const int cntp = (cnt + CJ - 1) / CJ * CJ;
+  for (int t = cnt + l; t < cntp + 2 * CJ; t += kWave) list[t] = pad;
+  __builtin_amdgcn_wave_barrier();
+  return cnt;
+}
+
+// Sum over the 16 lanes of a wave that share (lane & 3): four queries of a
+// 16-lane row by DPP rotation, then across the four rows.
+__device__ __forceinline__ float sum_over_queries16(float x) {
+  x += dpp_f<0x124>(x);  // row_ror:4
+  x += dpp_f<0x128>(x);  // row_ror:8
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+}  // namespace dwarf
