@@ -169,7 +169,7 @@ __global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_kernel(const dwarf_dsqg_
 // (dsqg:1734-1955).
 constexpr int kKPW = 16;       // keys per wave
 constexpr int kKPB = 64;       // keys per workgroup
-constexpr int kChunkKv = 2;    // offsets per prefetch chunk
+constexpr int kChunkKv = 1;    // offsets per prefetch chunk
 constexpr int kERowKv = 72;    // bf16 E row stride (elements)
 
 struct KvLayout {
@@ -199,7 +199,7 @@ struct KvChunk {
 };
 
 template <int SHIFT, int CJ>
-__global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
+__global__ __launch_bounds__(kBlock, 3) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
                                                                    const float* __restrict__ delta_ws, int tiles,
                                                                    int total) {
   constexpr float kC = 0.125f * kLog2e;

@@ -164,7 +164,7 @@ __global__ __launch_bounds__(kBlock) void dsqg_fwd_kernel(const dwarf_dsqg_fwd_a
 constexpr int kLanesQ = 4;                  // lanes per query
 constexpr int kQPW = kWave / kLanesQ;       // 16 queries per wave
 constexpr int kQPB = kBlock / kLanesQ;      // 64 queries per workgroup
-constexpr int kChunkFwd = 2;                // offsets per prefetch chunk (the launch's choice)
+constexpr int kChunkFwd = 1;                // offsets per prefetch chunk (the launch's choice)
 constexpr int kERowFwd = 72;                // bf16 E row stride (elements)
 // LDS: s_pb[JE] f32, s_off[JE] i32, s_ph[JL4][4] float2, s_list[4][list_len] int2,
 // then one region that first holds the bf16 E rows (sE[JE][72]) and, after a
