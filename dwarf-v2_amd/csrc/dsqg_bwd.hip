@@ -490,14 +490,13 @@ RedPlan make_red_plan(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
   char* base = static_cast<char*>(a.workspace);
   float* red = reinterpret_cast<float*>(base + ws.red_off);
-  const int R = f.B * ws.dq_ntg;
   RedPlan p;
   p.arr[0] = {reinterpret_cast<const float*>(base + ws.part_se_off), red, 1, ws.dq_wgs, f.J * kHeadDim,
               ws.red_groups_se};
   red += static_cast<size_t>(ws.red_groups_se) * f.J * kHeadDim;
-  p.arr[1] = {reinterpret_cast<const float*>(base + ws.part_pb_off), red, f.H, R, f.J, ws.red_groups_pb};
+  p.arr[1] = {reinterpret_cast<const float*>(base + ws.part_pb_off), red, f.H, ws.pb_rows, f.J, ws.red_groups_pb};
   red += static_cast<size_t>(f.H) * ws.red_groups_pb * f.J;
-  p.arr[2] = {reinterpret_cast<const float*>(base + ws.part_ph_off), red, f.H, 4 * R, f.J_large * 8,
+  p.arr[2] = {reinterpret_cast<const float*>(base + ws.part_ph_off), red, f.H, ws.ph_rows, f.J_large * 8,
               ws.red_groups_ph};
   for (int i = 0; i < 3; ++i) {
     const RedArray& A = p.arr[i];
@@ -541,19 +540,30 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   const int kTile = dq_tile_queries(f.dtype);
   w.dq_tiles = (f.N + kTile - 1) / kTile;
   const int total_tiles = w.dq_tiles * f.B * f.H;
-  // Two 4-wave workgroups fit per CU (VGPR/LDS bound): size the tile groups so
-  // every workgroup is resident at once (at most 512 on 256 CUs).
-  w.dq_tpw = (total_tiles + 511) / 512;
-  if (w.dq_tpw < 1) w.dq_tpw = 1;
-  if (w.dq_tpw > 16) w.dq_tpw = 16;
-  if (w.dq_tpw > w.dq_tiles) w.dq_tpw = w.dq_tiles > 0 ? w.dq_tiles : 1;
-  w.dq_ntg = (w.dq_tiles + w.dq_tpw - 1) / w.dq_tpw;
-  w.dq_wgs = f.B * f.H * w.dq_ntg;
   const int JL = f.J_large > 0 ? f.J_large : 1;
-  const int R = f.B * w.dq_ntg;
+  if (f.dtype == DWARF_BF16) {
+    // Persistent workgroups, two per CU, all resident; each accumulates dSE in
+    // its own slot, dPB / dPhase partials are per tile (head-major rows).
+    w.dq_tpw = 0;
+    w.dq_ntg = 0;
+    w.dq_wgs = total_tiles < 512 ? (total_tiles > 0 ? total_tiles : 1) : 512;
+    w.pb_rows = f.B * w.dq_tiles;
+    w.ph_rows = f.B * w.dq_tiles;
+  } else {
+    // Two 4-wave workgroups fit per CU: size the tile groups so every
+    // workgroup is resident at once (at most 512 on 256 CUs).
+    w.dq_tpw = (total_tiles + 511) / 512;
+    if (w.dq_tpw < 1) w.dq_tpw = 1;
+    if (w.dq_tpw > 16) w.dq_tpw = 16;
+    if (w.dq_tpw > w.dq_tiles) w.dq_tpw = w.dq_tiles > 0 ? w.dq_tiles : 1;
+    w.dq_ntg = (w.dq_tiles + w.dq_tpw - 1) / w.dq_tpw;
+    w.dq_wgs = f.B * f.H * w.dq_ntg;
+    w.pb_rows = f.B * w.dq_ntg;
+    w.ph_rows = 4 * f.B * w.dq_ntg;   // one row per wave
+  }
   w.red_groups_se = (w.dq_wgs + kRedRows - 1) / kRedRows;
-  w.red_groups_pb = (R + kRedRows - 1) / kRedRows;
-  w.red_groups_ph = (4 * R + kRedRows - 1) / kRedRows;
+  w.red_groups_pb = (w.pb_rows + kRedRows - 1) / kRedRows;
+  w.red_groups_ph = (w.ph_rows + kRedRows - 1) / kRedRows;
   size_t off = 0;
   w.delta_off = off;
   w.delta_bytes = static_cast<size_t>(f.B) * f.H * f.N * sizeof(float);
@@ -562,10 +572,10 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   w.part_se_bytes = static_cast<size_t>(w.dq_wgs) * f.J * kHeadDim * sizeof(float);
   off += align256(w.part_se_bytes);
   w.part_pb_off = off;
-  w.part_pb_bytes = static_cast<size_t>(w.dq_wgs) * f.J * sizeof(float);
+  w.part_pb_bytes = static_cast<size_t>(f.H) * w.pb_rows * f.J * sizeof(float);
   off += align256(w.part_pb_bytes);
   w.part_ph_off = off;
-  w.part_ph_bytes = static_cast<size_t>(w.dq_wgs) * 4 * JL * 8 * sizeof(float);
+  w.part_ph_bytes = static_cast<size_t>(f.H) * w.ph_rows * JL * 8 * sizeof(float);
   off += align256(w.part_ph_bytes);
   w.red_off = off;
   w.red_bytes = (static_cast<size_t>(w.red_groups_se) * f.J * kHeadDim +

@@ -510,8 +510,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_v2(const dwarf_dsqg_bwd
 // ---------------------------------------------------------------------------
 // bf16 dQ launch, four lanes per query (the forward's mapping).
 //
-// A workgroup of 4 waves walks every n_tg-th 64-query tile of one (b, h);
-// wave w owns queries 16w..16w+15 of a tile and lane g of a query holds head
+// A persistent workgroup of 4 waves walks a sequence of 64-query tiles (the
+// order is described at the tile loop); wave w owns queries 16w..16w+15 of a tile and lane g of a query holds head
 // dims [16g, 16g+16).  Each wave walks its offset list (offsets that give one
 // of its queries a source row) in chunks of CJ with the next chunk's K/V/z
 // loads in flight; a lane without a source reads zeros (out-of-range buffer
@@ -522,10 +522,10 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_v2(const dwarf_dsqg_bwd
 // high and low parts):
 //   dQe^T = E^T dS^T   (added to dQ through an LDS transpose)
 //   dSE   = dS^T Q     (wave w: dims 16w..16w+15), dPB = dS^T 1 (wave 0)
-// accumulated into the workgroup's partial slots.  dPhase sums over the
-// wave's 16 queries are reduced per chunk (DPP + lane shuffles) into a
-// per-wave LDS table written to the partial slot at the end, so every sum has
-// a fixed order.
+// dSE accumulates in the workgroup's slot, dPB goes to the tile's row.  dPhase
+// sums over the wave's 16 queries are reduced per chunk (DPP + lane shuffles)
+// into a per-wave LDS table whose four waves are added in a fixed order into
+// the tile's row, so every sum has a fixed order.
 // ---------------------------------------------------------------------------
 constexpr int kQT = 64;           // queries per tile
 constexpr int kQPW = 16;          // queries per wave
@@ -569,8 +569,7 @@ struct DqChunk {
 template <int SHIFT, int CJ>
 __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsqg_bwd_args a, float* __restrict__ delta_ws,
                                                                  float* __restrict__ part_se, float* __restrict__ part_pb,
-                                                                 float* __restrict__ part_ph, int tiles, int tpw, int n_tg,
-                                                                 int total) {
+                                                                 float* __restrict__ part_ph, int tiles) {
   constexpr float kC = 0.125f * kLog2e;
   constexpr float kScale = 0.125f;
   static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
@@ -579,7 +578,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
   const DqT4Layout lay = dq_t4_layout(J, JL, CJ);
   extern __shared__ float smem[];
   char* sm = reinterpret_cast<char*>(smem);
-  float* s_pb2 = smem;                                        // log2(e) * pb_j
+  float* s_pb2 = smem;                                        // log2(e) * pb_j of the tile's head
   int* s_off = reinterpret_cast<int*>(smem + lay.JE);
   float2* s_ph = reinterpret_cast<float2*>(sm + lay.off_ph);
   int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
@@ -587,14 +586,6 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
   uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
   uint16_t* sEt = reinterpret_cast<uint16_t*>(sm + lay.off_et);
   float* s_ds = reinterpret_cast<float*>(sm + lay.off_ds);
-
-  const int work = xcd_remap(blockIdx.x, total);
-  const int bh = work / n_tg;
-  const int tg = work - bh * n_tg;
-  const int b = bh / f.H;
-  const int h = bh - b * f.H;
-  const int hk = h / (f.H / f.H_kv);
-  const int slot = (h * f.B + b) * n_tg + tg;   // head-major partial slot
 
   for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
     const int j = i / kHeadDim, d = i - j * kHeadDim;
@@ -607,16 +598,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
     sE[j * kERowT + d] = bits;
     sEt[d * lay.jt + j] = bits;
   }
-  for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
-    s_pb2[j] = j < J ? kLog2e * f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]] : 0.f;
-    s_off[j] = j < J ? f.offsets[j] : 0;
-  }
-  for (int t = threadIdx.x; t < JL * kPlanes; t += kBlock) {
-    const int i = t / kPlanes, r = t - i * kPlanes;
-    s_ph[t] = make_float2(f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r],
-                          f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r]);
-  }
-  for (int t = threadIdx.x; t < 4 * lay.JL4 * 8; t += kBlock) s_dph_all[t] = 0.f;
+  for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
 
   const int lane = threadIdx.x;
   const int w = lane / kWave;
@@ -626,23 +608,47 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
   const int lr = l & 15, lc = l >> 4;
   int2* s_list = s_list_all + w * lay.list_len;
   float* s_dph = s_dph_all + w * lay.JL4 * 8;
-
-  const bf16* qb = reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1];
-  const bf16* dob = reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1];
-  const bf16* ob = reinterpret_cast<const bf16*>(f.out) + b * f.out_stride[0] + h * f.out_stride[1];
   const int ks_b = static_cast<int>(f.k_stride[2]) * 2, vs_b = static_cast<int>(f.v_stride[2]) * 2;
   const int zs_b = static_cast<int>(f.z_stride[2]) * 4, qs_b = static_cast<int>(f.q_stride[2]) * 2;
-  const __amdgpu_buffer_rsrc_t rk =
-      rows_rsrc(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1], ks_b, N, 128);
-  const __amdgpu_buffer_rsrc_t rv =
-      rows_rsrc(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1], vs_b, N, 128);
-  const __amdgpu_buffer_rsrc_t rz = rows_rsrc(f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1], zs_b, N, 16);
-  const __amdgpu_buffer_rsrc_t rq = rows_rsrc(qb, qs_b, N, 128);
 
-  // Tiles tg, tg + n_tg, tg + 2 n_tg, ...: every workgroup gets early (few
-  // valid offsets) and late tiles of the sequence alike.
-  for (int t = tg; t < tiles; t += n_tg) {
-    const bool first = t == tg;
+  // Tile order.  Workgroups are dealt round-robin over the 8 XCDs; XCD x owns
+  // a contiguous range of the (b, h)-major tiles and its U workgroups take
+  // them in steps of U consecutive tiles (about two (b, h) at a time, so the
+  // K/V rows they gather stay in that XCD's L2).  Within a step the tiles are
+  // rotated by 7 per step, so each workgroup sees early (few valid offsets)
+  // and late positions of the sequence alike.
+  const int W = gridDim.x;
+  const int x = blockIdx.x % kXcds, u = blockIdx.x / kXcds;
+  const int Ux = (W - x + kXcds - 1) / kXcds;
+  int cum_x = 0;
+  for (int y = 0; y < x; ++y) cum_x += (W - y + kXcds - 1) / kXcds;
+  const int64_t total_tiles = static_cast<int64_t>(tiles) * f.B * f.H;
+  const int T0 = static_cast<int>(total_tiles * cum_x / W);
+  const int T1 = static_cast<int>(total_tiles * (cum_x + Ux) / W);
+  const int slot = blockIdx.x;
+  bool first = true;
+  int cur_h = -1;
+
+  for (int kstep = 0; kstep * Ux < T1 - T0; ++kstep) {
+    const int Lt = kstep * Ux + (u + 7 * kstep) % Ux;
+    if (Lt >= T1 - T0) continue;
+    const int T = T0 + Lt;
+    const int bh = T / tiles;
+    const int t = T - bh * tiles;
+    const int b = bh / f.H;
+    const int h = bh - b * f.H;
+    const int hk = h / (f.H / f.H_kv);
+    const int64_t prow = static_cast<int64_t>(h * f.B + b) * tiles + t;   // head-major partial row
+    const bf16* qb = reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1];
+    const bf16* dob = reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1];
+    const bf16* ob = reinterpret_cast<const bf16*>(f.out) + b * f.out_stride[0] + h * f.out_stride[1];
+    const __amdgpu_buffer_rsrc_t rk =
+        rows_rsrc(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1], ks_b, N, 128);
+    const __amdgpu_buffer_rsrc_t rv =
+        rows_rsrc(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1], vs_b, N, 128);
+    const __amdgpu_buffer_rsrc_t rz = rows_rsrc(f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1], zs_b, N, 16);
+    const __amdgpu_buffer_rsrc_t rq = rows_rsrc(qb, qs_b, N, 128);
+
     const int n0 = t * kQT;
     const int n0w = n0 + kQPW * w;
     const int n = n0w + qi;
@@ -681,8 +687,19 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
     const int vb_lane = n_eff * vs_b + 32 * g;
     const int zb_lane = n_eff * zs_b + 4 * g;
 
-    __syncthreads();   // the previous tile's dQe staging reads are done
+    __syncthreads();   // the previous tile's dQe staging and partial reads are done
     for (int i = lane; i < lay.JE * kQT; i += kBlock) s_ds[(i / kQT) * kDsRowT + (i % kQT)] = 0.f;
+    for (int i = lane; i < 4 * lay.JL4 * 8; i += kBlock) s_dph_all[i] = 0.f;
+    if (h != cur_h) {
+      cur_h = h;
+      for (int j = lane; j < lay.JE; j += kBlock)
+        s_pb2[j] = j < J ? kLog2e * f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]] : 0.f;
+      for (int i = lane; i < JL * kPlanes; i += kBlock) {
+        const int ii = i / kPlanes, r = i - ii * kPlanes;
+        s_ph[i] = make_float2(f.phase_base[ii * f.pbase_stride[0] + h * f.pbase_stride[1] + r],
+                              f.phase_gain[ii * f.pgain_stride[0] + h * f.pgain_stride[1] + r]);
+      }
+    }
     int cnt = 0;
     if (n0w < N) cnt = build_offset_list<CJ>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
     const int cntp = (cnt + CJ - 1) / CJ * CJ;
@@ -841,14 +858,16 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
             float* dst = part_se + (static_cast<int64_t>(slot) * J + j) * kHeadDim + 16 * w + lr;
             const float v = kScale * c[r];
             *dst = first ? v : *dst + v;
-            if (w == 0 && lr == 0) {
-              float* dp = part_pb + static_cast<int64_t>(slot) * J + j;
-              *dp = first ? c1[r] : *dp + c1[r];
-            }
+            if (w == 0 && lr == 0) part_pb[prow * J + j] = c1[r];
           }
         }
       }
     }
+    // dPhase of this tile: the four waves' sums in a fixed order
+    for (int i = lane; i < JL * 8; i += kBlock)
+      part_ph[prow * JL * 8 + i] = ((s_dph_all[i] + s_dph_all[lay.JL4 * 8 + i]) + s_dph_all[2 * lay.JL4 * 8 + i]) +
+                                   s_dph_all[3 * lay.JL4 * 8 + i];
+    first = false;
     __syncthreads();   // every wave is done reading s_ds; it now stages dQe
     float* stage = s_ds + w * kQPW * kDsRowT;   // [16 q][68]
 #pragma unroll
@@ -878,10 +897,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
       a.dy_pre[(static_cast<int64_t>(bh) * N + n) * kPlanes + g] = dy;
     }
   }
-  __syncthreads();
-  for (int t = lane; t < 4 * JL * 8; t += kBlock) {
-    const int ww = t / (JL * 8), rest = t - ww * JL * 8;
-    part_ph[(static_cast<int64_t>(slot) * 4 + ww) * JL * 8 + rest] = s_dph_all[ww * lay.JL4 * 8 + rest];
+  if (first) {   // no tile for this workgroup: its dSE slot still enters the reduction
+    for (int i = lane; i < J * kHeadDim; i += kBlock) part_se[static_cast<int64_t>(slot) * J * kHeadDim + i] = 0.f;
   }
 }
 
@@ -898,7 +915,7 @@ hipError_t launch_dq_bf16_t4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& w
 #define DWARF_DQT4_CASE(S)                                                                                       \
   case S:                                                                                                       \
     hipLaunchKernelGGL((dsqg_bwd_dq_bf16_t4<S, CJ>), dim3(ws.dq_wgs), dim3(kBlock), lds, stream, a, delta,        \
-                       part_se, part_pb, part_ph, ws.dq_tiles, ws.dq_tpw, ws.dq_ntg, ws.dq_wgs);                  \
+                       part_se, part_pb, part_ph, ws.dq_tiles);                                                  \
     break;
   switch (f.plane_shift) {
     DWARF_DQT4_CASE(0) DWARF_DQT4_CASE(1) DWARF_DQT4_CASE(2) DWARF_DQT4_CASE(3) DWARF_DQT4_CASE(4)

@@ -16,8 +16,10 @@ constexpr int kBlock = 256;  // threads per workgroup for the DSQG kernels
 // Workgroup index -> work item, so that consecutive work items (the query
 // tiles of one (b, h), which share K/V rows) land on the same XCD and share
 // its L2.  Workgroups are dealt round-robin over the 8 XCDs of an MI355X.
+constexpr int kXcds = 8;   // XCDs of an MI355X; workgroups are dealt round-robin over them
+
 __device__ __forceinline__ int xcd_remap(int block_linear, int total) {
-  constexpr int kXcd = 8;
+  constexpr int kXcd = kXcds;
   const int per = total / kXcd, rem = total % kXcd;
   const int xcd = block_linear % kXcd, idx = block_linear / kXcd;
   return xcd * per + (xcd < rem ? xcd : rem) + idx;
@@ -38,14 +40,15 @@ hipError_t launch_dsqg_fwd(const dwarf_dsqg_fwd_args& a, hipStream_t stream);
 struct BwdWorkspace {
   size_t delta_off, delta_bytes;        // [B,H,N] fp32
   size_t part_se_off, part_se_bytes;    // [W][J][64] fp32
-  size_t part_pb_off, part_pb_bytes;    // [W][J] fp32
-  size_t part_ph_off, part_ph_bytes;    // [W][4 waves][J_L][8] fp32
+  size_t part_pb_off, part_pb_bytes;    // [H][pb_rows][J] fp32
+  size_t part_ph_off, part_ph_bytes;    // [H][ph_rows][J_L][8] fp32
   size_t red_off, red_bytes;            // stage-1 sums of the reduction
   size_t total;
-  int dq_tiles;   // 128-query tiles per (b, h)
-  int dq_tpw;     // tiles per workgroup
-  int dq_ntg;     // workgroups per (b, h)
-  int dq_wgs;     // W = B * H * dq_ntg
+  int dq_tiles;   // query tiles per (b, h)
+  int dq_tpw;     // tiles per workgroup (fp32 launch)
+  int dq_ntg;     // workgroups per (b, h) (fp32 launch)
+  int dq_wgs;     // W: workgroups of the dq launch = dSE partial slots
+  int pb_rows, ph_rows;   // dPB / dPhase partial rows per head
   int red_groups_se, red_groups_pb, red_groups_ph;  // stage-1 row groups per segment
 };
 BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a);
