@@ -566,7 +566,7 @@ struct DqChunk {
   int j[CJ];
 };
 
-template <int SHIFT, int CJ>
+template <int SHIFT, int CJ, int MB>
 __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsqg_bwd_args a, float* __restrict__ delta_ws,
                                                                  float* __restrict__ part_se, float* __restrict__ part_pb,
                                                                  float* __restrict__ part_ph, int tiles) {
@@ -626,8 +626,11 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
   const int T0 = static_cast<int>(total_tiles * cum_x / W);
   const int T1 = static_cast<int>(total_tiles * (cum_x + Ux) / W);
   const int slot = blockIdx.x;
-  bool first = true;
   int cur_h = -1;
+  // dSE[16 mb + 4 lc + r][16 w + lr] of this workgroup, over all its tiles (MB >= JE / 16)
+  f32x4 dse[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) dse[mb] = zero4();
 
   for (int kstep = 0; kstep * Ux < T1 - T0; ++kstep) {
     const int Lt = kstep * Ux + (u + 7 * kstep) % Ux;
@@ -835,8 +838,10 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
         }
 #pragma unroll
       for (int e = 0; e < 8; ++e) one[e] = static_cast<__bf16>(lr == 0 ? 1.f : 0.f);
-      for (int mb = 0; mb < lay.JE / 16; ++mb) {
-        f32x4 c = zero4(), c1 = zero4();
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        if (16 * mb >= lay.JE) break;
+        f32x4 c1 = zero4();
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           const float4* src = reinterpret_cast<const float4*>(s_ds + (16 * mb + lr) * kDsRowT + 32 * ks + 8 * lc);
@@ -844,8 +849,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
           const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
           bf16x8 ahi, alo;
           split_bf16x8(x, ahi, alo);
-          c = mfma16_bf16(ahi, bq[ks], c);
-          c = mfma16_bf16(alo, bq[ks], c);
+          dse[mb] = mfma16_bf16(ahi, bq[ks], dse[mb]);
+          dse[mb] = mfma16_bf16(alo, bq[ks], dse[mb]);
           if (w == 0) {
             c1 = mfma16_bf16(ahi, one, c1);
             c1 = mfma16_bf16(alo, one, c1);
@@ -854,12 +859,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = 16 * mb + 4 * lc + r;
-          if (j < J) {
-            float* dst = part_se + (static_cast<int64_t>(slot) * J + j) * kHeadDim + 16 * w + lr;
-            const float v = kScale * c[r];
-            *dst = first ? v : *dst + v;
-            if (w == 0 && lr == 0) part_pb[prow * J + j] = c1[r];
-          }
+          if (w == 0 && lr == 0 && j < J) part_pb[prow * J + j] = c1[r];
         }
       }
     }
@@ -867,7 +867,6 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
     for (int i = lane; i < JL * 8; i += kBlock)
       part_ph[prow * JL * 8 + i] = ((s_dph_all[i] + s_dph_all[lay.JL4 * 8 + i]) + s_dph_all[2 * lay.JL4 * 8 + i]) +
                                    s_dph_all[3 * lay.JL4 * 8 + i];
-    first = false;
     __syncthreads();   // every wave is done reading s_ds; it now stages dQe
     float* stage = s_ds + w * kQPW * kDsRowT;   // [16 q][68]
 #pragma unroll
@@ -897,12 +896,17 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
       a.dy_pre[(static_cast<int64_t>(bh) * N + n) * kPlanes + g] = dy;
     }
   }
-  if (first) {   // no tile for this workgroup: its dSE slot still enters the reduction
-    for (int i = lane; i < J * kHeadDim; i += kBlock) part_se[static_cast<int64_t>(slot) * J * kHeadDim + i] = 0.f;
-  }
+  // the workgroup's dSE slot (zeros if it had no tile)
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * mb + 4 * lc + r;
+      if (j < J) part_se[(static_cast<int64_t>(slot) * J + j) * kHeadDim + 16 * w + lr] = kScale * dse[mb][r];
+    }
 }
 
-template <int CJ>
+template <int CJ, int MB>
 hipError_t launch_dq_bf16_t4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
   char* base = static_cast<char*>(a.workspace);
@@ -914,7 +918,7 @@ hipError_t launch_dq_bf16_t4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& w
   const size_t lds = dq_t4_layout(f.J, f.J_large, CJ).bytes;
 #define DWARF_DQT4_CASE(S)                                                                                       \
   case S:                                                                                                       \
-    hipLaunchKernelGGL((dsqg_bwd_dq_bf16_t4<S, CJ>), dim3(ws.dq_wgs), dim3(kBlock), lds, stream, a, delta,        \
+    hipLaunchKernelGGL((dsqg_bwd_dq_bf16_t4<S, CJ, MB>), dim3(ws.dq_wgs), dim3(kBlock), lds, stream, a, delta,    \
                        part_se, part_pb, part_ph, ws.dq_tiles);                                                  \
     break;
   switch (f.plane_shift) {
@@ -961,7 +965,12 @@ size_t dq_lds_bytes(int J, int J_large, int dtype) {
 int dq_tile_queries(int dtype) { return dtype == DWARF_BF16 ? kQT : kQ; }
 
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
-  if (a.fwd.dtype == DWARF_BF16) return launch_dq_bf16_t4<kChunkDq>(a, ws, stream);
+  if (a.fwd.dtype == DWARF_BF16) {
+    // dSE accumulator blocks per wave: JE / 16 with JE = roundup16(J + 1)
+    const int blocks = (a.fwd.J + 1 + 15) / 16;
+    if (blocks <= 7) return launch_dq_bf16_t4<kChunkDq, 7>(a, ws, stream);
+    return launch_dq_bf16_t4<kChunkDq, 17>(a, ws, stream);
+  }
   return launch_dq_typed<float>(a, ws, stream);
 }
 
