@@ -23,6 +23,7 @@ hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const i
 hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream);
 hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream);
 int q6_max_decode_offsets();
+int q6_max_decode_heads();
 }  // namespace dwarf
 
 namespace {
@@ -314,6 +315,10 @@ int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t s
   if (rc) return rc;
   if (a.J > dwarf::q6_max_decode_offsets())
     return fail(DWARF_ERR_UNSUPPORTED, "decode supports at most %d offsets", dwarf::q6_max_decode_offsets());
+  if (a.H > dwarf::q6_max_decode_heads())
+    return fail(DWARF_ERR_UNSUPPORTED, "decode runs one wave per head: at most %d heads", dwarf::q6_max_decode_heads());
+  if (static_cast<int64_t>(a.Ncache) * DWARF_Q6_SLOT_BYTES >= (int64_t(1) << 31))
+    return fail(DWARF_ERR_UNSUPPORTED, "decode gathers with 32-bit offsets: Ncache x 128 B must stay below 2 GiB");
   if ((rc = check_rows("q", a.q, a.q_stride, 3, DWARF_BF16))) return rc;
   if (!a.out || a.out_stride[3] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "out is NULL or not unit-stride");
   if ((rc = check_cache(a.cache, a.cache_stride, 3))) return rc;

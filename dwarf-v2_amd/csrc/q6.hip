@@ -15,6 +15,7 @@
 // A gathered offset therefore reads exactly one 128-byte line.
 #include "common.h"
 #include "dsqg_internal.h"
+#include "gather.h"
 
 namespace dwarf {
 namespace {
@@ -282,140 +283,242 @@ __global__ __launch_bounds__(kBlock) void q6_prefill_kernel(const dwarf_dsqg_q6_
 }
 
 // ---------------------------------------------------------------------------
-// Decode.  One wave per (sequence, layer, head).  Lane pair (jl, g): offset
-// jl of each 32-offset round, group g of the head dims.  Scores of all
-// offsets are kept in registers, the softmax is reduced over the wave, and
-// the weighted V rows are summed through LDS.
+// Decode.  One workgroup per (sequence, layer), one wave per head.
+//
+// A slot's codes come in 12-byte chunks of 16 head dims (K at 12c, V at
+// 52 + 12c), so four lanes per gathered row -- lane c holding dims
+// [16c, 16c+16) of K and of V -- cover a whole 128-byte slot, and one wave
+// load instruction fetches 16 slots.  Each wave lists the offsets whose row
+// t - delta is inside the cache, then walks the list in batches of 16 rows
+// with the next batch's loads in flight.  Per row the lanes dequantise on
+// read (v_bfe_i32 of the 6-bit fields, the fp16 group scale applied to the
+// partial sums), form <q, k + e_j> (E staged in LDS, bf16-rounded as the GPU
+// path does), run an online base-2 softmax over the batches and accumulate
+// P * R V; lane c rotates the MOVT pair of plane c.  The 16 row groups are
+// summed with DPP and lane shuffles at the end.
 // ---------------------------------------------------------------------------
-constexpr int kDecRounds = 4;  // up to 128 offsets
+constexpr int kDecRows = 16;      // rows per batch (one per 4-lane group)
+constexpr int kMaxDecHeads = 16;  // waves per workgroup
+
+struct DecBatch {
+  uint32_t k0, k1, k2, v0, v1, v2;
+  uint32_t ks, vs;   // fp16 scale pairs of the two groups
+  float z, pb2, base, gain;
+  bool ok;
+};
+
+__device__ __forceinline__ uint32_t cache_dword(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// Sixteen signed 6-bit codes of a 12-byte chunk (bits [6i, 6i+6) of w0:w1:w2).
+// v_bfe_i32 sign-extends the field; the builtin is typed unsigned, so the
+// result is reinterpreted as int before the conversion to float.
+__device__ __forceinline__ float sfield6(uint32_t w, int bit) {
+  return static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(w, bit, 6)));
+}
+
+__device__ __forceinline__ void q6_codes16(uint32_t w0, uint32_t w1, uint32_t w2, float* c) {
+#pragma unroll
+  for (int i = 0; i < 5; ++i) c[i] = sfield6(w0, 6 * i);
+  c[5] = sfield6(__builtin_amdgcn_alignbit(w1, w0, 30), 0);
+#pragma unroll
+  for (int i = 6; i < 10; ++i) c[i] = sfield6(w1, 6 * i - 32);
+  c[10] = sfield6(__builtin_amdgcn_alignbit(w2, w1, 28), 0);
+#pragma unroll
+  for (int i = 11; i < 16; ++i) c[i] = sfield6(w2, 6 * i - 64);
+}
+
+__device__ __forceinline__ float half_lo_or_hi(uint32_t pair, bool hi) {
+  return half_bits_to_f32(static_cast<uint16_t>(hi ? pair >> 16 : pair));
+}
+
+struct DecLayout {
+  int list_len;
+  size_t off_off, off_list, bytes;
+};
+
+__host__ __device__ inline DecLayout dec_layout(int J, int H) {
+  DecLayout L;
+  L.list_len = (J + 3 * kDecRows + 1) / 2 * 2;
+  L.off_off = static_cast<size_t>(J + 1) * kHeadDim * 4;           // sE[J + 1][64] (row J = 0)
+  L.off_list = L.off_off + static_cast<size_t>((J + 3) / 4 * 4) * 4;  // s_off[J]
+  L.bytes = L.off_list + static_cast<size_t>(H) * L.list_len * 8;   // s_list[H][list_len] int2
+  return L;
+}
 
 template <int SHIFT>
-__global__ __launch_bounds__(kBlock) void q6_decode_kernel(const dwarf_dsqg_q6_decode_args a, int items) {
-  constexpr int L = 2, DPL = 32, HD = kHeadDim, SEG = HD / kPlanes, OPR = kWave / L;
-  __shared__ float s_red[kBlock / kWave][OPR][HD + 1];
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  const int item = blockIdx.x * (kBlock / kWave) + wave;  // (s, l, h)
-  if (item >= items) return;  // whole wave leaves together; no block barriers
-  const int h = item % a.H;
-  const int ly = (item / a.H) % a.L;
-  const int sq = item / (a.H * a.L);
-  const int hk = h / (a.H / a.H_kv);
-  const int g = lane % L;
-  const int jl = lane / L;
-  const int t = a.pos[sq];
+__global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const dwarf_dsqg_q6_decode_args a) {
+  constexpr float kC = 0.125f * kLog2e;
+  constexpr float kSlack2 = 8.0f * kLog2e;
+  static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's chunk");
+  const int J = a.J, H = a.H;
+  const DecLayout lay = dec_layout(J, H);
+  extern __shared__ float smem[];
+  char* sm = reinterpret_cast<char*>(smem);
+  float* sE = smem;
+  int* s_off = reinterpret_cast<int*>(sm + lay.off_off);
+  int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
 
-  float q[DPL];
-  load_f32<bf16, DPL>(reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1] +
-                          h * a.q_stride[2] + g * DPL, q);
-  const float* qp = a.query_probes + ly * a.qprobe_layer_stride;
-  float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) {
-    ss = fmaf(q[d], q[d], ss);
-#pragma unroll
-    for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(q[d], qp[r * HD + g * DPL + d], yp[r]);
-  }
-  ss = group_sum<L>(ss);
-  const float qinv = rsqrtf(ss + 1e-6f * HD);
-  float ys[4];
-#pragma unroll
-  for (int r = 0; r < kPlanes; ++r) ys[r] = group_sum<L>(yp[r]) * qinv;
-
-  const float* pb = a.pos_bias + ly * a.pb_stride[0];
+  const int sq = blockIdx.x / a.L;
+  const int ly = blockIdx.x - sq * a.L;
   const float* se = a.scale_embed + ly * a.se_stride[0];
-  const float* pbase = a.phase_base + ly * a.pbase_stride[0];
-  const float* pgain = a.phase_gain + ly * a.pgain_stride[0];
-  const uint8_t* cbase = a.cache + ly * a.cache_stride[0] + sq * a.cache_stride[1] + hk * a.cache_stride[2];
-  constexpr float scale = 0.125f;
+  for (int i = threadIdx.x; i < (J + 1) * kHeadDim; i += blockDim.x) {
+    const int j = i / kHeadDim, d = i - j * kHeadDim;
+    float e = 0.f;
+    if (j < J) {
+      e = se[j * a.se_stride[1] + d];
+      if (a.se_round_bf16) e = round_bf16(e);
+    }
+    sE[i] = e;
+  }
+  for (int j = threadIdx.x; j < J; j += blockDim.x) s_off[j] = a.offsets[j];
+  __syncthreads();
 
-  float sc[kDecRounds];
-  float mloc = -INFINITY;
+  const int h = uniform(threadIdx.x / kWave);   // head = wave index
+  const int l = threadIdx.x % kWave;
+  const int c = l & 3;        // 16-dim chunk
+  const int rr = l >> 2;      // row of the batch
+  const int hk = h / (H / a.H_kv);
+  const int t = a.pos[sq];
+  const int Nc = a.Ncache;
+  int2* list = s_list_all + h * lay.list_len;
+  // rows t - delta in [0, Nc); the sentinel offset t + 1 gives row -1
+  const int cnt = build_offset_list<kDecRows>(list, s_off, J, t, t, Nc, 1, make_int2(J, t + 1));
+  const int cntp = (cnt + kDecRows - 1) / kDecRows * kDecRows;
+
+  // this lane's q chunk, |q|^2 and the probe features y (in-kernel, as dsqg:3231-3249)
+  float qf[16];
+  {
+    const uint4* q4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] +
+                                                     ly * a.q_stride[1] + h * a.q_stride[2] + 16 * c);
+    const uint4 x0 = q4[0], x1 = q4[1];
+    const uint32_t w[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-  for (int rd = 0; rd < kDecRounds; ++rd) {
-    sc[rd] = -INFINITY;
-    if (rd * OPR >= a.J) continue;  // uniform
-    const int j = rd * OPR + jl;
-    const int jc = j < a.J ? j : a.J - 1;
-    const int s = t - a.offsets[jc];
-    const bool ok = j < a.J && s >= 0 && s < a.Ncache;  // identical for both lanes of a pair
-    float part = 0.f;
-    if (ok) {
-      const uint8_t* slot = cbase + static_cast<int64_t>(s) * a.cache_stride[3];
-      float c[DPL];
-      q6_codes(slot + kKCodes + 24 * g, c);
-      const float ksc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kKScales + 2 * g));
-      const float* e = se + jc * a.se_stride[1] + g * DPL;
-      float dk = 0.f, de = 0.f;
-#pragma unroll
-      for (int d = 0; d < DPL; ++d) {
-        const float ev = a.se_round_bf16 ? round_bf16(e[d]) : e[d];
-        dk = fmaf(q[d], c[d], dk);
-        de = fmaf(q[d], ev, de);
-      }
-      part = fmaf(dk, ksc, de);
-    }
-    part = group_sum<L>(part);
-    if (ok) sc[rd] = fmaf(part, scale, pb[jc * a.pb_stride[1] + h * a.pb_stride[2]]);
-    mloc = fmaxf(mloc, sc[rd]);
+    for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(w[i]); qf[2 * i + 1] = bf16_hi(w[i]); }
   }
-  // wave max
+  float yg;
+  {
+    const float* qp = a.query_probes + ly * a.qprobe_layer_stride;
+    float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o));
-  float acc[DPL];
+    for (int d = 0; d < 16; ++d) {
+      ss = fmaf(qf[d], qf[d], ss);
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
-  float lsum = 0.f;
+      for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(qf[d], qp[r * kHeadDim + 16 * c + d], yp[r]);
+    }
+    ss = group_sum<4>(ss);
 #pragma unroll
-  for (int rd = 0; rd < kDecRounds; ++rd) {
-    if (rd * OPR >= a.J) continue;
-    const int j = rd * OPR + jl;
-    if (sc[rd] == -INFINITY) continue;
-    const float p = __expf(sc[rd] - mloc);
+    for (int r = 0; r < kPlanes; ++r) yp[r] = group_sum<4>(yp[r]);
+    const float qinv = rsqrtf(ss + 1e-6f * kHeadDim);
+    yg = (c == 0 ? yp[0] : c == 1 ? yp[1] : c == 2 ? yp[2] : yp[3]) * qinv;
+  }
+
+  const uint8_t* cb = a.cache + ly * a.cache_stride[0] + sq * a.cache_stride[1] + hk * a.cache_stride[2];
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(cb), 0, static_cast<int>(static_cast<int64_t>(Nc) * kSlot), 0x00020000);
+  const float* pb = a.pos_bias + ly * a.pb_stride[0] + h * a.pb_stride[2];
+  const float* pbase = a.phase_base + ly * a.pbase_stride[0] + h * a.pbase_stride[2] + c;
+  const float* pgain = a.phase_gain + ly * a.pgain_stride[0] + h * a.pgain_stride[2] + c;
+  const bool khi = c >= 2;    // K/V group of this chunk: scale in the high half of the pair
+
+  auto fetch = [&](int k0, DecBatch& b) {
+    const int2 e = list[k0 + rr];
+    const int j = e.x;
+    const int row = t - e.y;
+    b.ok = static_cast<uint32_t>(row) < static_cast<uint32_t>(Nc);
+    const uint32_t base = b.ok ? static_cast<uint32_t>(row) * kSlot : kOutOfRange;
+    const auto kx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kKCodes + 12 * c, 0, 0);
+    const auto vx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kVCodes + 12 * c, 0, 0);
+    b.k0 = kx[0]; b.k1 = kx[1]; b.k2 = kx[2];
+    b.v0 = vx[0]; b.v1 = vx[1]; b.v2 = vx[2];
+    b.ks = cache_dword(rc, base + kKScales);
+    b.vs = cache_dword(rc, base + kVScales);
+    const bool far = j >= a.J_small && j < J;
+    b.z = __builtin_bit_cast(float, cache_dword(rc, far ? base + kZ + 4 * c : kOutOfRange));
+    b.pb2 = j < J ? kLog2e * pb[j * a.pb_stride[1]] : 0.f;
+    const int i = far ? j - a.J_small : 0;
+    b.base = far ? pbase[i * a.pbase_stride[1]] : 0.f;
+    b.gain = far ? pgain[i * a.pgain_stride[1]] : 0.f;
+  };
+
+  float acc[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+  float m = -3.0e38f, lsum = 0.f;
+
+  auto consume = [&](int k0, const DecBatch& b) {
+    const int j = list[k0 + rr].x;
+    float cf[16];
+    q6_codes16(b.k0, b.k1, b.k2, cf);
+    const float4* e4 = reinterpret_cast<const float4*>(sE + j * kHeadDim + 16 * c);
+    float kd = 0.f, ed = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 ev = e4[i];
+      kd = fmaf(qf[4 * i], cf[4 * i], kd);
+      kd = fmaf(qf[4 * i + 1], cf[4 * i + 1], kd);
+      kd = fmaf(qf[4 * i + 2], cf[4 * i + 2], kd);
+      kd = fmaf(qf[4 * i + 3], cf[4 * i + 3], kd);
+      ed = fmaf(qf[4 * i], ev.x, ed);
+      ed = fmaf(qf[4 * i + 1], ev.y, ed);
+      ed = fmaf(qf[4 * i + 2], ev.z, ed);
+      ed = fmaf(qf[4 * i + 3], ev.w, ed);
+    }
+    const float dot = group_sum<4>(fmaf(kd, half_lo_or_hi(b.ks, khi), ed));
+    const float s2 = b.ok ? fmaf(dot, kC, b.pb2) : -INFINITY;
+    float mb = fmaxf(s2, dpp_f<0x124>(s2));    // rows of the 16-lane row: rotations by 4, 8
+    mb = fmaxf(mb, dpp_f<0x128>(mb));
+    mb = fmaxf(mb, __shfl_xor(mb, 16));
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    if (mb > m + kSlack2) {   // wave-uniform
+      const float f = __builtin_amdgcn_exp2f(m - mb);
+#pragma unroll
+      for (int d = 0; d < 16; ++d) acc[d] *= f;
+      lsum *= f;
+      m = mb;
+    }
+    const float p = __builtin_amdgcn_exp2f(s2 - m);
     lsum += p;
-    const int s = t - a.offsets[j];
-    const uint8_t* slot = cbase + static_cast<int64_t>(s) * a.cache_stride[3];
-    float c[DPL];
-    q6_codes(slot + kVCodes + 24 * g, c);
-    const float vsc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kVScales + 2 * g));
+    q6_codes16(b.v0, b.v1, b.v2, cf);
+    const float vsc = half_lo_or_hi(b.vs, khi);
+    const float wgt = p * vsc;
+    // MOVT pair of plane c (dims 16c + SHIFT, +1); near rows have angle 0
+    float sn, cs;
+    dsincos<true>(fmaf(b.gain * yg, b.z, b.base), &sn, &cs);
+    const float va = cf[SHIFT], vb = cf[SHIFT + 1];
+    cf[SHIFT] = cs * va - sn * vb;
+    cf[SHIFT + 1] = sn * va + cs * vb;
 #pragma unroll
-    for (int d = 0; d < DPL; ++d) c[d] *= vsc;
-    if (j >= a.J_small) {
-      const int i = j - a.J_small;
-      const float4 zk = *reinterpret_cast<const float4*>(slot + kZ);
-      const float zs[4] = {zk.x, zk.y, zk.z, zk.w};
-#pragma unroll
-      for (int r = 0; r < kPlanes; ++r) {
-        const int ch = r * SEG + SHIFT;
-        if (ch / DPL != g) continue;
-        const int la = ch % DPL;
-        const float theta = pbase[i * a.pbase_stride[1] + h * a.pbase_stride[2] + r] +
-                            pgain[i * a.pgain_stride[1] + h * a.pgain_stride[2] + r] * ys[r] * zs[r];
-        float sn, cs;
-        dsincos<true>(theta, &sn, &cs);
-        const float va = c[la], vb = c[la + 1];
-        c[la] = cs * va - sn * vb;
-        c[la + 1] = sn * va + cs * vb;
-      }
+    for (int d = 0; d < 16; ++d) acc[d] = fmaf(wgt, cf[d], acc[d]);
+  };
+
+  if (cnt > 0) {
+    DecBatch b0, b1;
+    fetch(0, b0);
+    for (int k0 = 0; k0 < cntp; k0 += 2 * kDecRows) {
+      fetch(k0 + kDecRows, b1);
+      consume(k0, b0);
+      fetch(k0 + 2 * kDecRows, b0);
+      consume(k0 + kDecRows, b1);
     }
-#pragma unroll
-    for (int d = 0; d < DPL; ++d) acc[d] = fmaf(p, c[d], acc[d]);
   }
-  // lsum counts each offset twice (both lanes of a pair).
+  // sum the 16 row groups (lanes with the same chunk)
+  lsum = sum_over_queries16(lsum);
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) lsum += __shfl_xor(lsum, o);
-  lsum *= 0.5f;
-  // Sum acc over the 32 offset slots of each group through LDS.
-#pragma unroll
-  for (int d = 0; d < DPL; ++d) s_red[wave][jl][g * DPL + d] = acc[d];
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float o = 0.f;
-  for (int k = 0; k < OPR; ++k) o += s_red[wave][k][lane];
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  reinterpret_cast<uint16_t*>(a.out)[sq * a.out_stride[0] + ly * a.out_stride[1] + h * a.out_stride[2] + lane] =
-      f32_to_bf16_bits(o * inv);
+  for (int d = 0; d < 16; ++d) acc[d] = sum_over_queries16(acc[d]);
+  if (rr == 0) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.out) + sq * a.out_stride[0] + ly * a.out_stride[1] +
+                                         h * a.out_stride[2] + 16 * c);
+    uint4 x;
+    x.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);   x.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    x.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);   x.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
+    o4[0] = x;
+    x.x = pack_bf16x2(acc[8] * inv, acc[9] * inv);   x.y = pack_bf16x2(acc[10] * inv, acc[11] * inv);
+    x.z = pack_bf16x2(acc[12] * inv, acc[13] * inv); x.w = pack_bf16x2(acc[14] * inv, acc[15] * inv);
+    o4[1] = x;
+  }
 }
 
 }  // namespace
@@ -463,10 +566,10 @@ hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t st
 }
 
 hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream) {
-  const int items = a.S * a.L * a.H;
-  const int blocks = (items + kBlock / kWave - 1) / (kBlock / kWave);
+  const int blocks = a.S * a.L;
+  const size_t lds = dec_layout(a.J, a.H).bytes;
 #define DWARF_Q6D_CASE(S) \
-  case S: hipLaunchKernelGGL(q6_decode_kernel<S>, dim3(blocks), dim3(kBlock), 0, stream, a, items); break;
+  case S: hipLaunchKernelGGL(q6_decode_kernel<S>, dim3(blocks), dim3(kWave * a.H), lds, stream, a); break;
   switch (a.plane_shift) {
     DWARF_Q6D_CASE(0) DWARF_Q6D_CASE(1) DWARF_Q6D_CASE(2) DWARF_Q6D_CASE(3) DWARF_Q6D_CASE(4)
     DWARF_Q6D_CASE(5) DWARF_Q6D_CASE(6) DWARF_Q6D_CASE(7) DWARF_Q6D_CASE(8) DWARF_Q6D_CASE(9)
@@ -477,6 +580,7 @@ hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stre
   return hipGetLastError();
 }
 
-int q6_max_decode_offsets() { return kDecRounds * (kWave / 2); }
+int q6_max_decode_offsets() { return 256; }
+int q6_max_decode_heads() { return kMaxDecHeads; }
 
 }  // namespace dwarf

@@ -93,5 +93,8 @@ def test_validation_errors_without_gpu(pkg, lib):
     with pytest.raises(ValueError):
         L.check(lib.dwarf_ema_fwd(ctypes.byref(e), None), "dwarf_ema_fwd")
     d = L.Q6DecodeArgs()
-    d.S, d.L, d.H, d.H_kv, d.Ncache, d.head_dim, d.J, d.J_small, d.J_large = 1, 1, 1, 1, 64, 64, 200, 100, 100
-    assert lib.dwarf_dsqg_q6_decode(ctypes.byref(d), None) == L.DWARF_ERR_UNSUPPORTED
+    d.S, d.L, d.H, d.H_kv, d.Ncache, d.head_dim, d.J, d.J_small, d.J_large = 1, 1, 1, 1, 64, 64, 300, 150, 150
+    assert lib.dwarf_dsqg_q6_decode(ctypes.byref(d), None) == L.DWARF_ERR_UNSUPPORTED   # more than 256 offsets
+    d.J, d.J_small, d.J_large, d.H, d.H_kv = 96, 17, 79, 32, 32
+    assert lib.dwarf_dsqg_q6_decode(ctypes.byref(d), None) == L.DWARF_ERR_UNSUPPORTED   # one wave per head, <= 16
+    assert b"heads" in lib.dwarf_last_error()
