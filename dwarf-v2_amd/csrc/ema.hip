@@ -5,15 +5,16 @@
 // channels of one (b, chunk), so a wave reads 64*VEC consecutive channels of
 // one token per load.
 //   forward:  local  - chunk end state with zero carry-in (reads x)
-//             carry  - one lane per (b, channel) walks the chunk ends and
+//             carry  - one wave per (b, channel) scans the chunk ends and
 //                      writes each chunk's carry-in (tiny)
 //             apply  - rescans the chunk from its carry-in, writes y
 //   backward: the same three stages run in reverse time on dy for the
 //             adjoint lambda[t] = dy[t] + (1 - a) lambda[t+1]; the apply
 //             stage writes dx = a * lambda and a per-lane partial of
-//             dalpha = sum lambda[t] (x[t] - y[t-1]); a final kernel sums the
-//             partials in a fixed order and applies the projected-clamp rule
-//             of ema:357-364.
+//             dalpha = sum lambda[t] (x[t] - y[t-1]); one wave per channel
+//             sums the partials in a fixed order and applies the
+//             projected-clamp rule of ema:357-364.
+// The carry stage is a fixed-shape parallel scan over the chunks.
 // Alpha may be one value (the reference contract, ema:557-558) or one per
 // channel; the clamp to [floor, ceiling] happens in-kernel (ema:274-277).
 #include "common.h"
@@ -81,11 +82,18 @@ __device__ __forceinline__ float clamp_alpha(const float* alpha, int per_channel
   return fminf(fmaxf(a, lo), hi);
 }
 
+// Rows of one chunk are loaded in blocks of kRows<T> (all loads of a block
+// are issued before the recurrence consumes them), so a lane keeps a block of
+// rows in flight instead of one.
+template <typename T>
+constexpr int kRows = sizeof(T) == 2 ? 16 : 8;
+
 // ---- forward --------------------------------------------------------------
 template <typename T, int VEC>
 __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__ x, int64_t sxb, int64_t sxn,
                                                           const float* __restrict__ alpha, float* __restrict__ ends,
                                                           EmaGeom g) {
+  constexpr int R = kRows<T>;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * kEmaBlock + threadIdx.x;
   const int dv = tid % g.DV;
   const int c = (tid / g.DV) % g.NC;
@@ -96,43 +104,66 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__
 #pragma unroll
   for (int i = 0; i < VEC; ++i) { a[i] = clamp_alpha(alpha, g.per_channel, d0 + i, g.lo, g.hi); st[i] = 0.f; }
   const int t0 = c * kChunkT;
-  const int t1 = min(t0 + kChunkT, g.N);
+  const int len = min(kChunkT, g.N - t0);
   const T* p = x + b * sxb + static_cast<int64_t>(t0) * sxn + d0;
-  for (int t = t0; t < t1; ++t, p += sxn) {
-    float xv[VEC];
-    ldv<T, VEC>(p, xv);
+  for (int tb = 0; tb < len; tb += R) {
+    float xv[R][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) st[i] = fmaf(a[i], xv[i], (1.f - a[i]) * st[i]);
+    for (int r = 0; r < R; ++r)
+      if (tb + r < len) ldv<T, VEC>(p + static_cast<int64_t>(tb + r) * sxn, xv[r]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (tb + r < len) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) st[i] = fmaf(a[i], xv[r][i], (1.f - a[i]) * st[i]);
+      }
   }
   float* e = ends + (static_cast<int64_t>(b) * g.NC + c) * g.D + d0;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) e[i] = st[i];
 }
 
-// One lane per (b, channel): carries[c] = state entering chunk c.  When
-// REVERSE, chunks are walked from the last and carries[c] is the adjoint
-// entering chunk c from the future.
+// One wave per (b, channel): carries[c] = state entering chunk c (REVERSE:
+// the adjoint entering chunk c from the future).  With A = decay^kChunkT the
+// chunks compose as s(next) = A s + ends[c]; each lane folds a contiguous
+// segment of chunks into (A_seg, B_seg), a Hillis-Steele scan over the 64
+// lanes (fixed shape) gives every segment its incoming state, and the lane
+// then writes the carries of its chunks.
 template <bool REVERSE>
 __global__ __launch_bounds__(kEmaBlock) void ema_carry(const float* __restrict__ ends, float* __restrict__ carries,
                                                       const float* __restrict__ alpha, EmaGeom g) {
-  const int tid = blockIdx.x * kEmaBlock + threadIdx.x;
-  if (tid >= g.B * g.D) return;
-  const int b = tid / g.D, d = tid - b * g.D;
-  const float a = clamp_alpha(alpha, g.per_channel, d, g.lo, g.hi);
-  const float decay = 1.f - a;
-  float full = 1.f;  // decay^kChunkT, by repeated multiplication as the serial scan applies it
+  const int wave = (blockIdx.x * kEmaBlock + threadIdx.x) / kWave;
+  const int l = threadIdx.x % kWave;
+  if (wave >= g.B * g.D) return;   // whole wave
+  const int b = wave / g.D, d = wave - b * g.D;
+  const float decay = 1.f - clamp_alpha(alpha, g.per_channel, d, g.lo, g.hi);
+  float full = 1.f;  // decay^kChunkT, by repeated multiplication as a serial scan applies it
   for (int i = 0; i < kChunkT; ++i) full *= decay;
-  const int last_len = g.N - (g.NC - 1) * kChunkT;
-  float last = 1.f;
-  for (int i = 0; i < last_len; ++i) last *= decay;
   const float* e = ends + static_cast<int64_t>(b) * g.NC * g.D + d;
   float* cr = carries + static_cast<int64_t>(b) * g.NC * g.D + d;
-  float carry = 0.f;
-  for (int k = 0; k < g.NC; ++k) {
-    const int c = REVERSE ? g.NC - 1 - k : k;
-    cr[static_cast<int64_t>(c) * g.D] = carry;
-    const float pw = (c == g.NC - 1) ? last : full;
-    carry = fmaf(pw, carry, e[static_cast<int64_t>(c) * g.D]);
+  const int seg = (g.NC + kWave - 1) / kWave;    // chunks per lane, in scan order
+  const int k0 = l * seg;
+  auto chunk = [&](int k) { return REVERSE ? g.NC - 1 - k : k; };
+  float A = 1.f, Bv = 0.f;
+  for (int k = k0; k < min(k0 + seg, g.NC); ++k) {
+    Bv = fmaf(full, Bv, e[static_cast<int64_t>(chunk(k)) * g.D]);
+    A *= full;
+  }
+  // inclusive scan: (earlier) then (this) = (A_this A_earlier, A_this B_earlier + B_this)
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float Ae = __shfl_up(A, o), Be = __shfl_up(Bv, o);
+    if (l >= o) {
+      Bv = fmaf(A, Be, Bv);
+      A *= Ae;
+    }
+  }
+  float s = __shfl_up(Bv, 1);
+  if (l == 0) s = 0.f;
+  for (int k = k0; k < min(k0 + seg, g.NC); ++k) {
+    const int c = chunk(k);
+    cr[static_cast<int64_t>(c) * g.D] = s;
+    s = fmaf(full, s, e[static_cast<int64_t>(c) * g.D]);
   }
 }
 
@@ -141,6 +172,7 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_apply(const T* __restrict__
                                                           T* __restrict__ y, int64_t syb, int64_t syn,
                                                           const float* __restrict__ alpha,
                                                           const float* __restrict__ carries, EmaGeom g) {
+  constexpr int R = kRows<T>;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * kEmaBlock + threadIdx.x;
   const int dv = tid % g.DV;
   const int c = (tid / g.DV) % g.NC;
@@ -152,15 +184,21 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_apply(const T* __restrict__
 #pragma unroll
   for (int i = 0; i < VEC; ++i) { a[i] = clamp_alpha(alpha, g.per_channel, d0 + i, g.lo, g.hi); st[i] = cr[i]; }
   const int t0 = c * kChunkT;
-  const int t1 = min(t0 + kChunkT, g.N);
+  const int len = min(kChunkT, g.N - t0);
   const T* px = x + b * sxb + static_cast<int64_t>(t0) * sxn + d0;
   T* py = y + b * syb + static_cast<int64_t>(t0) * syn + d0;
-  for (int t = t0; t < t1; ++t, px += sxn, py += syn) {
-    float xv[VEC];
-    ldv<T, VEC>(px, xv);
+  for (int tb = 0; tb < len; tb += R) {
+    float xv[R][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) st[i] = fmaf(a[i], xv[i], (1.f - a[i]) * st[i]);
-    stv<T, VEC>(py, st);
+    for (int r = 0; r < R; ++r)
+      if (tb + r < len) ldv<T, VEC>(px + static_cast<int64_t>(tb + r) * sxn, xv[r]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (tb + r < len) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) st[i] = fmaf(a[i], xv[r][i], (1.f - a[i]) * st[i]);
+        stv<T, VEC>(py + static_cast<int64_t>(tb + r) * syn, st);
+      }
   }
 }
 
@@ -169,6 +207,7 @@ template <typename T, int VEC>
 __global__ __launch_bounds__(kEmaBlock) void ema_bwd_local(const T* __restrict__ dy, int64_t sgb, int64_t sgn,
                                                           const float* __restrict__ alpha, float* __restrict__ starts,
                                                           EmaGeom g) {
+  constexpr int R = kRows<T>;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * kEmaBlock + threadIdx.x;
   const int dv = tid % g.DV;
   const int c = (tid / g.DV) % g.NC;
@@ -179,13 +218,19 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_local(const T* __restrict__
 #pragma unroll
   for (int i = 0; i < VEC; ++i) { dec[i] = 1.f - clamp_alpha(alpha, g.per_channel, d0 + i, g.lo, g.hi); st[i] = 0.f; }
   const int t0 = c * kChunkT;
-  const int t1 = min(t0 + kChunkT, g.N);
-  const T* p = dy + b * sgb + static_cast<int64_t>(t1 - 1) * sgn + d0;
-  for (int t = t1 - 1; t >= t0; --t, p -= sgn) {
-    float gv[VEC];
-    ldv<T, VEC>(p, gv);
+  const int len = min(kChunkT, g.N - t0);
+  const T* p = dy + b * sgb + static_cast<int64_t>(t0) * sgn + d0;
+  for (int tb = len - 1; tb >= 0; tb -= R) {   // rows tb, tb-1, ..., tb-R+1
+    float gv[R][VEC];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) st[i] = fmaf(dec[i], st[i], gv[i]);
+    for (int r = 0; r < R; ++r)
+      if (tb - r >= 0) ldv<T, VEC>(p + static_cast<int64_t>(tb - r) * sgn, gv[r]);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (tb - r >= 0) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) st[i] = fmaf(dec[i], st[i], gv[r][i]);
+      }
   }
   float* e = starts + (static_cast<int64_t>(b) * g.NC + c) * g.D + d0;
 #pragma unroll
@@ -200,6 +245,7 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
                                                           const float* __restrict__ alpha,
                                                           const float* __restrict__ carries,
                                                           float* __restrict__ da_part, EmaGeom g) {
+  constexpr int R = kRows<T> / 2;
   const int64_t tid = static_cast<int64_t>(blockIdx.x) * kEmaBlock + threadIdx.x;
   const int dv = tid % g.DV;
   const int c = (tid / g.DV) % g.NC;
@@ -215,64 +261,85 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
     da[i] = 0.f;
   }
   const int t0 = c * kChunkT;
-  const int t1 = min(t0 + kChunkT, g.N);
-  for (int t = t1 - 1; t >= t0; --t) {
-    float gv[VEC], xv[VEC], yp[VEC];
-    ldv<T, VEC>(dy + b * sgb + static_cast<int64_t>(t) * sgn + d0, gv);
-    ldv<T, VEC>(x + b * sxb + static_cast<int64_t>(t) * sxn + d0, xv);
-    if (t > 0) {
-      ldv<T, VEC>(y + b * syb + static_cast<int64_t>(t - 1) * syn + d0, yp);
-    } else {
+  const int len = min(kChunkT, g.N - t0);
+  const T* pg = dy + b * sgb + static_cast<int64_t>(t0) * sgn + d0;
+  const T* pxx = x + b * sxb + static_cast<int64_t>(t0) * sxn + d0;
+  const T* pyy = y + b * syb + static_cast<int64_t>(t0) * syn + d0;
+  T* pd = dx + b * sdb + static_cast<int64_t>(t0) * sdn + d0;
+  for (int tb = len - 1; tb >= 0; tb -= R) {
+    float gv[R][VEC], xv[R][VEC], yp[R][VEC];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) yp[i] = 0.f;
-    }
-    float out[VEC];
+    for (int r = 0; r < R; ++r) {
+      const int t = tb - r;
+      if (t >= 0) {
+        ldv<T, VEC>(pg + static_cast<int64_t>(t) * sgn, gv[r]);
+        ldv<T, VEC>(pxx + static_cast<int64_t>(t) * sxn, xv[r]);
+        if (t0 + t > 0) {
+          ldv<T, VEC>(pyy + static_cast<int64_t>(t - 1) * syn, yp[r]);
+        } else {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      st[i] = fmaf(1.f - a[i], st[i], gv[i]);
-      out[i] = a[i] * st[i];
-      da[i] = fmaf(st[i], xv[i] - yp[i], da[i]);
+          for (int i = 0; i < VEC; ++i) yp[r][i] = 0.f;
+        }
+      }
     }
-    stv<T, VEC>(dx + b * sdb + static_cast<int64_t>(t) * sdn + d0, out);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int t = tb - r;
+      if (t >= 0) {
+        float out[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          st[i] = fmaf(1.f - a[i], st[i], gv[r][i]);
+          out[i] = a[i] * st[i];
+          da[i] = fmaf(st[i], xv[r][i] - yp[r][i], da[i]);
+        }
+        stv<T, VEC>(pd + static_cast<int64_t>(t) * sdn, out);
+      }
+    }
   }
   float* dp = da_part + (static_cast<int64_t>(b) * g.NC + c) * g.D + d0;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) dp[i] = da[i];
 }
 
-// dalpha[d] (or the single dalpha) = sum over (b, chunk) of the partials, in
-// order; then the projected-clamp rule.
-__global__ __launch_bounds__(kEmaBlock) void ema_dalpha_reduce(const float* __restrict__ da_part,
-                                                              const float* __restrict__ alpha,
-                                                              float* __restrict__ dalpha, EmaGeom g) {
-  __shared__ float s_red[kEmaBlock];
+// dalpha: one wave per channel sums its B * NC partial rows (lane k takes
+// rows k, k + 64, ... in order, then a fixed butterfly over the lanes).  For a
+// per-channel alpha the projected-clamp rule is applied per channel; for a
+// single alpha the channel sums go to `tmp` and a second pass adds them in
+// order.
+__global__ __launch_bounds__(kEmaBlock) void ema_dalpha_channels(const float* __restrict__ da_part,
+                                                                const float* __restrict__ alpha,
+                                                                float* __restrict__ out, EmaGeom g) {
+  const int d = (blockIdx.x * kEmaBlock + threadIdx.x) / kWave;
+  const int l = threadIdx.x % kWave;
+  if (d >= g.D) return;   // whole wave
   const int rows = g.B * g.NC;
-  if (g.per_channel) {
-    const int d = blockIdx.x * kEmaBlock + threadIdx.x;
-    if (d >= g.D) return;
-    float s = 0.f;
-    for (int r = 0; r < rows; ++r) s += da_part[static_cast<int64_t>(r) * g.D + d];
-    const float ai = alpha[d];
-    const bool blocked = (ai <= g.lo && s > 0.f) || (ai >= g.hi && s < 0.f);
-    dalpha[d] = blocked ? 0.f : s;
-    return;
-  }
-  // Scalar alpha: one workgroup; each lane sums a fixed set of channels
-  // over all rows, then a fixed-shape tree over the lanes.
   float s = 0.f;
-  for (int d = threadIdx.x; d < g.D; d += kEmaBlock)
-    for (int r = 0; r < rows; ++r) s += da_part[static_cast<int64_t>(r) * g.D + d];
-  s_red[threadIdx.x] = s;
-  __syncthreads();
-  for (int w = kEmaBlock / 2; w > 0; w >>= 1) {
-    if (threadIdx.x < w) s_red[threadIdx.x] += s_red[threadIdx.x + w];
-    __syncthreads();
+  for (int r = l; r < rows; r += kWave) s += da_part[static_cast<int64_t>(r) * g.D + d];
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) s += __shfl_xor(s, o);
+  if (l == 0) {
+    if (g.per_channel) {
+      const float ai = alpha[d];
+      const bool blocked = (ai <= g.lo && s > 0.f) || (ai >= g.hi && s < 0.f);
+      out[d] = blocked ? 0.f : s;
+    } else {
+      out[d] = s;
+    }
   }
-  if (threadIdx.x == 0) {
-    const float tot = s_red[0];
+}
+
+__global__ __launch_bounds__(kWave) void ema_dalpha_scalar(const float* __restrict__ chan, const float* __restrict__ alpha,
+                                                          float* __restrict__ dalpha, EmaGeom g) {
+  const int l = threadIdx.x;
+  float s = 0.f;
+  for (int d = l; d < g.D; d += kWave) s += chan[d];
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) s += __shfl_xor(s, o);
+  if (l == 0) {
     const float ai = alpha[0];
-    const bool blocked = (ai <= g.lo && tot > 0.f) || (ai >= g.hi && tot < 0.f);
-    dalpha[0] = blocked ? 0.f : tot;
+    const bool blocked = (ai <= g.lo && s > 0.f) || (ai >= g.hi && s < 0.f);
+    dalpha[0] = blocked ? 0.f : s;
   }
 }
 
@@ -302,8 +369,8 @@ hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
   T* y = static_cast<T*>(a.y);
   hipLaunchKernelGGL((ema_fwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], a.alpha, ends, g);
-  hipLaunchKernelGGL((ema_carry<false>), dim3((a.B * a.D + kEmaBlock - 1) / kEmaBlock), dim3(kEmaBlock), 0, stream,
-                     ends, carries, a.alpha, g);
+  hipLaunchKernelGGL((ema_carry<false>), dim3((a.B * a.D + kEmaBlock / kWave - 1) / (kEmaBlock / kWave)),
+                     dim3(kEmaBlock), 0, stream, ends, carries, a.alpha, g);
   hipLaunchKernelGGL((ema_fwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], y, a.y_stride[0], a.y_stride[1], a.alpha, carries, g);
   return hipGetLastError();
@@ -320,15 +387,21 @@ hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
   hipLaunchKernelGGL((ema_bwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
                      static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1], a.alpha, starts, g);
-  hipLaunchKernelGGL((ema_carry<true>), dim3((a.B * a.D + kEmaBlock - 1) / kEmaBlock), dim3(kEmaBlock), 0, stream,
-                     starts, carries, a.alpha, g);
+  hipLaunchKernelGGL((ema_carry<true>), dim3((a.B * a.D + kEmaBlock / kWave - 1) / (kEmaBlock / kWave)),
+                     dim3(kEmaBlock), 0, stream, starts, carries, a.alpha, g);
   hipLaunchKernelGGL((ema_bwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
                      static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<const T*>(a.y),
                      a.y_stride[0], a.y_stride[1], static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1],
                      static_cast<T*>(a.dx), a.dx_stride[0], a.dx_stride[1], a.alpha, carries, da_part, g);
   if (a.dalpha) {
-    const int rb = a.alpha_per_channel ? (a.D + kEmaBlock - 1) / kEmaBlock : 1;
-    hipLaunchKernelGGL(ema_dalpha_reduce, dim3(rb), dim3(kEmaBlock), 0, stream, da_part, a.alpha, a.dalpha, g);
+    const int rb = (a.D + kEmaBlock / kWave - 1) / (kEmaBlock / kWave);
+    if (a.alpha_per_channel) {
+      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kEmaBlock), 0, stream, da_part, a.alpha, a.dalpha, g);
+    } else {
+      float* chan = starts;   // free after the apply stage; D <= B * NC * D floats
+      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kEmaBlock), 0, stream, da_part, a.alpha, chan, g);
+      hipLaunchKernelGGL(ema_dalpha_scalar, dim3(1), dim3(kWave), 0, stream, chan, a.alpha, a.dalpha, g);
+    }
   }
   return hipGetLastError();
 }
