@@ -21,7 +21,7 @@
 
 namespace dwarf {
 
-constexpr int kChunkT = 64;
+constexpr int kChunkT = 32;
 constexpr int kEmaBlock = 256;
 
 namespace {
