@@ -11,7 +11,7 @@ Public surface (reference names, Lanerra/dwarf-v2):
   q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
 """
 
-from . import _lib, lattice, q6
+from . import _lib, lattice, ops, q6
 from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
 from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
 from .lattice import (

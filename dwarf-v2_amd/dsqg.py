@@ -92,6 +92,17 @@ def _device_offsets(offsets_dev: torch.Tensor, device: torch.device, j_val: int)
     return off
 
 
+def normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev, j_val):
+    """Layouts the kernels read: q/k/v rows with unit head-dim stride and 16-byte alignment (k/v in q's
+    dtype), contiguous fp32 tables and plane features, int32 offsets on q's device."""
+    q = _kernel_rows(q)
+    k, v = _kernel_rows(k.to(q.dtype)), _kernel_rows(v.to(q.dtype))
+    tables = [t.float().contiguous() for t in (pos_bias, scale_embed, phase_base, phase_gain)]
+    y_pre, z_pre = _planes(y_pre.float()), _planes(z_pre.float())
+    offsets = _device_offsets(offsets_dev, q.device, int(j_val))
+    return (q, k, v, *tables, y_pre, z_pre, offsets)
+
+
 def dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
                  j_small, j_large, plane_shift=0, query_start=0, *, events=None):
     """Raw forward launch: returns (out, lse).  q/k/v share one dtype (bf16 or fp32).
@@ -159,7 +170,12 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
 
 
 class _DSQGV18GroupedFn(torch.autograd.Function):
-    """Autograd wrapper with the reference's 25 positional arguments (dsqg:2197-2203)."""
+    """Autograd wrapper with the reference's 25 positional arguments (dsqg:2197-2203).
+
+    The launches are the custom ops ``torch.ops.dwarf.dsqg_fwd`` / ``dsqg_bwd``
+    (registered in ``ops.py`` with fake implementations), so the Function traces
+    under ``torch.compile``; validation here uses shapes only.
+    """
 
     @staticmethod
     def forward(ctx, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
@@ -190,17 +206,12 @@ class _DSQGV18GroupedFn(torch.autograd.Function):
                                f"(built for head_dim={HEAD_DIM}, {R_PLANES} planes)")
         if int(j_small) + int(j_large) != int(j_val):
             raise ValueError(f"j_val={j_val} != j_small={j_small} + j_large={j_large}")
-        q, k, v = _kernel_rows(q), _kernel_rows(k.to(q.dtype)), _kernel_rows(v.to(q.dtype))
-        pos_bias = pos_bias.float().contiguous()
-        scale_embed = scale_embed.float().contiguous()
-        phase_base = phase_base.float().contiguous()
-        phase_gain = phase_gain.float().contiguous()
-        y_pre, z_pre = _planes(y_pre.float()), _planes(z_pre.float())
-        offsets = _device_offsets(offsets_dev, q.device, int(j_val))
-        out, lse = dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets,
-                                int(j_small), int(j_large), int(plane_shift), query_start)
+        if offsets_dev.numel() != int(j_val):
+            raise ValueError(f"offsets_dev has {offsets_dev.numel()} entries, expected j_val={j_val}")
+        out, lse = torch.ops.dwarf.dsqg_fwd(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
+                                            offsets_dev, int(j_small), int(j_large), int(plane_shift), query_start)
         ctx.save_for_backward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
-                              out, lse, offsets)
+                              out, lse, offsets_dev)
         ctx.j_small, ctx.j_large = int(j_small), int(j_large)
         ctx.plane_shift, ctx.query_start = int(plane_shift), query_start
         return out
@@ -209,9 +220,13 @@ class _DSQGV18GroupedFn(torch.autograd.Function):
     def backward(ctx, dout):
         (q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
          out, lse, offsets) = ctx.saved_tensors
-        grads = dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
-                              offsets, out, lse, ctx.j_small, ctx.j_large, ctx.plane_shift, ctx.query_start)
-        return grads + (None,) * 16
+        grads = torch.ops.dwarf.dsqg_bwd(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre,
+                                         z_pre, offsets, out, lse, ctx.j_small, ctx.j_large, ctx.plane_shift,
+                                         ctx.query_start)
+        dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz = grads
+        return (dq, dk.to(k.dtype), dv.to(v.dtype), dpb.to(pos_bias.dtype), dse.to(scale_embed.dtype),
+                dpbase.to(phase_base.dtype), dpgain.to(phase_gain.dtype), dy.to(y_pre.dtype),
+                dz.to(z_pre.dtype)) + (None,) * 16
 
 
 def dsqg_attention_v18_grouped(

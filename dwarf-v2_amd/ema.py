@@ -49,6 +49,15 @@ def _btd(t: torch.Tensor) -> torch.Tensor:
     return t if _btd_ok(t) else t.contiguous()
 
 
+def normalize_x(x: torch.Tensor) -> torch.Tensor:
+    """[B,N,D] rows the kernels read: unit channel stride, 8/16-byte vectors when D % 4 == 0."""
+    return _btd(x)
+
+
+def normalize_alpha(alpha: torch.Tensor, device: torch.device) -> torch.Tensor:
+    return alpha.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+
+
 def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: float) -> torch.Tensor:
     """Raw launch: y with x's dtype.  alpha fp32 on x's device, numel 1 or D."""
     lib = _lib.load()
@@ -95,13 +104,13 @@ def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool):
 
 
 class _CausalEMAFn(torch.autograd.Function):
-    """Autograd wrapper (reference: ema:263-364)."""
+    """Autograd wrapper (reference: ema:263-364) over the custom ops ``torch.ops.dwarf.ema_fwd`` /
+    ``ema_bwd`` (registered in ``ops.py``)."""
 
     @staticmethod
     def forward(ctx, x, alpha_input, floor, ceiling):
-        x = _btd(x)
-        alpha = alpha_input.detach().to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
-        y = ema_forward(x, alpha, floor, ceiling)
+        alpha = alpha_input.detach().to(device=x.device, dtype=torch.float32).reshape(-1)
+        y = torch.ops.dwarf.ema_fwd(x, alpha, float(floor), float(ceiling))
         ctx.save_for_backward(x, y, alpha)
         ctx.floor, ctx.ceiling = float(floor), float(ceiling)
         ctx.alpha_shape, ctx.alpha_dtype = alpha_input.shape, alpha_input.dtype
@@ -110,9 +119,8 @@ class _CausalEMAFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x, y, alpha = ctx.saved_tensors
-        need = bool(ctx.needs_input_grad[1])
-        dx, dalpha = ema_backward(x, y, dy, alpha, ctx.floor, ctx.ceiling, need)
-        if not need:
+        dx, dalpha = torch.ops.dwarf.ema_bwd(x, y, dy, alpha, ctx.floor, ctx.ceiling)
+        if not ctx.needs_input_grad[1]:
             return dx, None, None, None
         return dx, dalpha.reshape(ctx.alpha_shape).to(ctx.alpha_dtype), None, None
 

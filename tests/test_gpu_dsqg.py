@@ -170,3 +170,26 @@ def test_training_shape_properties(pkg, device):
         sl["phase_gain"] = x["phase_gain"][:, h:h + 1]
         ref = dsqg_ref.dsqg_forward(*(sl[n].double() for n in NAMES), offsets, 17, query_start=1, round_se=True)
         assert max_abs(out[b:b + 1, h:h + 1], ref) < BF16_ABS
+
+
+def test_torch_compile_traces_without_graph_breaks(pkg, device):
+    """fullgraph compile (dynamo + AOTAutograd on the fake implementations) runs the same kernels."""
+    offsets = lattice(pkg)
+    x = make_inputs(1, 4, 2, 192, offsets, 17, seed=61, dtype=torch.bfloat16, plane_shift=3)
+    dout = torch.randn(1, 4, 192, 64, generator=torch.Generator().manual_seed(62)).to(torch.bfloat16).to(device)
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+
+    def step(*ts):
+        out = pkg.dsqg_attention_v18_grouped(*ts, 96, 17, 79, off, None, None, None, None, None, 3, 0, False, 0,
+                                             3, 1)
+        return (out.float() * dout.float()).sum()
+
+    results = []
+    for fn in (step, torch.compile(step, backend="aot_eager", fullgraph=True)):
+        xd = {n: t.to(device).requires_grad_(True) for n, t in x.items()}
+        loss = fn(*(xd[n] for n in NAMES))
+        loss.backward()
+        torch.cuda.synchronize()
+        results.append([loss.detach()] + [xd[n].grad for n in NAMES])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)

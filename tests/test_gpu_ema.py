@@ -68,3 +68,23 @@ def test_clamped_alpha_and_projection(pkg, device):
     assert rel_err(y, ry) < 1e-5
     _, rda = ema_ref.ema_adjoint(x.double(), ry, dy.double(), torch.tensor([0.7], dtype=torch.float64))
     assert (float(da) == 0.0) == (float(rda) == 0.0)
+
+
+def test_torch_compile_traces_without_graph_breaks(pkg, device):
+    x = torch.randn(2, 96, 64, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    raw = torch.randn(64, generator=torch.Generator().manual_seed(6))
+
+    def step(xx, rr):
+        y = pkg.causal_ema_scan(xx, pkg.bounded_ema_factor(rr))
+        return (y.float() ** 2).sum()
+
+    results = []
+    for fn in (step, torch.compile(step, backend="aot_eager", fullgraph=True)):
+        xx = x.to(device).requires_grad_(True)
+        rr = raw.to(device).requires_grad_(True)
+        loss = fn(xx, rr)
+        loss.backward()
+        torch.cuda.synchronize()
+        results.append((loss.detach(), xx.grad, rr.grad))
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
