@@ -218,7 +218,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
 
   const int work = xcd_remap(blockIdx.x, total);
   const int bh = work / tiles;
-  const int tile = work - bh * tiles;
+  // late query tiles (more valid offsets) of each (b, h) are dispatched first
+  const int tile = tiles - 1 - (work - bh * tiles);
   const int b = bh / a.H;
   const int h = bh - b * a.H;
   const int hk = h / (a.H / a.H_kv);
