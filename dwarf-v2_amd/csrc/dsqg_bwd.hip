@@ -170,6 +170,7 @@ __global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_kernel(const dwarf_dsqg_
 constexpr int kKPW = 16;       // keys per wave
 constexpr int kKPB = 64;       // keys per workgroup
 constexpr int kChunkKv = 1;    // offsets per prefetch chunk
+constexpr int kMinWgKv = 3;    // workgroups per CU the register budget is sized for
 constexpr int kERowKv = 72;    // bf16 E row stride (elements)
 
 struct KvLayout {
@@ -198,8 +199,8 @@ struct KvChunk {
   int j[CJ];
 };
 
-template <int SHIFT, int CJ>
-__global__ __launch_bounds__(kBlock, 3) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
+template <int SHIFT, int CJ, int MINWG>
+__global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
                                                                    const float* __restrict__ delta_ws, int tiles,
                                                                    int total) {
   constexpr float kC = 0.125f * kLog2e;
@@ -295,6 +296,8 @@ __global__ __launch_bounds__(kBlock, 3) void dsqg_bwd_dkdv_bf16_k4(const dwarf_d
   const int qs_b = static_cast<int>(f.q_stride[2]) * 2, ds_b = static_cast<int>(a.dout_stride[2]) * 2;
   const int ls_b = static_cast<int>(f.lse_stride[2]) * 4, ys_b = static_cast<int>(f.y_stride[2]) * 4;
   const int qstart = f.query_start;
+  const int qb_lane = m_eff * qs_b + 32 * g, db_lane = m_eff * ds_b + 32 * g;
+  const int lb_lane = m_eff * ls_b, yb_lane = m_eff * ys_b + 4 * g;
 
   for (int hh = 0; hh < group; ++hh) {
     const int h = hk * group + hh;
@@ -317,15 +320,16 @@ __global__ __launch_bounds__(kBlock, 3) void dsqg_bwd_dkdv_bf16_k4(const dwarf_d
         const int n = m_eff + d;
         c.j[jj] = j;
         c.ok[jj] = n >= qstart && n < N;
-        const uint32_t qo = static_cast<uint32_t>(n * qs_b + 32 * g);
-        const uint32_t dof = static_cast<uint32_t>(n * ds_b + 32 * g);
+        // lane bases plus wave-uniform products (no per-lane multiplies)
+        const uint32_t qo = static_cast<uint32_t>(qb_lane + d * qs_b);
+        const uint32_t dof = static_cast<uint32_t>(db_lane + d * ds_b);
         c.q[jj][0] = buf_load16(rq, qo);
         c.q[jj][1] = buf_load16(rq, qo + 16);
         c.d[jj][0] = buf_load16(rd, dof);
         c.d[jj][1] = buf_load16(rd, dof + 16);
-        c.lse[jj] = buf_load_f32(rl, static_cast<uint32_t>(n * ls_b));
-        c.dl[jj] = buf_load_f32(rdl, static_cast<uint32_t>(n * 4));
-        c.y[jj] = buf_load_f32(ry, (j >= J_small && j < J) ? static_cast<uint32_t>(n * ys_b + 4 * g) : kOutOfRange);
+        c.lse[jj] = buf_load_f32(rl, static_cast<uint32_t>(lb_lane + d * ls_b));
+        c.dl[jj] = buf_load_f32(rdl, static_cast<uint32_t>(4 * n));
+        c.y[jj] = buf_load_f32(ry, (j >= J_small && j < J) ? static_cast<uint32_t>(yb_lane + d * ys_b) : kOutOfRange);
       }
     };
 
@@ -368,6 +372,10 @@ __global__ __launch_bounds__(kBlock, 3) void dsqg_bwd_dkdv_bf16_k4(const dwarf_d
           dv[2 * i] = fmaf(P, bf16_lo(dw[i]), dv[2 * i]);
           dv[2 * i + 1] = fmaf(P, bf16_hi(dw[i]), dv[2 * i + 1]);
         }
+        // keep the accumulation here: sunk to the loop latch it holds every
+        // chunk's q/dO registers live and the prefetch turns into register copies
+        pin_regs<16>(dk);
+        pin_regs<16>(dv);
         if (far) {
           // dV gets R^T dO on the rotated pair; dZ gets d(theta) * gain * y
           dv[SHIFT] = fmaf(P, (cs - 1.f) * da + sn * db, dv[SHIFT]);
@@ -375,6 +383,7 @@ __global__ __launch_bounds__(kBlock, 3) void dsqg_bwd_dkdv_bf16_k4(const dwarf_d
           const float tq = P * (da * (-va * sn - vb * cs) + db * (va * cs - vb * sn));
           dz = fmaf(tq * pg, c.y[jj], dz);
         }
+        pin_regs<1>(&dz);
       }
     };
 
@@ -419,7 +428,10 @@ hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace&
   if (total == 0) return hipSuccess;
   const size_t lds = kv_layout(f.J, f.J_large, f.H / f.H_kv, kChunkKv).bytes;
 #define DWARF_KV4_CASE(S) \
-  case S: hipLaunchKernelGGL((dsqg_bwd_dkdv_bf16_k4<S, kChunkKv>), dim3(total), dim3(kBlock), lds, stream, a, delta, tiles, total); break;
+  case S:                                                                                                     \
+    hipLaunchKernelGGL((dsqg_bwd_dkdv_bf16_k4<S, kChunkKv, kMinWgKv>), dim3(total), dim3(kBlock), lds, stream, a, \
+                       delta, tiles, total);                                                                  \
+    break;
   switch (f.plane_shift) {
     DWARF_KV4_CASE(0) DWARF_KV4_CASE(1) DWARF_KV4_CASE(2) DWARF_KV4_CASE(3) DWARF_KV4_CASE(4)
     DWARF_KV4_CASE(5) DWARF_KV4_CASE(6) DWARF_KV4_CASE(7) DWARF_KV4_CASE(8) DWARF_KV4_CASE(9)

@@ -772,9 +772,13 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
           dq[2 * i] = fmaf(cds, bf16_lo(kw[i]), dq[2 * i]);
           dq[2 * i + 1] = fmaf(cds, bf16_hi(kw[i]), dq[2 * i + 1]);
         }
+        // keep the accumulation here: sunk to the loop latch it holds every
+        // chunk's K registers live and the prefetch turns into register copies
+        pin_regs<16>(dq);
         if (g == 0) s_ds[j * kDsRowT + kQPW * w + qi] = dS;
         const float tq = P * tq_pre;
         dy = fmaf(tq * pg, c.z[jj], dy);
+        pin_regs<1>(&dy);
         ph_sum[jj][0] = tq;
         ph_sum[jj][1] = tq * yg * c.z[jj];
       }

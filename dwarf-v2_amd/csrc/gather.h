@@ -16,6 +16,14 @@ __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
+// Zero-instruction barrier on register values: the computations that produce
+// them stay before this point (the compiler may not sink them into a later block).
+template <int CNT>
+__device__ __forceinline__ void pin_regs(float* v) {
+#pragma unroll
+  for (int i = 0; i < CNT; ++i) asm volatile("" : "+v"(v[i]));
+}
+
 __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return uint4{v[0], v[1], v[2], v[3]};
@@ -63,14 +71,24 @@ __device__ __forceinline__ int build_offset_list(int2* list, const int* s_off, i
   return cnt;
 }
 
+// x + x of lane ^ 16 (v_permlane16_swap on copies of x: rows 0/2 receive
+// rows 1/3 and the reverse) and x + x of lane ^ 32 (v_permlane32_swap, the
+// two halves).  Both stay in the VALU, without an LDS round trip.
+__device__ __forceinline__ float add_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sum over the 16 lanes of a wave that share (lane & 3): four queries of a
 // 16-lane row by DPP rotation, then across the four rows.
 __device__ __forceinline__ float sum_over_queries16(float x) {
   x += dpp_f<0x124>(x);  // row_ror:4
   x += dpp_f<0x128>(x);  // row_ror:8
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  return add_xor32(add_xor16(x));
 }
 
 }  // namespace dwarf
