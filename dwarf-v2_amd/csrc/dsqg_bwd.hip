@@ -473,6 +473,8 @@ __global__ __launch_bounds__(kBlock) void dsqg_bwd_reduce1(RedPlan p) {
   const int r1 = min(A.rows, r0 + kRedRows);
   const float* src = A.in + (static_cast<int64_t>(seg) * A.rows + r0) * A.cols + col;
   float sum = 0.f;
+  // the loads are independent; the adds keep row order
+#pragma unroll 16
   for (int r = r0; r < r1; ++r, src += A.cols) sum += *src;
   A.tmp[(static_cast<int64_t>(seg) * A.groups + grp) * A.cols + col] = sum;
 }
@@ -485,6 +487,7 @@ __global__ __launch_bounds__(kBlock) void dsqg_bwd_reduce2(RedPlan p, const dwar
   const int seg = idx / A.cols, col = idx - seg * A.cols;
   const float* src = A.tmp + static_cast<int64_t>(seg) * A.groups * A.cols + col;
   float sum = 0.f;
+#pragma unroll 8
   for (int gi = 0; gi < A.groups; ++gi, src += A.cols) sum += *src;
   const dwarf_dsqg_fwd_args& f = a.fwd;
   if (ai == 0) {
@@ -554,11 +557,15 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   const int total_tiles = w.dq_tiles * f.B * f.H;
   const int JL = f.J_large > 0 ? f.J_large : 1;
   if (f.dtype == DWARF_BF16) {
-    // Persistent workgroups, two per CU, all resident; each accumulates dSE in
-    // its own slot, dPB / dPhase partials are per tile (head-major rows).
+    // Persistent workgroups, all resident: the gather launch (dQ, dY, dS,
+    // dPhase partials per tile) and the dSE launch, whose workgroups
+    // accumulate dSE in their own slots (dPB partials per tile).
     w.dq_tpw = 0;
     w.dq_ntg = 0;
-    w.dq_wgs = total_tiles < 512 ? (total_tiles > 0 ? total_tiles : 1) : 512;
+    const int gather_max = 256 * dq_gather_wgs_per_cu();
+    w.dq_gather_wgs = total_tiles < gather_max ? total_tiles : gather_max;
+    const int dse_max = 256 * dq_dse_wgs_per_cu(f.J);
+    w.dq_wgs = total_tiles < dse_max ? (total_tiles > 0 ? total_tiles : 1) : dse_max;
     w.pb_rows = f.B * w.dq_tiles;
     w.ph_rows = f.B * w.dq_tiles;
   } else {
@@ -589,6 +596,9 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   w.part_ph_off = off;
   w.part_ph_bytes = static_cast<size_t>(f.H) * w.ph_rows * JL * 8 * sizeof(float);
   off += align256(w.part_ph_bytes);
+  w.ds_off = off;
+  w.ds_bytes = f.dtype == DWARF_BF16 ? static_cast<size_t>(f.B) * f.H * f.J * f.N * sizeof(float) : 0;
+  off += align256(w.ds_bytes);
   w.red_off = off;
   w.red_bytes = (static_cast<size_t>(w.red_groups_se) * f.J * kHeadDim +
                  static_cast<size_t>(f.H) * w.red_groups_pb * f.J +

@@ -510,51 +510,59 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_v2(const dwarf_dsqg_bwd
 // ---------------------------------------------------------------------------
 // bf16 dQ launch, four lanes per query (the forward's mapping).
 //
-// A persistent workgroup of 4 waves walks a sequence of 64-query tiles (the
-// order is described at the tile loop); wave w owns queries 16w..16w+15 of a tile and lane g of a query holds head
-// dims [16g, 16g+16).  Each wave walks its offset list (offsets that give one
-// of its queries a source row) in chunks of CJ with the next chunk's K/V/z
-// loads in flight; a lane without a source reads zeros (out-of-range buffer
-// offset) and gets P = 0.  Per pair the lanes form <q, k_s> + <q, e_j> and
-// <dO, v_s> with v_dot2_f32_bf16, the MOVT rotation of their one channel pair,
-// P, dS = P (g - delta) and dQ += c dS k_s, and write dS into the tile's
-// s_ds[j][q] matrix.  At the end of the tile, on MFMA (dS split into bf16
-// high and low parts):
-//   dQe^T = E^T dS^T   (added to dQ through an LDS transpose)
-//   dSE   = dS^T Q     (wave w: dims 16w..16w+15), dPB = dS^T 1 (wave 0)
-// dSE accumulates in the workgroup's slot, dPB goes to the tile's row.  dPhase
-// sums over the wave's 16 queries are reduced per chunk (DPP + lane shuffles)
-// into a per-wave LDS table whose four waves are added in a fixed order into
-// the tile's row, so every sum has a fixed order.
+// dsqg_bwd_dq_bf16_g4: a persistent workgroup of 4 waves walks a sequence of
+// 64-query tiles (the order is described at the tile loop); wave w owns
+// queries 16w..16w+15 of a tile and lane g of a query holds head dims
+// [16g, 16g+16).  Each wave walks its offset list (offsets that give one of
+// its queries a source row) in chunks of CJ with the next chunk's K/V/z loads
+// in flight; a lane without a source reads zeros (out-of-range buffer offset)
+// and gets P = 0.  Per pair the lanes form <q, k_s> + <q, e_j> and <dO, v_s>
+// with v_dot2_f32_bf16, the MOVT rotation of their one channel pair, P,
+// dS = P (g - delta) and dQ += c dS k_s.  dS goes to the workspace matrix
+// dS[b, h][j][n] (16 consecutive queries: one 64-byte store), and every four
+// offsets one v_mfma_f32_16x16x4_f32 per 16 head dims adds their
+// dS (16 queries x 4 offsets) times E (4 rows x 16 dims) into the wave's dQe
+// accumulator, which joins dQ through a wave-local LDS transpose at the end of
+// the tile.  dPhase sums over the wave's 16 queries are reduced per offset
+// (DPP + permlane swaps) into a per-wave LDS table whose four waves are added
+// in a fixed order into the tile's row.
+//
+// dsqg_bwd_dse_bf16: dSE = dS^T Q and dPB = dS^T 1 from the dS matrix, on
+// v_mfma_f32_16x16x32_bf16 with dS split into bf16 high and low parts (~2^-17
+// relative); a persistent workgroup accumulates dSE over its tiles in its own
+// slot (wave w: dims 16w..16w+15), dPB goes to the tile's row.  Entries of the
+// dS matrix that no wave wrote (offsets with no source for any query of a
+// wave) are exactly those with n < offset_j and are masked.  Every sum has a
+// fixed order.
 // ---------------------------------------------------------------------------
 constexpr int kQT = 64;           // queries per tile
 constexpr int kQPW = 16;          // queries per wave
-constexpr int kChunkDq = 2;       // offsets per prefetch chunk (the launch's choice)
-constexpr int kDsRowT = 68;       // s_ds[j][q] row (floats)
+constexpr int kStepDq = 4;        // offsets per loop step (one dQe MFMA step); one in flight ahead
 constexpr int kERowT = 72;        // bf16 E row stride (elements)
+constexpr int kStRow = 36;        // dQe staging row (half a head row + padding), floats
+constexpr int kGatherWgsPerCu = 3;
+// dSE launch: 16-row dS blocks per wave (JE / 16 dealt to 4 waves) and the
+// resident workgroups per CU its registers allow
+__host__ __device__ constexpr int dse_blocks_per_wave(int J) { return (J + 1 + 15) / 16 <= 8 ? 2 : 5; }
+__host__ __device__ constexpr int dse_wgs_per_cu(int mbw) { return mbw <= 2 ? 4 : 2; }
 
-struct DqT4Layout {
-  int JE, JK, jt, JL4, list_len;
-  size_t off_ph, off_list, off_dph, off_e, off_et, off_ds, bytes;
+struct DqG4Layout {
+  int JE, JL4, list_len;
+  size_t off_ph, off_list, off_dph, off_e, off_st, bytes;
 };
 
-// JE >= J + 1 keeps a sentinel row J; the MFMA reduction over j runs to JK
-// (a multiple of 32) and reads zeros for rows JE..JK-1 instead of storing them.
-__host__ __device__ inline DqT4Layout dq_t4_layout(int J, int J_large, int CJ) {
-  DqT4Layout L;
+// JE >= J + 1 keeps a sentinel row J of zeros in the E table.
+__host__ __device__ inline DqG4Layout dq_g4_layout(int J, int J_large) {
+  DqG4Layout L;
   L.JE = (J + 1 + 15) / 16 * 16;
-  L.JK = (L.JE + 31) / 32 * 32;
-  L.jt = L.JE + 8;
   L.JL4 = (J_large + 1) / 2 * 2;
-  L.list_len = (L.JE + 4 * CJ + 1) / 2 * 2;
+  L.list_len = (L.JE + 2 * kStepDq + 1) / 2 * 2;   // list + padding for the last step and its prefetch
   L.off_ph = static_cast<size_t>(2 * L.JE) * 4;                       // s_pb2[JE], s_off[JE]
   L.off_list = L.off_ph + static_cast<size_t>(L.JL4) * 4 * 8;         // s_ph[JL4][4] float2
   L.off_dph = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;   // s_list[4][list_len] int2
   L.off_e = L.off_dph + static_cast<size_t>(4 * L.JL4) * 8 * 4;       // s_dph[4][JL4][8]
-  L.off_et = L.off_e + static_cast<size_t>(L.JE) * kERowT * 2;        // sE[JE][72] bf16
-  L.off_ds = L.off_et + static_cast<size_t>(kHeadDim) * L.jt * 2;     // sEt[64][jt] bf16
-  const int ds_rows = L.JE > kQT ? L.JE : kQT;                       // the dQe staging needs 4 x 16 rows
-  L.bytes = L.off_ds + static_cast<size_t>(ds_rows) * kDsRowT * 4;    // s_ds[JE][68] (also dQe staging)
+  L.off_st = L.off_e + static_cast<size_t>(L.JE) * kERowT * 2;        // sE[JE][72] bf16
+  L.bytes = L.off_st + static_cast<size_t>(4 * kQPW * kStRow) * 4;    // dQe staging [4][16][36]
   return L;
 }
 
@@ -566,16 +574,42 @@ struct DqChunk {
   int j[CJ];
 };
 
-template <int SHIFT, int CJ, int MB>
-__global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsqg_bwd_args a, float* __restrict__ delta_ws,
-                                                                 float* __restrict__ part_se, float* __restrict__ part_pb,
-                                                                 float* __restrict__ part_ph, int tiles) {
+// Tile order of the persistent dQ launches.  Workgroups are dealt round-robin
+// over the 8 XCDs; XCD x owns a contiguous range of the (b, h)-major tiles and
+// its U workgroups take them in steps of U consecutive tiles (a few (b, h) at
+// a time, so the K/V rows they gather stay in that XCD's L2).  Within a step
+// the tiles are rotated by 7 per step, so each workgroup sees early (few
+// valid offsets) and late positions of the sequence alike.
+struct TileOrder {
+  int Ux, u, T0, T1;
+  __device__ TileOrder(int64_t total_tiles) {
+    const int W = gridDim.x;
+    const int x = blockIdx.x % kXcds;
+    u = blockIdx.x / kXcds;
+    Ux = (W - x + kXcds - 1) / kXcds;
+    int cum_x = 0;
+    for (int y = 0; y < x; ++y) cum_x += (W - y + kXcds - 1) / kXcds;
+    T0 = static_cast<int>(total_tiles * cum_x / W);
+    T1 = static_cast<int>(total_tiles * (cum_x + Ux) / W);
+  }
+  __device__ int steps() const { return (T1 - T0 + Ux - 1) / Ux; }
+  __device__ int tile(int kstep) const {   // -1: none this step
+    const int Lt = kstep * Ux + (u + 7 * kstep) % Ux;
+    return Lt < T1 - T0 ? T0 + Lt : -1;
+  }
+};
+
+template <int SHIFT>
+__global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
+    const dwarf_dsqg_bwd_args a, float* __restrict__ delta_ws, float* __restrict__ ds_ws, float* __restrict__ part_ph,
+    int tiles) {
   constexpr float kC = 0.125f * kLog2e;
   constexpr float kScale = 0.125f;
   static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
+  constexpr int CJ = 1;   // offsets per prefetch chunk
   const dwarf_dsqg_fwd_args& f = a.fwd;
   const int J = f.J, N = f.N, J_small = f.J_small, JL = f.J_large;
-  const DqT4Layout lay = dq_t4_layout(J, JL, CJ);
+  const DqG4Layout lay = dq_g4_layout(J, JL);
   extern __shared__ float smem[];
   char* sm = reinterpret_cast<char*>(smem);
   float* s_pb2 = smem;                                        // log2(e) * pb_j of the tile's head
@@ -584,8 +618,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
   int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
   float* s_dph_all = reinterpret_cast<float*>(sm + lay.off_dph);
   uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
-  uint16_t* sEt = reinterpret_cast<uint16_t*>(sm + lay.off_et);
-  float* s_ds = reinterpret_cast<float*>(sm + lay.off_ds);
+  float* s_st_all = reinterpret_cast<float*>(sm + lay.off_st);
 
   for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
     const int j = i / kHeadDim, d = i - j * kHeadDim;
@@ -594,9 +627,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
       e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
       if (f.se_round_bf16) e = round_bf16(e);
     }
-    const uint16_t bits = f32_to_bf16_bits(e);
-    sE[j * kERowT + d] = bits;
-    sEt[d * lay.jt + j] = bits;
+    sE[j * kERowT + d] = f32_to_bf16_bits(e);
   }
   for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
 
@@ -608,34 +639,15 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
   const int lr = l & 15, lc = l >> 4;
   int2* s_list = s_list_all + w * lay.list_len;
   float* s_dph = s_dph_all + w * lay.JL4 * 8;
+  float* s_st = s_st_all + w * kQPW * kStRow;
   const int ks_b = static_cast<int>(f.k_stride[2]) * 2, vs_b = static_cast<int>(f.v_stride[2]) * 2;
-  const int zs_b = static_cast<int>(f.z_stride[2]) * 4, qs_b = static_cast<int>(f.q_stride[2]) * 2;
+  const int zs_b = static_cast<int>(f.z_stride[2]) * 4;
 
-  // Tile order.  Workgroups are dealt round-robin over the 8 XCDs; XCD x owns
-  // a contiguous range of the (b, h)-major tiles and its U workgroups take
-  // them in steps of U consecutive tiles (about two (b, h) at a time, so the
-  // K/V rows they gather stay in that XCD's L2).  Within a step the tiles are
-  // rotated by 7 per step, so each workgroup sees early (few valid offsets)
-  // and late positions of the sequence alike.
-  const int W = gridDim.x;
-  const int x = blockIdx.x % kXcds, u = blockIdx.x / kXcds;
-  const int Ux = (W - x + kXcds - 1) / kXcds;
-  int cum_x = 0;
-  for (int y = 0; y < x; ++y) cum_x += (W - y + kXcds - 1) / kXcds;
-  const int64_t total_tiles = static_cast<int64_t>(tiles) * f.B * f.H;
-  const int T0 = static_cast<int>(total_tiles * cum_x / W);
-  const int T1 = static_cast<int>(total_tiles * (cum_x + Ux) / W);
-  const int slot = blockIdx.x;
+  const TileOrder order(static_cast<int64_t>(tiles) * f.B * f.H);
   int cur_h = -1;
-  // dSE[16 mb + 4 lc + r][16 w + lr] of this workgroup, over all its tiles (MB >= JE / 16)
-  f32x4 dse[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) dse[mb] = zero4();
-
-  for (int kstep = 0; kstep * Ux < T1 - T0; ++kstep) {
-    const int Lt = kstep * Ux + (u + 7 * kstep) % Ux;
-    if (Lt >= T1 - T0) continue;
-    const int T = T0 + Lt;
+  for (int kstep = 0; kstep < order.steps(); ++kstep) {
+    const int T = order.tile(kstep);
+    if (T < 0) continue;   // uniform over the workgroup
     const int bh = T / tiles;
     const int t = T - bh * tiles;
     const int b = bh / f.H;
@@ -650,10 +662,9 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
     const __amdgpu_buffer_rsrc_t rv =
         rows_rsrc(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1], vs_b, N, 128);
     const __amdgpu_buffer_rsrc_t rz = rows_rsrc(f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1], zs_b, N, 16);
-    const __amdgpu_buffer_rsrc_t rq = rows_rsrc(qb, qs_b, N, 128);
+    float* ds_bh = ds_ws + static_cast<int64_t>(bh) * J * N;
 
-    const int n0 = t * kQT;
-    const int n0w = n0 + kQPW * w;
+    const int n0w = t * kQT + kQPW * w;
     const int n = n0w + qi;
     const int n_hi = min(n0w + kQPW - 1, N - 1);
     const bool row_ok = n < N;
@@ -690,8 +701,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
     const int vb_lane = n_eff * vs_b + 32 * g;
     const int zb_lane = n_eff * zs_b + 4 * g;
 
-    __syncthreads();   // the previous tile's dQe staging and partial reads are done
-    for (int i = lane; i < lay.JE * kQT; i += kBlock) s_ds[(i / kQT) * kDsRowT + (i % kQT)] = 0.f;
+    __syncthreads();   // the previous tile's dPhase tables have been read
     for (int i = lane; i < 4 * lay.JL4 * 8; i += kBlock) s_dph_all[i] = 0.f;
     if (h != cur_h) {
       cur_h = h;
@@ -704,14 +714,17 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
       }
     }
     int cnt = 0;
-    if (n0w < N) cnt = build_offset_list<CJ>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
-    const int cntp = (cnt + CJ - 1) / CJ * CJ;
-    __syncthreads();   // s_ds cleared
+    // padded with the sentinel to a multiple of 4 plus 4: every step's reads and the next prefetch
+    if (n0w < N) cnt = build_offset_list<kStepDq / 2>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
+    __syncthreads();   // tables staged, dPhase tables cleared
 
     float dq[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) dq[i] = 0.f;
     float dy = 0.f;
+    f32x4 dqe[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) dqe[nb] = zero4();
 
     auto fetch = [&](int k0, DqChunk<SHIFT, CJ>& c) {
 #pragma unroll
@@ -731,7 +744,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
       }
     };
 
-    auto consume = [&](const DqChunk<SHIFT, CJ>& c) {
+    // per pair of the chunk: returns dS in ds_out[jj]
+    auto consume = [&](const DqChunk<SHIFT, CJ>& c, float* ds_out) {
       float ph_sum[CJ][2];
 #pragma unroll
       for (int jj = 0; jj < CJ; ++jj) {
@@ -775,7 +789,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
         // keep the accumulation here: sunk to the loop latch it holds every
         // chunk's K registers live and the prefetch turns into register copies
         pin_regs<16>(dq);
-        if (g == 0) s_ds[j * kDsRowT + kQPW * w + qi] = dS;
+        if (g == 0 && row_ok && j < J) ds_bh[static_cast<int64_t>(j) * N + n] = dS;
+        ds_out[jj] = dS;
         const float tq = P * tq_pre;
         dy = fmaf(tq * pg, c.z[jj], dy);
         pin_regs<1>(&dy);
@@ -797,97 +812,68 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
       }
     };
 
+    // dQe += dS (16 queries x the step's 4 offsets) E (4 rows x 64 dims):
+    // lane (lr, lc) supplies dS of query lr at offset lc (from the lane of
+    // query lr with g = lc) and E[j_lc][16 nb + lr].
+    auto dqe_step = [&](const float* ds4, const int* j4) {
+      const float sel = g == 0 ? ds4[0] : g == 1 ? ds4[1] : g == 2 ? ds4[2] : ds4[3];
+      const float av = __shfl(sel, 4 * lr + lc);
+      const int jsel = lc == 0 ? j4[0] : lc == 1 ? j4[1] : lc == 2 ? j4[2] : j4[3];
+      const uint16_t* er = sE + jsel * kERowT + lr;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        dqe[nb] = mfma16_f32(av, __uint_as_float(static_cast<uint32_t>(er[16 * nb]) << 16), dqe[nb]);
+    };
+
     if (cnt > 0) {
       DqChunk<SHIFT, CJ> c0, c1;
       fetch(0, c0);
-      for (int k0 = 0; k0 < cntp; k0 += 2 * CJ) {
-        fetch(k0 + CJ, c1);
-        consume(c0);
-        fetch(k0 + 2 * CJ, c0);
-        consume(c1);
+      for (int k0 = 0; k0 < cnt; k0 += kStepDq) {
+        float ds4[kStepDq];
+        int j4[kStepDq];
+        j4[0] = c0.j[0];
+        fetch(k0 + 1, c1);
+        consume(c0, ds4);
+        j4[1] = c1.j[0];
+        fetch(k0 + 2, c0);
+        consume(c1, ds4 + 1);
+        j4[2] = c0.j[0];
+        fetch(k0 + 3, c1);
+        consume(c0, ds4 + 2);
+        j4[3] = c1.j[0];
+        fetch(k0 + 4, c0);
+        consume(c1, ds4 + 3);
+        dqe_step(ds4, j4);
       }
     }
-    __syncthreads();   // the tile's dS matrix is complete
-
-    // ---- dQe^T = E^T dS^T for the wave's 16 queries (C^T[d][q]) ----------------
-    f32x4 dqe[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) dqe[nb] = zero4();
-    for (int ks = 0; ks < lay.JK / 32; ++ks) {
-      const int jb = 32 * ks + 8 * lc;   // rows jb..jb+7 exist iff jb < JE (JE is a multiple of 16)
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = jb < lay.JE ? s_ds[(jb + e) * kDsRowT + kQPW * w + lr] : 0.f;
-      bf16x8 bhi, blo;
-      split_bf16x8(x, bhi, blo);
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        uint4 xe = {0u, 0u, 0u, 0u};
-        if (jb < lay.JE) xe = *reinterpret_cast<const uint4*>(sEt + (16 * nb + lr) * lay.jt + jb);
-        const bf16x8 ae = bf16x8_from_bits(xe);
-        dqe[nb] = mfma16_bf16(ae, bhi, dqe[nb]);
-        dqe[nb] = mfma16_bf16(ae, blo, dqe[nb]);
-      }
-    }
-    // ---- dSE[j][16w + lr] += c sum_q dS[q][j] q[q][16w + lr]; dPB (wave 0) -------
-    {
-      bf16x8 bq[2], one;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int nq = n0 + 32 * ks + 8 * lc + e;
-          const uint32_t off = nq < N ? static_cast<uint32_t>(nq * qs_b + 2 * (16 * w + lr)) : kOutOfRange;
-          bq[ks][e] = __builtin_bit_cast(__bf16, buf_load_u16(rq, off));
-        }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) one[e] = static_cast<__bf16>(lr == 0 ? 1.f : 0.f);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        if (16 * mb >= lay.JE) break;
-        f32x4 c1 = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const float4* src = reinterpret_cast<const float4*>(s_ds + (16 * mb + lr) * kDsRowT + 32 * ks + 8 * lc);
-          const float4 x0 = src[0], x1 = src[1];
-          const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-          bf16x8 ahi, alo;
-          split_bf16x8(x, ahi, alo);
-          dse[mb] = mfma16_bf16(ahi, bq[ks], dse[mb]);
-          dse[mb] = mfma16_bf16(alo, bq[ks], dse[mb]);
-          if (w == 0) {
-            c1 = mfma16_bf16(ahi, one, c1);
-            c1 = mfma16_bf16(alo, one, c1);
-          }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * mb + 4 * lc + r;
-          if (w == 0 && lr == 0 && j < J) part_pb[prow * J + j] = c1[r];
-        }
-      }
-    }
+    __syncthreads();   // every wave's dPhase table is complete
     // dPhase of this tile: the four waves' sums in a fixed order
     for (int i = lane; i < JL * 8; i += kBlock)
       part_ph[prow * JL * 8 + i] = ((s_dph_all[i] + s_dph_all[lay.JL4 * 8 + i]) + s_dph_all[2 * lay.JL4 * 8 + i]) +
                                    s_dph_all[3 * lay.JL4 * 8 + i];
-    __syncthreads();   // every wave is done reading s_ds; it now stages dQe
-    float* stage = s_ds + w * kQPW * kDsRowT;   // [16 q][68]
+    // dQe rows move from the MFMA layout (query 4 lc + r, dim 16 nb + lr) to
+    // the lane layout through the wave's staging area, half a row at a time
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int half = 0; half < 2; ++half) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) stage[lr * kDsRowT + 16 * nb + 4 * lc + r] = dqe[nb][r];
-    __builtin_amdgcn_wave_barrier();
-    if (row_ok) {
-      const float4* src = reinterpret_cast<const float4*>(stage + qi * kDsRowT + 16 * g);
+      for (int nb = 2 * half; nb < 2 * half + 2; ++nb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 x = src[i];
-        dq[4 * i] = fmaf(kScale, x.x, dq[4 * i]);
-        dq[4 * i + 1] = fmaf(kScale, x.y, dq[4 * i + 1]);
-        dq[4 * i + 2] = fmaf(kScale, x.z, dq[4 * i + 2]);
-        dq[4 * i + 3] = fmaf(kScale, x.w, dq[4 * i + 3]);
+        for (int r = 0; r < 4; ++r) s_st[(4 * lc + r) * kStRow + 16 * (nb - 2 * half) + lr] = dqe[nb][r];
+      __builtin_amdgcn_wave_barrier();
+      if ((g >> 1) == half) {
+        const float4* src = reinterpret_cast<const float4*>(s_st + qi * kStRow + 16 * (g - 2 * half));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 x = src[i];
+          dq[4 * i] = fmaf(kScale, x.x, dq[4 * i]);
+          dq[4 * i + 1] = fmaf(kScale, x.y, dq[4 * i + 1]);
+          dq[4 * i + 2] = fmaf(kScale, x.z, dq[4 * i + 2]);
+          dq[4 * i + 3] = fmaf(kScale, x.w, dq[4 * i + 3]);
+        }
       }
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (row_ok) {
       uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dq) + b * a.dq_stride[0] + h * a.dq_stride[1] +
                                            nn * a.dq_stride[2] + 16 * g);
       uint4 x0, x1;
@@ -900,38 +886,159 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_bwd_dq_bf16_t4(const dwarf_dsq
       a.dy_pre[(static_cast<int64_t>(bh) * N + n) * kPlanes + g] = dy;
     }
   }
-  // the workgroup's dSE slot (zeros if it had no tile)
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = 16 * mb + 4 * lc + r;
-      if (j < J) part_se[(static_cast<int64_t>(slot) * J + j) * kHeadDim + 16 * w + lr] = kScale * dse[mb][r];
-    }
 }
 
-template <int CJ, int MB>
-hipError_t launch_dq_bf16_t4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+template <int MBW>
+__global__ __launch_bounds__(kBlock, dse_wgs_per_cu(MBW)) void dsqg_bwd_dse_bf16(const dwarf_dsqg_bwd_args a,
+                                                               const float* __restrict__ ds_ws,
+                                                               float* __restrict__ part_se,
+                                                               float* __restrict__ part_pb, int tiles) {
+  constexpr int kQRow = 72;   // bf16 row stride of the staged Q tile
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  const int J = f.J, N = f.N;
+  const int JB = (J + 1 + 15) / 16;   // 16-row blocks of dS; wave w takes blocks w, w + 4, ...
+  __shared__ int s_off[64 * MBW];
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[kQT * kQRow];
+  for (int j = threadIdx.x; j < 64 * MBW; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int lr = l & 15, lc = l >> 4;
+  const int qs_b = static_cast<int>(f.q_stride[2]) * 2;
+  // dSE[16 (w + 4 i) + 4 lc + r][16 nb + lr] of this workgroup, over all its tiles
+  f32x4 dse[MBW][4];
+#pragma unroll
+  for (int i = 0; i < MBW; ++i)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) dse[i][nb] = zero4();
+  bf16x8 one;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) one[e] = static_cast<__bf16>(lr == 0 ? 1.f : 0.f);
+
+  const TileOrder order(static_cast<int64_t>(tiles) * f.B * f.H);
+  for (int kstep = 0; kstep < order.steps(); ++kstep) {
+    const int T = order.tile(kstep);
+    if (T < 0) continue;   // uniform over the workgroup
+    const int bh = T / tiles;
+    const int t = T - bh * tiles;
+    const int b = bh / f.H;
+    const int h = bh - b * f.H;
+    const int64_t prow = static_cast<int64_t>(h * f.B + b) * tiles + t;
+    const int n0 = t * kQT;
+    const __amdgpu_buffer_rsrc_t rq =
+        rows_rsrc(reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1], qs_b, N, 128);
+    // the (b, h) slab of the dS matrix: J rows of N fp32
+    const __amdgpu_buffer_rsrc_t rds = rows_rsrc(ds_ws + static_cast<int64_t>(bh) * J * N, 4 * N, J, 4 * N);
+    // this wave's dS blocks and this lane's Q chunks, loaded before the barrier
+    uint4 xs[MBW][2][2], qv[2];
+#pragma unroll
+    for (int i = 0; i < MBW; ++i) {
+      const int j = 16 * (w + 4 * i) + lr;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int nb0 = n0 + 32 * ks + 8 * lc;
+        const uint32_t off = j < J ? static_cast<uint32_t>((j * N + nb0) * 4) : kOutOfRange;
+        xs[i][ks][0] = buf_load16(rds, off);
+        xs[i][ks][1] = buf_load16(rds, off + 16);
+      }
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int i = lane + kBlock * s2;   // 64 rows x 8 chunks of 16 bytes
+      const int nq = n0 + (i >> 3);
+      qv[s2] = buf_load16(rq, nq < N ? static_cast<uint32_t>(nq * qs_b + 16 * (i & 7)) : kOutOfRange);
+    }
+    __syncthreads();   // the previous tile's Q reads are done (and s_off is staged)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int i = lane + kBlock * s2;
+      *reinterpret_cast<uint4*>(s_q + (i >> 3) * kQRow + 8 * (i & 7)) = qv[s2];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MBW; ++i) {
+      const int mb = w + 4 * i;
+      if (mb >= JB) break;
+      const int j = 16 * mb + lr;
+      const int dj = s_off[j];
+      f32x4 c1 = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int nb0 = n0 + 32 * ks + 8 * lc;
+        const uint32_t xw[8] = {xs[i][ks][0].x, xs[i][ks][0].y, xs[i][ks][0].z, xs[i][ks][0].w,
+                                xs[i][ks][1].x, xs[i][ks][1].y, xs[i][ks][1].z, xs[i][ks][1].w};
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int nq = nb0 + e;
+          // written entries only: n - offset_j >= 0 and n < N
+          x[e] = (nq < N && nq >= dj) ? __uint_as_float(xw[e]) : 0.f;
+        }
+        bf16x8 ahi, alo;
+        split_bf16x8(x, ahi, alo);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          // Q rows 32 ks + 8 lc + (0..7), dim 16 nb + lr, read transposed
+          const uint16_t* src = s_q + (32 * ks + 8 * lc + (lr >> 2)) * kQRow + 16 * nb + 4 * (lr & 3);
+          const i16x4 lo4 = lds_read_tr16(src), hi4 = lds_read_tr16(src + 4 * kQRow);
+          const bf16x8 bq = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+          dse[i][nb] = mfma16_bf16(ahi, bq, dse[i][nb]);
+          dse[i][nb] = mfma16_bf16(alo, bq, dse[i][nb]);
+        }
+        c1 = mfma16_bf16(ahi, one, c1);
+        c1 = mfma16_bf16(alo, one, c1);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int jr = 16 * mb + 4 * lc + r;
+        if (lr == 0 && jr < J) part_pb[prow * J + jr] = c1[r];
+      }
+    }
+  }
+  constexpr float kScale = 0.125f;
+#pragma unroll
+  for (int i = 0; i < MBW; ++i)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * (w + 4 * i) + 4 * lc + r;
+        if (j < J)
+          part_se[(static_cast<int64_t>(blockIdx.x) * J + j) * kHeadDim + 16 * nb + lr] = kScale * dse[i][nb][r];
+      }
+}
+
+hipError_t launch_dq_bf16_g4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
   char* base = static_cast<char*>(a.workspace);
   float* delta = reinterpret_cast<float*>(base + ws.delta_off);
-  float* part_se = reinterpret_cast<float*>(base + ws.part_se_off);
-  float* part_pb = reinterpret_cast<float*>(base + ws.part_pb_off);
+  float* ds = reinterpret_cast<float*>(base + ws.ds_off);
   float* part_ph = reinterpret_cast<float*>(base + ws.part_ph_off);
-  if (ws.dq_wgs == 0) return hipSuccess;
-  const size_t lds = dq_t4_layout(f.J, f.J_large, CJ).bytes;
-#define DWARF_DQT4_CASE(S)                                                                                       \
-  case S:                                                                                                       \
-    hipLaunchKernelGGL((dsqg_bwd_dq_bf16_t4<S, CJ, MB>), dim3(ws.dq_wgs), dim3(kBlock), lds, stream, a, delta,    \
-                       part_se, part_pb, part_ph, ws.dq_tiles);                                                  \
+  if (ws.dq_gather_wgs == 0) return hipSuccess;
+  const size_t lds = dq_g4_layout(f.J, f.J_large).bytes;
+#define DWARF_DQG4_CASE(S)                                                                                     \
+  case S:                                                                                                      \
+    hipLaunchKernelGGL((dsqg_bwd_dq_bf16_g4<S>), dim3(ws.dq_gather_wgs), dim3(kBlock), lds, stream, a,     \
+                       delta, ds, part_ph, ws.dq_tiles);                                                       \
     break;
   switch (f.plane_shift) {
-    DWARF_DQT4_CASE(0) DWARF_DQT4_CASE(1) DWARF_DQT4_CASE(2) DWARF_DQT4_CASE(3) DWARF_DQT4_CASE(4)
-    DWARF_DQT4_CASE(5) DWARF_DQT4_CASE(6) DWARF_DQT4_CASE(7) DWARF_DQT4_CASE(8) DWARF_DQT4_CASE(9)
-    DWARF_DQT4_CASE(10) DWARF_DQT4_CASE(11) DWARF_DQT4_CASE(12) DWARF_DQT4_CASE(13) DWARF_DQT4_CASE(14)
+    DWARF_DQG4_CASE(0) DWARF_DQG4_CASE(1) DWARF_DQG4_CASE(2) DWARF_DQG4_CASE(3) DWARF_DQG4_CASE(4)
+    DWARF_DQG4_CASE(5) DWARF_DQG4_CASE(6) DWARF_DQG4_CASE(7) DWARF_DQG4_CASE(8) DWARF_DQG4_CASE(9)
+    DWARF_DQG4_CASE(10) DWARF_DQG4_CASE(11) DWARF_DQG4_CASE(12) DWARF_DQG4_CASE(13) DWARF_DQG4_CASE(14)
     default: return hipErrorInvalidValue;
   }
-#undef DWARF_DQT4_CASE
+#undef DWARF_DQG4_CASE
+  return hipGetLastError();
+}
+
+template <int MBW>
+hipError_t launch_dse_bf16(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+  char* base = static_cast<char*>(a.workspace);
+  const float* ds = reinterpret_cast<const float*>(base + ws.ds_off);
+  float* part_se = reinterpret_cast<float*>(base + ws.part_se_off);
+  float* part_pb = reinterpret_cast<float*>(base + ws.part_pb_off);
+  hipLaunchKernelGGL((dsqg_bwd_dse_bf16<MBW>), dim3(ws.dq_wgs), dim3(kBlock), 0, stream, a, ds, part_se, part_pb,
+                     ws.dq_tiles);
   return hipGetLastError();
 }
 
@@ -963,17 +1070,21 @@ hipError_t launch_dq_typed(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws,
 }  // namespace
 
 size_t dq_lds_bytes(int J, int J_large, int dtype) {
-  return dtype == DWARF_BF16 ? dq_t4_layout(J, J_large, kChunkDq).bytes : dq_lds<float>(J).bytes;
+  return dtype == DWARF_BF16 ? dq_g4_layout(J, J_large).bytes : dq_lds<float>(J).bytes;
 }
+
+int dq_gather_wgs_per_cu() { return kGatherWgsPerCu; }
+int dq_dse_wgs_per_cu(int J) { return dse_wgs_per_cu(dse_blocks_per_wave(J)); }
 
 int dq_tile_queries(int dtype) { return dtype == DWARF_BF16 ? kQT : kQ; }
 
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
   if (a.fwd.dtype == DWARF_BF16) {
-    // dSE accumulator blocks per wave: JE / 16 with JE = roundup16(J + 1)
-    const int blocks = (a.fwd.J + 1 + 15) / 16;
-    if (blocks <= 7) return launch_dq_bf16_t4<kChunkDq, 7>(a, ws, stream);
-    return launch_dq_bf16_t4<kChunkDq, 17>(a, ws, stream);
+    if (ws.dq_gather_wgs == 0) return hipSuccess;
+    hipError_t e = launch_dq_bf16_g4(a, ws, stream);
+    if (e != hipSuccess) return e;
+    if (dse_blocks_per_wave(a.fwd.J) == 2) return launch_dse_bf16<2>(a, ws, stream);
+    return launch_dse_bf16<5>(a, ws, stream);
   }
   return launch_dq_typed<float>(a, ws, stream);
 }

@@ -42,12 +42,14 @@ struct BwdWorkspace {
   size_t part_se_off, part_se_bytes;    // [W][J][64] fp32
   size_t part_pb_off, part_pb_bytes;    // [H][pb_rows][J] fp32
   size_t part_ph_off, part_ph_bytes;    // [H][ph_rows][J_L][8] fp32
+  size_t ds_off, ds_bytes;              // bf16 launch: dS [B*H][J][N] fp32
   size_t red_off, red_bytes;            // stage-1 sums of the reduction
   size_t total;
   int dq_tiles;   // query tiles per (b, h)
   int dq_tpw;     // tiles per workgroup (fp32 launch)
   int dq_ntg;     // workgroups per (b, h) (fp32 launch)
-  int dq_wgs;     // W: workgroups of the dq launch = dSE partial slots
+  int dq_wgs;     // W: workgroups of the dq launch = dSE partial slots (bf16: of the dSE launch)
+  int dq_gather_wgs;   // bf16: persistent workgroups of the dQ gather launch
   int pb_rows, ph_rows;   // dPB / dPhase partial rows per head
   int red_groups_se, red_groups_pb, red_groups_ph;  // stage-1 row groups per segment
 };
@@ -59,5 +61,7 @@ hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws,
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
 size_t dq_lds_bytes(int J, int J_large, int dtype);
 int dq_tile_queries(int dtype);   // queries per tile of the dQ launch
+int dq_gather_wgs_per_cu();       // resident workgroups per CU of the bf16 dQ gather launch
+int dq_dse_wgs_per_cu(int J);     // resident workgroups per CU of the bf16 dSE launch
 
 }  // namespace dwarf

@@ -140,8 +140,11 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     dv = torch.empty(v.shape, device=dev, dtype=v.dtype)
     dpb = torch.empty(pos_bias.shape, device=dev, dtype=torch.float32)
     dse = torch.empty(scale_embed.shape, device=dev, dtype=torch.float32)
-    dpbase = torch.zeros(phase_base.shape, device=dev, dtype=torch.float32)
-    dpgain = torch.zeros(phase_gain.shape, device=dev, dtype=torch.float32)
+    # the reduction writes every [J_large, H, 4] entry; the [1, H, 4] tables of a
+    # lattice without far offsets stay zero
+    alloc = torch.empty if j_large > 0 else torch.zeros
+    dpbase = alloc(phase_base.shape, device=dev, dtype=torch.float32)
+    dpgain = alloc(phase_gain.shape, device=dev, dtype=torch.float32)
     dy = torch.empty(y_pre.shape, device=dev, dtype=torch.float32)
     dz = torch.empty(z_pre.shape, device=dev, dtype=torch.float32)
     args = _lib.DsqgBwdArgs()
