@@ -5,7 +5,7 @@
 Headline workload (the training microbatch): one DSQG layer forward+backward,
 bf16, B=15, H=8, T=2048, head_dim=64, the 96-offset lattice, synthetic seeded
 inputs resident in HBM.  A step is dwarf_dsqg_fwd + dwarf_dsqg_bwd_dq +
-dwarf_dsqg_bwd_dkdv on the current stream.  value = tokens (B*T) per second.
+dwarf_dsqg_bwd_params + dwarf_dsqg_bwd_dkdv on the current stream.  value = tokens (B*T) per second.
 
 Also reported under "extra": the q6 decode step (256 sequences x 9 layers,
 cache length 2048), the q6 prefill forward (B=20) and the long-context
@@ -35,6 +35,7 @@ FWD_BYTES_PER_TH = 548       # q,k,v (3x128) + y,z (2x16) + out (128) + lse (4)
 BWD_BYTES_PER_TH = 1092      # read q,k,v,o,dO + lse + y,z; write dq,dk,dv + dy,dz
 DQ_BYTES_PER_TH = 820        # dq launch: read q,k,v,o,dO,lse,y,z; write dq,dy
 DKDV_BYTES_PER_TH = 820      # dkdv launch: read k,v,q,dO,lse,y,z; write dk,dv,dz
+PARAMS_BYTES_PER_TH = 128    # params launch: read q (dS^T q); the parameter gradients are the tables
 
 
 def log(msg: str) -> None:
@@ -84,7 +85,7 @@ def time_dsqg_step(pkg, t, js, jl, steps, warmup, flush=None):
         step()
     torch.cuda.synchronize()
     evs = [([torch.cuda.Event(enable_timing=True) for _ in range(2)],
-            [torch.cuda.Event(enable_timing=True) for _ in range(3)]) for _ in range(steps)]
+            [torch.cuda.Event(enable_timing=True) for _ in range(4)]) for _ in range(steps)]
     total_ms = 0.0
     if flush is None:
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -100,11 +101,12 @@ def time_dsqg_step(pkg, t, js, jl, steps, warmup, flush=None):
             flush()
             step(ef, eb)
         torch.cuda.synchronize()
-        total_ms = sum(ef[0].elapsed_time(eb[2]) for ef, eb in evs)
+        total_ms = sum(ef[0].elapsed_time(eb[3]) for ef, eb in evs)
     per = {
         "fwd": sum(ef[0].elapsed_time(ef[1]) for ef, _ in evs) / steps,
         "bwd_dq": sum(eb[0].elapsed_time(eb[1]) for _, eb in evs) / steps,
-        "bwd_dkdv": sum(eb[1].elapsed_time(eb[2]) for _, eb in evs) / steps,
+        "bwd_params": sum(eb[1].elapsed_time(eb[2]) for _, eb in evs) / steps,
+        "bwd_dkdv": sum(eb[2].elapsed_time(eb[3]) for _, eb in evs) / steps,
     }
     return total_ms / steps, per
 
@@ -288,7 +290,8 @@ def main() -> int:
     del flush_buf
     th = B * H * N
     bytes_launch = {"fwd": th * FWD_BYTES_PER_TH + TABLE_BYTES,
-                    "bwd_dq": th * DQ_BYTES_PER_TH + 2 * TABLE_BYTES,
+                    "bwd_dq": th * DQ_BYTES_PER_TH + TABLE_BYTES,
+                    "bwd_params": th * PARAMS_BYTES_PER_TH + TABLE_BYTES,
                     "bwd_dkdv": th * DKDV_BYTES_PER_TH + TABLE_BYTES}
     dominant = max(per, key=per.get)
     achieved = bytes_launch[dominant] / (per[dominant] * 1e-3)

@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "dwarf_dsqg_bwd_workspace_bytes",
     "dwarf_dsqg_bwd",
     "dwarf_dsqg_bwd_dq",
+    "dwarf_dsqg_bwd_params",
     "dwarf_dsqg_bwd_dkdv",
     "dwarf_ema_fwd_workspace_bytes",
     "dwarf_ema_fwd",
@@ -183,7 +184,7 @@ def load() -> ctypes.CDLL:
     lib.dwarf_dsqg_bwd_workspace_bytes.argtypes = [POINTER(DsqgBwdArgs)]
     lib.dwarf_dsqg_bwd.restype = c_int
     lib.dwarf_dsqg_bwd.argtypes = [POINTER(DsqgBwdArgs), c_void_p]
-    for name in ("dwarf_dsqg_bwd_dq", "dwarf_dsqg_bwd_dkdv"):
+    for name in ("dwarf_dsqg_bwd_dq", "dwarf_dsqg_bwd_params", "dwarf_dsqg_bwd_dkdv"):
         getattr(lib, name).restype = c_int
         getattr(lib, name).argtypes = [POINTER(DsqgBwdArgs), c_void_p]
     lib.dwarf_ema_fwd_workspace_bytes.restype = c_size_t

@@ -150,8 +150,8 @@ size_t dwarf_dsqg_bwd_workspace_bytes(const dwarf_dsqg_bwd_args* args) {
   return dwarf::bwd_workspace_layout(*args).total;
 }
 
-static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, bool do_dq, bool do_dkdv,
-                     const char* name) {
+static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, bool do_dq, bool do_params,
+                     bool do_dkdv, const char* name) {
   if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
   const dwarf_dsqg_bwd_args& a = *args;
   int rc = check_fwd(a.fwd);
@@ -161,10 +161,11 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
   if (dt == DWARF_BF16 && (rc = check_gather_span("dout", a.dout_stride[2], 2, a.fwd.N))) return rc;
   if (do_dq) {
     if ((rc = check_contig_rows("dq", a.dq, a.dq_stride, dt))) return rc;
-    if (!a.dpos_bias || !a.dscale_embed || !a.dphase_base || !a.dphase_gain || !a.dy_pre)
-      return fail(DWARF_ERR_INVALID_ARGUMENT, "a gradient output is NULL");
+    if (!a.dy_pre) return fail(DWARF_ERR_INVALID_ARGUMENT, "dy_pre is NULL");
     if (!aligned16(a.dy_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dy_pre must be 16-byte aligned");
   }
+  if (do_params && (!a.dpos_bias || !a.dscale_embed || !a.dphase_base || !a.dphase_gain))
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter gradient output is NULL");
   if (do_dkdv) {
     if ((rc = check_contig_rows("dk", a.dk, a.dk_stride, dt))) return rc;
     if ((rc = check_contig_rows("dv", a.dv, a.dv_stride, dt))) return rc;
@@ -177,19 +178,24 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", ws.total, a.workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(a.workspace) & 255u) != 0)
     return fail(DWARF_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  return hip_status(dwarf::launch_dsqg_bwd(a, ws, reinterpret_cast<hipStream_t>(stream), do_dq, do_dkdv), name);
+  return hip_status(
+      dwarf::launch_dsqg_bwd(a, ws, reinterpret_cast<hipStream_t>(stream), do_dq, do_params, do_dkdv), name);
 }
 
 int dwarf_dsqg_bwd(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
-  return bwd_stage(args, stream, true, true, "dwarf_dsqg_bwd");
+  return bwd_stage(args, stream, true, true, true, "dwarf_dsqg_bwd");
 }
 
 int dwarf_dsqg_bwd_dq(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
-  return bwd_stage(args, stream, true, false, "dwarf_dsqg_bwd_dq");
+  return bwd_stage(args, stream, true, false, false, "dwarf_dsqg_bwd_dq");
+}
+
+int dwarf_dsqg_bwd_params(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
+  return bwd_stage(args, stream, false, true, false, "dwarf_dsqg_bwd_params");
 }
 
 int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
-  return bwd_stage(args, stream, false, true, "dwarf_dsqg_bwd_dkdv");
+  return bwd_stage(args, stream, false, false, true, "dwarf_dsqg_bwd_dkdv");
 }
 
 // ---- EMA --------------------------------------------------------------------

@@ -609,9 +609,13 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
 }
 
 hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
-                           bool do_dkdv) {
+                           bool do_params, bool do_dkdv) {
   if (do_dq) {
-    hipError_t e = launch_dsqg_bwd_dq(a, ws, stream);
+    const hipError_t e = launch_dsqg_bwd_dq(a, ws, stream);
+    if (e != hipSuccess) return e;
+  }
+  if (do_params) {
+    hipError_t e = launch_dsqg_bwd_dse(a, ws, stream);
     if (e != hipSuccess) return e;
     const RedPlan p = make_red_plan(a, ws);
     const int b1 = p.blocks1[0] + p.blocks1[1] + p.blocks1[2];

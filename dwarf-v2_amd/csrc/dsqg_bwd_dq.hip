@@ -1079,14 +1079,14 @@ int dq_dse_wgs_per_cu(int J) { return dse_wgs_per_cu(dse_blocks_per_wave(J)); }
 int dq_tile_queries(int dtype) { return dtype == DWARF_BF16 ? kQT : kQ; }
 
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
-  if (a.fwd.dtype == DWARF_BF16) {
-    if (ws.dq_gather_wgs == 0) return hipSuccess;
-    hipError_t e = launch_dq_bf16_g4(a, ws, stream);
-    if (e != hipSuccess) return e;
-    if (dse_blocks_per_wave(a.fwd.J) == 2) return launch_dse_bf16<2>(a, ws, stream);
-    return launch_dse_bf16<5>(a, ws, stream);
-  }
+  if (a.fwd.dtype == DWARF_BF16) return launch_dq_bf16_g4(a, ws, stream);
   return launch_dq_typed<float>(a, ws, stream);
+}
+
+hipError_t launch_dsqg_bwd_dse(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+  if (a.fwd.dtype != DWARF_BF16 || ws.dq_gather_wgs == 0) return hipSuccess;   // fp32: partials come with dQ
+  if (dse_blocks_per_wave(a.fwd.J) == 2) return launch_dse_bf16<2>(a, ws, stream);
+  return launch_dse_bf16<5>(a, ws, stream);
 }
 
 }  // namespace dwarf

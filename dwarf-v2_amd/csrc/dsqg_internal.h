@@ -54,11 +54,14 @@ struct BwdWorkspace {
   int red_groups_se, red_groups_pb, red_groups_ph;  // stage-1 row groups per segment
 };
 BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a);
-// do_dq: delta + dQ/dY + parameter-gradient partials and their reduction;
-// do_dkdv: dK/dV/dZ (reads the delta written by the dq stage).
+// do_dq: delta + dQ/dY + the parameter-gradient inputs in the workspace (bf16:
+// the dS matrix and dPhase partials; fp32: all partials); do_params: the
+// parameter gradients from those (bf16: the dSE/dPB launch, then the fixed-
+// order reduction); do_dkdv: dK/dV/dZ (reads the delta of the dq stage).
 hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
-                           bool do_dkdv);
+                           bool do_params, bool do_dkdv);
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
+hipError_t launch_dsqg_bwd_dse(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
 size_t dq_lds_bytes(int J, int J_large, int dtype);
 int dq_tile_queries(int dtype);   // queries per tile of the dQ launch
 int dq_gather_wgs_per_cu();       // resident workgroups per CU of the bf16 dQ gather launch

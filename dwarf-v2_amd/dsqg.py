@@ -127,10 +127,11 @@ def dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, 
 
 def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
                   out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None):
-    """Raw backward: the dq launch then the dkdv launch on the current stream.
+    """Raw backward: the dq, params and dkdv stages on the current stream.
 
     Returns (dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz).  ``events``:
-    optional three torch.cuda.Events recorded before dq, between, and after dkdv.
+    optional four torch.cuda.Events recorded before dq, after dq, after params
+    and after dkdv.
     """
     lib = _lib.load()
     dev = q.device
@@ -166,9 +167,12 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     _lib.check(lib.dwarf_dsqg_bwd_dq(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dq")
     if events:
         events[1].record()
-    _lib.check(lib.dwarf_dsqg_bwd_dkdv(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dkdv")
+    _lib.check(lib.dwarf_dsqg_bwd_params(ctypes.byref(args), stream), "dwarf_dsqg_bwd_params")
     if events:
         events[2].record()
+    _lib.check(lib.dwarf_dsqg_bwd_dkdv(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dkdv")
+    if events:
+        events[3].record()
     return dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz
 
 

@@ -124,14 +124,20 @@ size_t dwarf_dsqg_bwd_workspace_bytes(const dwarf_dsqg_bwd_args* args);
 int dwarf_dsqg_bwd(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 
 /*
- * The same backward as two launches on one stream, in this order, sharing the
- * workspace.  dwarf_dsqg_bwd_dq replaces _compute_D_v18_grouped plus
- * _bwd_dq_v18_grouped (dsqg:2378-2454): it writes delta into the workspace,
- * dq, dy_pre and the four parameter gradients.  dwarf_dsqg_bwd_dkdv replaces
- * _bwd_dkdv_v18_grouped (dsqg:2456-2544): it reads that delta and writes dk,
- * dv and dz_pre.  Fields a stage does not write may be NULL.
+ * The same backward as three stages on one stream, sharing the workspace;
+ * dq runs first, params and dkdv after it in either order.
+ * dwarf_dsqg_bwd_dq replaces _compute_D_v18_grouped plus the query-centric
+ * part of _bwd_dq_v18_grouped (dsqg:2378-2454): it writes delta and the
+ * parameter-gradient inputs into the workspace, dq and dy_pre.
+ * dwarf_dsqg_bwd_params completes the atomic parameter-gradient sums of
+ * _bwd_dq_v18_grouped and _bwd_dkdv_v18_grouped (dsqg:1388-1392, 1464-1470, 1905-1907)
+ * as fixed-order reductions: dpos_bias, dscale_embed, dphase_base and
+ * dphase_gain.  dwarf_dsqg_bwd_dkdv replaces _bwd_dkdv_v18_grouped
+ * (dsqg:2456-2544): it reads delta and writes dk, dv and dz_pre.  Fields a
+ * stage does not write may be NULL.
  */
 int dwarf_dsqg_bwd_dq(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
+int dwarf_dsqg_bwd_params(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
