@@ -194,8 +194,8 @@ __host__ __device__ inline KvLayout kv_layout(int J, int J_large, int group, int
 template <int CJ>
 struct KvChunk {
   uint4 q[CJ][2], d[CJ][2];
-  float lse[CJ], dl[CJ], y[CJ];
-  bool ok[CJ];
+  float2 dl2[CJ];   // (delta, lse in log2 units; +inf without softmax mass)
+  float y[CJ];
   int j[CJ];
 };
 
@@ -294,10 +294,9 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   // a key past the end uses m_eff = m0w - 2N - 64: m_eff + delta < 0 for every listed delta
   const int m_eff = key_ok ? m : m0w - 2 * N - 64;
   const int qs_b = static_cast<int>(f.q_stride[2]) * 2, ds_b = static_cast<int>(a.dout_stride[2]) * 2;
-  const int ls_b = static_cast<int>(f.lse_stride[2]) * 4, ys_b = static_cast<int>(f.y_stride[2]) * 4;
-  const int qstart = f.query_start;
+  const int ys_b = static_cast<int>(f.y_stride[2]) * 4;
   const int qb_lane = m_eff * qs_b + 32 * g, db_lane = m_eff * ds_b + 32 * g;
-  const int lb_lane = m_eff * ls_b, yb_lane = m_eff * ys_b + 4 * g;
+  const int yb_lane = m_eff * ys_b + 4 * g;
 
   for (int hh = 0; hh < group; ++hh) {
     const int h = hk * group + hh;
@@ -306,8 +305,7 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
         rows_rsrc(reinterpret_cast<const bf16*>(f.q) + b * f.q_stride[0] + h * f.q_stride[1], qs_b, N, 128);
     const __amdgpu_buffer_rsrc_t rd = rows_rsrc(
         reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1], ds_b, N, 128);
-    const __amdgpu_buffer_rsrc_t rl = rows_rsrc(f.lse + b * f.lse_stride[0] + h * f.lse_stride[1], ls_b, N, 4);
-    const __amdgpu_buffer_rsrc_t rdl = rows_rsrc(delta_ws + static_cast<int64_t>(bh) * N, 4, N, 4);
+    const __amdgpu_buffer_rsrc_t rdl = rows_rsrc(delta_ws + 2 * static_cast<int64_t>(bh) * N, 8, N, 8);
     const __amdgpu_buffer_rsrc_t ry = rows_rsrc(f.y_pre + b * f.y_stride[0] + h * f.y_stride[1], ys_b, N, 16);
     const float* pb2 = s_pb2 + hh * lay.JE;
     const float2* ph_h = s_ph + hh * lay.JL4 * kPlanes;
@@ -319,16 +317,20 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
         const int j = uniform(e.x), d = uniform(e.y);
         const int n = m_eff + d;
         c.j[jj] = j;
-        c.ok[jj] = n >= qstart && n < N;
-        // lane bases plus wave-uniform products (no per-lane multiplies)
+        // lane bases plus wave-uniform products (no per-lane multiplies).  A
+        // query outside [0, N) reads zeros: its q and dO rows are 0, so the
+        // pair adds nothing whatever P is.
         const uint32_t qo = static_cast<uint32_t>(qb_lane + d * qs_b);
         const uint32_t dof = static_cast<uint32_t>(db_lane + d * ds_b);
         c.q[jj][0] = buf_load16(rq, qo);
         c.q[jj][1] = buf_load16(rq, qo + 16);
         c.d[jj][0] = buf_load16(rd, dof);
         c.d[jj][1] = buf_load16(rd, dof + 16);
-        c.lse[jj] = buf_load_f32(rl, static_cast<uint32_t>(lb_lane + d * ls_b));
-        c.dl[jj] = buf_load_f32(rdl, static_cast<uint32_t>(4 * n));
+        // the elements are copied out before reinterpreting: this compiler
+        // reads element 0 for __builtin_bit_cast of any element of the vector
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rdl, static_cast<uint32_t>(8 * n), 0, 0);
+        const uint32_t x0 = x[0], x1 = x[1];
+        c.dl2[jj] = make_float2(__uint_as_float(x0), __uint_as_float(x1));
         c.y[jj] = buf_load_f32(ry, (j >= J_small && j < J) ? static_cast<uint32_t>(yb_lane + d * ys_b) : kOutOfRange);
       }
     };
@@ -361,9 +363,8 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
         }
         dot = group_sum<4>(dot);
         gd = group_sum<4>(gd);
-        const bool live = c.ok[jj] && c.lse[jj] > -INFINITY;
-        const float P = live ? __builtin_amdgcn_exp2f(fmaf(dot, kC, pb2[j]) - c.lse[jj] * kLog2e) : 0.f;
-        const float dS = P * (gd - c.dl[jj]);
+        const float P = __builtin_amdgcn_exp2f(fmaf(dot, kC, pb2[j]) - c.dl2[jj].y);
+        const float dS = P * (gd - c.dl2[jj].x);
         const float cds = kScale * dS;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -584,8 +585,8 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   w.red_groups_pb = (w.pb_rows + kRedRows - 1) / kRedRows;
   w.red_groups_ph = (w.ph_rows + kRedRows - 1) / kRedRows;
   size_t off = 0;
-  w.delta_off = off;
-  w.delta_bytes = static_cast<size_t>(f.B) * f.H * f.N * sizeof(float);
+  w.delta_off = off;   // bf16: (delta, log2 lse) pairs; fp32: delta
+  w.delta_bytes = static_cast<size_t>(f.B) * f.H * f.N * 2 * sizeof(float);
   off += align256(w.delta_bytes);
   w.part_se_off = off;
   w.part_se_bytes = static_cast<size_t>(w.dq_wgs) * f.J * kHeadDim * sizeof(float);

@@ -695,7 +695,11 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
       yg = f.y_pre[b * f.y_stride[0] + h * f.y_stride[1] + nn * f.y_stride[2] + g];
     }
     dlt = group_sum<4>(dlt);
-    if (row_ok && g == 0) delta_ws[static_cast<int64_t>(bh) * N + n] = dlt;
+    // (delta, lse in log2 units) for the dK/dV launch; +inf makes P = 0 for a
+    // query without softmax mass or before query_start
+    if (row_ok && g == 0)
+      *reinterpret_cast<float2*>(delta_ws + 2 * (static_cast<int64_t>(bh) * N + n)) =
+          make_float2(dlt, mass ? lse2 : INFINITY);
     const int n_eff = mass ? n : n0w - 2 * N;   // no source for queries without softmax mass
     const int kb_lane = n_eff * ks_b + 32 * g;
     const int vb_lane = n_eff * vs_b + 32 * g;

@@ -38,7 +38,7 @@ hipError_t launch_dsqg_fwd(const dwarf_dsqg_fwd_args& a, hipStream_t stream);
 // launch writes one partial slot per workgroup (slot = (h*B + b)*n_tg + tg);
 // the reduce launch sums them in a fixed order.
 struct BwdWorkspace {
-  size_t delta_off, delta_bytes;        // [B,H,N] fp32
+  size_t delta_off, delta_bytes;        // bf16: [B,H,N] (delta, log2 lse) fp32 pairs; fp32: [B,H,N] delta
   size_t part_se_off, part_se_bytes;    // [W][J][64] fp32
   size_t part_pb_off, part_pb_bytes;    // [H][pb_rows][J] fp32
   size_t part_ph_off, part_ph_bytes;    // [H][ph_rows][J_L][8] fp32
