@@ -904,6 +904,7 @@ __global__ __launch_bounds__(kBlock, dse_wgs_per_cu(MBW)) void dsqg_bwd_dse_bf16
   __shared__ int s_off[64 * MBW];
   __shared__ __attribute__((aligned(16))) uint16_t s_q[kQT * kQRow];
   for (int j = threadIdx.x; j < 64 * MBW; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
+  __syncthreads();
   const int lane = threadIdx.x;
   const int w = lane / kWave;
   const int l = lane % kWave;
@@ -938,10 +939,13 @@ __global__ __launch_bounds__(kBlock, dse_wgs_per_cu(MBW)) void dsqg_bwd_dse_bf16
 #pragma unroll
     for (int i = 0; i < MBW; ++i) {
       const int j = 16 * (w + 4 * i) + lr;
+      const int dj = j < J ? s_off[j] : 0;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int nb0 = n0 + 32 * ks + 8 * lc;
-        const uint32_t off = j < J ? static_cast<uint32_t>((j * N + nb0) * 4) : kOutOfRange;
+        // eight entries that are all unwritten (n < offset_j) are not fetched
+        const bool any = j < J && nb0 + 7 >= dj && nb0 < N;
+        const uint32_t off = any ? static_cast<uint32_t>((j * N + nb0) * 4) : kOutOfRange;
         xs[i][ks][0] = buf_load16(rds, off);
         xs[i][ks][1] = buf_load16(rds, off + 16);
       }
@@ -952,7 +956,7 @@ __global__ __launch_bounds__(kBlock, dse_wgs_per_cu(MBW)) void dsqg_bwd_dse_bf16
       const int nq = n0 + (i >> 3);
       qv[s2] = buf_load16(rq, nq < N ? static_cast<uint32_t>(nq * qs_b + 16 * (i & 7)) : kOutOfRange);
     }
-    __syncthreads();   // the previous tile's Q reads are done (and s_off is staged)
+    __syncthreads();   // the previous tile's Q reads are done
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       const int i = lane + kBlock * s2;
