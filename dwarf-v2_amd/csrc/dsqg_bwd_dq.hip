@@ -569,7 +569,7 @@ __host__ __device__ inline DqG4Layout dq_g4_layout(int J, int J_large) {
 template <int SHIFT, int CJ>
 struct DqChunk {
   uint4 k[CJ][2], v[CJ][2];
-  float z[CJ];
+  float z[CJ], pb2[CJ];
   bool ok[CJ];
   int j[CJ];
 };
@@ -662,7 +662,8 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     const __amdgpu_buffer_rsrc_t rv =
         rows_rsrc(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1], vs_b, N, 128);
     const __amdgpu_buffer_rsrc_t rz = rows_rsrc(f.z_pre + b * f.z_stride[0] + hk * f.z_stride[1], zs_b, N, 16);
-    float* ds_bh = ds_ws + static_cast<int64_t>(bh) * J * N;
+    // the (b, h) slab of the dS matrix, J rows of N fp32; this lane's query column
+    const __amdgpu_buffer_rsrc_t rds = rows_rsrc(ds_ws + static_cast<int64_t>(bh) * J * N, 4 * N, J, 4 * N);
 
     const int n0w = t * kQT + kQPW * w;
     const int n = n0w + qi;
@@ -704,6 +705,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     const int kb_lane = n_eff * ks_b + 32 * g;
     const int vb_lane = n_eff * vs_b + 32 * g;
     const int zb_lane = n_eff * zs_b + 4 * g;
+    const uint32_t ds_lane = row_ok ? static_cast<uint32_t>(4 * n) : kOutOfRange;
 
     __syncthreads();   // the previous tile's dPhase tables have been read
     for (int i = lane; i < 4 * lay.JL4 * 8; i += kBlock) s_dph_all[i] = 0.f;
@@ -745,6 +747,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
         c.v[jj][0] = buf_load16(rv, vo);
         c.v[jj][1] = buf_load16(rv, vo + 16);
         c.z[jj] = buf_load_f32(rz, zo);
+        c.pb2[jj] = s_pb2[j];
       }
     };
 
@@ -782,7 +785,8 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
         }
         dot = group_sum<4>(dot);
         gd = group_sum<4>(gd);
-        const float P = c.ok[jj] ? __builtin_amdgcn_exp2f(fmaf(dot, kC, s_pb2[j]) - lse2) : 0.f;
+        // exp2(-inf) = 0 without a source (no branch around the exponential)
+        const float P = __builtin_amdgcn_exp2f(c.ok[jj] ? fmaf(dot, kC, c.pb2[jj]) - lse2 : -INFINITY);
         const float dS = P * (gd - dlt);
         const float cds = kScale * dS;
 #pragma unroll
@@ -793,7 +797,10 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
         // keep the accumulation here: sunk to the loop latch it holds every
         // chunk's K registers live and the prefetch turns into register copies
         pin_regs<16>(dq);
-        if (g == 0 && row_ok && j < J) ds_bh[static_cast<int64_t>(j) * N + n] = dS;
+        // the four lanes of a query store the same value; rows past N and the
+        // sentinel go out of range (dropped)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(dS), rds, j < J ? ds_lane + 4 * j * N : kOutOfRange, 0,
+                                              0);
         ds_out[jj] = dS;
         const float tq = P * tq_pre;
         dy = fmaf(tq * pg, c.z[jj], dy);
@@ -807,11 +814,8 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
         if (j >= J_small && j < J) {   // wave-uniform
           const float s0 = sum_over_queries16(ph_sum[jj][0]);
           const float s1 = sum_over_queries16(ph_sum[jj][1]);
-          if (l < 4) {
-            float* dst = s_dph + (j - J_small) * 8 + 2 * g;
-            dst[0] += s0;
-            dst[1] += s1;
-          }
+          // each far offset appears once in the list: a store, no accumulation
+          if (l < 4) *reinterpret_cast<float2*>(s_dph + (j - J_small) * 8 + 2 * g) = make_float2(s0, s1);
         }
       }
     };
