@@ -224,15 +224,7 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   const int b = bhk / f.H_kv;
   const int hk = bhk - b * f.H_kv;
 
-  for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
-    const int j = i / kHeadDim, d = i - j * kHeadDim;
-    float e = 0.f;
-    if (j < J) {
-      e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
-      if (f.se_round_bf16) e = round_bf16(e);
-    }
-    sE[j * kERowKv + d] = f32_to_bf16_bits(e);
-  }
+  stage_se_bf16(f.scale_embed, f.se_stride, J, lay.JE, sE, kERowKv);
   for (int t = threadIdx.x; t < group * lay.JE; t += kBlock) {
     const int hh = t / lay.JE, j = t - hh * lay.JE;
     const int h = hk * group + hh;

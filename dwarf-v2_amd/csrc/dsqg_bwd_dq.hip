@@ -620,15 +620,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
   uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
   float* s_st_all = reinterpret_cast<float*>(sm + lay.off_st);
 
-  for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
-    const int j = i / kHeadDim, d = i - j * kHeadDim;
-    float e = 0.f;
-    if (j < J) {
-      e = f.scale_embed[j * f.se_stride[0] + d * f.se_stride[1]];
-      if (f.se_round_bf16) e = round_bf16(e);
-    }
-    sE[j * kERowT + d] = f32_to_bf16_bits(e);
-  }
+  stage_se_bf16(f.scale_embed, f.se_stride, J, lay.JE, sE, kERowT);
   for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
 
   const int lane = threadIdx.x;

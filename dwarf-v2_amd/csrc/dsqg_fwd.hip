@@ -224,15 +224,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
   const int h = bh - b * a.H;
   const int hk = h / (a.H / a.H_kv);
 
-  for (int i = threadIdx.x; i < lay.JE * kHeadDim; i += kBlock) {
-    const int j = i / kHeadDim, d = i - j * kHeadDim;
-    float e = 0.f;
-    if (j < J) {
-      e = a.scale_embed[j * a.se_stride[0] + d * a.se_stride[1]];
-      if (a.se_round_bf16) e = round_bf16(e);
-    }
-    sE[j * kERowFwd + d] = f32_to_bf16_bits(e);
-  }
+  stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kERowFwd);
   for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
     s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
     s_off[j] = j < J ? a.offsets[j] : 0;

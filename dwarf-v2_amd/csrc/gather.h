@@ -16,6 +16,31 @@ __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
+// E (scale_embed [J][64] fp32) into LDS as bf16 rows of `row` elements, rows
+// J..JE-1 zero, rounded to nearest even (the reference GPU path's bf16 SE,
+// dsqg:760-763).  Four values per thread step: one 16-byte load, one 8-byte
+// LDS store when the rows are unit-stride and 16-byte aligned.
+__device__ __forceinline__ void stage_se_bf16(const float* se, const int64_t* se_stride, int J, int JE,
+                                              uint16_t* sE, int row) {
+  const bool vec = se_stride[1] == 1 && (se_stride[0] & 3) == 0 && (reinterpret_cast<uintptr_t>(se) & 15) == 0;
+  for (int i = threadIdx.x; i < JE * 16; i += blockDim.x) {
+    const int j = i >> 4, d = 4 * (i & 15);
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (j < J) {
+      const float* p = se + j * se_stride[0] + d * se_stride[1];
+      if (vec) {
+        x = *reinterpret_cast<const float4*>(p);
+      } else {
+        x = make_float4(p[0], p[se_stride[1]], p[2 * se_stride[1]], p[3 * se_stride[1]]);
+      }
+    }
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    const bf16x4_t h = {static_cast<__bf16>(x.x), static_cast<__bf16>(x.y), static_cast<__bf16>(x.z),
+                        static_cast<__bf16>(x.w)};
+    *reinterpret_cast<bf16x4_t*>(sE + j * row + d) = h;
+  }
+}
+
 // Zero-instruction barrier on register values: the computations that produce
 // them stay before this point (the compiler may not sink them into a later block).
 template <int CNT>
