@@ -224,6 +224,28 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   const int b = bhk / f.H_kv;
   const int hk = bhk - b * f.H_kv;
 
+  // this lane's key row (K, V slices and z) is requested first, so its latency
+  // overlaps the table staging
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int ki = l >> 2;
+  const int m0w = tile * kKPB + w * kKPW;
+  const int m = m0w + ki;
+  const bool key_ok = m < N;
+  const int64_t mm = m;
+  uint4 kx0 = {0u, 0u, 0u, 0u}, kx1 = {0u, 0u, 0u, 0u}, vx0 = {0u, 0u, 0u, 0u}, vx1 = {0u, 0u, 0u, 0u};
+  float zg = 0.f;
+  if (key_ok) {
+    const uint4* k4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] +
+                                                     hk * f.k_stride[1] + mm * f.k_stride[2] + 16 * g);
+    const uint4* v4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] +
+                                                     hk * f.v_stride[1] + mm * f.v_stride[2] + 16 * g);
+    kx0 = k4[0]; kx1 = k4[1]; vx0 = v4[0]; vx1 = v4[1];
+    zg = f.z_pre[b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2] + g];
+  }
+
   stage_se_bf16(f.scale_embed, f.se_stride, J, lay.JE, sE, kERowKv);
   for (int t = threadIdx.x; t < group * lay.JE; t += kBlock) {
     const int hh = t / lay.JE, j = t - hh * lay.JE;
@@ -241,39 +263,16 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   }
   __syncthreads();
 
-  const int lane = threadIdx.x;
-  const int w = lane / kWave;
-  const int l = lane % kWave;
-  const int g = l & 3;
-  const int ki = l >> 2;
-  const int m0w = tile * kKPB + w * kKPW;
   if (m0w >= N) return;                       // whole wave past the end (no block barriers below)
-  const int m = m0w + ki;
   const int m_hi = min(m0w + kKPW - 1, N - 1);
-  const bool key_ok = m < N;
-  const int64_t mm = m;
   int2* s_list = s_list_all + w * lay.list_len;
   // offsets giving some key m0w..m_hi a query m + delta in [0, N); the
   // sentinel offset N + 16 - m0w puts every key's query past the end.
   const int cnt = build_offset_list<CJ>(s_list, s_off, J, m0w, m_hi, N, -1, make_int2(J, N + 16 - m0w));
   const int cntp = (cnt + CJ - 1) / CJ * CJ;
 
-  uint32_t k32[8], v32[8];
-  float zg = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) { k32[i] = 0u; v32[i] = 0u; }
-  if (key_ok) {
-    const uint4* k4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] +
-                                                     hk * f.k_stride[1] + mm * f.k_stride[2] + 16 * g);
-    const uint4* v4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] +
-                                                     hk * f.v_stride[1] + mm * f.v_stride[2] + 16 * g);
-    const uint4 x0 = k4[0], x1 = k4[1], y0 = v4[0], y1 = v4[1];
-    k32[0] = x0.x; k32[1] = x0.y; k32[2] = x0.z; k32[3] = x0.w;
-    k32[4] = x1.x; k32[5] = x1.y; k32[6] = x1.z; k32[7] = x1.w;
-    v32[0] = y0.x; v32[1] = y0.y; v32[2] = y0.z; v32[3] = y0.w;
-    v32[4] = y1.x; v32[5] = y1.y; v32[6] = y1.z; v32[7] = y1.w;
-    zg = f.z_pre[b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2] + g];
-  }
+  const uint32_t k32[8] = {kx0.x, kx0.y, kx0.z, kx0.w, kx1.x, kx1.y, kx1.z, kx1.w};
+  const uint32_t v32[8] = {vx0.x, vx0.y, vx0.z, vx0.w, vx1.x, vx1.y, vx1.z, vx1.w};
   // own V pair of plane g (dims 16g + SHIFT, +1)
   const float va = (SHIFT & 1) ? bf16_hi(v32[SHIFT >> 1]) : bf16_lo(v32[SHIFT >> 1]);
   const float vb = ((SHIFT + 1) & 1) ? bf16_hi(v32[(SHIFT + 1) >> 1]) : bf16_lo(v32[(SHIFT + 1) >> 1]);

@@ -224,6 +224,39 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
   const int h = bh - b * a.H;
   const int hk = h / (a.H / a.H_kv);
 
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int qi = l >> 2;
+  const int lr = l & 15, lc = l >> 4;
+  const int n0w = tile * kQPB + w * kQPW;
+  const int n = n0w + qi;
+  const int n_hi = min(n0w + kQPW - 1, N - 1);
+  const bool row_ok = n < N;
+  const bool live = row_ok && n >= a.query_start;
+  const int64_t nn = n;
+  float* s_qe = s_qe_all + w * kQPW * lay.qe_row;
+  int2* s_list = s_list_all + w * lay.list_len;
+
+  // The wave's q rows (MFMA operand layout and this lane's slice) and y are
+  // requested first, so their latency overlaps the table staging.
+  const bf16* qbase = reinterpret_cast<const bf16*>(a.q) + b * a.q_stride[0] + h * a.q_stride[1];
+  uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if (n0w + lr < N) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      xa[ks] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(n0w + lr) * a.q_stride[2] + 32 * ks + 8 * lc);
+  }
+  uint4 qx0 = {0u, 0u, 0u, 0u}, qx1 = {0u, 0u, 0u, 0u};
+  float yg = 0.f;
+  if (live) {
+    const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * a.q_stride[2] + 16 * g);
+    qx0 = q4[0];
+    qx1 = q4[1];
+    yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
+  }
+
   stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kERowFwd);
   for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
     s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
@@ -236,33 +269,10 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
   }
   __syncthreads();
 
-  const int lane = threadIdx.x;
-  const int w = lane / kWave;
-  const int l = lane % kWave;
-  const int g = l & 3;
-  const int qi = l >> 2;
-  const int n0w = tile * kQPB + w * kQPW;
-  const int n = n0w + qi;
-  const int n_hi = min(n0w + kQPW - 1, N - 1);
-  const bool row_ok = n < N;
-  const bool live = row_ok && n >= a.query_start;
-  const int64_t nn = n;
-  float* s_qe = s_qe_all + w * kQPW * lay.qe_row;
-  int2* s_list = s_list_all + w * lay.list_len;
-
-  const bf16* qbase = reinterpret_cast<const bf16*>(a.q) + b * a.q_stride[0] + h * a.q_stride[1];
   // s_qe[query][j] = log2(e) * (<q, e_j> / 8 + pb_j) for the wave's 16 queries:
   // products into registers, a barrier (every wave is done reading sE), then
   // the tables are written over sE.
   {
-    const int lr = l & 15, lc = l >> 4;
-    const int nq = n0w + lr;
-    uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-    if (nq < N) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        xa[ks] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(nq) * a.q_stride[2] + 32 * ks + 8 * lc);
-    }
     f32x4 c[kMaxQeBlocks];
 #pragma unroll
     for (int bi = 0; bi < kMaxQeBlocks; ++bi) {
@@ -291,17 +301,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
   const int cnt = build_offset_list<CJ>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
   const int cntp = (cnt + CJ - 1) / CJ * CJ;
 
-  uint32_t q32[8];
-  float yg = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) q32[i] = 0u;
-  if (live) {
-    const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * a.q_stride[2] + 16 * g);
-    const uint4 x0 = q4[0], x1 = q4[1];
-    q32[0] = x0.x; q32[1] = x0.y; q32[2] = x0.z; q32[3] = x0.w;
-    q32[4] = x1.x; q32[5] = x1.y; q32[6] = x1.z; q32[7] = x1.w;
-    yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
-  }
+  const uint32_t q32[8] = {qx0.x, qx0.y, qx0.z, qx0.w, qx1.x, qx1.y, qx1.z, qx1.w};
   // Per-lane byte offsets of row 0 shifted by the lane's query; a lane without
   // a live query uses n_eff = n0w - 2N, so n_eff - d < 0 for every listed d.
   const int n_eff = live ? n : n0w - 2 * N;
