@@ -16,6 +16,7 @@
 #include "common.h"
 #include "dsqg_internal.h"
 #include "gather.h"
+#include "mfma.h"
 
 namespace dwarf {
 namespace {
@@ -155,131 +156,284 @@ __global__ __launch_bounds__(kBlock) void q6_unpack_kernel(int B, int Hkv, int N
   for (int e = 0; e < kGroup; ++e) dst[e] = c[e] * sc;
 }
 
+// Slot reads shared by prefill and decode.
+__device__ __forceinline__ uint32_t cache_dword(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+// Sixteen signed 6-bit codes of a 12-byte chunk (bits [6i, 6i+6) of w0:w1:w2).
+// v_bfe_i32 sign-extends the field; the builtin is typed unsigned, so the
+// result is reinterpreted as int before the conversion to float.
+__device__ __forceinline__ float sfield6(uint32_t w, int bit) {
+  return static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(w, bit, 6)));
+}
+
+__device__ __forceinline__ void q6_codes16(uint32_t w0, uint32_t w1, uint32_t w2, float* c) {
+#pragma unroll
+  for (int i = 0; i < 5; ++i) c[i] = sfield6(w0, 6 * i);
+  c[5] = sfield6(__builtin_amdgcn_alignbit(w1, w0, 30), 0);
+#pragma unroll
+  for (int i = 6; i < 10; ++i) c[i] = sfield6(w1, 6 * i - 32);
+  c[10] = sfield6(__builtin_amdgcn_alignbit(w2, w1, 28), 0);
+#pragma unroll
+  for (int i = 11; i < 16; ++i) c[i] = sfield6(w2, 6 * i - 64);
+}
+
+__device__ __forceinline__ float half_lo_or_hi(uint32_t pair, bool hi) {
+  return half_bits_to_f32(static_cast<uint16_t>(hi ? pair >> 16 : pair));
+}
+
 // ---------------------------------------------------------------------------
-// Prefill forward.  Two lanes per query, each owning one 32-wide group, so a
-// lane dequantises exactly the K and V groups it multiplies.  q.k is formed
-// on the integer codes and scaled once per group.
+// Prefill forward, four lanes per query (the bf16 forward's mapping).
+//
+// A workgroup of 4 waves handles 64 queries of one (b, h); lane c of a query
+// holds head dims [16c, 16c+16).  A gathered slot is read as the lane's 12
+// bytes of K codes and of V codes, the two fp16 scale pairs and (far offsets)
+// its z plane, so the four lanes of a query read one 128-byte slot.  Codes are
+// dequantised on read (v_bfe_i32 of the 6-bit fields); q.k is formed on the
+// integer codes and scaled once by the fp16 group scale, and the V codes are
+// rotated (MOVT pair of plane c) and accumulated with weight P * scale.
+// <q, e_j> + pb_j for the wave's 16 queries and all offsets is one MFMA pass
+// at the start (E staged in bf16, as the GPU path rounds it).  y is computed
+// in-kernel from q and the query probes (dsqg:3234-3249); z is read from the
+// slot.  Each wave walks its list of offsets with a source for one of its
+// queries, the next offset's slot reads in flight.
 // ---------------------------------------------------------------------------
-constexpr float kRescaleSlack = 8.0f;
+constexpr int kPfQPW = 16;          // queries per wave
+constexpr int kPfQPB = 64;          // queries per workgroup
+constexpr int kPfERow = 72;         // bf16 E row stride (elements)
+constexpr int kPfMaxBlocks = 17;    // JE / 16 for J <= 256 plus the sentinel
+
+struct PfLayout {
+  int JE, JL4, qe_row, list_len;
+  size_t off_ph, off_qp, off_list, off_big, bytes;
+};
+
+__host__ __device__ inline PfLayout pf_layout(int J, int J_large) {
+  PfLayout L;
+  L.JE = (J + 1 + 15) / 16 * 16;
+  L.JL4 = (J_large + 1) / 2 * 2;
+  L.qe_row = L.JE + 4;
+  L.list_len = (L.JE + 4 + 1) / 2 * 2;
+  L.off_ph = static_cast<size_t>(2 * L.JE) * 4;                       // s_pb[JE], s_off[JE]
+  L.off_qp = L.off_ph + static_cast<size_t>(L.JL4) * 4 * 8;           // s_ph[JL4][4] float2
+  L.off_list = L.off_qp + static_cast<size_t>(kPlanes * kHeadDim) * 4;   // s_qp[4][64]
+  L.off_big = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;    // s_list[4][list_len] int2
+  const size_t e_bytes = static_cast<size_t>(L.JE) * kPfERow * 2;
+  const size_t qe_bytes = static_cast<size_t>(4 * kPfQPW * L.qe_row) * 4;
+  L.bytes = L.off_big + (e_bytes > qe_bytes ? e_bytes : qe_bytes);  // sE, then s_qe
+  return L;
+}
+
+struct PfSlot {
+  uint32_t k0, k1, k2, v0, v1, v2, ks, vs;
+  float z;
+  bool ok;
+  int j;
+};
 
 template <int SHIFT>
-__global__ __launch_bounds__(kBlock) void q6_prefill_kernel(const dwarf_dsqg_q6_prefill_args a, int tiles, int total) {
-  constexpr int L = 2, DPL = 32, QPB = kBlock / L, HD = kHeadDim, SEG = HD / kPlanes;
+__global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_prefill_args a, int tiles, int total) {
+  constexpr float kC = 0.125f * kLog2e;
+  constexpr float kSlack2 = 8.0f * kLog2e;
+  static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
+  const int J = a.J, N = a.N, J_small = a.J_small;
+  const PfLayout lay = pf_layout(J, a.J_large);
   extern __shared__ float smem[];
-  float* s_se = smem;                       // [J][64]
-  float* s_pb = s_se + a.J * HD;            // [J]
-  float* s_qp = s_pb + a.J;                 // [4][64] query probes
-  int* s_off = reinterpret_cast<int*>(s_qp + kPlanes * HD);
+  char* sm = reinterpret_cast<char*>(smem);
+  float* s_pb = smem;
+  int* s_off = reinterpret_cast<int*>(smem + lay.JE);
+  float2* s_ph = reinterpret_cast<float2*>(sm + lay.off_ph);
+  float* s_qp = reinterpret_cast<float*>(sm + lay.off_qp);
+  int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
+  uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_big);
+  float* s_qe_all = reinterpret_cast<float*>(sm + lay.off_big);   // replaces sE after the second barrier
 
   const int work = xcd_remap(blockIdx.x, total);
   const int bh = work / tiles;
-  const int tile = work - bh * tiles;
+  const int tile = tiles - 1 - (work - bh * tiles);   // late query tiles first
   const int b = bh / a.H;
   const int h = bh - b * a.H;
   const int hk = h / (a.H / a.H_kv);
-  for (int i = threadIdx.x; i < a.J * HD; i += kBlock) {
-    const int j = i / HD, d = i - j * HD;
-    const float e = a.scale_embed[j * a.se_stride[0] + d * a.se_stride[1]];
-    s_se[i] = a.se_round_bf16 ? round_bf16(e) : e;
-  }
-  for (int j = threadIdx.x; j < a.J; j += kBlock) {
-    s_pb[j] = a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]];
-    s_off[j] = a.offsets[j];
-  }
-  for (int i = threadIdx.x; i < kPlanes * HD; i += kBlock) s_qp[i] = a.query_probes[i];
-  __syncthreads();
 
   const int lane = threadIdx.x;
-  const int g = lane % L;
-  const int n = tile * QPB + lane / L;
-  const int wave_n_last = uniform(tile * QPB + (lane / kWave) * (kWave / L)) + kWave / L - 1;
-  if (n >= a.N) return;
-  bf16* orow = reinterpret_cast<bf16*>(a.out) + b * a.out_stride[0] + h * a.out_stride[1] +
-               static_cast<int64_t>(n) * a.out_stride[2] + g * DPL;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int qi = l >> 2;
+  const int lr = l & 15, lc = l >> 4;
+  const int n0w = tile * kPfQPB + w * kPfQPW;
+  const int n = n0w + qi;
+  const int n_hi = min(n0w + kPfQPW - 1, N - 1);
+  const bool row_ok = n < N;
+  const bool live = row_ok && n >= a.query_start;
+  const int64_t nn = n;
+  float* s_qe = s_qe_all + w * kPfQPW * lay.qe_row;
+  int2* s_list = s_list_all + w * lay.list_len;
 
-  float acc[DPL];
+  // the wave's q rows (MFMA layout) and this lane's slice, requested first
+  const bf16* qbase = reinterpret_cast<const bf16*>(a.q) + b * a.q_stride[0] + h * a.q_stride[1];
+  uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if (n0w + lr < N) {
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
-  float m = -INFINITY, l = 0.f;
+    for (int ks = 0; ks < 2; ++ks)
+      xa[ks] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(n0w + lr) * a.q_stride[2] + 32 * ks + 8 * lc);
+  }
+  uint4 qx0 = {0u, 0u, 0u, 0u}, qx1 = {0u, 0u, 0u, 0u};
+  if (live) {
+    const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * a.q_stride[2] + 16 * g);
+    qx0 = q4[0];
+    qx1 = q4[1];
+  }
 
-  if (n >= a.query_start) {
-    float q[DPL];
-    load_f32<bf16, DPL>(reinterpret_cast<const bf16*>(a.q) + b * a.q_stride[0] + h * a.q_stride[1] +
-                            static_cast<int64_t>(n) * a.q_stride[2] + g * DPL, q);
-    // y[r] = <q, probe_r> / sqrt(|q|^2 + 1e-6 hd)  (dsqg:3234-3249)
-    float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < DPL; ++d) {
-      ss = fmaf(q[d], q[d], ss);
-#pragma unroll
-      for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(q[d], s_qp[r * HD + g * DPL + d], yp[r]);
-    }
-    ss = group_sum<L>(ss);
-    const float qinv = rsqrtf(ss + 1e-6f * HD);
-    float ys[4];
-#pragma unroll
-    for (int r = 0; r < kPlanes; ++r) ys[r] = group_sum<L>(yp[r]) * qinv;
+  stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kPfERow);
+  for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
+    s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
+    s_off[j] = j < J ? a.offsets[j] : 0;
+  }
+  for (int t = threadIdx.x; t < a.J_large * kPlanes; t += kBlock) {
+    const int i = t / kPlanes, r = t - i * kPlanes;
+    s_ph[t] = make_float2(a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r],
+                          a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r]);
+  }
+  for (int i = threadIdx.x; i < kPlanes * kHeadDim; i += kBlock) s_qp[i] = a.query_probes[i];
+  __syncthreads();
 
-    const uint8_t* cbase = a.cache + b * a.cache_stride[0] + hk * a.cache_stride[1];
-    constexpr float scale = 0.125f;
-    for (int j = 0; j < a.J; ++j) {
-      const int delta = s_off[j];
-      if (wave_n_last < delta) continue;
-      const int s = n - delta;
-      if (s < 0 || s >= a.N) continue;
-      const uint8_t* slot = cbase + static_cast<int64_t>(s) * a.cache_stride[2];
-      float c[DPL];
-      q6_codes(slot + kKCodes + 24 * g, c);
-      const float ksc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kKScales + 2 * g));
-      const float* e = s_se + j * HD + g * DPL;
-      float dk = 0.f, de = 0.f;
+  // s_qe[query][j] = log2(e) * (<q, e_j> / 8 + pb_j): products into registers,
+  // a barrier (every wave is done reading sE), then the tables over sE.
+  {
+    f32x4 c[kPfMaxBlocks];
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) { dk = fmaf(q[d], c[d], dk); de = fmaf(q[d], e[d], de); }
-      const float dot = group_sum<L>(fmaf(dk, ksc, de));
-      const float score = fmaf(dot, scale, s_pb[j]);
-
-      q6_codes(slot + kVCodes + 24 * g, c);
-      const float vsc = half_bits_to_f32(*reinterpret_cast<const uint16_t*>(slot + kVScales + 2 * g));
+    for (int bi = 0; bi < kPfMaxBlocks; ++bi) {
+      c[bi] = zero4();
+      if (bi * 16 < lay.JE) {
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) c[d] *= vsc;
-      if (j >= a.J_small) {
-        const int i = j - a.J_small;
-        const float4 zk = *reinterpret_cast<const float4*>(slot + kZ);
-        const float zs[4] = {zk.x, zk.y, zk.z, zk.w};
-#pragma unroll
-        for (int r = 0; r < kPlanes; ++r) {
-          const int ch = r * SEG + SHIFT;
-          if (ch / DPL != g) continue;
-          const int la = ch % DPL;
-          const float theta = a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r] +
-                              a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r] * ys[r] * zs[r];
-          float sn, cs;
-          dsincos<true>(theta, &sn, &cs);
-          const float va = c[la], vb = c[la + 1];
-          c[la] = cs * va - sn * vb;
-          c[la + 1] = sn * va + cs * vb;
+        for (int ks = 0; ks < 2; ++ks) {
+          const uint4 xb = *reinterpret_cast<const uint4*>(sE + (bi * 16 + lr) * kPfERow + 32 * ks + 8 * lc);
+          c[bi] = mfma16_bf16(bf16x8_from_bits(xa[ks]), bf16x8_from_bits(xb), c[bi]);
         }
       }
-      if (score > m + kRescaleSlack) {
-        const float cc = __expf(m - score);
+    }
+    __syncthreads();
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) acc[d] *= cc;
-        l *= cc;
-        m = score;
+    for (int bi = 0; bi < kPfMaxBlocks; ++bi) {
+      if (bi * 16 < lay.JE) {
+        const float pb8 = 8.0f * s_pb[bi * 16 + lr];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_qe[(4 * lc + r) * lay.qe_row + bi * 16 + lr] = (c[bi][r] + pb8) * kC;
       }
-      const float p = __expf(score - m);
-      l += p;
-#pragma unroll
-      for (int d = 0; d < DPL; ++d) acc[d] = fmaf(p, c[d], acc[d]);
     }
   }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (n0w >= N) return;                       // whole wave past the end (no block barriers below)
+  const int cnt = build_offset_list<1>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
+
+  // this lane's q slice in fp32, and y of plane g = <q, probe_g> / sqrt(|q|^2 + 1e-6 hd)
+  float qf[16];
+  {
+    const uint32_t w8[8] = {qx0.x, qx0.y, qx0.z, qx0.w, qx1.x, qx1.y, qx1.z, qx1.w};
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) acc[d] *= inv;
-  store_from_f32<bf16, DPL>(orow, acc);
+    for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(w8[i]); qf[2 * i + 1] = bf16_hi(w8[i]); }
+  }
+  float yg;
+  {
+    float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+      ss = fmaf(qf[d], qf[d], ss);
+#pragma unroll
+      for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(qf[d], s_qp[r * kHeadDim + 16 * g + d], yp[r]);
+    }
+    ss = group_sum<4>(ss);
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) yp[r] = group_sum<4>(yp[r]);
+    yg = (g == 0 ? yp[0] : g == 1 ? yp[1] : g == 2 ? yp[2] : yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
+  }
+
+  const int n_eff = live ? n : n0w - 2 * N;   // no source for a query that is not live
+  const uint8_t* cb = a.cache + b * a.cache_stride[0] + hk * a.cache_stride[1];
+  const int sstride = static_cast<int>(a.cache_stride[2]);
+  const __amdgpu_buffer_rsrc_t rc = rows_rsrc(cb, sstride, N, kSlot);
+  const int sb_lane = n_eff * sstride;
+  const bool khi = g >= 2;   // this lane's 16 dims are in group g / 2: scale in the high half
+
+  float acc[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+  float m = -3.0e38f, lsum = 0.f;
+
+  auto fetch = [&](int k0, PfSlot& s) {
+    const int2 e = s_list[k0];
+    const int j = uniform(e.x), d = uniform(e.y);
+    s.j = j;
+    s.ok = static_cast<uint32_t>(n_eff - d) < static_cast<uint32_t>(N);
+    const uint32_t base = static_cast<uint32_t>(sb_lane - d * sstride);
+    const auto kx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kKCodes + 12 * g, 0, 0);
+    const auto vx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kVCodes + 12 * g, 0, 0);
+    s.k0 = kx[0]; s.k1 = kx[1]; s.k2 = kx[2];
+    s.v0 = vx[0]; s.v1 = vx[1]; s.v2 = vx[2];
+    s.ks = cache_dword(rc, base + kKScales);
+    s.vs = cache_dword(rc, base + kVScales);
+    const bool far = j >= J_small && j < J;
+    s.z = __uint_as_float(cache_dword(rc, far ? base + kZ + 4 * g : kOutOfRange));
+  };
+
+  auto consume = [&](const PfSlot& s) {
+    float cf[16];
+    q6_codes16(s.k0, s.k1, s.k2, cf);
+    float kd = 0.f;
+#pragma unroll
+    for (int d = 0; d < 16; ++d) kd = fmaf(qf[d], cf[d], kd);
+    const float dot = group_sum<4>(kd * half_lo_or_hi(s.ks, khi));
+    const float s2 = s.ok ? fmaf(dot, kC, s_qe[qi * lay.qe_row + s.j]) : -INFINITY;
+    if (s2 > m + kSlack2) {
+      const float f = __builtin_amdgcn_exp2f(m - s2);   // 0 on the first valid offset
+#pragma unroll
+      for (int d = 0; d < 16; ++d) acc[d] *= f;
+      lsum *= f;
+      m = s2;
+    }
+    const float p = __builtin_amdgcn_exp2f(s2 - m);   // m is finite: 0 without a source
+    lsum += p;
+    q6_codes16(s.v0, s.v1, s.v2, cf);
+    if (s.j >= J_small && s.j < J) {   // wave-uniform
+      const float2 ph = s_ph[(s.j - J_small) * kPlanes + g];
+      float sn, cs;
+      dsincos<true>(fmaf(ph.y * yg, s.z, ph.x), &sn, &cs);
+      const float va = cf[SHIFT], vb = cf[SHIFT + 1];
+      cf[SHIFT] = cs * va - sn * vb;
+      cf[SHIFT + 1] = sn * va + cs * vb;
+    }
+    const float wgt = p * half_lo_or_hi(s.vs, khi);
+#pragma unroll
+    for (int d = 0; d < 16; ++d) acc[d] = fmaf(wgt, cf[d], acc[d]);
+    pin_regs<16>(acc);
+  };
+
+  if (cnt > 0) {
+    PfSlot s0, s1;
+    fetch(0, s0);
+    for (int k0 = 0; k0 < cnt; k0 += 2) {
+      fetch(k0 + 1, s1);   // past the list end this reads the sentinel: zeros
+      consume(s0);
+      fetch(k0 + 2, s0);
+      consume(s1);
+    }
+  }
+
+  if (!row_ok) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.out) + b * a.out_stride[0] + h * a.out_stride[1] +
+                                       nn * a.out_stride[2] + 16 * g);
+  uint4 x0, x1;
+  x0.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);   x0.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  x0.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);   x0.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
+  x1.x = pack_bf16x2(acc[8] * inv, acc[9] * inv);   x1.y = pack_bf16x2(acc[10] * inv, acc[11] * inv);
+  x1.z = pack_bf16x2(acc[12] * inv, acc[13] * inv); x1.w = pack_bf16x2(acc[14] * inv, acc[15] * inv);
+  o4[0] = x0;
+  o4[1] = x1;
   if (a.lse && g == 0)
-    a.lse[b * a.lse_stride[0] + h * a.lse_stride[1] + static_cast<int64_t>(n) * a.lse_stride[2]] =
-        l > 0.f ? m + __logf(l) : -INFINITY;
+    a.lse[b * a.lse_stride[0] + h * a.lse_stride[1] + nn * a.lse_stride[2]] =
+        lsum > 0.f ? (m + __builtin_amdgcn_logf(lsum)) * kLn2 : -INFINITY;
 }
 
 // ---------------------------------------------------------------------------
@@ -306,32 +460,6 @@ struct DecBatch {
   float z, pb2, base, gain;
   bool ok;
 };
-
-__device__ __forceinline__ uint32_t cache_dword(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-
-// Sixteen signed 6-bit codes of a 12-byte chunk (bits [6i, 6i+6) of w0:w1:w2).
-// v_bfe_i32 sign-extends the field; the builtin is typed unsigned, so the
-// result is reinterpreted as int before the conversion to float.
-__device__ __forceinline__ float sfield6(uint32_t w, int bit) {
-  return static_cast<float>(static_cast<int>(__builtin_amdgcn_sbfe(w, bit, 6)));
-}
-
-__device__ __forceinline__ void q6_codes16(uint32_t w0, uint32_t w1, uint32_t w2, float* c) {
-#pragma unroll
-  for (int i = 0; i < 5; ++i) c[i] = sfield6(w0, 6 * i);
-  c[5] = sfield6(__builtin_amdgcn_alignbit(w1, w0, 30), 0);
-#pragma unroll
-  for (int i = 6; i < 10; ++i) c[i] = sfield6(w1, 6 * i - 32);
-  c[10] = sfield6(__builtin_amdgcn_alignbit(w2, w1, 28), 0);
-#pragma unroll
-  for (int i = 11; i < 16; ++i) c[i] = sfield6(w2, 6 * i - 64);
-}
-
-__device__ __forceinline__ float half_lo_or_hi(uint32_t pair, bool hi) {
-  return half_bits_to_f32(static_cast<uint16_t>(hi ? pair >> 16 : pair));
-}
 
 struct DecLayout {
   int list_len;
@@ -549,12 +677,12 @@ hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const i
 }
 
 hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream) {
-  constexpr int QPB = kBlock / 2;
-  const int tiles = (a.N + QPB - 1) / QPB;
+  const int tiles = (a.N + kPfQPB - 1) / kPfQPB;
   const int total = tiles * a.B * a.H;
-  const size_t lds = (static_cast<size_t>(a.J) * (kHeadDim + 2) + kPlanes * kHeadDim) * sizeof(float);
+  if (total == 0) return hipSuccess;
+  const size_t lds = pf_layout(a.J, a.J_large).bytes;
 #define DWARF_Q6P_CASE(S) \
-  case S: hipLaunchKernelGGL(q6_prefill_kernel<S>, dim3(total), dim3(kBlock), lds, stream, a, tiles, total); break;
+  case S: hipLaunchKernelGGL(q6_prefill_q4<S>, dim3(total), dim3(kBlock), lds, stream, a, tiles, total); break;
   switch (a.plane_shift) {
     DWARF_Q6P_CASE(0) DWARF_Q6P_CASE(1) DWARF_Q6P_CASE(2) DWARF_Q6P_CASE(3) DWARF_Q6P_CASE(4)
     DWARF_Q6P_CASE(5) DWARF_Q6P_CASE(6) DWARF_Q6P_CASE(7) DWARF_Q6P_CASE(8) DWARF_Q6P_CASE(9)

@@ -44,7 +44,7 @@ def test_pack_matches_cpu_codec_bit_exact(pkg, device, dtype):
     assert np.allclose(z, rz, rtol=1e-5, atol=1e-6)
 
 
-def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs):
+def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs, return_lse=False):
     kd, vd, _ = q6_ref.unpack_slots(cache_np)
     inp = dict(x)
     inp["k"] = torch.from_numpy(kd).double()
@@ -52,7 +52,7 @@ def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs):
     inp["y_pre"] = features(x["q"].double(), qp).double()
     inp["z_pre"] = features(torch.from_numpy(kd).double(), kp).double()
     return dsqg_ref.dsqg_forward(*(inp[n].double() for n in NAMES), offsets, js, plane_shift=shift,
-                                 query_start=qs, round_se=True)
+                                 query_start=qs, round_se=True, return_lse=return_lse)
 
 
 def test_prefill_matches_oracle(pkg, device):
@@ -64,10 +64,14 @@ def test_prefill_matches_oracle(pkg, device):
     xd = {n: t.to(device) for n, t in x.items()}
     cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
     off = torch.tensor(offsets, dtype=torch.int32, device=device)
-    out = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"],
-                            xd["phase_gain"], qp.to(device), off, 17, 79, shift, 1)
-    ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, shift, qp, kp, 1)
+    out, lse = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"],
+                                 xd["phase_gain"], qp.to(device), off, 17, 79, shift, 1, return_lse=True)
+    ref, rlse = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, shift, qp, kp, 1, return_lse=True)
     assert max_abs(out, ref) < 2e-2
+    # lse (natural log, -inf before query_start) within the bf16 bar
+    assert torch.equal(torch.isinf(lse.cpu()), torch.isinf(rlse))
+    fin = torch.isfinite(rlse)
+    assert (lse.cpu().double()[fin] - rlse[fin]).abs().max().item() < 2e-2
 
 
 def test_decode_matches_oracle(pkg, device):
