@@ -469,7 +469,7 @@ struct DecLayout {
 __host__ __device__ inline DecLayout dec_layout(int J, int H) {
   DecLayout L;
   L.list_len = (J + 3 * kDecRows + 1) / 2 * 2;
-  L.off_off = static_cast<size_t>(J + 1) * kHeadDim * 4;           // sE[J + 1][64] (row J = 0)
+  L.off_off = static_cast<size_t>(J + 1) * kHeadDim * 4;           // sE hi and lo bf16 [2][J + 1][64] (row J = 0)
   L.off_list = L.off_off + static_cast<size_t>((J + 3) / 4 * 4) * 4;  // s_off[J]
   L.bytes = L.off_list + static_cast<size_t>(H) * L.list_len * 8;   // s_list[H][list_len] int2
   return L;
@@ -484,7 +484,8 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
   const DecLayout lay = dec_layout(J, H);
   extern __shared__ float smem[];
   char* sm = reinterpret_cast<char*>(smem);
-  float* sE = smem;
+  uint16_t* sEh = reinterpret_cast<uint16_t*>(smem);             // bf16(E)
+  uint16_t* sEl = sEh + (J + 1) * kHeadDim;                      // bf16(E - hi), without SE rounding
   int* s_off = reinterpret_cast<int*>(sm + lay.off_off);
   int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
 
@@ -493,12 +494,10 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
   const float* se = a.scale_embed + ly * a.se_stride[0];
   for (int i = threadIdx.x; i < (J + 1) * kHeadDim; i += blockDim.x) {
     const int j = i / kHeadDim, d = i - j * kHeadDim;
-    float e = 0.f;
-    if (j < J) {
-      e = se[j * a.se_stride[1] + d];
-      if (a.se_round_bf16) e = round_bf16(e);
-    }
-    sE[i] = e;
+    const float e = j < J ? se[j * a.se_stride[1] + d] : 0.f;
+    const uint16_t hi = f32_to_bf16_bits(e);
+    sEh[i] = hi;
+    sEl[i] = a.se_round_bf16 ? 0 : f32_to_bf16_bits(e - __uint_as_float(static_cast<uint32_t>(hi) << 16));
   }
   for (int j = threadIdx.x; j < J; j += blockDim.x) s_off[j] = a.offsets[j];
   __syncthreads();
@@ -517,13 +516,15 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
 
   // this lane's q chunk, |q|^2 and the probe features y (in-kernel, as dsqg:3231-3249)
   float qf[16];
+  uint32_t q32[8];
   {
     const uint4* q4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] +
                                                      ly * a.q_stride[1] + h * a.q_stride[2] + 16 * c);
     const uint4 x0 = q4[0], x1 = q4[1];
-    const uint32_t w[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    q32[0] = x0.x; q32[1] = x0.y; q32[2] = x0.z; q32[3] = x0.w;
+    q32[4] = x1.x; q32[5] = x1.y; q32[6] = x1.z; q32[7] = x1.w;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(w[i]); qf[2 * i + 1] = bf16_hi(w[i]); }
+    for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(q32[i]); qf[2 * i + 1] = bf16_hi(q32[i]); }
   }
   float yg;
   {
@@ -579,26 +580,29 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
     const int j = list[k0 + rr].x;
     float cf[16];
     q6_codes16(b.k0, b.k1, b.k2, cf);
-    const float4* e4 = reinterpret_cast<const float4*>(sE + j * kHeadDim + 16 * c);
     float kd = 0.f, ed = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 ev = e4[i];
-      kd = fmaf(qf[4 * i], cf[4 * i], kd);
-      kd = fmaf(qf[4 * i + 1], cf[4 * i + 1], kd);
-      kd = fmaf(qf[4 * i + 2], cf[4 * i + 2], kd);
-      kd = fmaf(qf[4 * i + 3], cf[4 * i + 3], kd);
-      ed = fmaf(qf[4 * i], ev.x, ed);
-      ed = fmaf(qf[4 * i + 1], ev.y, ed);
-      ed = fmaf(qf[4 * i + 2], ev.z, ed);
-      ed = fmaf(qf[4 * i + 3], ev.w, ed);
+    for (int d = 0; d < 16; ++d) kd = fmaf(qf[d], cf[d], kd);
+    {
+      // <q, e_j> on packed bf16 pairs (E high part; the low part when SE is not rounded)
+      const uint4* eh = reinterpret_cast<const uint4*>(sEh + j * kHeadDim + 16 * c);
+      const uint4 e0 = eh[0], e1 = eh[1];
+      const uint32_t ew[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ed = dot2bf(q32[i], ew[i], ed);
+      if (!a.se_round_bf16) {
+        const uint4* el = reinterpret_cast<const uint4*>(sEl + j * kHeadDim + 16 * c);
+        const uint4 l0 = el[0], l1 = el[1];
+        const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ed = dot2bf(q32[i], lw[i], ed);
+      }
     }
     const float dot = group_sum<4>(fmaf(kd, half_lo_or_hi(b.ks, khi), ed));
     const float s2 = b.ok ? fmaf(dot, kC, b.pb2) : -INFINITY;
     float mb = fmaxf(s2, dpp_f<0x124>(s2));    // rows of the 16-lane row: rotations by 4, 8
     mb = fmaxf(mb, dpp_f<0x128>(mb));
-    mb = fmaxf(mb, __shfl_xor(mb, 16));
-    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    mb = max_xor32(max_xor16(mb));
     if (mb > m + kSlack2) {   // wave-uniform
       const float f = __builtin_amdgcn_exp2f(m - mb);
 #pragma unroll
@@ -611,12 +615,16 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
     q6_codes16(b.v0, b.v1, b.v2, cf);
     const float vsc = half_lo_or_hi(b.vs, khi);
     const float wgt = p * vsc;
-    // MOVT pair of plane c (dims 16c + SHIFT, +1); near rows have angle 0
-    float sn, cs;
-    dsincos<true>(fmaf(b.gain * yg, b.z, b.base), &sn, &cs);
-    const float va = cf[SHIFT], vb = cf[SHIFT + 1];
-    cf[SHIFT] = cs * va - sn * vb;
-    cf[SHIFT + 1] = sn * va + cs * vb;
+    // MOVT pair of plane c (dims 16c + SHIFT, +1); near rows have angle 0.
+    // The list is ordered by offset index, so a batch whose last row is near
+    // has no far row.
+    if (uniform(list[k0 + kDecRows - 1].x) >= a.J_small) {
+      float sn, cs;
+      dsincos<true>(fmaf(b.gain * yg, b.z, b.base), &sn, &cs);
+      const float va = cf[SHIFT], vb = cf[SHIFT + 1];
+      cf[SHIFT] = cs * va - sn * vb;
+      cf[SHIFT + 1] = sn * va + cs * vb;
+    }
 #pragma unroll
     for (int d = 0; d < 16; ++d) acc[d] = fmaf(wgt, cf[d], acc[d]);
   };
