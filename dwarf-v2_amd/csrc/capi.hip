@@ -331,6 +331,9 @@ int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t s
   if (!a.pos || !a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "positions, a parameter table, probes or offsets is NULL");
   if (a.se_stride[2] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "scale_embed needs unit stride on head_dim");
+  if (a.pbase_stride[1] < 0 || a.pgain_stride[1] < 0 ||
+      (a.pbase_stride[1] + a.pgain_stride[1] + DWARF_R_PLANES) * 4 * static_cast<int64_t>(a.J_large) >= (int64_t(1) << 31))
+    return fail(DWARF_ERR_UNSUPPORTED, "decode reads a head's phase tables with 32-bit offsets (span below 2 GiB)");
   if (a.S == 0 || a.L == 0) return ok();
   return hip_status(dwarf::launch_q6_decode(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_q6_decode");
 }

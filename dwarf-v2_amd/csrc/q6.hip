@@ -443,13 +443,21 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
 // 52 + 12c), so four lanes per gathered row -- lane c holding dims
 // [16c, 16c+16) of K and of V -- cover a whole 128-byte slot, and one wave
 // load instruction fetches 16 slots.  Each wave lists the offsets whose row
-// t - delta is inside the cache, then walks the list in batches of 16 rows
-// with the next batch's loads in flight.  Per row the lanes dequantise on
-// read (v_bfe_i32 of the 6-bit fields, the fp16 group scale applied to the
-// partial sums), form <q, k + e_j> (E staged in LDS, bf16-rounded as the GPU
-// path does), run an online base-2 softmax over the batches and accumulate
-// P * R V; lane c rotates the MOVT pair of plane c.  The 16 row groups are
-// summed with DPP and lane shuffles at the end.
+// t - delta is inside the cache and requests its first batch of 16 rows
+// before the shared set-up:
+//   - the table T[head][j] = log2(e) (<q_head, e_j> / 8 + pb_j) for all heads
+//     of the workgroup and all offsets, one MFMA pass over 16-offset tiles
+//     (E in bf16, as the GPU path rounds it; a bf16 low part is added when SE
+//     is not rounded);
+//   - y of the head's query, one wave reduction per probe plane.
+// The wave then walks its list in batches of 16 rows with the next batch in
+// flight.  Per row, q.k is formed on the codes: each pair of 6-bit codes is
+// turned into the bf16 pair (160 + c_a, 160 + c_b) with three integer
+// instructions and consumed by v_dot2_f32_bf16, and 160 * sum(q) is
+// subtracted once; the fp16 group scale multiplies the lane's partial sum.
+// V codes are widened to fp32 (v_bfe_i32), rotated by the MOVT pair of plane
+// c and accumulated with weight P * scale under an online base-2 softmax.
+// The 16 row groups are summed with DPP and lane swaps at the end.
 // ---------------------------------------------------------------------------
 constexpr int kDecRows = 16;      // rows per batch (one per 4-lane group)
 constexpr int kMaxDecHeads = 16;  // waves per workgroup
@@ -457,103 +465,93 @@ constexpr int kMaxDecHeads = 16;  // waves per workgroup
 struct DecBatch {
   uint32_t k0, k1, k2, v0, v1, v2;
   uint32_t ks, vs;   // fp16 scale pairs of the two groups
-  float z, pb2, base, gain;
+  float z, base, gain;
+  int j;
   bool ok;
 };
 
 struct DecLayout {
-  int list_len;
-  size_t off_off, off_list, bytes;
+  int JE, list_len;
+  size_t off_list, bytes;
 };
 
 __host__ __device__ inline DecLayout dec_layout(int J, int H) {
   DecLayout L;
+  L.JE = (J + 1 + 15) / 16 * 16;                                   // offsets, the sentinel column, padding
   L.list_len = (J + 3 * kDecRows + 1) / 2 * 2;
-  L.off_off = static_cast<size_t>(J + 1) * kHeadDim * 4;           // sE hi and lo bf16 [2][J + 1][64] (row J = 0)
-  L.off_list = L.off_off + static_cast<size_t>((J + 3) / 4 * 4) * 4;  // s_off[J]
-  L.bytes = L.off_list + static_cast<size_t>(H) * L.list_len * 8;   // s_list[H][list_len] int2
+  L.off_list = static_cast<size_t>(H) * L.JE * 4;                  // s_T[H][JE]
+  L.bytes = L.off_list + static_cast<size_t>(H) * L.list_len * 8;  // s_list[H][list_len] int2
   return L;
 }
 
+// The bf16 pair (160 + c_a, 160 + c_b) of the two 6-bit codes in bits
+// [0, 12) of t (c_a low): code c in two's complement with its sign bit
+// flipped is c + 32, and bf16 0x4300 | m is 128 + m.
+__device__ __forceinline__ uint32_t code_pair_bf16(uint32_t t) {
+  const uint32_t f = t & 0xfffu;
+  return ((f | (f << 10)) & 0x003f003fu) ^ 0x43204320u;
+}
+
+// sum_d q_d (160 + c_d) over the 16 codes of a 12-byte chunk, on bf16 pairs.
+__device__ __forceinline__ float q6_dot16_biased(const uint32_t* q32, uint32_t w0, uint32_t w1, uint32_t w2) {
+  float s = 0.f;
+  s = dot2bf(q32[0], code_pair_bf16(w0), s);
+  s = dot2bf(q32[1], code_pair_bf16(w0 >> 12), s);
+  s = dot2bf(q32[2], code_pair_bf16(__builtin_amdgcn_alignbit(w1, w0, 24)), s);
+  s = dot2bf(q32[3], code_pair_bf16(w1 >> 4), s);
+  s = dot2bf(q32[4], code_pair_bf16(w1 >> 16), s);
+  s = dot2bf(q32[5], code_pair_bf16(__builtin_amdgcn_alignbit(w2, w1, 28)), s);
+  s = dot2bf(q32[6], code_pair_bf16(w2 >> 8), s);
+  s = dot2bf(q32[7], code_pair_bf16(w2 >> 20), s);
+  return s;
+}
+
+// Sum over all 64 lanes, in every lane.
+__device__ __forceinline__ float wave_allsum(float x) { return sum_over_queries16(group_sum<4>(x)); }
+
 template <int SHIFT>
-__global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const dwarf_dsqg_q6_decode_args a) {
+__global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf_dsqg_q6_decode_args a) {
   constexpr float kC = 0.125f * kLog2e;
   constexpr float kSlack2 = 8.0f * kLog2e;
   static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's chunk");
-  const int J = a.J, H = a.H;
+  const int J = a.J, H = a.H, J_small = a.J_small;
   const DecLayout lay = dec_layout(J, H);
   extern __shared__ float smem[];
-  char* sm = reinterpret_cast<char*>(smem);
-  uint16_t* sEh = reinterpret_cast<uint16_t*>(smem);             // bf16(E)
-  uint16_t* sEl = sEh + (J + 1) * kHeadDim;                      // bf16(E - hi), without SE rounding
-  int* s_off = reinterpret_cast<int*>(sm + lay.off_off);
-  int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
+  float* s_T = smem;
+  int2* s_list_all = reinterpret_cast<int2*>(reinterpret_cast<char*>(smem) + lay.off_list);
 
   const int sq = blockIdx.x / a.L;
   const int ly = blockIdx.x - sq * a.L;
-  const float* se = a.scale_embed + ly * a.se_stride[0];
-  for (int i = threadIdx.x; i < (J + 1) * kHeadDim; i += blockDim.x) {
-    const int j = i / kHeadDim, d = i - j * kHeadDim;
-    const float e = j < J ? se[j * a.se_stride[1] + d] : 0.f;
-    const uint16_t hi = f32_to_bf16_bits(e);
-    sEh[i] = hi;
-    sEl[i] = a.se_round_bf16 ? 0 : f32_to_bf16_bits(e - __uint_as_float(static_cast<uint32_t>(hi) << 16));
-  }
-  for (int j = threadIdx.x; j < J; j += blockDim.x) s_off[j] = a.offsets[j];
-  __syncthreads();
-
   const int h = uniform(threadIdx.x / kWave);   // head = wave index
   const int l = threadIdx.x % kWave;
   const int c = l & 3;        // 16-dim chunk
   const int rr = l >> 2;      // row of the batch
+  const int lr = l & 15, lc = l >> 4;
   const int hk = h / (H / a.H_kv);
-  const int t = a.pos[sq];
+  const int t = uniform(a.pos[sq]);
   const int Nc = a.Ncache;
   int2* list = s_list_all + h * lay.list_len;
-  // rows t - delta in [0, Nc); the sentinel offset t + 1 gives row -1
-  const int cnt = build_offset_list<kDecRows>(list, s_off, J, t, t, Nc, 1, make_int2(J, t + 1));
+  // rows t - delta in [0, Nc); the sentinel (J, t + 1) gives row -1
+  const int cnt = build_offset_list<kDecRows>(list, a.offsets, J, t, t, Nc, 1, make_int2(J, t + 1));
   const int cntp = (cnt + kDecRows - 1) / kDecRows * kDecRows;
 
-  // this lane's q chunk, |q|^2 and the probe features y (in-kernel, as dsqg:3231-3249)
-  float qf[16];
-  uint32_t q32[8];
-  {
-    const uint4* q4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] +
-                                                     ly * a.q_stride[1] + h * a.q_stride[2] + 16 * c);
-    const uint4 x0 = q4[0], x1 = q4[1];
-    q32[0] = x0.x; q32[1] = x0.y; q32[2] = x0.z; q32[3] = x0.w;
-    q32[4] = x1.x; q32[5] = x1.y; q32[6] = x1.z; q32[7] = x1.w;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(q32[i]); qf[2 * i + 1] = bf16_hi(q32[i]); }
-  }
-  float yg;
-  {
-    const float* qp = a.query_probes + ly * a.qprobe_layer_stride;
-    float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < 16; ++d) {
-      ss = fmaf(qf[d], qf[d], ss);
-#pragma unroll
-      for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(qf[d], qp[r * kHeadDim + 16 * c + d], yp[r]);
-    }
-    ss = group_sum<4>(ss);
-#pragma unroll
-    for (int r = 0; r < kPlanes; ++r) yp[r] = group_sum<4>(yp[r]);
-    const float qinv = rsqrtf(ss + 1e-6f * kHeadDim);
-    yg = (c == 0 ? yp[0] : c == 1 ? yp[1] : c == 2 ? yp[2] : yp[3]) * qinv;
-  }
-
   const uint8_t* cb = a.cache + ly * a.cache_stride[0] + sq * a.cache_stride[1] + hk * a.cache_stride[2];
-  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(cb), 0, static_cast<int>(static_cast<int64_t>(Nc) * kSlot), 0x00020000);
-  const float* pb = a.pos_bias + ly * a.pb_stride[0] + h * a.pb_stride[2];
-  const float* pbase = a.phase_base + ly * a.pbase_stride[0] + h * a.pbase_stride[2] + c;
-  const float* pgain = a.phase_gain + ly * a.pgain_stride[0] + h * a.pgain_stride[2] + c;
+  const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(cb), 0, Nc * kSlot,
+                                                                      0x00020000);
+  // MOVT angle parameters of this head (uniform resources): far index i,
+  // plane c at byte i * step + 4c
+  const int ph_step = static_cast<int>(a.pbase_stride[1]) * 4, pg_step = static_cast<int>(a.pgain_stride[1]) * 4;
+  const __amdgpu_buffer_rsrc_t rpb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.phase_base + ly * a.pbase_stride[0] + h * a.pbase_stride[2]), 0,
+      a.J_large > 0 ? (a.J_large - 1) * ph_step + 4 * kPlanes : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rpg = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.phase_gain + ly * a.pgain_stride[0] + h * a.pgain_stride[2]), 0,
+      a.J_large > 0 ? (a.J_large - 1) * pg_step + 4 * kPlanes : 0, 0x00020000);
   const bool khi = c >= 2;    // K/V group of this chunk: scale in the high half of the pair
 
   auto fetch = [&](int k0, DecBatch& b) {
     const int2 e = list[k0 + rr];
-    const int j = e.x;
+    b.j = e.x;
     const int row = t - e.y;
     b.ok = static_cast<uint32_t>(row) < static_cast<uint32_t>(Nc);
     const uint32_t base = b.ok ? static_cast<uint32_t>(row) * kSlot : kOutOfRange;
@@ -563,13 +561,88 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
     b.v0 = vx[0]; b.v1 = vx[1]; b.v2 = vx[2];
     b.ks = cache_dword(rc, base + kKScales);
     b.vs = cache_dword(rc, base + kVScales);
-    const bool far = j >= a.J_small && j < J;
+    const bool far = e.x >= J_small && e.x < J;
     b.z = __builtin_bit_cast(float, cache_dword(rc, far ? base + kZ + 4 * c : kOutOfRange));
-    b.pb2 = j < J ? kLog2e * pb[j * a.pb_stride[1]] : 0.f;
-    const int i = far ? j - a.J_small : 0;
-    b.base = far ? pbase[i * a.pbase_stride[1]] : 0.f;
-    b.gain = far ? pgain[i * a.pgain_stride[1]] : 0.f;
+    const int i = e.x - J_small;
+    b.base = buf_load_f32(rpb, far ? static_cast<uint32_t>(i * ph_step + 4 * c) : kOutOfRange);
+    b.gain = buf_load_f32(rpg, far ? static_cast<uint32_t>(i * pg_step + 4 * c) : kOutOfRange);
   };
+
+  DecBatch b0, b1;
+  if (cnt > 0) fetch(0, b0);
+
+  // T[i][j] for the workgroup's heads i: A = q rows (head i in row i), B = E^T
+  const bf16* qrows = reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1];
+  {
+    uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (lr < H) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        xa[ks] = *reinterpret_cast<const uint4*>(qrows + lr * a.q_stride[2] + 32 * ks + 8 * lc);
+    }
+    const float* se = a.scale_embed + ly * a.se_stride[0];
+    const float* pbl = a.pos_bias + ly * a.pb_stride[0];
+    for (int tile = h; tile < lay.JE / 16; tile += H) {   // wave-uniform
+      const int j = tile * 16 + lr;
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float e8[8];
+        if (j < J) {
+          const float4* p = reinterpret_cast<const float4*>(se + j * a.se_stride[1] + 32 * ks + 8 * lc);
+          const float4 u0 = p[0], u1 = p[1];
+          e8[0] = u0.x; e8[1] = u0.y; e8[2] = u0.z; e8[3] = u0.w;
+          e8[4] = u1.x; e8[5] = u1.y; e8[6] = u1.z; e8[7] = u1.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) e8[e] = 0.f;
+        }
+        if (a.se_round_bf16) {
+          bf16x8 hi;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hi[e] = static_cast<__bf16>(e8[e]);
+          acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), hi, acc);
+        } else {
+          bf16x8 hi, lo;
+          split_bf16x8(e8, hi, lo);
+          acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), hi, acc);
+          acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), lo, acc);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 4 * lc + r;
+        if (i < H) s_T[i * lay.JE + j] = j < J ? (acc[r] + 8.0f * pbl[j * a.pb_stride[1] + i * a.pb_stride[2]]) * kC : 0.f;
+      }
+    }
+  }
+
+  // this head's query: lane c's 16 dims as bf16 pairs, their sum, and y of
+  // plane c = <q, probe_c> / sqrt(|q|^2 + 1e-6 hd) (dsqg:3231-3249)
+  const bf16* qh = qrows + h * a.q_stride[2];
+  uint32_t q32[8];
+  {
+    const uint4* q4 = reinterpret_cast<const uint4*>(qh + 16 * c);
+    const uint4 x0 = q4[0], x1 = q4[1];
+    q32[0] = x0.x; q32[1] = x0.y; q32[2] = x0.z; q32[3] = x0.w;
+    q32[4] = x1.x; q32[5] = x1.y; q32[6] = x1.z; q32[7] = x1.w;
+  }
+  float qbias = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qbias = dot2bf(q32[i], 0x3f803f80u, qbias);   // (1, 1) in bf16
+  qbias *= -160.f;
+  float yg;
+  {
+    const float qd = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(qh)[l]) << 16);
+    const float* qp = a.query_probes + ly * a.qprobe_layer_stride;
+    const float ss = wave_allsum(qd * qd);
+    float yp[kPlanes];
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) yp[r] = wave_allsum(qd * qp[r * kHeadDim + l]);
+    yg = (c == 0 ? yp[0] : c == 1 ? yp[1] : c == 2 ? yp[2] : yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
+  }
+  const float* Th = s_T + h * lay.JE;
+  __syncthreads();   // T complete
 
   float acc[16];
 #pragma unroll
@@ -577,29 +650,9 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
   float m = -3.0e38f, lsum = 0.f;
 
   auto consume = [&](int k0, const DecBatch& b) {
-    const int j = list[k0 + rr].x;
-    float cf[16];
-    q6_codes16(b.k0, b.k1, b.k2, cf);
-    float kd = 0.f, ed = 0.f;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) kd = fmaf(qf[d], cf[d], kd);
-    {
-      // <q, e_j> on packed bf16 pairs (E high part; the low part when SE is not rounded)
-      const uint4* eh = reinterpret_cast<const uint4*>(sEh + j * kHeadDim + 16 * c);
-      const uint4 e0 = eh[0], e1 = eh[1];
-      const uint32_t ew[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ed = dot2bf(q32[i], ew[i], ed);
-      if (!a.se_round_bf16) {
-        const uint4* el = reinterpret_cast<const uint4*>(sEl + j * kHeadDim + 16 * c);
-        const uint4 l0 = el[0], l1 = el[1];
-        const uint32_t lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ed = dot2bf(q32[i], lw[i], ed);
-      }
-    }
-    const float dot = group_sum<4>(fmaf(kd, half_lo_or_hi(b.ks, khi), ed));
-    const float s2 = b.ok ? fmaf(dot, kC, b.pb2) : -INFINITY;
+    const float kd = q6_dot16_biased(q32, b.k0, b.k1, b.k2) + qbias;
+    const float dot = group_sum<4>(kd * half_lo_or_hi(b.ks, khi));
+    const float s2 = b.ok ? fmaf(dot, kC, Th[b.j]) : -INFINITY;
     float mb = fmaxf(s2, dpp_f<0x124>(s2));    // rows of the 16-lane row: rotations by 4, 8
     mb = fmaxf(mb, dpp_f<0x128>(mb));
     mb = max_xor32(max_xor16(mb));
@@ -612,26 +665,25 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_kernel(const d
     }
     const float p = __builtin_amdgcn_exp2f(s2 - m);
     lsum += p;
+    float cf[16];
     q6_codes16(b.v0, b.v1, b.v2, cf);
-    const float vsc = half_lo_or_hi(b.vs, khi);
-    const float wgt = p * vsc;
     // MOVT pair of plane c (dims 16c + SHIFT, +1); near rows have angle 0.
     // The list is ordered by offset index, so a batch whose last row is near
     // has no far row.
-    if (uniform(list[k0 + kDecRows - 1].x) >= a.J_small) {
+    if (uniform(list[k0 + kDecRows - 1].x) >= J_small) {
       float sn, cs;
       dsincos<true>(fmaf(b.gain * yg, b.z, b.base), &sn, &cs);
       const float va = cf[SHIFT], vb = cf[SHIFT + 1];
       cf[SHIFT] = cs * va - sn * vb;
       cf[SHIFT + 1] = sn * va + cs * vb;
     }
+    const float wgt = p * half_lo_or_hi(b.vs, khi);
 #pragma unroll
     for (int d = 0; d < 16; ++d) acc[d] = fmaf(wgt, cf[d], acc[d]);
+    pin_regs<16>(acc);
   };
 
   if (cnt > 0) {
-    DecBatch b0, b1;
-    fetch(0, b0);
     for (int k0 = 0; k0 < cntp; k0 += 2 * kDecRows) {
       fetch(k0 + kDecRows, b1);
       consume(k0, b0);
@@ -705,7 +757,7 @@ hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stre
   const int blocks = a.S * a.L;
   const size_t lds = dec_layout(a.J, a.H).bytes;
 #define DWARF_Q6D_CASE(S) \
-  case S: hipLaunchKernelGGL(q6_decode_kernel<S>, dim3(blocks), dim3(kWave * a.H), lds, stream, a); break;
+  case S: hipLaunchKernelGGL(q6_decode_q4<S>, dim3(blocks), dim3(kWave * a.H), lds, stream, a); break;
   switch (a.plane_shift) {
     DWARF_Q6D_CASE(0) DWARF_Q6D_CASE(1) DWARF_Q6D_CASE(2) DWARF_Q6D_CASE(3) DWARF_Q6D_CASE(4)
     DWARF_Q6D_CASE(5) DWARF_Q6D_CASE(6) DWARF_Q6D_CASE(7) DWARF_Q6D_CASE(8) DWARF_Q6D_CASE(9)

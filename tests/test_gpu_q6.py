@@ -97,3 +97,27 @@ def test_decode_matches_oracle(pkg, device):
         for s in range(S):
             t = int(pos[s])
             assert max_abs(out[s, l], ref[s, :, t]) < 2e-2, (s, l)
+
+
+def test_decode_full_lattice_eight_heads(pkg, device):
+    """H = H_kv = 8 (one table tile per wave but one), plane shift 5, a row
+    with no valid offset (t = 0 gives out = 0), a row with only near offsets
+    and one past the largest offset (all 96 valid)."""
+    offsets = list(pkg.ALL_OFFSETS)
+    shift = 5
+    S, H, N = 4, 8, 2300
+    x = make_inputs(S, H, H, N, offsets, 17, seed=91, dtype=torch.bfloat16, plane_shift=shift, gain_std=6.0)
+    pos = torch.tensor([0, 40, 1000, 2250], dtype=torch.int32)
+    qp, kp = orthogonal_probes(64, shift)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    cache = pkg.q6.pack_kv(x["k"].to(device), x["v"].to(device), kp.to(device))
+    qdec = torch.stack([x["q"][s, :, int(pos[s])] for s in range(S)]).unsqueeze(1)
+    tables = {n: x[n].unsqueeze(0).to(device) for n in ("pos_bias", "scale_embed", "phase_base", "phase_gain")}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_decode(qdec.to(device), pos.to(device), cache.unsqueeze(0), tables["pos_bias"],
+                           tables["scale_embed"], tables["phase_base"], tables["phase_gain"],
+                           qp.unsqueeze(0).to(device), off, 17, 79, shift).cpu()
+    assert not out[0].any()
+    ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, shift, qp, kp, 0)
+    for s in range(S):
+        assert max_abs(out[s, 0], ref[s, :, int(pos[s])]) < 2e-2, s
