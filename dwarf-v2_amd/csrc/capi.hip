@@ -326,7 +326,7 @@ int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t s
   if (static_cast<int64_t>(a.Ncache) * DWARF_Q6_SLOT_BYTES >= (int64_t(1) << 31))
     return fail(DWARF_ERR_UNSUPPORTED, "decode gathers with 32-bit offsets: Ncache x 128 B must stay below 2 GiB");
   if ((rc = check_rows("q", a.q, a.q_stride, 3, DWARF_BF16))) return rc;
-  if (!a.out || a.out_stride[3] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "out is NULL or not unit-stride");
+  if ((rc = check_rows("out", a.out, a.out_stride, 3, DWARF_BF16))) return rc;
   if ((rc = check_cache(a.cache, a.cache_stride, 3))) return rc;
   if (!a.pos || !a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "positions, a parameter table, probes or offsets is NULL");

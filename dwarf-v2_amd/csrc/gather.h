@@ -108,6 +108,20 @@ __device__ __forceinline__ float add_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Reduce-scatter halves of the two swaps: v_permlane32_swap exchanges the
+// upper 32 lanes of its first operand with the lower 32 lanes of its second,
+// so the sum of the two results is x + x of lane ^ 32 in lanes 0-31 and
+// y + y of lane ^ 32 in lanes 32-63.  v_permlane16_swap does the same per
+// pair of 16-lane rows: x sums in rows 0 and 2, y sums in rows 1 and 3.
+__device__ __forceinline__ float add_swap32(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_swap16(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float max_xor16(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));

@@ -456,8 +456,10 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
 // instructions and consumed by v_dot2_f32_bf16, and 160 * sum(q) is
 // subtracted once; the fp16 group scale multiplies the lane's partial sum.
 // V codes are widened to fp32 (v_bfe_i32), rotated by the MOVT pair of plane
-// c and accumulated with weight P * scale under an online base-2 softmax.
-// The 16 row groups are summed with DPP and lane swaps at the end.
+// c and accumulated with weight P * scale under an online base-2 softmax in
+// which each row group keeps its own running maximum.  At the end the groups
+// are put on the wave's largest maximum and summed (lane swaps that
+// reduce-scatter the 16 dims of a lane, then DPP row rotations).
 // ---------------------------------------------------------------------------
 constexpr int kDecRows = 16;      // rows per batch (one per 4-lane group)
 constexpr int kMaxDecHeads = 16;  // waves per workgroup
@@ -653,15 +655,12 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
     const float kd = q6_dot16_biased(q32, b.k0, b.k1, b.k2) + qbias;
     const float dot = group_sum<4>(kd * half_lo_or_hi(b.ks, khi));
     const float s2 = b.ok ? fmaf(dot, kC, Th[b.j]) : -INFINITY;
-    float mb = fmaxf(s2, dpp_f<0x124>(s2));    // rows of the 16-lane row: rotations by 4, 8
-    mb = fmaxf(mb, dpp_f<0x128>(mb));
-    mb = max_xor32(max_xor16(mb));
-    if (mb > m + kSlack2) {   // wave-uniform
-      const float f = __builtin_amdgcn_exp2f(m - mb);
+    if (s2 > m + kSlack2) {   // per row group; the groups are put on one scale at the end
+      const float f = __builtin_amdgcn_exp2f(m - s2);
 #pragma unroll
       for (int d = 0; d < 16; ++d) acc[d] *= f;
       lsum *= f;
-      m = mb;
+      m = s2;
     }
     const float p = __builtin_amdgcn_exp2f(s2 - m);
     lsum += p;
@@ -691,21 +690,36 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
       consume(k0 + kDecRows, b1);
     }
   }
-  // sum the 16 row groups (lanes with the same chunk)
-  lsum = sum_over_queries16(lsum);
+  // Row groups onto the wave's largest reference, then the sum over the 16
+  // groups of each (chunk, dim), reduce-scattered: after the two lane swaps
+  // lane l holds dims 16c + 8 (l >> 5) + 4 ((l >> 4) & 1) + [0, 4) of four
+  // groups, and two row rotations add the other twelve.
+  float M = fmaxf(m, dpp_f<0x124>(m));
+  M = fmaxf(M, dpp_f<0x128>(M));
+  M = max_xor32(max_xor16(M));
+  const float sc = __builtin_amdgcn_exp2f(m - M);   // 0 for a group that saw no row
+  lsum = sum_over_queries16(lsum * sc);
+  float o[4];
+  {
+    float r[8];
 #pragma unroll
-  for (int d = 0; d < 16; ++d) acc[d] = sum_over_queries16(acc[d]);
-  if (rr == 0) {
+    for (int i = 0; i < 8; ++i) r[i] = add_swap32(acc[i] * sc, acc[i + 8] * sc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = add_swap16(r[i], r[i + 4]);
+      x += dpp_f<0x124>(x);   // row_ror:4
+      x += dpp_f<0x128>(x);   // row_ror:8
+      o[i] = x;
+    }
+  }
+  if ((rr & 3) == 0) {
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.out) + sq * a.out_stride[0] + ly * a.out_stride[1] +
-                                         h * a.out_stride[2] + 16 * c);
-    uint4 x;
-    x.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);   x.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
-    x.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);   x.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
-    o4[0] = x;
-    x.x = pack_bf16x2(acc[8] * inv, acc[9] * inv);   x.y = pack_bf16x2(acc[10] * inv, acc[11] * inv);
-    x.z = pack_bf16x2(acc[12] * inv, acc[13] * inv); x.w = pack_bf16x2(acc[14] * inv, acc[15] * inv);
-    o4[1] = x;
+    const int d0 = 16 * c + 8 * (l >> 5) + 4 * ((l >> 4) & 1);
+    uint2 x;
+    x.x = pack_bf16x2(o[0] * inv, o[1] * inv);
+    x.y = pack_bf16x2(o[2] * inv, o[3] * inv);
+    *reinterpret_cast<uint2*>(reinterpret_cast<bf16*>(a.out) + sq * a.out_stride[0] + ly * a.out_stride[1] +
+                              h * a.out_stride[2] + d0) = x;
   }
 }
 
