@@ -5,23 +5,24 @@
 // channels of one (b, chunk), so a wave reads 64*VEC consecutive channels of
 // one token per load.
 //   forward:  local  - chunk end state with zero carry-in (reads x)
-//             carry  - one wave per (b, channel) scans the chunk ends and
-//                      writes each chunk's carry-in (tiny)
+//             carry  - one workgroup per (b, 64 channels) scans the chunk
+//                      ends and writes each chunk's carry-in (tiny)
 //             apply  - rescans the chunk from its carry-in, writes y
 //   backward: the same three stages run in reverse time on dy for the
 //             adjoint lambda[t] = dy[t] + (1 - a) lambda[t+1]; the apply
 //             stage writes dx = a * lambda and a per-lane partial of
-//             dalpha = sum lambda[t] (x[t] - y[t-1]); one wave per channel
-//             sums the partials in a fixed order and applies the
+//             dalpha = sum lambda[t] (x[t] - y[t-1]); one workgroup per 64
+//             channels sums the partials in a fixed order and applies the
 //             projected-clamp rule of ema:357-364.
-// The carry stage is a fixed-shape parallel scan over the chunks.
+// The carry and dalpha stages read the [B][NC][D] per-chunk arrays in
+// coalesced rows (lane = channel) and combine in a fixed order.
 // Alpha may be one value (the reference contract, ema:557-558) or one per
 // channel; the clamp to [floor, ceiling] happens in-kernel (ema:274-277).
 #include "common.h"
 
 namespace dwarf {
 
-constexpr int kChunkT = 32;
+constexpr int kChunkT = 16;
 constexpr int kEmaBlock = 256;
 
 namespace {
@@ -123,47 +124,69 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__
   for (int i = 0; i < VEC; ++i) e[i] = st[i];
 }
 
-// One wave per (b, channel): carries[c] = state entering chunk c (REVERSE:
-// the adjoint entering chunk c from the future).  With A = decay^kChunkT the
-// chunks compose as s(next) = A s + ends[c]; each lane folds a contiguous
-// segment of chunks into (A_seg, B_seg), a Hillis-Steele scan over the 64
-// lanes (fixed shape) gives every segment its incoming state, and the lane
-// then writes the carries of its chunks.
+// Carry stage, one workgroup of kCarryWaves waves per (b, block of 64
+// channels): carries[c] = state entering chunk c (REVERSE: the adjoint
+// entering chunk c from the future).  Lane l owns channel d0 + l, so every
+// access is a coalesced row of the [B][NC][D] chunk-state arrays; wave w owns
+// a contiguous segment of chunks in scan order.  With A = decay^kChunkT the
+// chunks compose as s(next) = A s + ends[c]: each lane folds its segment into
+// (A_seg, B_seg), the segments are combined in order through LDS, and the
+// lane rescans its segment writing each chunk's incoming state.
+constexpr int kCarryWaves = 16;
+constexpr int kCarrySeg = 32;   // chunk states a lane holds in registers per pass
+constexpr int kDaRows = 16;     // dalpha partials loaded per block
+
 template <bool REVERSE>
-__global__ __launch_bounds__(kEmaBlock) void ema_carry(const float* __restrict__ ends, float* __restrict__ carries,
-                                                      const float* __restrict__ alpha, EmaGeom g) {
-  const int wave = (blockIdx.x * kEmaBlock + threadIdx.x) / kWave;
-  const int l = threadIdx.x % kWave;
-  if (wave >= g.B * g.D) return;   // whole wave
-  const int b = wave / g.D, d = wave - b * g.D;
-  const float decay = 1.f - clamp_alpha(alpha, g.per_channel, d, g.lo, g.hi);
+__global__ __launch_bounds__(kWave * kCarryWaves) void ema_carry(const float* __restrict__ ends,
+                                                                 float* __restrict__ carries,
+                                                                 const float* __restrict__ alpha, EmaGeom g) {
+  __shared__ float sA[kCarryWaves][kWave], sB[kCarryWaves][kWave];
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  const int nblk = (g.D + kWave - 1) / kWave;
+  const int b = blockIdx.x / nblk;
+  const int d = (blockIdx.x - b * nblk) * kWave + l;
+  const bool live = d < g.D;
+  const float decay = live ? 1.f - clamp_alpha(alpha, g.per_channel, d, g.lo, g.hi) : 0.f;
   float full = 1.f;  // decay^kChunkT, by repeated multiplication as a serial scan applies it
   for (int i = 0; i < kChunkT; ++i) full *= decay;
+  const int seg = (g.NC + kCarryWaves - 1) / kCarryWaves;
+  const int k0 = w * seg, k1 = min(k0 + seg, g.NC);
+  auto chunk = [&](int k) { return REVERSE ? g.NC - 1 - k : k; };
   const float* e = ends + static_cast<int64_t>(b) * g.NC * g.D + d;
   float* cr = carries + static_cast<int64_t>(b) * g.NC * g.D + d;
-  const int seg = (g.NC + kWave - 1) / kWave;    // chunks per lane, in scan order
-  const int k0 = l * seg;
-  auto chunk = [&](int k) { return REVERSE ? g.NC - 1 - k : k; };
+  // fold the segment: s_out = A s_in + Bv
   float A = 1.f, Bv = 0.f;
-  for (int k = k0; k < min(k0 + seg, g.NC); ++k) {
-    Bv = fmaf(full, Bv, e[static_cast<int64_t>(chunk(k)) * g.D]);
-    A *= full;
-  }
-  // inclusive scan: (earlier) then (this) = (A_this A_earlier, A_this B_earlier + B_this)
+  float ev[kCarrySeg];   // the segment's first kCarrySeg chunk states, kept for the second pass
+  if (live) {
+    for (int kb = k0; kb < k1; kb += kCarrySeg) {
 #pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const float Ae = __shfl_up(A, o), Be = __shfl_up(Bv, o);
-    if (l >= o) {
-      Bv = fmaf(A, Be, Bv);
-      A *= Ae;
+      for (int r = 0; r < kCarrySeg; ++r) ev[r] = kb + r < k1 ? e[static_cast<int64_t>(chunk(kb + r)) * g.D] : 0.f;
+#pragma unroll
+      for (int r = 0; r < kCarrySeg; ++r)
+        if (kb + r < k1) {
+          Bv = fmaf(full, Bv, ev[r]);
+          A *= full;
+        }
     }
   }
-  float s = __shfl_up(Bv, 1);
-  if (l == 0) s = 0.f;
-  for (int k = k0; k < min(k0 + seg, g.NC); ++k) {
-    const int c = chunk(k);
-    cr[static_cast<int64_t>(c) * g.D] = s;
-    s = fmaf(full, s, e[static_cast<int64_t>(c) * g.D]);
+  sA[w][l] = A;
+  sB[w][l] = Bv;
+  __syncthreads();
+  float s = 0.f;   // state entering this wave's segment
+  for (int v = 0; v < w; ++v) s = fmaf(sA[v][l], s, sB[v][l]);
+  if (live) {
+    for (int kb = k0; kb < k1; kb += kCarrySeg) {
+      if (kb != k0 || seg > kCarrySeg) {   // reload unless the whole segment is still in registers
+#pragma unroll
+        for (int r = 0; r < kCarrySeg; ++r) ev[r] = kb + r < k1 ? e[static_cast<int64_t>(chunk(kb + r)) * g.D] : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < kCarrySeg; ++r)
+        if (kb + r < k1) {
+          cr[static_cast<int64_t>(chunk(kb + r)) * g.D] = s;
+          s = fmaf(full, s, ev[r]);
+        }
+    }
   }
 }
 
@@ -302,29 +325,44 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
   for (int i = 0; i < VEC; ++i) dp[i] = da[i];
 }
 
-// dalpha: one wave per channel sums its B * NC partial rows (lane k takes
-// rows k, k + 64, ... in order, then a fixed butterfly over the lanes).  For a
-// per-channel alpha the projected-clamp rule is applied per channel; for a
-// single alpha the channel sums go to `tmp` and a second pass adds them in
-// order.
-__global__ __launch_bounds__(kEmaBlock) void ema_dalpha_channels(const float* __restrict__ da_part,
-                                                                const float* __restrict__ alpha,
-                                                                float* __restrict__ out, EmaGeom g) {
-  const int d = (blockIdx.x * kEmaBlock + threadIdx.x) / kWave;
-  const int l = threadIdx.x % kWave;
-  if (d >= g.D) return;   // whole wave
+// dalpha, one workgroup of kCarryWaves waves per block of 64 channels: wave w
+// sums rows w, w + kCarryWaves, ... of the [B * NC][D] partials for lane l's
+// channel (coalesced rows, in row order), then wave 0 adds the wave sums in
+// wave order.  For a per-channel alpha the projected-clamp rule is applied per
+// channel; for a single alpha the channel sums go to `out` and a second pass
+// adds them in order.
+__global__ __launch_bounds__(kWave * kCarryWaves) void ema_dalpha_channels(const float* __restrict__ da_part,
+                                                                           const float* __restrict__ alpha,
+                                                                           float* __restrict__ out, EmaGeom g) {
+  __shared__ float sS[kCarryWaves][kWave];
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  const int d = blockIdx.x * kWave + l;
+  const bool live = d < g.D;
   const int rows = g.B * g.NC;
   float s = 0.f;
-  for (int r = l; r < rows; r += kWave) s += da_part[static_cast<int64_t>(r) * g.D + d];
+  if (live) {
+    for (int r0 = w; r0 < rows; r0 += kCarryWaves * kDaRows) {
+      float v[kDaRows];
 #pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) s += __shfl_xor(s, o);
-  if (l == 0) {
+      for (int i = 0; i < kDaRows; ++i) {
+        const int r = r0 + i * kCarryWaves;
+        v[i] = r < rows ? da_part[static_cast<int64_t>(r) * g.D + d] : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < kDaRows; ++i) s += v[i];
+    }
+  }
+  sS[w][l] = s;
+  __syncthreads();
+  if (w == 0 && live) {
+    float t = 0.f;
+    for (int v = 0; v < kCarryWaves; ++v) t += sS[v][l];
     if (g.per_channel) {
       const float ai = alpha[d];
-      const bool blocked = (ai <= g.lo && s > 0.f) || (ai >= g.hi && s < 0.f);
-      out[d] = blocked ? 0.f : s;
+      const bool blocked = (ai <= g.lo && t > 0.f) || (ai >= g.hi && t < 0.f);
+      out[d] = blocked ? 0.f : t;
     } else {
-      out[d] = s;
+      out[d] = t;
     }
   }
 }
@@ -369,8 +407,9 @@ hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
   T* y = static_cast<T*>(a.y);
   hipLaunchKernelGGL((ema_fwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], a.alpha, ends, g);
-  hipLaunchKernelGGL((ema_carry<false>), dim3((a.B * a.D + kEmaBlock / kWave - 1) / (kEmaBlock / kWave)),
-                     dim3(kEmaBlock), 0, stream, ends, carries, a.alpha, g);
+  const int cblocks = a.B * ((a.D + kWave - 1) / kWave);
+  hipLaunchKernelGGL((ema_carry<false>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, ends, carries,
+                     a.alpha, g);
   hipLaunchKernelGGL((ema_fwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], y, a.y_stride[0], a.y_stride[1], a.alpha, carries, g);
   return hipGetLastError();
@@ -387,19 +426,22 @@ hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
   hipLaunchKernelGGL((ema_bwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
                      static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1], a.alpha, starts, g);
-  hipLaunchKernelGGL((ema_carry<true>), dim3((a.B * a.D + kEmaBlock / kWave - 1) / (kEmaBlock / kWave)),
-                     dim3(kEmaBlock), 0, stream, starts, carries, a.alpha, g);
+  const int cblocks = a.B * ((a.D + kWave - 1) / kWave);
+  hipLaunchKernelGGL((ema_carry<true>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, starts, carries,
+                     a.alpha, g);
   hipLaunchKernelGGL((ema_bwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
                      static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<const T*>(a.y),
                      a.y_stride[0], a.y_stride[1], static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1],
                      static_cast<T*>(a.dx), a.dx_stride[0], a.dx_stride[1], a.alpha, carries, da_part, g);
   if (a.dalpha) {
-    const int rb = (a.D + kEmaBlock / kWave - 1) / (kEmaBlock / kWave);
+    const int rb = (a.D + kWave - 1) / kWave;
     if (a.alpha_per_channel) {
-      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kEmaBlock), 0, stream, da_part, a.alpha, a.dalpha, g);
+      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kWave * kCarryWaves), 0, stream, da_part, a.alpha,
+                         a.dalpha, g);
     } else {
       float* chan = starts;   // free after the apply stage; D <= B * NC * D floats
-      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kEmaBlock), 0, stream, da_part, a.alpha, chan, g);
+      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kWave * kCarryWaves), 0, stream, da_part, a.alpha,
+                         chan, g);
       hipLaunchKernelGGL(ema_dalpha_scalar, dim3(1), dim3(kWave), 0, stream, chan, a.alpha, a.dalpha, g);
     }
   }

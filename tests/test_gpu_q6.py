@@ -121,3 +121,41 @@ def test_decode_full_lattice_eight_heads(pkg, device):
     ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, shift, qp, kp, 0)
     for s in range(S):
         assert max_abs(out[s, 0], ref[s, :, int(pos[s])]) < 2e-2, s
+
+
+def test_decode_graph_replay_matches_eager(pkg, device):
+    """The decode launch captured in a HIP graph: each replay (eager work and
+    synchronisations between them) equals the eager output bit for bit."""
+    offsets = list(pkg.ALL_OFFSETS)
+    S, H, N = 5, 8, 600
+    x = make_inputs(S, H, 2, N, offsets, 17, seed=13, dtype=torch.bfloat16, plane_shift=2, gain_std=3.0)
+    qp, kp = orthogonal_probes(64, 2)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    cache = pkg.q6.pack_kv(x["k"].to(device), x["v"].to(device), kp.to(device)).unsqueeze(0)
+    pos = torch.tensor([99, 300, 599, 150, 420], dtype=torch.int32, device=device)
+    qdec = torch.stack([x["q"][s, :, int(pos[s])] for s in range(S)]).unsqueeze(1).to(device)
+    tab = {n: x[n].unsqueeze(0).to(device) for n in ("pos_bias", "scale_embed", "phase_base", "phase_gain")}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    qps = qp.unsqueeze(0).to(device)
+
+    def step():
+        return pkg.q6.q6_decode(qdec, pos, cache, tab["pos_bias"], tab["scale_embed"], tab["phase_base"],
+                                tab["phase_gain"], qps, off, 17, 79, 2)
+
+    ref = step().clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    for _ in range(3):
+        other = pkg.q6.pack_kv(x["v"].to(device), x["k"].to(device), kp.to(device))   # eager work
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        del other
