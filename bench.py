@@ -281,6 +281,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context"],
+                    help="run only this extra workload and print its JSON (for per-workload profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 10 times (scales HBM byte counters)")
     args = ap.parse_args()
@@ -303,6 +305,11 @@ def main() -> int:
         return 0
     pkg = importlib.import_module("dwarf-v2_amd")
     pkg._lib.load()
+    if args.extra_only:
+        fn = {"q6_decode": q6_decode_extra, "q6_prefill": q6_prefill_extra,
+              "long_context": long_context_extra}[args.extra_only]
+        print(json.dumps({args.extra_only: fn(pkg, device, args.steps, args.warmup)}), flush=True)
+        return 0
     B, H, N = 15, 8, 2048
     log("training microbatch: DSQG fwd+bwd B15 H8 T2048 bf16")
     t, js, jl = synth(pkg, B, H, N, 0, device)

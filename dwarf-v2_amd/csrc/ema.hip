@@ -5,20 +5,21 @@
 // channels of one (b, chunk), so a wave reads 64*VEC consecutive channels of
 // one token per load.
 //   forward:  local  - chunk end state with zero carry-in (reads x)
-//             carry  - one workgroup per (b, 64 channels) scans the chunk
+//             carry  - one workgroup per (b, 16 channels) scans the chunk
 //                      ends and writes each chunk's carry-in (tiny)
 //             apply  - rescans the chunk from its carry-in, writes y
 //   backward: the same three stages run in reverse time on dy for the
 //             adjoint lambda[t] = dy[t] + (1 - a) lambda[t+1]; the apply
 //             stage writes dx = a * lambda and a per-lane partial of
-//             dalpha = sum lambda[t] (x[t] - y[t-1]); one workgroup per 64
+//             dalpha = sum lambda[t] (x[t] - y[t-1]); one workgroup per 16
 //             channels sums the partials in a fixed order and applies the
 //             projected-clamp rule of ema:357-364.
-// The carry and dalpha stages read the [B][NC][D] per-chunk arrays in
-// coalesced rows (lane = channel) and combine in a fixed order.
+// The carry and dalpha stages read the [B][NC][D] per-chunk arrays in runs of
+// 16 channels (lane = channel within the run) and combine in a fixed order.
 // Alpha may be one value (the reference contract, ema:557-558) or one per
 // channel; the clamp to [floor, ceiling] happens in-kernel (ema:274-277).
 #include "common.h"
+#include "gather.h"
 
 namespace dwarf {
 
@@ -124,15 +125,19 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__
   for (int i = 0; i < VEC; ++i) e[i] = st[i];
 }
 
-// Carry stage, one workgroup of kCarryWaves waves per (b, block of 64
-// channels): carries[c] = state entering chunk c (REVERSE: the adjoint
-// entering chunk c from the future).  Lane l owns channel d0 + l, so every
-// access is a coalesced row of the [B][NC][D] chunk-state arrays; wave w owns
-// a contiguous segment of chunks in scan order.  With A = decay^kChunkT the
+// Carry stage, one workgroup of kCarryWaves waves per (b, block of
+// kCarryChannels channels): carries[c] = state entering chunk c (REVERSE: the
+// adjoint entering chunk c from the future).  Lane l takes channel
+// l % kCarryChannels and segment p = 4 w + l / kCarryChannels of the chunks
+// in scan order (kCarrySegs segments), so each access reads a
+// kCarryChannels-wide run of a [B][NC][D] row.  With A = decay^kChunkT the
 // chunks compose as s(next) = A s + ends[c]: each lane folds its segment into
-// (A_seg, B_seg), the segments are combined in order through LDS, and the
-// lane rescans its segment writing each chunk's incoming state.
+// (A_seg, B_seg), the lane folds the earlier segments' pairs from LDS in order
+// into its incoming state, and rescans its segment writing each chunk's
+// incoming state.
 constexpr int kCarryWaves = 16;
+constexpr int kCarryChannels = 16;
+constexpr int kCarrySegs = kCarryWaves * (kWave / kCarryChannels);
 constexpr int kCarrySeg = 32;   // chunk states a lane holds in registers per pass
 constexpr int kDaRows = 16;     // dalpha partials loaded per block
 
@@ -140,17 +145,19 @@ template <bool REVERSE>
 __global__ __launch_bounds__(kWave * kCarryWaves) void ema_carry(const float* __restrict__ ends,
                                                                  float* __restrict__ carries,
                                                                  const float* __restrict__ alpha, EmaGeom g) {
-  __shared__ float sA[kCarryWaves][kWave], sB[kCarryWaves][kWave];
+  __shared__ float2 sAB[kCarrySegs][kCarryChannels];
   const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
-  const int nblk = (g.D + kWave - 1) / kWave;
+  const int ch = l % kCarryChannels;
+  const int p = w * (kWave / kCarryChannels) + l / kCarryChannels;
+  const int nblk = (g.D + kCarryChannels - 1) / kCarryChannels;
   const int b = blockIdx.x / nblk;
-  const int d = (blockIdx.x - b * nblk) * kWave + l;
+  const int d = (blockIdx.x - b * nblk) * kCarryChannels + ch;
   const bool live = d < g.D;
   const float decay = live ? 1.f - clamp_alpha(alpha, g.per_channel, d, g.lo, g.hi) : 0.f;
   float full = 1.f;  // decay^kChunkT, by repeated multiplication as a serial scan applies it
   for (int i = 0; i < kChunkT; ++i) full *= decay;
-  const int seg = (g.NC + kCarryWaves - 1) / kCarryWaves;
-  const int k0 = w * seg, k1 = min(k0 + seg, g.NC);
+  const int seg = (g.NC + kCarrySegs - 1) / kCarrySegs;
+  const int k0 = p * seg, k1 = min(k0 + seg, g.NC);
   auto chunk = [&](int k) { return REVERSE ? g.NC - 1 - k : k; };
   const float* e = ends + static_cast<int64_t>(b) * g.NC * g.D + d;
   float* cr = carries + static_cast<int64_t>(b) * g.NC * g.D + d;
@@ -169,11 +176,13 @@ __global__ __launch_bounds__(kWave * kCarryWaves) void ema_carry(const float* __
         }
     }
   }
-  sA[w][l] = A;
-  sB[w][l] = Bv;
+  sAB[p][ch] = make_float2(A, Bv);
   __syncthreads();
-  float s = 0.f;   // state entering this wave's segment
-  for (int v = 0; v < w; ++v) s = fmaf(sA[v][l], s, sB[v][l]);
+  float s = 0.f;   // state entering this lane's segment: the earlier segments in order
+  for (int v = 0; v < p; ++v) {
+    const float2 ab = sAB[v][ch];
+    s = fmaf(ab.x, s, ab.y);
+  }
   if (live) {
     for (int kb = k0; kb < k1; kb += kCarrySeg) {
       if (kb != k0 || seg > kCarrySeg) {   // reload unless the whole segment is still in registers
@@ -325,36 +334,43 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
   for (int i = 0; i < VEC; ++i) dp[i] = da[i];
 }
 
-// dalpha, one workgroup of kCarryWaves waves per block of 64 channels: wave w
-// sums rows w, w + kCarryWaves, ... of the [B * NC][D] partials for lane l's
-// channel (coalesced rows, in row order), then wave 0 adds the wave sums in
-// wave order.  For a per-channel alpha the projected-clamp rule is applied per
-// channel; for a single alpha the channel sums go to `out` and a second pass
-// adds them in order.
+// dalpha, one workgroup of kCarryWaves waves per block of kDaChannels
+// channels: lane l takes channel l % kDaChannels and row phase
+// p = 4 w + l / kDaChannels, and sums rows p, p + 64, ... of the [B * NC][D]
+// partials in row order; the four phases of a wave are added by lane swaps
+// and the waves in wave order.  For a per-channel alpha the projected-clamp
+// rule is applied per channel; for a single alpha the channel sums go to
+// `out` and a second pass adds them in order.
+constexpr int kDaChannels = 16;
+constexpr int kDaPhases = kCarryWaves * (kWave / kDaChannels);
+
 __global__ __launch_bounds__(kWave * kCarryWaves) void ema_dalpha_channels(const float* __restrict__ da_part,
                                                                            const float* __restrict__ alpha,
                                                                            float* __restrict__ out, EmaGeom g) {
-  __shared__ float sS[kCarryWaves][kWave];
+  __shared__ float sS[kCarryWaves][kDaChannels];
   const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
-  const int d = blockIdx.x * kWave + l;
+  const int ch = l % kDaChannels;
+  const int phase = w * (kWave / kDaChannels) + l / kDaChannels;
+  const int d = blockIdx.x * kDaChannels + ch;
   const bool live = d < g.D;
   const int rows = g.B * g.NC;
   float s = 0.f;
   if (live) {
-    for (int r0 = w; r0 < rows; r0 += kCarryWaves * kDaRows) {
+    for (int r0 = phase; r0 < rows; r0 += kDaPhases * kDaRows) {
       float v[kDaRows];
 #pragma unroll
       for (int i = 0; i < kDaRows; ++i) {
-        const int r = r0 + i * kCarryWaves;
+        const int r = r0 + i * kDaPhases;
         v[i] = r < rows ? da_part[static_cast<int64_t>(r) * g.D + d] : 0.f;
       }
 #pragma unroll
       for (int i = 0; i < kDaRows; ++i) s += v[i];
     }
   }
-  sS[w][l] = s;
+  s = add_xor32(add_xor16(s));   // the wave's four phases, fixed order
+  if (l < kDaChannels) sS[w][l] = s;
   __syncthreads();
-  if (w == 0 && live) {
+  if (w == 0 && l < kDaChannels && live) {
     float t = 0.f;
     for (int v = 0; v < kCarryWaves; ++v) t += sS[v][l];
     if (g.per_channel) {
@@ -407,7 +423,7 @@ hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
   T* y = static_cast<T*>(a.y);
   hipLaunchKernelGGL((ema_fwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], a.alpha, ends, g);
-  const int cblocks = a.B * ((a.D + kWave - 1) / kWave);
+  const int cblocks = a.B * ((a.D + kCarryChannels - 1) / kCarryChannels);
   hipLaunchKernelGGL((ema_carry<false>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, ends, carries,
                      a.alpha, g);
   hipLaunchKernelGGL((ema_fwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
@@ -426,7 +442,7 @@ hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
   hipLaunchKernelGGL((ema_bwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
                      static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1], a.alpha, starts, g);
-  const int cblocks = a.B * ((a.D + kWave - 1) / kWave);
+  const int cblocks = a.B * ((a.D + kCarryChannels - 1) / kCarryChannels);
   hipLaunchKernelGGL((ema_carry<true>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, starts, carries,
                      a.alpha, g);
   hipLaunchKernelGGL((ema_bwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
@@ -434,7 +450,7 @@ hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
                      a.y_stride[0], a.y_stride[1], static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1],
                      static_cast<T*>(a.dx), a.dx_stride[0], a.dx_stride[1], a.alpha, carries, da_part, g);
   if (a.dalpha) {
-    const int rb = (a.D + kWave - 1) / kWave;
+    const int rb = (a.D + kDaChannels - 1) / kDaChannels;
     if (a.alpha_per_channel) {
       hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kWave * kCarryWaves), 0, stream, da_part, a.alpha,
                          a.dalpha, g);
