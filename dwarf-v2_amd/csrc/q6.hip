@@ -179,6 +179,28 @@ __device__ __forceinline__ void q6_codes16(uint32_t w0, uint32_t w1, uint32_t w2
   for (int i = 11; i < 16; ++i) c[i] = sfield6(w2, 6 * i - 64);
 }
 
+// The bf16 pair (160 + c_a, 160 + c_b) of the two 6-bit codes in bits
+// [0, 12) of t (c_a low): code c in two's complement with its sign bit
+// flipped is c + 32, and bf16 0x4300 | m is 128 + m.
+__device__ __forceinline__ uint32_t code_pair_bf16(uint32_t t) {
+  const uint32_t f = t & 0xfffu;
+  return ((f | (f << 10)) & 0x003f003fu) ^ 0x43204320u;
+}
+
+// sum_d q_d (160 + c_d) over the 16 codes of a 12-byte chunk, on bf16 pairs.
+__device__ __forceinline__ float q6_dot16_biased(const uint32_t* q32, uint32_t w0, uint32_t w1, uint32_t w2) {
+  float s = 0.f;
+  s = dot2bf(q32[0], code_pair_bf16(w0), s);
+  s = dot2bf(q32[1], code_pair_bf16(w0 >> 12), s);
+  s = dot2bf(q32[2], code_pair_bf16(__builtin_amdgcn_alignbit(w1, w0, 24)), s);
+  s = dot2bf(q32[3], code_pair_bf16(w1 >> 4), s);
+  s = dot2bf(q32[4], code_pair_bf16(w1 >> 16), s);
+  s = dot2bf(q32[5], code_pair_bf16(__builtin_amdgcn_alignbit(w2, w1, 28)), s);
+  s = dot2bf(q32[6], code_pair_bf16(w2 >> 8), s);
+  s = dot2bf(q32[7], code_pair_bf16(w2 >> 20), s);
+  return s;
+}
+
 __device__ __forceinline__ float half_lo_or_hi(uint32_t pair, bool hi) {
   return half_bits_to_f32(static_cast<uint16_t>(hi ? pair >> 16 : pair));
 }
@@ -189,9 +211,9 @@ __device__ __forceinline__ float half_lo_or_hi(uint32_t pair, bool hi) {
 // A workgroup of 4 waves handles 64 queries of one (b, h); lane c of a query
 // holds head dims [16c, 16c+16).  A gathered slot is read as the lane's 12
 // bytes of K codes and of V codes, the two fp16 scale pairs and (far offsets)
-// its z plane, so the four lanes of a query read one 128-byte slot.  Codes are
-// dequantised on read (v_bfe_i32 of the 6-bit fields); q.k is formed on the
-// integer codes and scaled once by the fp16 group scale, and the V codes are
+// its z plane, so the four lanes of a query read one 128-byte slot.  q.k is
+// formed on the codes as biased bf16 pairs (q6_dot16_biased) and scaled once
+// by the fp16 group scale; the V codes are widened to fp32 (v_bfe_i32),
 // rotated (MOVT pair of plane c) and accumulated with weight P * scale.
 // <q, e_j> + pb_j for the wave's 16 queries and all offsets is one MFMA pass
 // at the start (E staged in bf16, as the GPU path rounds it).  y is computed
@@ -327,13 +349,16 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
   if (n0w >= N) return;                       // whole wave past the end (no block barriers below)
   const int cnt = build_offset_list<1>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
 
-  // this lane's q slice in fp32, and y of plane g = <q, probe_g> / sqrt(|q|^2 + 1e-6 hd)
+  // this lane's q slice (bf16 pairs and fp32), 160 * sum(q) for the biased
+  // code pairs, and y of plane g = <q, probe_g> / sqrt(|q|^2 + 1e-6 hd)
+  const uint32_t q32[8] = {qx0.x, qx0.y, qx0.z, qx0.w, qx1.x, qx1.y, qx1.z, qx1.w};
   float qf[16];
-  {
-    const uint32_t w8[8] = {qx0.x, qx0.y, qx0.z, qx0.w, qx1.x, qx1.y, qx1.z, qx1.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(w8[i]); qf[2 * i + 1] = bf16_hi(w8[i]); }
-  }
+  for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(q32[i]); qf[2 * i + 1] = bf16_hi(q32[i]); }
+  float qbias = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qbias = dot2bf(q32[i], 0x3f803f80u, qbias);   // (1, 1) in bf16
+  qbias *= -160.f;
   float yg;
   {
     float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
@@ -379,10 +404,7 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
 
   auto consume = [&](const PfSlot& s) {
     float cf[16];
-    q6_codes16(s.k0, s.k1, s.k2, cf);
-    float kd = 0.f;
-#pragma unroll
-    for (int d = 0; d < 16; ++d) kd = fmaf(qf[d], cf[d], kd);
+    const float kd = q6_dot16_biased(q32, s.k0, s.k1, s.k2) + qbias;
     const float dot = group_sum<4>(kd * half_lo_or_hi(s.ks, khi));
     const float s2 = s.ok ? fmaf(dot, kC, s_qe[qi * lay.qe_row + s.j]) : -INFINITY;
     if (s2 > m + kSlack2) {
@@ -484,28 +506,6 @@ __host__ __device__ inline DecLayout dec_layout(int J, int H) {
   L.off_list = static_cast<size_t>(H) * L.JE * 4;                  // s_T[H][JE]
   L.bytes = L.off_list + static_cast<size_t>(H) * L.list_len * 8;  // s_list[H][list_len] int2
   return L;
-}
-
-// The bf16 pair (160 + c_a, 160 + c_b) of the two 6-bit codes in bits
-// [0, 12) of t (c_a low): code c in two's complement with its sign bit
-// flipped is c + 32, and bf16 0x4300 | m is 128 + m.
-__device__ __forceinline__ uint32_t code_pair_bf16(uint32_t t) {
-  const uint32_t f = t & 0xfffu;
-  return ((f | (f << 10)) & 0x003f003fu) ^ 0x43204320u;
-}
-
-// sum_d q_d (160 + c_d) over the 16 codes of a 12-byte chunk, on bf16 pairs.
-__device__ __forceinline__ float q6_dot16_biased(const uint32_t* q32, uint32_t w0, uint32_t w1, uint32_t w2) {
-  float s = 0.f;
-  s = dot2bf(q32[0], code_pair_bf16(w0), s);
-  s = dot2bf(q32[1], code_pair_bf16(w0 >> 12), s);
-  s = dot2bf(q32[2], code_pair_bf16(__builtin_amdgcn_alignbit(w1, w0, 24)), s);
-  s = dot2bf(q32[3], code_pair_bf16(w1 >> 4), s);
-  s = dot2bf(q32[4], code_pair_bf16(w1 >> 16), s);
-  s = dot2bf(q32[5], code_pair_bf16(__builtin_amdgcn_alignbit(w2, w1, 28)), s);
-  s = dot2bf(q32[6], code_pair_bf16(w2 >> 8), s);
-  s = dot2bf(q32[7], code_pair_bf16(w2 >> 20), s);
-  return s;
 }
 
 // Sum over all 64 lanes, in every lane.
