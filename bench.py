@@ -248,6 +248,24 @@ def graph_ms(fn, steps, warmup, reps=10):
     return a.elapsed_time(b) / (n * reps)
 
 
+def phase_probe_extra(pkg, device, steps, warmup):
+    """phase_probe_features fwd and bwd (with dprobes) on q of the training microbatch."""
+    B, H, N = 15, 8, 2048
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, H, N, 64, generator=g).to(torch.bfloat16).to(device)
+    p = torch.nn.functional.normalize(torch.randn(4, 64, generator=g), dim=-1).to(device)
+    dout = torch.randn(B, H, N, 4, generator=g).to(device)
+    probe = importlib.import_module("dwarf-v2_amd.probe")
+    ms_f = graph_ms(lambda: probe.probe_forward(x, p, 0, N), max(steps, 20), warmup)
+    ms_b = graph_ms(lambda: probe.probe_backward(x, p, dout, 0, N, True), max(steps, 20), warmup)
+    rows = B * H * N
+    fb, bb = rows * (128 + 16), rows * (128 + 16 + 128)
+    return {"ms_fwd": ms_f, "ms_bwd": ms_b, "fwd_hbm_frac": fb / (ms_f * 1e-3) / HBM_PEAK,
+            "bwd_hbm_frac": bb / (ms_b * 1e-3) / HBM_PEAK, "fwd_bytes": fb, "bwd_bytes": bb,
+            "config": "q [15,8,2048,64] bf16, 4 probes; fwd 144 B/row (x + y), bwd 272 B/row (x + dy + dx) "
+                      "plus dprobes; timed from HIP-graph replays"}
+
+
 def long_context_extra(pkg, device, steps, warmup):
     B, H, N = 4, 8, 8192
     t, js, jl = synth(pkg, B, H, N, 4, device)
@@ -281,7 +299,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context"],
+    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe"],
                     help="run only this extra workload and print its JSON (for per-workload profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 10 times (scales HBM byte counters)")
@@ -307,7 +325,7 @@ def main() -> int:
     pkg._lib.load()
     if args.extra_only:
         fn = {"q6_decode": q6_decode_extra, "q6_prefill": q6_prefill_extra,
-              "long_context": long_context_extra}[args.extra_only]
+              "long_context": long_context_extra, "phase_probe": phase_probe_extra}[args.extra_only]
         print(json.dumps({args.extra_only: fn(pkg, device, args.steps, args.warmup)}), flush=True)
         return 0
     B, H, N = 15, 8, 2048
@@ -339,6 +357,8 @@ def main() -> int:
         extra["q6_prefill"] = q6_prefill_extra(pkg, device, args.steps, args.warmup)
         log("long context: B4 T8192 DSQG fwd+bwd + EMA fwd+bwd")
         extra["long_context"] = long_context_extra(pkg, device, max(3, args.steps // 4), 2)
+        log("phase-probe features: q of the training microbatch")
+        extra["phase_probe"] = phase_probe_extra(pkg, device, args.steps, args.warmup)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):

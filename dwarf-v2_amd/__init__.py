@@ -8,12 +8,14 @@ Public surface (reference names, Lanerra/dwarf-v2):
   ALL_OFFSETS, R_PLANES and the lattice helpers      kernels/dsqg_attention_v22.py
   causal_ema_scan, bounded_ema_factor,
   inverse_bounded_ema_factor                         kernels/causal_ema_scan.py
+  phase_probe_features, _PhaseProbeFn                kernels/dsqg_attention_v22.py
   q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
 """
 
-from . import _lib, lattice, ops, q6
+from . import _lib, lattice, ops, probe, q6
 from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
 from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
+from .probe import _PhaseProbeFn, phase_probe_features
 from .lattice import (
     ALL_OFFSETS,
     GROUPED_MODE_IDS,
@@ -30,6 +32,7 @@ __all__ = [
     "GROUPED_MODE_IDS",
     "R_PLANES",
     "_DSQGV18GroupedFn",
+    "_PhaseProbeFn",
     "_canonicalize_offsets",
     "_normalize_plane_shift",
     "_orthogonal_phase_probes",
@@ -41,6 +44,7 @@ __all__ = [
     "dsqg_backward",
     "dsqg_forward",
     "inverse_bounded_ema_factor",
+    "phase_probe_features",
     "q6",
 ]
 

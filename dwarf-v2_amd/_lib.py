@@ -41,6 +41,9 @@ EXPORTED_SYMBOLS = (
     "dwarf_q6_unpack_kv",
     "dwarf_dsqg_q6_prefill_fwd",
     "dwarf_dsqg_q6_decode",
+    "dwarf_phase_probe_fwd",
+    "dwarf_phase_probe_bwd_workspace_bytes",
+    "dwarf_phase_probe_bwd",
 )
 
 
@@ -155,6 +158,27 @@ class Q6DecodeArgs(ctypes.Structure):
 _LIB = None
 
 
+class PhaseProbeFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int32), ("H", c_int32), ("N", c_int32), ("head_dim", c_int32), ("R", c_int32),
+        ("start", c_int32), ("end", c_int32),
+        ("dtype", c_int32),
+        ("x", c_void_p), ("x_stride", _i64(4)),
+        ("probes", c_void_p),
+        ("out", c_void_p), ("out_stride", _i64(4)),
+    ]
+
+
+class PhaseProbeBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", PhaseProbeFwdArgs),
+        ("dout", c_void_p), ("dout_stride", _i64(4)),
+        ("dx", c_void_p), ("dx_stride", _i64(4)),
+        ("dprobes", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The HIP library is missing, stale or failed a call."""
 
@@ -210,6 +234,12 @@ def load() -> ctypes.CDLL:
     lib.dwarf_dsqg_q6_prefill_fwd.argtypes = [POINTER(Q6PrefillArgs), c_void_p]
     lib.dwarf_dsqg_q6_decode.restype = c_int
     lib.dwarf_dsqg_q6_decode.argtypes = [POINTER(Q6DecodeArgs), c_void_p]
+    lib.dwarf_phase_probe_fwd.restype = c_int
+    lib.dwarf_phase_probe_fwd.argtypes = [POINTER(PhaseProbeFwdArgs), c_void_p]
+    lib.dwarf_phase_probe_bwd_workspace_bytes.restype = c_size_t
+    lib.dwarf_phase_probe_bwd_workspace_bytes.argtypes = [POINTER(PhaseProbeBwdArgs)]
+    lib.dwarf_phase_probe_bwd.restype = c_int
+    lib.dwarf_phase_probe_bwd.argtypes = [POINTER(PhaseProbeBwdArgs), c_void_p]
     version = lib.dwarf_abi_version()
     if version != ABI_VERSION:
         raise NativeLibraryError(f"{LIB_NAME} ABI {version} does not match the binding's ABI {ABI_VERSION}")

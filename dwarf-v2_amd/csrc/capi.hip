@@ -24,6 +24,9 @@ hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t st
 hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream);
 int q6_max_decode_offsets();
 int q6_max_decode_heads();
+size_t phase_probe_bwd_workspace(const dwarf_phase_probe_bwd_args& a);
+hipError_t launch_phase_probe_fwd(const dwarf_phase_probe_fwd_args& a, hipStream_t stream);
+hipError_t launch_phase_probe_bwd(const dwarf_phase_probe_bwd_args& a, hipStream_t stream);
 }  // namespace dwarf
 
 namespace {
@@ -256,6 +259,49 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream) {
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
   return hip_status(dwarf::launch_ema_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_ema_bwd");
+}
+
+// ---- phase-probe features ---------------------------------------------------
+static int check_probe_fwd(const dwarf_phase_probe_fwd_args& a, bool need_out) {
+  if (a.B < 0 || a.H < 0 || a.N < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes B=%d H=%d N=%d", a.B, a.H, a.N);
+  if (a.head_dim != dwarf::kHeadDim || a.R != DWARF_R_PLANES)
+    return fail(DWARF_ERR_UNSUPPORTED, "phase probes are built for head_dim %d and %d planes (got %d, %d)",
+                dwarf::kHeadDim, DWARF_R_PLANES, a.head_dim, a.R);
+  if (a.dtype != DWARF_BF16 && a.dtype != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", a.dtype);
+  if (static_cast<int64_t>(a.B) * a.H * a.N >= (int64_t(1) << 31))
+    return fail(DWARF_ERR_UNSUPPORTED, "B*H*N must stay below 2^31 rows");
+  int rc = check_rows("x", a.x, a.x_stride, 3, a.dtype);
+  if (rc) return rc;
+  if (!a.probes || !aligned16(a.probes)) return fail(DWARF_ERR_INVALID_ARGUMENT, "probes NULL or not 16-byte aligned");
+  if (need_out && !a.out) return fail(DWARF_ERR_INVALID_ARGUMENT, "out is NULL");
+  return DWARF_OK;
+}
+
+int dwarf_phase_probe_fwd(const dwarf_phase_probe_fwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  int rc = check_probe_fwd(*args, true);
+  if (rc) return rc;
+  return hip_status(dwarf::launch_phase_probe_fwd(*args, reinterpret_cast<hipStream_t>(stream)),
+                    "dwarf_phase_probe_fwd");
+}
+
+size_t dwarf_phase_probe_bwd_workspace_bytes(const dwarf_phase_probe_bwd_args* args) {
+  return args ? dwarf::phase_probe_bwd_workspace(*args) : 0;
+}
+
+int dwarf_phase_probe_bwd(const dwarf_phase_probe_bwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_phase_probe_bwd_args& a = *args;
+  int rc = check_probe_fwd(a.fwd, false);
+  if (rc) return rc;
+  if (!a.dout) return fail(DWARF_ERR_INVALID_ARGUMENT, "dout is NULL");
+  if ((rc = check_rows("dx", a.dx, a.dx_stride, 3, a.fwd.dtype))) return rc;
+  if (a.dprobes) {
+    const size_t need = dwarf::phase_probe_bwd_workspace(a);
+    if (need && (!a.workspace || a.workspace_bytes < need))
+      return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  }
+  return hip_status(dwarf::launch_phase_probe_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_phase_probe_bwd");
 }
 
 // ---- q6 ---------------------------------------------------------------------

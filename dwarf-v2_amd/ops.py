@@ -1,14 +1,15 @@
 """torch.library registration of the HIP launches.
 
-``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::ema_fwd`` and
-``dwarf::ema_bwd`` are custom ops with fake (shape-only) implementations, so
-``torch.compile`` traces the DSQG and EMA autograd Functions without graph
-breaks (the trainer compiles the model, train:1083).  The real
+``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::ema_fwd``,
+``dwarf::ema_bwd``, ``dwarf::phase_probe_fwd`` and ``dwarf::phase_probe_bwd``
+are custom ops with fake (shape-only) implementations, so ``torch.compile``
+traces the DSQG, EMA and phase-probe autograd Functions without graph breaks
+(the trainer compiles the model, train:1083).  The real
 implementations normalise layouts (unit head-dim stride, 16-byte rows,
 contiguous fp32 tables and plane features, int32 offsets on the device) and
 call the C ABI on the current stream.  The op names follow the drop-in
-boundary of the reference op (kernels/dsqg_attention_v22.py:2691-2777,
-kernels/causal_ema_scan.py:263-364).
+boundary of the reference ops (kernels/dsqg_attention_v22.py:2691-2777 and
+371-451, kernels/causal_ema_scan.py:263-364).
 """
 
 from __future__ import annotations
@@ -17,6 +18,7 @@ import torch
 
 from . import dsqg as _dsqg
 from . import ema as _ema
+from . import probe as _probe
 
 Tensor = torch.Tensor
 
@@ -83,3 +85,30 @@ def ema_bwd(x: Tensor, y: Tensor, dy: Tensor, alpha: Tensor, floor: float, ceili
 @ema_bwd.register_fake
 def _ema_bwd_fake(x, y, dy, alpha, floor, ceiling):
     return x.new_empty(x.shape), x.new_empty((alpha.numel(),), dtype=torch.float32)
+
+
+# ---- phase-probe features ------------------------------------------------------------------
+@torch.library.custom_op("dwarf::phase_probe_fwd", mutates_args=())
+def phase_probe_fwd(values: Tensor, probes: Tensor, start: int, end: int) -> Tensor:
+    """y [B,H,N,R] fp32; rows outside [start, end) are 0."""
+    return _probe.probe_forward(values, probes, start, end)
+
+
+@phase_probe_fwd.register_fake
+def _phase_probe_fwd_fake(values, probes, start, end):
+    return values.new_empty((*values.shape[:3], probes.shape[0]), dtype=torch.float32)
+
+
+@torch.library.custom_op("dwarf::phase_probe_bwd", mutates_args=())
+def phase_probe_bwd(values: Tensor, probes: Tensor, dout: Tensor, start: int, end: int,
+                    need_dprobes: bool) -> tuple[Tensor, Tensor]:
+    """(dx in the kernel dtype, dprobes fp32 [R,hd]; empty [0] when not needed)."""
+    dx, dprobes = _probe.probe_backward(values, probes, dout, start, end, need_dprobes)
+    return dx, dprobes if dprobes is not None else values.new_empty((0,), dtype=torch.float32)
+
+
+@phase_probe_bwd.register_fake
+def _phase_probe_bwd_fake(values, probes, dout, start, end, need_dprobes):
+    dt = values.dtype if values.dtype in (torch.bfloat16, torch.float32) else torch.float32
+    dp = probes.shape if need_dprobes else (0,)
+    return values.new_empty(values.shape, dtype=dt), values.new_empty(dp, dtype=torch.float32)

@@ -190,6 +190,48 @@ size_t dwarf_ema_bwd_workspace_bytes(const dwarf_ema_bwd_args* args);
 int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Phase-probe features  y[b,h,n,r] = <x, p_r> / sqrt(|x|^2 + 1e-6 hd)       */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * x [B,H,N,hd] of `dtype` (unit stride on hd, 16-byte aligned rows); probes
+ * [R,hd] fp32, contiguous and 16-byte aligned; R = DWARF_R_PLANES, hd = 64.
+ * out [B,H,N,R] fp32, any strides.  Rows n in [start, end) get the features
+ * and every other row is written 0; start and end are clamped to [0, N] as
+ * dsqg:377-379 does.
+ */
+typedef struct {
+  int32_t B, H, N, head_dim, R;
+  int32_t start, end;
+  int32_t dtype;
+  const void* x; int64_t x_stride[4];
+  const float* probes;
+  float* out; int64_t out_stride[4];
+} dwarf_phase_probe_fwd_args;
+
+/* Replaces _PhaseProbeFn.forward's launch (dsqg:371-392; kernel dsqg:275-306). */
+int dwarf_phase_probe_fwd(const dwarf_phase_probe_fwd_args* args, dwarf_stream_t stream);
+
+/*
+ * dout [B,H,N,R] fp32, any strides.  dx like x (unit stride on hd, 16-byte
+ * aligned rows), written, 0 outside [start, end).  dprobes [R,hd] fp32
+ * written in a fixed summation order, or NULL when the probes need no
+ * gradient.  fwd.out is not used.
+ */
+typedef struct {
+  dwarf_phase_probe_fwd_args fwd;
+  const float* dout; int64_t dout_stride[4];
+  void* dx; int64_t dx_stride[4];
+  float* dprobes;
+  void* workspace; size_t workspace_bytes;
+} dwarf_phase_probe_bwd_args;
+
+size_t dwarf_phase_probe_bwd_workspace_bytes(const dwarf_phase_probe_bwd_args* args);
+
+/* Replaces _PhaseProbeFn.backward's launch (dsqg:394-419; kernel dsqg:309-369). */
+int dwarf_phase_probe_bwd(const dwarf_phase_probe_bwd_args* args, dwarf_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* q6 K/V cache (no reference counterpart in the reference repository;      */
 /* signed 6-bit codes, 4 codes per 3 bytes, group 32, fp16 absmax scale)     */
 /* ------------------------------------------------------------------------ */

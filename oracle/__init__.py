@@ -9,4 +9,5 @@ The product (dwarf-v2_amd/) never imports it and has no CPU fallback.
             GPU path's conventions (dsqg:760-763, 845-851, 2265-2268)
   ema_ref   kernels/causal_ema_scan.py:3-11, 511-538
   q6_ref    the q6 cache format (no reference counterpart)
+  probe_ref phase-probe features, dsqg:275-369 (kernels), 422-451 (eager)
 """

@@ -29,7 +29,7 @@ def lib(pkg):
 
 def test_exports_every_declared_symbol(pkg, lib):
     names = declared_functions()
-    assert len(names) == 16
+    assert len(names) == 19
     assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
     for name in names:
         assert hasattr(lib, name), name
@@ -43,6 +43,8 @@ STRUCTS = {
     "dwarf_ema_bwd_args": "EmaBwdArgs",
     "dwarf_dsqg_q6_prefill_args": "Q6PrefillArgs",
     "dwarf_dsqg_q6_decode_args": "Q6DecodeArgs",
+    "dwarf_phase_probe_fwd_args": "PhaseProbeFwdArgs",
+    "dwarf_phase_probe_bwd_args": "PhaseProbeBwdArgs",
 }
 
 
@@ -98,3 +100,13 @@ def test_validation_errors_without_gpu(pkg, lib):
     d.J, d.J_small, d.J_large, d.H, d.H_kv = 96, 17, 79, 32, 32
     assert lib.dwarf_dsqg_q6_decode(ctypes.byref(d), None) == L.DWARF_ERR_UNSUPPORTED   # one wave per head, <= 16
     assert b"heads" in lib.dwarf_last_error()
+    p = L.PhaseProbeFwdArgs()
+    p.B, p.H, p.N, p.head_dim, p.R, p.end = 1, 1, 8, 32, 4, 8
+    assert lib.dwarf_phase_probe_fwd(ctypes.byref(p), None) == L.DWARF_ERR_UNSUPPORTED   # head_dim 64 only
+    p.head_dim, p.R = 64, 3
+    assert lib.dwarf_phase_probe_fwd(ctypes.byref(p), None) == L.DWARF_ERR_UNSUPPORTED   # four probes only
+    p.R, p.dtype = 4, L.DWARF_BF16
+    assert lib.dwarf_phase_probe_fwd(ctypes.byref(p), None) == L.DWARF_ERR_INVALID_ARGUMENT   # x is NULL
+    pb = L.PhaseProbeBwdArgs()
+    pb.fwd = p
+    assert lib.dwarf_phase_probe_bwd(ctypes.byref(pb), None) == L.DWARF_ERR_INVALID_ARGUMENT
