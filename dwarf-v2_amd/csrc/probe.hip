@@ -51,6 +51,31 @@ __device__ __forceinline__ PrRow pr_row(const PrGeom& gm, int64_t row) {
   return r;
 }
 
+// Row wave_row + i (i < 16) from the decomposition of the wave's first row,
+// which is uniform and so divided on the scalar unit; with N >= 16 the 16
+// rows cross at most one (b, h) boundary.
+__device__ __forceinline__ PrRow pr_row_wave(const PrGeom& gm, int64_t wave_row, int i) {
+  if (gm.N < 16) return pr_row(gm, wave_row + i);
+  const uint32_t w0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(wave_row)));
+  const uint32_t bh0 = w0 / static_cast<uint32_t>(gm.N);
+  const int n0 = static_cast<int>(w0 - bh0 * static_cast<uint32_t>(gm.N));
+  const int b0 = static_cast<int>(bh0 / static_cast<uint32_t>(gm.H));
+  const int h0 = static_cast<int>(bh0) - b0 * gm.H;
+  PrRow r;
+  r.n = n0 + i;
+  r.h = h0;
+  r.b = b0;
+  if (r.n >= gm.N) {
+    r.n -= gm.N;
+    if (++r.h == gm.H) {
+      r.h = 0;
+      ++r.b;
+    }
+  }
+  r.live = r.n >= gm.start && r.n < gm.end;
+  return r;
+}
+
 template <typename T>
 __device__ __forceinline__ void store16(T* p, const float* v);
 template <>
@@ -141,7 +166,7 @@ __global__ __launch_bounds__(kBlock, kPrWgsPerCu) void phase_probe_fwd_kernel(
     const int64_t row = r0 + w * 16 + (l >> 2);
     st.ok = row < gm.rows;
     if (st.ok) {
-      st.rw = pr_row(gm, row);
+      st.rw = pr_row_wave(gm, r0 + w * 16, l >> 2);
       if (st.rw.live) load_raw(x + st.rw.b * sx0 + st.rw.h * sx1 + static_cast<int64_t>(st.rw.n) * sx2 + kPrDims * g, st.x);
     }
   };
@@ -187,7 +212,7 @@ __global__ __launch_bounds__(kBlock, pr_bwd_wgs_per_cu(DPROBES)) void phase_prob
     const int64_t row = r0 + w * 16 + (l >> 2);
     st.ok = row < gm.rows;
     if (st.ok) {
-      st.rw = pr_row(gm, row);
+      st.rw = pr_row_wave(gm, r0 + w * 16, l >> 2);
       if (st.rw.live) {
         load_raw(x + st.rw.b * sx0 + st.rw.h * sx1 + static_cast<int64_t>(st.rw.n) * sx2 + kPrDims * g, st.x);
         st.gown = dout[st.rw.b * sg0 + st.rw.h * sg1 + static_cast<int64_t>(st.rw.n) * sg2 + g * sg3];

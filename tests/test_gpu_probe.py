@@ -37,7 +37,8 @@ def run(pkg, x, p, dout, device, span, need_probes=True):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape,span,transposed", [((2, 3, 37), (0, None), False), ((1, 8, 300), (5, 290), True),
+@pytest.mark.parametrize("shape,span,transposed", [((2, 3, 37), (0, None), False), ((2, 3, 9), (2, 7), False),
+                                                    ((1, 8, 300), (5, 290), True),
                                                     ((3, 2, 64), (64, None), False), ((2, 8, 2048), (1, None), False)])
 def test_matches_oracle(pkg, device, dtype, shape, span, transposed):
     B, H, N = shape
