@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -98,6 +98,7 @@ class EmaFwdArgs(ctypes.Structure):
         ("alpha", c_void_p),
         ("y", c_void_p), ("y_stride", _i64(3)),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("reset", c_void_p), ("reset_stride", _i64(2)),
     ]
 
 
@@ -113,6 +114,7 @@ class EmaBwdArgs(ctypes.Structure):
         ("dx", c_void_p), ("dx_stride", _i64(3)),
         ("dalpha", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+        ("reset", c_void_p), ("reset_stride", _i64(2)),
     ]
 
 

@@ -231,6 +231,14 @@ size_t dwarf_ema_bwd_workspace_bytes(const dwarf_ema_bwd_args* a) {
   return a ? dwarf::ema_bwd_workspace(a->B, a->N, a->D) : 0;
 }
 
+static int check_reset(const uint8_t* reset, const int64_t* rs, int B, int N) {
+  if (!reset) return DWARF_OK;
+  if (rs[0] < 0 || rs[1] < 0 || (B > 1 && rs[0] == 0) || (N > 1 && rs[1] == 0))
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "reset strides (%lld, %lld) do not address a [B,N] mask",
+                static_cast<long long>(rs[0]), static_cast<long long>(rs[1]));
+  return DWARF_OK;
+}
+
 int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream) {
   if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
   const dwarf_ema_fwd_args& a = *args;
@@ -238,6 +246,7 @@ int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream) {
   if (rc) return rc;
   if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
   if ((rc = check_btd("y", a.y, a.y_stride, a.dtype, a.D))) return rc;
+  if ((rc = check_reset(a.reset, a.reset_stride, a.B, a.N))) return rc;
   if (a.B == 0 || a.N == 0 || a.D == 0) return ok();
   const size_t need = dwarf::ema_fwd_workspace(a.B, a.N, a.D);
   if (!a.workspace || a.workspace_bytes < need)
@@ -254,6 +263,7 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream) {
   if ((rc = check_btd("y", a.y, a.y_stride, a.dtype, a.D))) return rc;
   if ((rc = check_btd("dy", a.dy, a.dy_stride, a.dtype, a.D))) return rc;
   if ((rc = check_btd("dx", a.dx, a.dx_stride, a.dtype, a.D))) return rc;
+  if ((rc = check_reset(a.reset, a.reset_stride, a.B, a.N))) return rc;
   if (a.B == 0 || a.N == 0 || a.D == 0) return ok();
   const size_t need = dwarf::ema_bwd_workspace(a.B, a.N, a.D);
   if (!a.workspace || a.workspace_bytes < need)

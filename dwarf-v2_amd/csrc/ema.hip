@@ -18,6 +18,12 @@
 // 16 channels (lane = channel within the run) and combine in a fixed order.
 // Alpha may be one value (the reference contract, ema:557-558) or one per
 // channel; the clamp to [floor, ceiling] happens in-kernel (ema:274-277).
+// Optional reset flags [B,N] zero the state before the tokens they mark
+// (the reset-aware scan, ema:368-509): the local and apply stages apply them
+// inside the chunk, the local stage records whether a chunk contains one, and
+// the carry stage gives such a chunk a zero transfer factor.  In reverse
+// time a reset at token t + 1 cuts the adjoint flowing into t, and y[t-1]
+// does not enter dalpha at a reset token.
 #include "common.h"
 #include "gather.h"
 
@@ -77,7 +83,15 @@ struct EmaGeom {
   int B, N, D, NC, DV;  // DV = D / VEC lanes per row
   int per_channel;
   float lo, hi;
+  const uint8_t* reset;   // [B,N] reset flags (RESET kernels only)
+  int64_t srb, srn;
+  uint8_t* cut;           // [B][NC]: the chunk cuts the carry (a reset inside, see ema_carry)
 };
+
+// The state is zeroed before a token whose reset flag is set (ema:533-535).
+__device__ __forceinline__ bool reset_at(const EmaGeom& g, int b, int t) {
+  return g.reset[b * g.srb + static_cast<int64_t>(t) * g.srn] != 0;
+}
 
 __device__ __forceinline__ float clamp_alpha(const float* alpha, int per_channel, int d, float lo, float hi) {
   const float a = alpha[per_channel ? d : 0];
@@ -91,7 +105,7 @@ template <typename T>
 constexpr int kRows = sizeof(T) == 2 ? 16 : 8;
 
 // ---- forward --------------------------------------------------------------
-template <typename T, int VEC>
+template <typename T, int VEC, bool RESET>
 __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__ x, int64_t sxb, int64_t sxn,
                                                           const float* __restrict__ alpha, float* __restrict__ ends,
                                                           EmaGeom g) {
@@ -108,6 +122,7 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__
   const int t0 = c * kChunkT;
   const int len = min(kChunkT, g.N - t0);
   const T* p = x + b * sxb + static_cast<int64_t>(t0) * sxn + d0;
+  bool cut = false;
   for (int tb = 0; tb < len; tb += R) {
     float xv[R][VEC];
 #pragma unroll
@@ -116,6 +131,13 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__
 #pragma unroll
     for (int r = 0; r < R; ++r)
       if (tb + r < len) {
+        if constexpr (RESET) {
+          if (reset_at(g, b, t0 + tb + r)) {
+            cut = true;
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) st[i] = 0.f;
+          }
+        }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) st[i] = fmaf(a[i], xv[r][i], (1.f - a[i]) * st[i]);
       }
@@ -123,6 +145,7 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__
   float* e = ends + (static_cast<int64_t>(b) * g.NC + c) * g.D + d0;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) e[i] = st[i];
+  if (RESET && dv == 0) g.cut[b * g.NC + c] = cut;   // a reset in [t0, t0 + len)
 }
 
 // Carry stage, one workgroup of kCarryWaves waves per (b, block of
@@ -134,14 +157,15 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_local(const T* __restrict__
 // chunks compose as s(next) = A s + ends[c]: each lane folds its segment into
 // (A_seg, B_seg), the lane folds the earlier segments' pairs from LDS in order
 // into its incoming state, and rescans its segment writing each chunk's
-// incoming state.
+// incoming state.  With resets a chunk whose cut flag is set has A = 0: its
+// end state does not depend on the state entering it.
 constexpr int kCarryWaves = 16;
 constexpr int kCarryChannels = 16;
 constexpr int kCarrySegs = kCarryWaves * (kWave / kCarryChannels);
 constexpr int kCarrySeg = 32;   // chunk states a lane holds in registers per pass
 constexpr int kDaRows = 16;     // dalpha partials loaded per block
 
-template <bool REVERSE>
+template <bool REVERSE, bool RESET>
 __global__ __launch_bounds__(kWave * kCarryWaves) void ema_carry(const float* __restrict__ ends,
                                                                  float* __restrict__ carries,
                                                                  const float* __restrict__ alpha, EmaGeom g) {
@@ -161,6 +185,7 @@ __global__ __launch_bounds__(kWave * kCarryWaves) void ema_carry(const float* __
   auto chunk = [&](int k) { return REVERSE ? g.NC - 1 - k : k; };
   const float* e = ends + static_cast<int64_t>(b) * g.NC * g.D + d;
   float* cr = carries + static_cast<int64_t>(b) * g.NC * g.D + d;
+  auto factor = [&](int k) { return RESET && g.cut[b * g.NC + chunk(k)] ? 0.f : full; };
   // fold the segment: s_out = A s_in + Bv
   float A = 1.f, Bv = 0.f;
   float ev[kCarrySeg];   // the segment's first kCarrySeg chunk states, kept for the second pass
@@ -171,8 +196,9 @@ __global__ __launch_bounds__(kWave * kCarryWaves) void ema_carry(const float* __
 #pragma unroll
       for (int r = 0; r < kCarrySeg; ++r)
         if (kb + r < k1) {
-          Bv = fmaf(full, Bv, ev[r]);
-          A *= full;
+          const float f = factor(kb + r);
+          Bv = fmaf(f, Bv, ev[r]);
+          A *= f;
         }
     }
   }
@@ -193,13 +219,13 @@ __global__ __launch_bounds__(kWave * kCarryWaves) void ema_carry(const float* __
       for (int r = 0; r < kCarrySeg; ++r)
         if (kb + r < k1) {
           cr[static_cast<int64_t>(chunk(kb + r)) * g.D] = s;
-          s = fmaf(full, s, ev[r]);
+          s = fmaf(factor(kb + r), s, ev[r]);
         }
     }
   }
 }
 
-template <typename T, int VEC>
+template <typename T, int VEC, bool RESET>
 __global__ __launch_bounds__(kEmaBlock) void ema_fwd_apply(const T* __restrict__ x, int64_t sxb, int64_t sxn,
                                                           T* __restrict__ y, int64_t syb, int64_t syn,
                                                           const float* __restrict__ alpha,
@@ -227,6 +253,12 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_apply(const T* __restrict__
 #pragma unroll
     for (int r = 0; r < R; ++r)
       if (tb + r < len) {
+        if constexpr (RESET) {
+          if (reset_at(g, b, t0 + tb + r)) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) st[i] = 0.f;
+          }
+        }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) st[i] = fmaf(a[i], xv[r][i], (1.f - a[i]) * st[i]);
         stv<T, VEC>(py + static_cast<int64_t>(tb + r) * syn, st);
@@ -235,7 +267,7 @@ __global__ __launch_bounds__(kEmaBlock) void ema_fwd_apply(const T* __restrict__
 }
 
 // ---- backward -------------------------------------------------------------
-template <typename T, int VEC>
+template <typename T, int VEC, bool RESET>
 __global__ __launch_bounds__(kEmaBlock) void ema_bwd_local(const T* __restrict__ dy, int64_t sgb, int64_t sgn,
                                                           const float* __restrict__ alpha, float* __restrict__ starts,
                                                           EmaGeom g) {
@@ -260,6 +292,12 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_local(const T* __restrict__
 #pragma unroll
     for (int r = 0; r < R; ++r)
       if (tb - r >= 0) {
+        if constexpr (RESET) {   // a reset at token t + 1 cuts the adjoint flowing back into t
+          if (tb - r + 1 < len && reset_at(g, b, t0 + tb - r + 1)) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) st[i] = 0.f;
+          }
+        }
 #pragma unroll
         for (int i = 0; i < VEC; ++i) st[i] = fmaf(dec[i], st[i], gv[r][i]);
       }
@@ -267,9 +305,14 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_local(const T* __restrict__
   float* e = starts + (static_cast<int64_t>(b) * g.NC + c) * g.D + d0;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) e[i] = st[i];
+  if (RESET && dv == 0) {   // a reset in [t0 + 1, t0 + len] (tokens inside the sequence)
+    bool cut = false;
+    for (int t = t0 + 1; t <= t0 + len && t < g.N; ++t) cut = cut || reset_at(g, b, t);
+    g.cut[b * g.NC + c] = cut;
+  }
 }
 
-template <typename T, int VEC>
+template <typename T, int VEC, bool RESET>
 __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__ x, int64_t sxb, int64_t sxn,
                                                           const T* __restrict__ y, int64_t syb, int64_t syn,
                                                           const T* __restrict__ dy, int64_t sgb, int64_t sgn,
@@ -318,6 +361,16 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
     for (int r = 0; r < R; ++r) {
       const int t = tb - r;
       if (t >= 0) {
+        if constexpr (RESET) {
+          if (t0 + t + 1 < g.N && reset_at(g, b, t0 + t + 1)) {   // cut from the future (or the carry)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) st[i] = 0.f;
+          }
+          if (reset_at(g, b, t0 + t)) {   // y[t-1] does not feed token t (ema:445-448)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) yp[r][i] = 0.f;
+          }
+        }
         float out[VEC];
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
@@ -402,50 +455,64 @@ inline size_t ws_floats(int B, int N, int D) {
   return static_cast<size_t>(B) * NC * D;
 }
 
-inline EmaGeom make_geom(int B, int N, int D, int vec, int per_channel, float lo, float hi) {
+// the per-chunk cut flags, after the float arrays
+inline size_t ws_cut_bytes(int B, int N) {
+  const int NC = (N + kChunkT - 1) / kChunkT;
+  return (static_cast<size_t>(B) * NC + 255) / 256 * 256;
+}
+
+inline EmaGeom make_geom(int B, int N, int D, int vec, int per_channel, float lo, float hi, const uint8_t* reset,
+                         const int64_t* reset_stride, void* workspace, size_t nfloats) {
   EmaGeom g;
   g.B = B; g.N = N; g.D = D;
   g.NC = (N + kChunkT - 1) / kChunkT;
   g.DV = D / vec;
   g.per_channel = per_channel;
   g.lo = lo; g.hi = hi;
+  g.reset = reset;
+  g.srb = reset ? reset_stride[0] : 0;
+  g.srn = reset ? reset_stride[1] : 0;
+  g.cut = static_cast<uint8_t*>(workspace) + nfloats * sizeof(float);
   return g;
 }
 
-template <typename T, int VEC>
+template <typename T, int VEC, bool RESET>
 hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
-  const EmaGeom g = make_geom(a.B, a.N, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling);
+  const size_t nf = ws_floats(a.B, a.N, a.D);
+  const EmaGeom g = make_geom(a.B, a.N, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
+                              a.reset_stride, a.workspace, 2 * nf);
   float* ends = static_cast<float*>(a.workspace);
-  float* carries = ends + ws_floats(a.B, a.N, a.D);
+  float* carries = ends + nf;
   const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
   const T* x = static_cast<const T*>(a.x);
   T* y = static_cast<T*>(a.y);
-  hipLaunchKernelGGL((ema_fwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
+  hipLaunchKernelGGL((ema_fwd_local<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], a.alpha, ends, g);
   const int cblocks = a.B * ((a.D + kCarryChannels - 1) / kCarryChannels);
-  hipLaunchKernelGGL((ema_carry<false>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, ends, carries,
+  hipLaunchKernelGGL((ema_carry<false, RESET>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, ends, carries,
                      a.alpha, g);
-  hipLaunchKernelGGL((ema_fwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
+  hipLaunchKernelGGL((ema_fwd_apply<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], y, a.y_stride[0], a.y_stride[1], a.alpha, carries, g);
   return hipGetLastError();
 }
 
-template <typename T, int VEC>
+template <typename T, int VEC, bool RESET>
 hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
-  const EmaGeom g = make_geom(a.B, a.N, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling);
   const size_t nf = ws_floats(a.B, a.N, a.D);
+  const EmaGeom g = make_geom(a.B, a.N, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
+                              a.reset_stride, a.workspace, 3 * nf);
   float* starts = static_cast<float*>(a.workspace);
   float* carries = starts + nf;
   float* da_part = carries + nf;
   const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
-  hipLaunchKernelGGL((ema_bwd_local<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
+  hipLaunchKernelGGL((ema_bwd_local<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream,
                      static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1], a.alpha, starts, g);
   const int cblocks = a.B * ((a.D + kCarryChannels - 1) / kCarryChannels);
-  hipLaunchKernelGGL((ema_carry<true>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, starts, carries,
+  hipLaunchKernelGGL((ema_carry<true, RESET>), dim3(cblocks), dim3(kWave * kCarryWaves), 0, stream, starts, carries,
                      a.alpha, g);
-  hipLaunchKernelGGL((ema_bwd_apply<T, VEC>), dim3(blocks), dim3(kEmaBlock), 0, stream,
+  hipLaunchKernelGGL((ema_bwd_apply<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream,
                      static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<const T*>(a.y),
                      a.y_stride[0], a.y_stride[1], static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1],
                      static_cast<T*>(a.dx), a.dx_stride[0], a.dx_stride[1], a.alpha, carries, da_part, g);
@@ -466,19 +533,35 @@ hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
 
 }  // namespace
 
-size_t ema_fwd_workspace(int B, int N, int D) { return 2 * ws_floats(B, N, D) * sizeof(float); }
-size_t ema_bwd_workspace(int B, int N, int D) { return 3 * ws_floats(B, N, D) * sizeof(float); }
+size_t ema_fwd_workspace(int B, int N, int D) {
+  return 2 * ws_floats(B, N, D) * sizeof(float) + ws_cut_bytes(B, N);
+}
+size_t ema_bwd_workspace(int B, int N, int D) {
+  return 3 * ws_floats(B, N, D) * sizeof(float) + ws_cut_bytes(B, N);
+}
+
+template <bool RESET>
+hipError_t launch_ema_fwd_r(const dwarf_ema_fwd_args& a, hipStream_t stream) {
+  const bool vec4 = (a.D % 4) == 0;
+  if (a.dtype == DWARF_BF16)
+    return vec4 ? ema_fwd_typed<bf16, 4, RESET>(a, stream) : ema_fwd_typed<bf16, 1, RESET>(a, stream);
+  return vec4 ? ema_fwd_typed<float, 4, RESET>(a, stream) : ema_fwd_typed<float, 1, RESET>(a, stream);
+}
+
+template <bool RESET>
+hipError_t launch_ema_bwd_r(const dwarf_ema_bwd_args& a, hipStream_t stream) {
+  const bool vec4 = (a.D % 4) == 0;
+  if (a.dtype == DWARF_BF16)
+    return vec4 ? ema_bwd_typed<bf16, 4, RESET>(a, stream) : ema_bwd_typed<bf16, 1, RESET>(a, stream);
+  return vec4 ? ema_bwd_typed<float, 4, RESET>(a, stream) : ema_bwd_typed<float, 1, RESET>(a, stream);
+}
 
 hipError_t launch_ema_fwd(const dwarf_ema_fwd_args& a, hipStream_t stream) {
-  const bool vec4 = (a.D % 4) == 0;
-  if (a.dtype == DWARF_BF16) return vec4 ? ema_fwd_typed<bf16, 4>(a, stream) : ema_fwd_typed<bf16, 1>(a, stream);
-  return vec4 ? ema_fwd_typed<float, 4>(a, stream) : ema_fwd_typed<float, 1>(a, stream);
+  return a.reset ? launch_ema_fwd_r<true>(a, stream) : launch_ema_fwd_r<false>(a, stream);
 }
 
 hipError_t launch_ema_bwd(const dwarf_ema_bwd_args& a, hipStream_t stream) {
-  const bool vec4 = (a.D % 4) == 0;
-  if (a.dtype == DWARF_BF16) return vec4 ? ema_bwd_typed<bf16, 4>(a, stream) : ema_bwd_typed<bf16, 1>(a, stream);
-  return vec4 ? ema_bwd_typed<float, 4>(a, stream) : ema_bwd_typed<float, 1>(a, stream);
+  return a.reset ? launch_ema_bwd_r<true>(a, stream) : launch_ema_bwd_r<false>(a, stream);
 }
 
 }  // namespace dwarf

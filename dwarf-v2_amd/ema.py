@@ -6,7 +6,9 @@ arguments and errors.  The scan runs the HIP kernels of libdwarf_dsqg.so:
 y[t] = a x[t] + (1 - a) y[t-1] with fp32 state, a = clamp(ema_factor, floor,
 ceiling).  ``ema_factor`` may hold one value (the reference contract) or one
 value per channel of x (an extension used by the long-context benchmark).
-The reset-aware variant (``reset_mask``, ema:368-509) is not built here.
+With ``reset_mask`` [B,N] the state is zeroed before the marked tokens, the
+reset-aware scan of ``_CausalEMAResetFn`` (ema:368-509), on the same chunked
+kernels.
 """
 
 from __future__ import annotations
@@ -58,8 +60,23 @@ def normalize_alpha(alpha: torch.Tensor, device: torch.device) -> torch.Tensor:
     return alpha.detach().to(device=device, dtype=torch.float32).reshape(-1).contiguous()
 
 
-def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: float) -> torch.Tensor:
-    """Raw launch: y with x's dtype.  alpha fp32 on x's device, numel 1 or D."""
+def normalize_reset(reset_mask: torch.Tensor | None, x: torch.Tensor) -> torch.Tensor | None:
+    """[B,N] one byte per token on x's device (torch.bool), or None."""
+    if reset_mask is None:
+        return None
+    if tuple(reset_mask.shape) != tuple(x.shape[:2]):
+        raise ValueError(f"reset_mask must have shape {tuple(x.shape[:2])}")
+    return reset_mask.to(device=x.device, dtype=torch.bool)
+
+
+def _set_reset(a, reset: torch.Tensor | None) -> None:
+    if reset is not None:
+        a.reset, a.reset_stride = reset.data_ptr(), _lib.i64_array(reset.stride())
+
+
+def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: float,
+                reset: torch.Tensor | None = None) -> torch.Tensor:
+    """Raw launch: y with x's dtype.  alpha fp32 on x's device, numel 1 or D; reset [B,N] bool or None."""
     lib = _lib.load()
     B, N, D = x.shape
     y = torch.empty((B, N, D), device=x.device, dtype=x.dtype)
@@ -71,6 +88,7 @@ def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: flo
     a.x, a.x_stride = x.data_ptr(), _lib.i64_array(x.stride())
     a.alpha = alpha.data_ptr()
     a.y, a.y_stride = y.data_ptr(), _lib.i64_array(y.stride())
+    _set_reset(a, reset)
     ws = torch.empty(max(int(lib.dwarf_ema_fwd_workspace_bytes(ctypes.byref(a))), 16), device=x.device,
                      dtype=torch.uint8)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
@@ -78,8 +96,8 @@ def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: flo
     return y
 
 
-def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool):
-    """Raw launch: (dx, dalpha or None); dalpha already clamp-projected."""
+def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool, reset: torch.Tensor | None = None):
+    """Raw launch: (dx, dalpha or None); dalpha already clamp-projected; reset as in ema_forward."""
     lib = _lib.load()
     B, N, D = x.shape
     dy = _btd(dy.to(x.dtype))
@@ -96,6 +114,7 @@ def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool):
     a.alpha = alpha.data_ptr()
     a.dx, a.dx_stride = dx.data_ptr(), _lib.i64_array(dx.stride())
     a.dalpha = dalpha.data_ptr() if dalpha is not None else None
+    _set_reset(a, reset)
     ws = torch.empty(max(int(lib.dwarf_ema_bwd_workspace_bytes(ctypes.byref(a))), 16), device=x.device,
                      dtype=torch.uint8)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
@@ -125,6 +144,29 @@ class _CausalEMAFn(torch.autograd.Function):
         return dx, dalpha.reshape(ctx.alpha_shape).to(ctx.alpha_dtype), None, None
 
 
+class _CausalEMAResetFn(torch.autograd.Function):
+    """Reset-aware scan (reference: ema:455-509, same arguments and gradient slots) over the
+    same custom ops with a reset mask."""
+
+    @staticmethod
+    def forward(ctx, x, alpha_input, reset_mask, floor, ceiling):
+        reset = normalize_reset(reset_mask, x)
+        alpha = alpha_input.detach().to(device=x.device, dtype=torch.float32).reshape(-1)
+        y = torch.ops.dwarf.ema_fwd(x, alpha, float(floor), float(ceiling), reset)
+        ctx.save_for_backward(x, y, alpha, reset)
+        ctx.floor, ctx.ceiling = float(floor), float(ceiling)
+        ctx.alpha_shape, ctx.alpha_dtype = alpha_input.shape, alpha_input.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, y, alpha, reset = ctx.saved_tensors
+        dx, dalpha = torch.ops.dwarf.ema_bwd(x, y, dy, alpha, ctx.floor, ctx.ceiling, reset)
+        if not ctx.needs_input_grad[1]:
+            return dx, None, None, None, None
+        return dx, dalpha.reshape(ctx.alpha_shape).to(ctx.alpha_dtype), None, None, None
+
+
 def causal_ema_scan(x: torch.Tensor, ema_factor: torch.Tensor, floor: float = 1e-5, ceiling: float = 0.5, *,
                     reset_mask: torch.Tensor | None = None) -> torch.Tensor:
     """Causal EMA of x[B,N,D] on the HIP kernels (reference signature: ema:541-567)."""
@@ -134,11 +176,13 @@ def causal_ema_scan(x: torch.Tensor, ema_factor: torch.Tensor, floor: float = 1e
         raise ValueError("ema_factor must contain one scalar or one value per channel")
     if not (0 < float(floor) < float(ceiling) < 1):
         raise ValueError("EMA bounds must satisfy 0 < floor < ceiling < 1")
-    if reset_mask is not None:
-        raise NotImplementedError("the reset-aware EMA scan is not built in this library")
+    if reset_mask is not None and tuple(reset_mask.shape) != tuple(x.shape[:2]):
+        raise ValueError(f"reset_mask must have shape {tuple(x.shape[:2])}")
     if not x.is_cuda:
         raise RuntimeError("the EMA HIP kernels require device tensors")
-    if x.dtype not in (torch.float32, torch.bfloat16):
-        out = _CausalEMAFn.apply(x.to(torch.bfloat16), ema_factor, float(floor), float(ceiling))
-        return out.to(x.dtype)
-    return _CausalEMAFn.apply(x, ema_factor, float(floor), float(ceiling))
+    xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.bfloat16)
+    if reset_mask is not None:
+        out = _CausalEMAResetFn.apply(xin, ema_factor, reset_mask, float(floor), float(ceiling))
+    else:
+        out = _CausalEMAFn.apply(xin, ema_factor, float(floor), float(ceiling))
+    return out if out.dtype == x.dtype else out.to(x.dtype)

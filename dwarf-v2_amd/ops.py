@@ -14,6 +14,8 @@ boundary of the reference ops (kernels/dsqg_attention_v22.py:2691-2777 and
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 
 from . import dsqg as _dsqg
@@ -64,26 +66,29 @@ def _dsqg_bwd_fake(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain,
 
 # ---- EMA -------------------------------------------------------------------------------------
 @torch.library.custom_op("dwarf::ema_fwd", mutates_args=())
-def ema_fwd(x: Tensor, alpha: Tensor, floor: float, ceiling: float) -> Tensor:
-    """y = causal EMA of x [B,N,D] (x's dtype); alpha fp32 with 1 or D values."""
-    return _ema.ema_forward(_ema.normalize_x(x), _ema.normalize_alpha(alpha, x.device), floor, ceiling)
+def ema_fwd(x: Tensor, alpha: Tensor, floor: float, ceiling: float, reset: Optional[Tensor] = None) -> Tensor:
+    """y = causal EMA of x [B,N,D] (x's dtype); alpha fp32 with 1 or D values; reset [B,N] bool or None."""
+    return _ema.ema_forward(_ema.normalize_x(x), _ema.normalize_alpha(alpha, x.device), floor, ceiling,
+                            _ema.normalize_reset(reset, x))
 
 
 @ema_fwd.register_fake
-def _ema_fwd_fake(x, alpha, floor, ceiling):
+def _ema_fwd_fake(x, alpha, floor, ceiling, reset=None):
     return x.new_empty(x.shape)
 
 
 @torch.library.custom_op("dwarf::ema_bwd", mutates_args=())
-def ema_bwd(x: Tensor, y: Tensor, dy: Tensor, alpha: Tensor, floor: float, ceiling: float) -> tuple[Tensor, Tensor]:
+def ema_bwd(x: Tensor, y: Tensor, dy: Tensor, alpha: Tensor, floor: float, ceiling: float,
+            reset: Optional[Tensor] = None) -> tuple[Tensor, Tensor]:
     """(dx like x, dalpha fp32 [alpha.numel()], clamp-projected)."""
     dx, dalpha = _ema.ema_backward(_ema.normalize_x(x), _ema.normalize_x(y), dy,
-                                   _ema.normalize_alpha(alpha, x.device), floor, ceiling, True)
+                                   _ema.normalize_alpha(alpha, x.device), floor, ceiling, True,
+                                   _ema.normalize_reset(reset, x))
     return dx, dalpha
 
 
 @ema_bwd.register_fake
-def _ema_bwd_fake(x, y, dy, alpha, floor, ceiling):
+def _ema_bwd_fake(x, y, dy, alpha, floor, ceiling, reset=None):
     return x.new_empty(x.shape), x.new_empty((alpha.numel(),), dtype=torch.float32)
 
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 1
+#define DWARF_ABI_VERSION 2
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
@@ -147,7 +147,9 @@ int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 /*
  * x, y [B,N,D] of `dtype` (unit stride on D); alpha fp32 on the device, one
  * value (alpha_per_channel = 0, the reference's contract, ema:557-558) or D
- * values (alpha_per_channel = 1).  State is fp32.
+ * values (alpha_per_channel = 1).  State is fp32.  reset, when not NULL,
+ * holds one byte per (b, t): nonzero zeroes the state before token t, the
+ * reset-aware scan of _CausalEMAResetFn (ema:368-509).
  */
 typedef struct {
   int32_t B, N, D;
@@ -158,11 +160,13 @@ typedef struct {
   const float* alpha;
   void* y; int64_t y_stride[3];
   void* workspace; size_t workspace_bytes;
+  const uint8_t* reset; int64_t reset_stride[2];  /* [B,N] bool (1 byte), or NULL */
 } dwarf_ema_fwd_args;
 
 size_t dwarf_ema_fwd_workspace_bytes(const dwarf_ema_fwd_args* args);
 
-/* Replaces _CausalEMAFn.forward's three launches (ema:265-313). */
+/* Replaces _CausalEMAFn.forward's three launches (ema:265-313) and, with
+ * reset flags, _CausalEMAResetFn.forward's serial launch (ema:455-476). */
 int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream);
 
 /*
@@ -182,11 +186,13 @@ typedef struct {
   void* dx; int64_t dx_stride[3];
   float* dalpha;
   void* workspace; size_t workspace_bytes;
+  const uint8_t* reset; int64_t reset_stride[2];  /* the forward's reset flags, or NULL */
 } dwarf_ema_bwd_args;
 
 size_t dwarf_ema_bwd_workspace_bytes(const dwarf_ema_bwd_args* args);
 
-/* Replaces _CausalEMAFn.backward's three launches (ema:315-364). */
+/* Replaces _CausalEMAFn.backward's three launches (ema:315-364) and, with
+ * reset flags, _CausalEMAResetFn.backward's serial launch (ema:478-509). */
 int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */

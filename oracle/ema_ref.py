@@ -4,7 +4,9 @@ Follows the reference recurrence (kernels/causal_ema_scan.py:3-11) and its
 eager ``_reference`` (ema:511-538): a = clamp(alpha, floor, ceiling),
 y[t] = a x[t] + (1 - a) y[t-1], y[-1] = 0, with float64 state for float64
 inputs and float32 state otherwise.  alpha may be one value or one per
-channel ([D]); ``_reference`` broadcasts a [D] alpha the same way.
+channel ([D]); ``_reference`` broadcasts a [D] alpha the same way.  An
+optional reset_mask [B,N] zeroes the state before the tokens it marks
+(ema:368-509, 533-535).
 """
 
 from __future__ import annotations
@@ -12,7 +14,9 @@ from __future__ import annotations
 import torch
 
 
-def ema_scan(x: torch.Tensor, alpha: torch.Tensor, floor: float = 1e-5, ceiling: float = 0.5) -> torch.Tensor:
+def ema_scan(x: torch.Tensor, alpha: torch.Tensor, floor: float = 1e-5, ceiling: float = 0.5,
+             reset_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """reset_mask [B,N] bool: the state is zeroed before token t where set (ema:533-535)."""
     acc = torch.float64 if x.dtype == torch.float64 else torch.float32
     a = alpha.to(acc).clamp(floor, ceiling).reshape(-1)
     decay = 1.0 - a
@@ -20,6 +24,8 @@ def ema_scan(x: torch.Tensor, alpha: torch.Tensor, floor: float = 1e-5, ceiling:
     state = torch.zeros(x.shape[0], x.shape[2], dtype=acc)
     rows = []
     for t in range(x.shape[1]):
+        if reset_mask is not None:
+            state = torch.where(reset_mask[:, t, None], torch.zeros_like(state), state)
         state = a * xf[:, t] + decay * state
         rows.append(state)
     if not rows:
@@ -40,10 +46,12 @@ def ema_closed_form(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
 
 
 def ema_adjoint(x: torch.Tensor, y: torch.Tensor, dy: torch.Tensor, alpha: torch.Tensor,
-                floor: float = 1e-5, ceiling: float = 0.5):
+                floor: float = 1e-5, ceiling: float = 0.5, reset_mask: torch.Tensor | None = None):
     """Reverse adjoint (ema:3-11): lambda[t] = dy[t] + (1-a) lambda[t+1], dx = a lambda,
     dalpha = sum lambda[t] (x[t] - y[t-1]); dalpha per channel summed over batch and time,
-    then zeroed where the clamp blocks it (ema:357-364)."""
+    then zeroed where the clamp blocks it (ema:357-364).  With reset_mask
+    (ema:427-451): lambda[t+1] is cut where token t+1 resets, and y[t-1] is 0
+    where token t resets."""
     acc = torch.float64 if x.dtype == torch.float64 else torch.float32
     a_in = alpha.to(acc).reshape(-1)
     a = a_in.clamp(floor, ceiling)
@@ -52,10 +60,15 @@ def ema_adjoint(x: torch.Tensor, y: torch.Tensor, dy: torch.Tensor, alpha: torch
     lam = torch.zeros(B, D, dtype=acc)
     dx = torch.zeros(B, N, D, dtype=acc)
     da = torch.zeros(B, D, dtype=acc)
+    zero = torch.zeros(B, D, dtype=acc)
     for t in range(N - 1, -1, -1):
+        if reset_mask is not None and t + 1 < N:
+            lam = torch.where(reset_mask[:, t + 1, None], zero, lam)
         lam = g[:, t] + (1 - a) * lam
         dx[:, t] = a * lam
-        prev = yf[:, t - 1] if t > 0 else torch.zeros(B, D, dtype=acc)
+        prev = yf[:, t - 1] if t > 0 else zero
+        if reset_mask is not None:
+            prev = torch.where(reset_mask[:, t, None], zero, prev)
         da += lam * (xf[:, t] - prev)
     da = da.sum(0)
     if a_in.numel() == 1:

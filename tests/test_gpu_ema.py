@@ -124,3 +124,59 @@ def test_graph_replay_matches_eager(pkg, device):
         for o, r in zip(outs, ref):
             assert torch.equal(o, r)
         del other
+
+
+def run_reset(pkg, x, alpha, dy, reset, device):
+    xd = x.to(device).requires_grad_(True)
+    ad = alpha.to(device).requires_grad_(True)
+    y = pkg.causal_ema_scan(xd, ad, reset_mask=reset.to(device))
+    y.backward(dy.to(device=device, dtype=y.dtype))
+    torch.cuda.synchronize()
+    return y.detach().cpu(), xd.grad.cpu(), ad.grad.cpu()
+
+
+def reset_pattern(B, N, g, kind):
+    r = torch.zeros(B, N, dtype=torch.bool)
+    if kind == "chunk_edges":      # at chunk starts, chunk ends, the first and last token, back to back
+        for t in (0, 15, 16, 17, 31, 32, 33, 47, 48, N - 1):
+            if t < N:
+                r[:, t] = True
+    else:
+        r = torch.rand(B, N, generator=g) < 0.05
+    return r
+
+
+@pytest.mark.parametrize("B,N,D,per_channel,kind", [(2, 300, 64, False, "random"), (2, 257, 64, True, "chunk_edges"),
+                                                    (3, 130, 7, True, "random"), (2, 49, 8, False, "chunk_edges"),
+                                                    (1, 1000, 512, True, "random")])
+def test_reset_fp32(pkg, device, B, N, D, per_channel, kind):
+    """Reset-aware scan (ema:368-509) against the float64 oracle: y, dx, dalpha <= 1e-5 relative."""
+    g = torch.Generator().manual_seed(N + D + 1)
+    x = torch.randn(B, N, D, generator=g)
+    alpha = torch.rand(D if per_channel else 1, generator=g) * 0.2 + 0.01
+    dy = torch.randn(B, N, D, generator=g)
+    reset = reset_pattern(B, N, g, kind)
+    y, dx, da = run_reset(pkg, x, alpha, dy, reset, device)
+    ry = ema_ref.ema_scan(x.double(), alpha.double(), reset_mask=reset)
+    rdx, rda = ema_ref.ema_adjoint(x.double(), ry, dy.double(), alpha.double(), reset_mask=reset)
+    assert rel_err(y, ry) < 1e-5
+    assert rel_err(dx, rdx) < 1e-5
+    assert rel_err(da, rda) < 1e-5
+
+
+def test_reset_bf16_and_all_false_mask(pkg, device):
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(2, 3000, 512, generator=g).to(torch.bfloat16)
+    alpha = 1.0 - (0.90 + 0.099 * torch.rand(512, generator=g))
+    dy = torch.randn(2, 3000, 512, generator=g).to(torch.bfloat16)
+    reset = torch.rand(2, 3000, generator=g) < 0.01
+    y, dx, da = run_reset(pkg, x, alpha, dy, reset, device)
+    ry = ema_ref.ema_scan(x.float(), alpha, reset_mask=reset)
+    assert max_abs(y, ry) < 2e-2
+    rdx, rda = ema_ref.ema_adjoint(x.float(), y.float(), dy.float(), alpha, reset_mask=reset)
+    assert max_abs(dx, rdx) < 2e-2
+    assert rel_err(da, rda) < 1e-3
+    # an all-false mask runs the reset kernels and gives the plain scan's results bit for bit
+    none = torch.zeros(2, 3000, dtype=torch.bool)
+    assert all(torch.equal(a, b) for a, b in zip(run_reset(pkg, x, alpha, dy, none, device),
+                                                 run(pkg, x, alpha, dy, device)))

@@ -82,7 +82,9 @@ def test_ema_errors(pkg):
         pkg.causal_ema_scan(x, torch.tensor([0.1, 0.2]))
     with pytest.raises(ValueError):
         pkg.causal_ema_scan(x, a, 0.6, 0.5)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):   # reset_mask must be [B,N] (ema:463-464)
+        pkg.causal_ema_scan(x, a, reset_mask=torch.zeros(2, 4, dtype=torch.bool))
+    with pytest.raises(RuntimeError):
         pkg.causal_ema_scan(x, a, reset_mask=torch.zeros(2, 5, dtype=torch.bool))
     with pytest.raises(RuntimeError):
         pkg.causal_ema_scan(x, a)

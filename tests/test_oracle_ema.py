@@ -69,3 +69,37 @@ def test_gradcheck_through_bounded_factor():
         ema.inverse_bounded_ema_factor(0.6)
     with pytest.raises(ValueError):
         ema.bounded_ema_factor(raw, floor=0.5, ceiling=0.4)
+
+
+def test_reset_scan_is_independent_segments():
+    """With resets the scan restarts: each segment between resets equals the
+    closed form over that segment alone."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 40, 3, generator=g, dtype=torch.float64)
+    alpha = torch.tensor([0.2, 0.05, 0.4], dtype=torch.float64)
+    reset = torch.zeros(2, 40, dtype=torch.bool)
+    reset[0, [0, 7, 8, 31]] = True
+    reset[1, [39]] = True
+    y = ema_ref.ema_scan(x, alpha, reset_mask=reset)
+    for b in range(2):
+        cuts = [0] + [t for t in range(1, 40) if reset[b, t]] + [40]
+        for s0, s1 in zip(cuts[:-1], cuts[1:]):
+            want = ema_ref.ema_closed_form(x[b:b + 1, s0:s1], alpha)
+            assert float((y[b:b + 1, s0:s1] - want).abs().max()) < 1e-13
+    assert torch.equal(ema_ref.ema_scan(x, alpha, reset_mask=torch.zeros(2, 40, dtype=torch.bool)),
+                       ema_ref.ema_scan(x, alpha))
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_reset_adjoint_equals_autograd(per_channel):
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(2, 23, 4, generator=g, dtype=torch.float64, requires_grad=True)
+    alpha = (torch.rand(4 if per_channel else 1, generator=g, dtype=torch.float64) * 0.3 + 0.05).requires_grad_(True)
+    reset = torch.rand(2, 23, generator=g) < 0.2
+    reset[:, 22] = True
+    dy = torch.randn(2, 23, 4, generator=g, dtype=torch.float64)
+    y = ema_ref.ema_scan(x, alpha, reset_mask=reset)
+    gx, ga = torch.autograd.grad(y, (x, alpha), dy)
+    dx, da = ema_ref.ema_adjoint(x.detach(), y.detach(), dy, alpha.detach(), reset_mask=reset)
+    assert float((dx - gx).abs().max()) < 1e-12
+    assert float((da - ga).abs().max()) < 1e-11
