@@ -743,9 +743,9 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
       }
     };
 
-    // per pair of the chunk: returns dS in ds_out[jj]
-    auto consume = [&](const DqChunk<SHIFT, CJ>& c, float* ds_out) {
-      float ph_sum[CJ][2];
+    // per pair of the chunk: returns dS in ds_out[jj] and the lane's dPhase
+    // terms (tq, tq y z) in ph_out[2 jj], ph_out[2 jj + 1]
+    auto consume = [&](const DqChunk<SHIFT, CJ>& c, float* ds_out, float* ph_out) {
 #pragma unroll
       for (int jj = 0; jj < CJ; ++jj) {
         const int j = c.j[jj];
@@ -797,18 +797,8 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
         const float tq = P * tq_pre;
         dy = fmaf(tq * pg, c.z[jj], dy);
         pin_regs<1>(&dy);
-        ph_sum[jj][0] = tq;
-        ph_sum[jj][1] = tq * yg * c.z[jj];
-      }
-#pragma unroll
-      for (int jj = 0; jj < CJ; ++jj) {
-        const int j = c.j[jj];
-        if (j >= J_small && j < J) {   // wave-uniform
-          const float s0 = sum_over_queries16(ph_sum[jj][0]);
-          const float s1 = sum_over_queries16(ph_sum[jj][1]);
-          // each far offset appears once in the list: a store, no accumulation
-          if (l < 4) *reinterpret_cast<float2*>(s_dph + (j - J_small) * 8 + 2 * g) = make_float2(s0, s1);
-        }
+        ph_out[2 * jj] = tq;
+        ph_out[2 * jj + 1] = tq * yg * c.z[jj];
       }
     };
 
@@ -825,25 +815,46 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
         dqe[nb] = mfma16_f32(av, __uint_as_float(static_cast<uint32_t>(er[16 * nb]) << 16), dqe[nb]);
     };
 
+    // dPhase of the step's four offsets summed over the wave's 16 queries,
+    // reduce-scattered: after the two lane swaps 16-lane row k holds offset k
+    // (tq in u0, tq y z in u1) for four queries per plane, and two row
+    // rotations add the other twelve.  Far offsets are stored (each appears
+    // once in the list: a store, no accumulation).
+    auto dphase_step = [&](const float* ph8, const int* j4) {
+      float r[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = add_swap32(ph8[i], ph8[i + 4]);
+      float u0 = add_swap16(r[0], r[2]), u1 = add_swap16(r[1], r[3]);
+      u0 += dpp_f<0x124>(u0);   // row_ror:4
+      u1 += dpp_f<0x124>(u1);
+      u0 += dpp_f<0x128>(u0);   // row_ror:8
+      u1 += dpp_f<0x128>(u1);
+      const int k = l >> 4;
+      const int jk = k == 0 ? j4[0] : k == 1 ? j4[1] : k == 2 ? j4[2] : j4[3];
+      if (((l >> 2) & 3) == 0 && jk >= J_small && jk < J)
+        *reinterpret_cast<float2*>(s_dph + (jk - J_small) * 8 + 2 * g) = make_float2(u0, u1);
+    };
+
     if (cnt > 0) {
       DqChunk<SHIFT, CJ> c0, c1;
       fetch(0, c0);
       for (int k0 = 0; k0 < cnt; k0 += kStepDq) {
-        float ds4[kStepDq];
+        float ds4[kStepDq], ph8[2 * kStepDq];
         int j4[kStepDq];
         j4[0] = c0.j[0];
         fetch(k0 + 1, c1);
-        consume(c0, ds4);
+        consume(c0, ds4, ph8);
         j4[1] = c1.j[0];
         fetch(k0 + 2, c0);
-        consume(c1, ds4 + 1);
+        consume(c1, ds4 + 1, ph8 + 2);
         j4[2] = c0.j[0];
         fetch(k0 + 3, c1);
-        consume(c0, ds4 + 2);
+        consume(c0, ds4 + 2, ph8 + 4);
         j4[3] = c1.j[0];
         fetch(k0 + 4, c0);
-        consume(c1, ds4 + 3);
+        consume(c1, ds4 + 3, ph8 + 6);
         dqe_step(ds4, j4);
+        dphase_step(ph8, j4);
       }
     }
     __syncthreads();   // every wave's dPhase table is complete
