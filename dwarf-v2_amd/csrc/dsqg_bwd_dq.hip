@@ -693,6 +693,14 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     if (row_ok && g == 0)
       *reinterpret_cast<float2*>(delta_ws + 2 * (static_cast<int64_t>(bh) * N + n)) =
           make_float2(dlt, mass ? lse2 : INFINITY);
+    // the wave's q rows as the B operand of the per-step <q, e_j> MFMA: lane
+    // (lr, lc) holds dims 32 ks + 8 lc + [0, 8) of query n0w + lr
+    uint4 xq[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (n0w + lr < N) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        xq[ks] = *reinterpret_cast<const uint4*>(qb + static_cast<int64_t>(n0w + lr) * f.q_stride[2] + 32 * ks + 8 * lc);
+    }
     const int n_eff = mass ? n : n0w - 2 * N;   // no source for queries without softmax mass
     const int kb_lane = n_eff * ks_b + 32 * g;
     const int vb_lane = n_eff * vs_b + 32 * g;
@@ -743,23 +751,20 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
       }
     };
 
-    // per pair of the chunk: returns dS in ds_out[jj] and the lane's dPhase
-    // terms (tq, tq y z) in ph_out[2 jj], ph_out[2 jj + 1]
-    auto consume = [&](const DqChunk<SHIFT, CJ>& c, float* ds_out, float* ph_out) {
+    // per pair of the chunk (qe: <q, e_j> of the lane's query, from the step's
+    // MFMA): returns dS in ds_out[jj] and the lane's dPhase terms (tq, tq y z)
+    // in ph_out[2 jj], ph_out[2 jj + 1]
+    auto consume = [&](const DqChunk<SHIFT, CJ>& c, float* ds_out, float* ph_out, float qe) {
 #pragma unroll
       for (int jj = 0; jj < CJ; ++jj) {
         const int j = c.j[jj];
         const bool far = j >= J_small && j < J;
         const uint32_t* kw = reinterpret_cast<const uint32_t*>(&c.k[jj][0]);
         const uint32_t* vw = reinterpret_cast<const uint32_t*>(&c.v[jj][0]);
-        const uint4* e4 = reinterpret_cast<const uint4*>(sE + j * kERowT + 16 * g);
-        const uint4 e0 = e4[0], e1 = e4[1];
-        const uint32_t ew[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
         float dot = 0.f, gd = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           dot = dot2bf(q32[i], kw[i], dot);
-          dot = dot2bf(q32[i], ew[i], dot);
           gd = dot2bf(d32[i], vw[i], gd);
         }
         float tq_pre = 0.f, pg = 0.f;
@@ -775,7 +780,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
           gd += da * (cs * va - sn * vb - va) + db * (sn * va + cs * vb - vb);
           tq_pre = da * (-va * sn - vb * cs) + db * (va * cs - vb * sn);
         }
-        dot = group_sum<4>(dot);
+        dot = group_sum<4>(dot) + qe;
         gd = group_sum<4>(gd);
         // exp2(-inf) = 0 without a source (no branch around the exponential)
         const float P = __builtin_amdgcn_exp2f(c.ok[jj] ? fmaf(dot, kC, c.pb2[jj]) - lse2 : -INFINITY);
@@ -841,18 +846,33 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
       for (int k0 = 0; k0 < cnt; k0 += kStepDq) {
         float ds4[kStepDq], ph8[2 * kStepDq];
         int j4[kStepDq];
+        // <q, e_j> of the wave's 16 queries for the step's four offsets:
+        // A = the four E rows (rows 4..15 zero), B = q^T; lane q (< 16)
+        // receives offset k in register k
+        f32x4 qe = zero4();
+        {
+          uint4 ea[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+          if (lr < kStepDq) {
+            const int jr = s_list[k0 + lr].x;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+              ea[ks] = *reinterpret_cast<const uint4*>(sE + jr * kERowT + 32 * ks + 8 * lc);
+          }
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) qe = mfma16_bf16(bf16x8_from_bits(ea[ks]), bf16x8_from_bits(xq[ks]), qe);
+        }
         j4[0] = c0.j[0];
         fetch(k0 + 1, c1);
-        consume(c0, ds4, ph8);
+        consume(c0, ds4, ph8, __shfl(qe[0], qi));
         j4[1] = c1.j[0];
         fetch(k0 + 2, c0);
-        consume(c1, ds4 + 1, ph8 + 2);
+        consume(c1, ds4 + 1, ph8 + 2, __shfl(qe[1], qi));
         j4[2] = c0.j[0];
         fetch(k0 + 3, c1);
-        consume(c0, ds4 + 2, ph8 + 4);
+        consume(c0, ds4 + 2, ph8 + 4, __shfl(qe[2], qi));
         j4[3] = c1.j[0];
         fetch(k0 + 4, c0);
-        consume(c1, ds4 + 3, ph8 + 6);
+        consume(c1, ds4 + 3, ph8 + 6, __shfl(qe[3], qi));
         dqe_step(ds4, j4);
         dphase_step(ph8, j4);
       }
