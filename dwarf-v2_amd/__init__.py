@@ -9,12 +9,14 @@ Public surface (reference names, Lanerra/dwarf-v2):
   causal_ema_scan, bounded_ema_factor,
   inverse_bounded_ema_factor                         kernels/causal_ema_scan.py
   phase_probe_features, _PhaseProbeFn                kernels/dsqg_attention_v22.py
+  npci_rotate                                        kernels/dsqg_attention_v22.py
   q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
 """
 
-from . import _lib, lattice, ops, probe, q6
+from . import _lib, lattice, npci, ops, probe, q6
 from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
 from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
+from .npci import npci_rotate
 from .probe import _PhaseProbeFn, phase_probe_features
 from .lattice import (
     ALL_OFFSETS,
@@ -44,6 +46,7 @@ __all__ = [
     "dsqg_backward",
     "dsqg_forward",
     "inverse_bounded_ema_factor",
+    "npci_rotate",
     "phase_probe_features",
     "q6",
 ]

@@ -44,6 +44,9 @@ EXPORTED_SYMBOLS = (
     "dwarf_phase_probe_fwd",
     "dwarf_phase_probe_bwd_workspace_bytes",
     "dwarf_phase_probe_bwd",
+    "dwarf_npci_fwd",
+    "dwarf_npci_bwd_workspace_bytes",
+    "dwarf_npci_bwd",
 )
 
 
@@ -181,6 +184,29 @@ class PhaseProbeBwdArgs(ctypes.Structure):
     ]
 
 
+class NpciFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int32), ("H", c_int32), ("T", c_int32), ("head_dim", c_int32),
+        ("x_dtype", c_int32), ("delta_dtype", c_int32),
+        ("strength_tau", c_float),
+        ("x", c_void_p), ("x_stride", _i64(4)),
+        ("delta", c_void_p), ("delta_stride", _i64(4)),
+        ("theta", c_void_p),
+        ("out", c_void_p), ("out_stride", _i64(4)),
+    ]
+
+
+class NpciBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", NpciFwdArgs),
+        ("grad", c_void_p), ("grad_stride", _i64(4)),
+        ("dx", c_void_p), ("dx_stride", _i64(4)),
+        ("ddelta", c_void_p), ("ddelta_stride", _i64(4)),
+        ("dtheta", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The HIP library is missing, stale or failed a call."""
 
@@ -242,6 +268,12 @@ def load() -> ctypes.CDLL:
     lib.dwarf_phase_probe_bwd_workspace_bytes.argtypes = [POINTER(PhaseProbeBwdArgs)]
     lib.dwarf_phase_probe_bwd.restype = c_int
     lib.dwarf_phase_probe_bwd.argtypes = [POINTER(PhaseProbeBwdArgs), c_void_p]
+    lib.dwarf_npci_fwd.restype = c_int
+    lib.dwarf_npci_fwd.argtypes = [POINTER(NpciFwdArgs), c_void_p]
+    lib.dwarf_npci_bwd_workspace_bytes.restype = c_size_t
+    lib.dwarf_npci_bwd_workspace_bytes.argtypes = [POINTER(NpciBwdArgs)]
+    lib.dwarf_npci_bwd.restype = c_int
+    lib.dwarf_npci_bwd.argtypes = [POINTER(NpciBwdArgs), c_void_p]
     version = lib.dwarf_abi_version()
     if version != ABI_VERSION:
         raise NativeLibraryError(f"{LIB_NAME} ABI {version} does not match the binding's ABI {ABI_VERSION}")

@@ -25,6 +25,9 @@ hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stre
 int q6_max_decode_offsets();
 int q6_max_decode_heads();
 size_t phase_probe_bwd_workspace(const dwarf_phase_probe_bwd_args& a);
+size_t npci_bwd_workspace(const dwarf_npci_bwd_args& a);
+hipError_t launch_npci_fwd(const dwarf_npci_fwd_args& a, hipStream_t stream);
+hipError_t launch_npci_bwd(const dwarf_npci_bwd_args& a, hipStream_t stream);
 hipError_t launch_phase_probe_fwd(const dwarf_phase_probe_fwd_args& a, hipStream_t stream);
 hipError_t launch_phase_probe_bwd(const dwarf_phase_probe_bwd_args& a, hipStream_t stream);
 }  // namespace dwarf
@@ -312,6 +315,51 @@ int dwarf_phase_probe_bwd(const dwarf_phase_probe_bwd_args* args, dwarf_stream_t
       return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
   }
   return hip_status(dwarf::launch_phase_probe_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_phase_probe_bwd");
+}
+
+// ---- NPCI rotation ----------------------------------------------------------
+static int check_npci(const dwarf_npci_fwd_args& a, bool need_out) {
+  if (a.B < 0 || a.H < 0 || a.T < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes B=%d H=%d T=%d", a.B, a.H, a.T);
+  if (a.head_dim != dwarf::kHeadDim)
+    return fail(DWARF_ERR_UNSUPPORTED, "NPCI is built for head_dim %d (got %d)", dwarf::kHeadDim, a.head_dim);
+  if (!(a.strength_tau > 0.f) || !(a.strength_tau < 3.0e38f))
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "strength_tau must be finite and positive");
+  for (int dt : {a.x_dtype, a.delta_dtype})
+    if (dt != DWARF_BF16 && dt != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", dt);
+  if (static_cast<int64_t>(a.B) * a.H * a.T >= (int64_t(1) << 31))
+    return fail(DWARF_ERR_UNSUPPORTED, "B*H*T must stay below 2^31 rows");
+  int rc = check_rows("x", a.x, a.x_stride, 3, a.x_dtype);
+  if (rc) return rc;
+  if ((rc = check_rows("delta", a.delta, a.delta_stride, 3, a.delta_dtype))) return rc;
+  if (!a.theta) return fail(DWARF_ERR_INVALID_ARGUMENT, "theta is NULL");
+  if (need_out && (rc = check_rows("out", a.out, a.out_stride, 3, a.x_dtype))) return rc;
+  return DWARF_OK;
+}
+
+int dwarf_npci_fwd(const dwarf_npci_fwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  int rc = check_npci(*args, true);
+  if (rc) return rc;
+  return hip_status(dwarf::launch_npci_fwd(*args, reinterpret_cast<hipStream_t>(stream)), "dwarf_npci_fwd");
+}
+
+size_t dwarf_npci_bwd_workspace_bytes(const dwarf_npci_bwd_args* args) {
+  return args ? dwarf::npci_bwd_workspace(*args) : 0;
+}
+
+int dwarf_npci_bwd(const dwarf_npci_bwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_npci_bwd_args& a = *args;
+  int rc = check_npci(a.fwd, false);
+  if (rc) return rc;
+  if ((rc = check_rows("grad", a.grad, a.grad_stride, 3, a.fwd.x_dtype))) return rc;
+  if ((rc = check_rows("dx", a.dx, a.dx_stride, 3, a.fwd.x_dtype))) return rc;
+  if ((rc = check_rows("ddelta", a.ddelta, a.ddelta_stride, 3, a.fwd.delta_dtype))) return rc;
+  if (!a.dtheta) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtheta is NULL");
+  const size_t need = dwarf::npci_bwd_workspace(a);
+  if (need && (!a.workspace || a.workspace_bytes < need))
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  return hip_status(dwarf::launch_npci_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_npci_bwd");
 }
 
 // ---- q6 ---------------------------------------------------------------------

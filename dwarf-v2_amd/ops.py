@@ -1,15 +1,16 @@
 """torch.library registration of the HIP launches.
 
 ``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::ema_fwd``,
-``dwarf::ema_bwd``, ``dwarf::phase_probe_fwd`` and ``dwarf::phase_probe_bwd``
-are custom ops with fake (shape-only) implementations, so ``torch.compile``
-traces the DSQG, EMA and phase-probe autograd Functions without graph breaks
-(the trainer compiles the model, train:1083).  The real
+``dwarf::ema_bwd``, ``dwarf::phase_probe_fwd``, ``dwarf::phase_probe_bwd``,
+``dwarf::npci_fwd`` and ``dwarf::npci_bwd`` are custom ops with fake
+(shape-only) implementations, so ``torch.compile`` traces the DSQG, EMA,
+phase-probe and NPCI autograd Functions without graph breaks (the trainer
+compiles the model, train:1083).  The real
 implementations normalise layouts (unit head-dim stride, 16-byte rows,
 contiguous fp32 tables and plane features, int32 offsets on the device) and
 call the C ABI on the current stream.  The op names follow the drop-in
-boundary of the reference ops (kernels/dsqg_attention_v22.py:2691-2777 and
-371-451, kernels/causal_ema_scan.py:263-364).
+boundary of the reference ops (kernels/dsqg_attention_v22.py:2691-2777,
+371-451 and 221-254, kernels/causal_ema_scan.py:263-509).
 """
 
 from __future__ import annotations
@@ -20,6 +21,7 @@ import torch
 
 from . import dsqg as _dsqg
 from . import ema as _ema
+from . import npci as _npci
 from . import probe as _probe
 
 Tensor = torch.Tensor
@@ -117,3 +119,31 @@ def _phase_probe_bwd_fake(values, probes, dout, start, end, need_dprobes):
     dt = values.dtype if values.dtype in (torch.bfloat16, torch.float32) else torch.float32
     dp = probes.shape if need_dprobes else (0,)
     return values.new_empty(values.shape, dtype=dt), values.new_empty(dp, dtype=torch.float32)
+
+
+# ---- NPCI rotation ---------------------------------------------------------------------------
+@torch.library.custom_op("dwarf::npci_fwd", mutates_args=())
+def npci_fwd(x: Tensor, x_delta: Tensor, theta_h: Tensor, tau: float) -> Tensor:
+    """Rotated rows [B,H,T,hd] (kernel dtype of x)."""
+    return _npci.npci_forward(x, x_delta, theta_h, tau)
+
+
+def _npci_dtype(t):
+    return t.dtype if t.dtype in (torch.bfloat16, torch.float32) else torch.float32
+
+
+@npci_fwd.register_fake
+def _npci_fwd_fake(x, x_delta, theta_h, tau):
+    return x.new_empty(x.shape, dtype=_npci_dtype(x))
+
+
+@torch.library.custom_op("dwarf::npci_bwd", mutates_args=())
+def npci_bwd(x: Tensor, x_delta: Tensor, theta_h: Tensor, grad: Tensor, tau: float) -> tuple[Tensor, Tensor, Tensor]:
+    """(dx, dx_delta, dtheta [H] fp32)."""
+    return _npci.npci_backward(x, x_delta, theta_h, grad, tau)
+
+
+@npci_bwd.register_fake
+def _npci_bwd_fake(x, x_delta, theta_h, grad, tau):
+    return (x.new_empty(x.shape, dtype=_npci_dtype(x)), x.new_empty(x.shape, dtype=_npci_dtype(x_delta)),
+            x.new_empty((theta_h.numel(),), dtype=torch.float32))

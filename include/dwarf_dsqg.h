@@ -238,6 +238,49 @@ size_t dwarf_phase_probe_bwd_workspace_bytes(const dwarf_phase_probe_bwd_args* a
 int dwarf_phase_probe_bwd(const dwarf_phase_probe_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* NPCI rotation of K/V rows toward an injected delta (kv_inject)            */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * x, delta [B,H,T,hd] (unit stride on hd, 16-byte aligned rows; x bf16 or
+ * fp32 as x_dtype, delta as delta_dtype), theta [H] fp32, strength_tau > 0;
+ * out [B,H,T,hd] of x_dtype.  Per row: n = max(|x|, 1e-12), u = x/n,
+ * p = d - (d.u)u, m = |p|; where m > 1e-7 n, out = cos(a) x + sin(a) n p/m
+ * with a = theta_h tanh(m / (tau n + 1e-12)), else out = x.  hd = 64.
+ */
+typedef struct {
+  int32_t B, H, T, head_dim;
+  int32_t x_dtype, delta_dtype;
+  float strength_tau;
+  const void* x; int64_t x_stride[4];
+  const void* delta; int64_t delta_stride[4];
+  const float* theta;
+  void* out; int64_t out_stride[4];
+} dwarf_npci_fwd_args;
+
+/* Replaces npci_rotate's forward (dsqg:221-254), as applied at dsqg:3196-3229. */
+int dwarf_npci_fwd(const dwarf_npci_fwd_args* args, dwarf_stream_t stream);
+
+/*
+ * grad [B,H,T,hd] of x_dtype (the output's gradient); dx of x_dtype and
+ * ddelta of delta_dtype (both written, same layout rules as x); dtheta [H]
+ * fp32 written in a fixed summation order.  fwd.out is not used.
+ */
+typedef struct {
+  dwarf_npci_fwd_args fwd;
+  const void* grad; int64_t grad_stride[4];
+  void* dx; int64_t dx_stride[4];
+  void* ddelta; int64_t ddelta_stride[4];
+  float* dtheta;
+  void* workspace; size_t workspace_bytes;
+} dwarf_npci_bwd_args;
+
+size_t dwarf_npci_bwd_workspace_bytes(const dwarf_npci_bwd_args* args);
+
+/* The gradients autograd forms for npci_rotate (dsqg:221-254): x, delta, theta. */
+int dwarf_npci_bwd(const dwarf_npci_bwd_args* args, dwarf_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* q6 K/V cache (no reference counterpart in the reference repository;      */
 /* signed 6-bit codes, 4 codes per 3 bytes, group 32, fp16 absmax scale)     */
 /* ------------------------------------------------------------------------ */

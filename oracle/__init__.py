@@ -10,4 +10,5 @@ The product (dwarf-v2_amd/) never imports it and has no CPU fallback.
   ema_ref   kernels/causal_ema_scan.py:3-11, 511-538
   q6_ref    the q6 cache format (no reference counterpart)
   probe_ref phase-probe features, dsqg:275-369 (kernels), 422-451 (eager)
+  npci_ref  NPCI kv_inject rotation, dsqg:221-254 (called at 3213-3224)
 """

@@ -29,7 +29,7 @@ def lib(pkg):
 
 def test_exports_every_declared_symbol(pkg, lib):
     names = declared_functions()
-    assert len(names) == 19
+    assert len(names) == 22
     assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
     for name in names:
         assert hasattr(lib, name), name
@@ -45,6 +45,8 @@ STRUCTS = {
     "dwarf_dsqg_q6_decode_args": "Q6DecodeArgs",
     "dwarf_phase_probe_fwd_args": "PhaseProbeFwdArgs",
     "dwarf_phase_probe_bwd_args": "PhaseProbeBwdArgs",
+    "dwarf_npci_fwd_args": "NpciFwdArgs",
+    "dwarf_npci_bwd_args": "NpciBwdArgs",
 }
 
 
@@ -110,3 +112,10 @@ def test_validation_errors_without_gpu(pkg, lib):
     pb = L.PhaseProbeBwdArgs()
     pb.fwd = p
     assert lib.dwarf_phase_probe_bwd(ctypes.byref(pb), None) == L.DWARF_ERR_INVALID_ARGUMENT
+    n = L.NpciFwdArgs()
+    n.B, n.H, n.T, n.head_dim, n.strength_tau = 1, 1, 4, 32, 0.25
+    assert lib.dwarf_npci_fwd(ctypes.byref(n), None) == L.DWARF_ERR_UNSUPPORTED   # head_dim 64 only
+    n.head_dim, n.strength_tau = 64, -1.0
+    assert lib.dwarf_npci_fwd(ctypes.byref(n), None) == L.DWARF_ERR_INVALID_ARGUMENT   # tau must be positive
+    n.strength_tau = 0.25
+    assert lib.dwarf_npci_fwd(ctypes.byref(n), None) == L.DWARF_ERR_INVALID_ARGUMENT   # x is NULL
