@@ -266,6 +266,27 @@ def phase_probe_extra(pkg, device, steps, warmup):
                       "plus dprobes; timed from HIP-graph replays"}
 
 
+def npci_extra(pkg, device, steps, warmup):
+    """npci_rotate fwd and bwd (dx, ddelta, dtheta) on the training microbatch's keys: x a [B,N,H,hd] storage
+    viewed as [B,H,N,hd], as the DSQG block hands it over, bf16 deltas."""
+    B, H, N = 15, 8, 2048
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, N, H, 64, generator=g).to(torch.bfloat16).to(device).transpose(1, 2)
+    d = (0.3 * torch.randn(B, H, N, 64, generator=g)).to(torch.bfloat16).to(device)
+    theta = (0.5 * torch.tanh(torch.randn(H, generator=g))).to(device)
+    dy = torch.randn(B, H, N, 64, generator=g).to(torch.bfloat16).to(device)
+    npci = importlib.import_module("dwarf-v2_amd.npci")
+    ms_f = graph_ms(lambda: npci.npci_forward(x, d, theta, 0.25), max(steps, 20), warmup)
+    ms_b = graph_ms(lambda: npci.npci_backward(x, d, theta, dy, 0.25), max(steps, 20), warmup)
+    rows = B * H * N
+    fb, bb = rows * 3 * 128, rows * (5 * 128 + 8)
+    return {"ms_fwd": ms_f, "ms_bwd": ms_b, "fwd_hbm_frac": fb / (ms_f * 1e-3) / HBM_PEAK,
+            "bwd_hbm_frac": bb / (ms_b * 1e-3) / HBM_PEAK, "fwd_bytes": fb, "bwd_bytes": bb,
+            "config": "k [15,8,2048,64] bf16 (head-interleaved storage), bf16 delta, tau 0.25; fwd 384 B/row "
+                      "(x + delta + out), bwd 648 B/row (x + delta + dy + dx + ddelta + the per-row dtheta "
+                      "term written and read); timed from HIP-graph replays"}
+
+
 def long_context_extra(pkg, device, steps, warmup):
     B, H, N = 4, 8, 8192
     t, js, jl = synth(pkg, B, H, N, 4, device)
@@ -299,7 +320,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe"],
+    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe", "npci"],
                     help="run only this extra workload and print its JSON (for per-workload profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 10 times (scales HBM byte counters)")
@@ -325,7 +346,8 @@ def main() -> int:
     pkg._lib.load()
     if args.extra_only:
         fn = {"q6_decode": q6_decode_extra, "q6_prefill": q6_prefill_extra,
-              "long_context": long_context_extra, "phase_probe": phase_probe_extra}[args.extra_only]
+              "long_context": long_context_extra, "phase_probe": phase_probe_extra,
+              "npci": npci_extra}[args.extra_only]
         print(json.dumps({args.extra_only: fn(pkg, device, args.steps, args.warmup)}), flush=True)
         return 0
     B, H, N = 15, 8, 2048
@@ -359,6 +381,7 @@ def main() -> int:
         extra["long_context"] = long_context_extra(pkg, device, max(3, args.steps // 4), 2)
         log("phase-probe features: q of the training microbatch")
         extra["phase_probe"] = phase_probe_extra(pkg, device, args.steps, args.warmup)
+        extra["npci"] = npci_extra(pkg, device, args.steps, args.warmup)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):

@@ -93,6 +93,37 @@ __device__ __forceinline__ void load_f32<float, 16>(const float* p, float* dst) 
 template <>
 __device__ __forceinline__ void load_f32<float, 8>(const float* p, float* dst) { load_f32_f32<8>(p, dst); }
 
+// 16 consecutive values as raw 16-byte vectors, so that a later step's row
+// can be requested before the current one is used (software prefetch).
+template <typename T>
+struct RawSlice16 {
+  uint4 w[16 * sizeof(T) / 16];
+};
+
+template <typename T>
+__device__ __forceinline__ void load_raw(const T* p, RawSlice16<T>& r) {
+  const uint4* v = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int i = 0; i < 16 * static_cast<int>(sizeof(T)) / 16; ++i) r.w[i] = v[i];
+}
+
+__device__ __forceinline__ void widen(const RawSlice16<bf16>& r, float* x) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    x[8 * i + 0] = bf16_lo(r.w[i].x); x[8 * i + 1] = bf16_hi(r.w[i].x);
+    x[8 * i + 2] = bf16_lo(r.w[i].y); x[8 * i + 3] = bf16_hi(r.w[i].y);
+    x[8 * i + 4] = bf16_lo(r.w[i].z); x[8 * i + 5] = bf16_hi(r.w[i].z);
+    x[8 * i + 6] = bf16_lo(r.w[i].w); x[8 * i + 7] = bf16_hi(r.w[i].w);
+  }
+}
+__device__ __forceinline__ void widen(const RawSlice16<float>& r, float* x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[4 * i + 0] = __uint_as_float(r.w[i].x); x[4 * i + 1] = __uint_as_float(r.w[i].y);
+    x[4 * i + 2] = __uint_as_float(r.w[i].z); x[4 * i + 3] = __uint_as_float(r.w[i].w);
+  }
+}
+
 template <typename T, int CNT>
 __device__ __forceinline__ void store_from_f32(T* __restrict__ p, const float* __restrict__ src);
 

@@ -6,12 +6,14 @@
 //   active = m > 1e-7 n, e = p / m, s = tanh(m / (tau n + 1e-12)),
 //   a = theta_h s, r = cos(a) x + sin(a) n e   (r = x where not active).
 // The backward forms the vector-Jacobian products of that expression for x,
-// d and theta (the reference leaves them to autograd); dtheta goes through a
-// per-row buffer and a fixed-order sum per head.
+// d and theta (the reference leaves them to autograd) as per-row
+// combinations of g, p and x; dtheta goes through a per-row buffer (head
+// major) and a fixed-order sum per head.
 //
 // Four lanes per row (lane g holds dims [16g, 16g+16)), 16 rows per wave, 64
 // rows per workgroup step, persistent workgroups; each row's dot products are
-// quarter-row partials summed over the lane quad.
+// quarter-row partials summed over the lane quad.  (Requesting the next step's
+// rows before computing the current one measured slower here.)
 #include "common.h"
 #include "dsqg_internal.h"
 #include "gather.h"
@@ -76,38 +78,41 @@ __device__ __forceinline__ void store16<float>(float* p, const float* v) {
 
 __device__ __forceinline__ float quad_sum(float v) { return group_sum<4>(v); }
 
-// Forward quantities of one row from the lane's slices of x and d.
-struct NpFwd {
-  float u[kNpDims], p[kNpDims];
-  float norm, c1, m, s, sa, ca, theta;
+// Forward scalars of one row from the lane's slices of x and d; p (the part
+// of d orthogonal to x) is left in the lane's slice.  c1 = d.u with u = x / n,
+// and p = d - c1 u = d - (c1 / n) x.
+struct NpRowFwd {
+  float ss, norm, inv_n, c1, m, s, sa, ca, den;
   bool active, clamped;
 };
 
-__device__ __forceinline__ void np_forward(const float* xv, const float* dv, float theta, float tau, NpFwd& f) {
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < kNpDims; ++k) ss = fmaf(xv[k], xv[k], ss);
-  const float raw = sqrtf(quad_sum(ss));
-  f.clamped = raw < 1e-12f;
-  f.norm = fmaxf(raw, 1e-12f);
-  float c1 = 0.f;
+__device__ __forceinline__ NpRowFwd np_forward(const float* xv, const float* dv, float theta, float tau, float* p) {
+  NpRowFwd f;
+  float ss = 0.f, dx = 0.f;
 #pragma unroll
   for (int k = 0; k < kNpDims; ++k) {
-    f.u[k] = xv[k] / f.norm;
-    c1 = fmaf(dv[k], f.u[k], c1);
+    ss = fmaf(xv[k], xv[k], ss);
+    dx = fmaf(dv[k], xv[k], dx);
   }
-  f.c1 = quad_sum(c1);
+  f.ss = quad_sum(ss);
+  const float raw = sqrtf(f.ss);
+  f.clamped = raw < 1e-12f;
+  f.norm = fmaxf(raw, 1e-12f);
+  f.inv_n = 1.f / f.norm;
+  f.c1 = quad_sum(dx) * f.inv_n;
+  const float cu = f.c1 * f.inv_n;
   float m2 = 0.f;
 #pragma unroll
   for (int k = 0; k < kNpDims; ++k) {
-    f.p[k] = fmaf(-f.c1, f.u[k], dv[k]);
-    m2 = fmaf(f.p[k], f.p[k], m2);
+    p[k] = fmaf(-cu, xv[k], dv[k]);
+    m2 = fmaf(p[k], p[k], m2);
   }
   f.m = sqrtf(quad_sum(m2));
   f.active = f.m > f.norm * 1e-7f;
-  f.s = tanhf(f.m / (tau * f.norm + 1e-12f));
-  f.theta = theta;
+  f.den = fmaf(tau, f.norm, 1e-12f);
+  f.s = tanhf(f.m / f.den);
   sincosf(theta * f.s, &f.sa, &f.ca);
+  return f;
 }
 
 template <typename TX, typename TD>
@@ -122,19 +127,34 @@ __global__ __launch_bounds__(kBlock, kNpWgsPerCu) void npci_fwd_kernel(
     const int64_t row = r0 + w * 16 + (l >> 2);   // the same in the four lanes of a quad
     if (row >= gm.rows) continue;
     const NpRow rw = np_row(gm, r0 + w * 16, l >> 2);
-    float xv[kNpDims], dv[kNpDims];
+    float xv[kNpDims], dv[kNpDims], p[kNpDims];
     load_f32<TX, kNpDims>(x + rw.b * sx0 + rw.h * sx1 + static_cast<int64_t>(rw.t) * sx2 + kNpDims * g, xv);
     load_f32<TD, kNpDims>(d + rw.b * sd0 + rw.h * sd1 + static_cast<int64_t>(rw.t) * sd2 + kNpDims * g, dv);
-    NpFwd f;
-    np_forward(xv, dv, theta[rw.h], gm.tau, f);
+    const NpRowFwd f = np_forward(xv, dv, theta[rw.h], gm.tau, p);
+    // r = cos(a) x + sin(a) n p / m on active rows, x elsewhere
+    const float cx = f.active ? f.ca : 1.f;
+    const float cp = f.active ? f.sa * f.norm / fmaxf(f.m, 1e-20f) : 0.f;
     float out[kNpDims];
-    const float sn = f.sa * f.norm / fmaxf(f.m, 1e-20f);
 #pragma unroll
-    for (int k = 0; k < kNpDims; ++k) out[k] = f.active ? fmaf(f.ca, xv[k], sn * f.p[k]) : xv[k];
+    for (int k = 0; k < kNpDims; ++k) out[k] = fmaf(cx, xv[k], cp * p[k]);
     store16<TX>(r + rw.b * sr0 + rw.h * sr1 + static_cast<int64_t>(rw.t) * sr2 + kNpDims * g, out);
   }
 }
 
+// The vector-Jacobian products of one row, with e = p / m, u = x / n:
+//   ga = -sin(a) (g.x) + cos(a) n (g.e)          (dL/da; dtheta += ga s)
+//   gw = ga theta (1 - s^2),  gm = gw / den,  gn = sin(a) (g.e) - gw m tau / den^2
+//   gp = A g + B p  with A = sin(a) n / m,  B = (gm - A (g.e)) / m
+//   gd = gp - (u.gp) u
+//   gx = cos(a) g + (gu - (u.gu) u) / n + gn u,  gu = -c1 gp - (u.gp) d
+// and u.gp = A (g.x) / n + B (u.p), u.p = 0 (c1 (1 - |u|^2) when |x| < 1e-12
+// clamps n; then gx = cos(a) g + gu / n, as n no longer depends on x).  With
+// d = p + c1 u and u.gu = -2 c1 (u.gp) for a unit u, both products are
+// combinations of the row's g, p and x, formed per row on the scalar values:
+//   gd = A g + B p - (u.gp) / n x
+//   gx = (cos(a) - c1 A / n) g - (c1 B + u.gp) / n p + cx x,
+//   cx = (c1 (u.gp) / n + gn) / n, or -c1 (u.gp) / n^2 when n is clamped.
+// Inactive rows pass g through to x and give d and theta nothing.
 template <typename TX, typename TD>
 __global__ __launch_bounds__(kBlock, kNpWgsPerCu) void npci_bwd_kernel(
     const TX* __restrict__ x, int64_t sx0, int64_t sx1, int64_t sx2, const TD* __restrict__ d, int64_t sd0,
@@ -149,73 +169,79 @@ __global__ __launch_bounds__(kBlock, kNpWgsPerCu) void npci_bwd_kernel(
     const int64_t row = r0 + w * 16 + (l >> 2);
     if (row >= gm.rows) continue;
     const NpRow rw = np_row(gm, r0 + w * 16, l >> 2);
-    float xv[kNpDims], dv[kNpDims], gv[kNpDims];
+    float xv[kNpDims], dv[kNpDims], gv[kNpDims], p[kNpDims];
     load_f32<TX, kNpDims>(x + rw.b * sx0 + rw.h * sx1 + static_cast<int64_t>(rw.t) * sx2 + kNpDims * g, xv);
     load_f32<TD, kNpDims>(d + rw.b * sd0 + rw.h * sd1 + static_cast<int64_t>(rw.t) * sd2 + kNpDims * g, dv);
     load_f32<TX, kNpDims>(gr + rw.b * sg0 + rw.h * sg1 + static_cast<int64_t>(rw.t) * sg2 + kNpDims * g, gv);
-    NpFwd f;
-    np_forward(xv, dv, theta[rw.h], tau, f);
-    const float inv_m = 1.f / fmaxf(f.m, 1e-20f);
-    float sgx = 0.f, sge = 0.f;
+    const float th = theta[rw.h];
+    const NpRowFwd f = np_forward(xv, dv, th, tau, p);
+    float sgx = 0.f, sgp = 0.f;
 #pragma unroll
     for (int k = 0; k < kNpDims; ++k) {
       sgx = fmaf(gv[k], xv[k], sgx);
-      sge = fmaf(gv[k], f.p[k] * inv_m, sge);
+      sgp = fmaf(gv[k], p[k], sgp);
     }
     sgx = quad_sum(sgx);
-    sge = quad_sum(sge);
+    const float inv_m = 1.f / fmaxf(f.m, 1e-20f);
+    const float sge = quad_sum(sgp) * inv_m;
     const float ga = fmaf(-f.sa, sgx, f.ca * f.norm * sge);
-    const float den = tau * f.norm + 1e-12f;
-    const float gw = ga * f.theta * (1.f - f.s * f.s);
-    const float gm_ = gw / den;
-    const float gn = fmaf(f.sa, sge, -gw * f.m * tau / (den * den));
-    // gp = (ge - e (e.ge)) / m + gm e with ge = sin(a) n g and e.ge = sin(a) n sge
-    const float san = f.sa * f.norm;
-    float gp[kNpDims];
-    float ugp = 0.f;
-#pragma unroll
-    for (int k = 0; k < kNpDims; ++k) {
-      const float e = f.p[k] * inv_m;
-      gp[k] = fmaf(san * inv_m, fmaf(-e, sge, gv[k]), gm_ * e);
-      ugp = fmaf(f.u[k], gp[k], ugp);
-    }
-    ugp = quad_sum(ugp);
-    float gd[kNpDims], gu[kNpDims];
-    float ugu = 0.f;
-#pragma unroll
-    for (int k = 0; k < kNpDims; ++k) {
-      gd[k] = fmaf(-f.u[k], ugp, gp[k]);
-      gu[k] = fmaf(-f.c1, gp[k], -dv[k] * ugp);
-      ugu = fmaf(f.u[k], gu[k], ugu);
-    }
-    ugu = quad_sum(ugu);
+    const float inv_den = 1.f / f.den;
+    const float gw = ga * th * (1.f - f.s * f.s);
+    const float gn = fmaf(f.sa, sge, -gw * f.m * tau * inv_den * inv_den);
+    const float A = f.sa * f.norm * inv_m;
+    const float Bc = fmaf(-A, sge, gw * inv_den) * inv_m;
+    const float up = f.clamped ? f.c1 * (1.f - f.ss * f.inv_n * f.inv_n) : 0.f;
+    const float ugp = fmaf(A * f.inv_n, sgx, Bc * up);
+    const float c1n = f.c1 * f.inv_n;
+    const float cx_n = f.clamped ? -c1n * ugp * f.inv_n : fmaf(c1n, ugp, gn) * f.inv_n;
+    // gx = xg g + xp p + xx x, gd = dg g + dp p + dx_ x
+    const float xg = f.active ? fmaf(-c1n, A, f.ca) : 1.f;
+    const float xp = f.active ? -fmaf(f.c1, Bc, ugp) * f.inv_n : 0.f;
+    const float xx = f.active ? cx_n : 0.f;
+    const float dg = f.active ? A : 0.f;
+    const float dp = f.active ? Bc : 0.f;
+    const float dx_ = f.active ? -ugp * f.inv_n : 0.f;
     float gxo[kNpDims], gdo[kNpDims];
-    const float inv_n = 1.f / f.norm;
 #pragma unroll
     for (int k = 0; k < kNpDims; ++k) {
-      const float gxu = f.clamped ? gu[k] * inv_n : fmaf(-f.u[k], ugu, gu[k]) * inv_n;
-      const float gxn = f.clamped ? 0.f : gn * f.u[k];
-      gxo[k] = f.active ? fmaf(f.ca, gv[k], gxu + gxn) : gv[k];
-      gdo[k] = f.active ? gd[k] : 0.f;
+      gxo[k] = fmaf(xg, gv[k], fmaf(xp, p[k], xx * xv[k]));
+      gdo[k] = fmaf(dg, gv[k], fmaf(dp, p[k], dx_ * xv[k]));
     }
     store16<TX>(dx + rw.b * sdx0 + rw.h * sdx1 + static_cast<int64_t>(rw.t) * sdx2 + kNpDims * g, gxo);
     store16<TD>(dd + rw.b * sdd0 + rw.h * sdd1 + static_cast<int64_t>(rw.t) * sdd2 + kNpDims * g, gdo);
-    if (g == 0) trow[(static_cast<int64_t>(rw.b) * gm.H + rw.h) * gm.T + rw.t] = f.active ? ga * f.s : 0.f;
+    if (g == 0) trow[(static_cast<int64_t>(rw.h) * gm.B + rw.b) * gm.T + rw.t] = f.active ? ga * f.s : 0.f;
   }
 }
 
-// dtheta[h] = sum over (b, t) of trow[b][h][t]: one workgroup per head; thread
-// i adds entries i, i + 1024, ... of the head's B*T values in order, the wave
-// sums by a fixed butterfly, the waves in wave order.
+// dtheta[h] = sum of the head's B*T entries of trow (stored head-major): one
+// workgroup per head; thread i adds the entries of 16-byte vectors i, i + 1024,
+// ... in order (eight vectors in flight; single entries when B*T is not a
+// multiple of 4 or the buffer not 16-byte aligned), the wave sums by a fixed butterfly, the waves in wave order.
 __global__ __launch_bounds__(kWave * kNpRedWaves) void npci_dtheta_reduce(const float* __restrict__ trow,
                                                                         float* __restrict__ dtheta, NpGeom gm) {
+  constexpr int kThreads = kWave * kNpRedWaves;
+  constexpr int kInFlight = 8;
   __shared__ float s_w[kNpRedWaves];
-  const int h = blockIdx.x;
   const int64_t per_head = static_cast<int64_t>(gm.B) * gm.T;
+  const float* src = trow + static_cast<int64_t>(blockIdx.x) * per_head;
   float s = 0.f;
-  for (int64_t i = threadIdx.x; i < per_head; i += kWave * kNpRedWaves) {
-    const int b = static_cast<int>(i / gm.T), t = static_cast<int>(i - static_cast<int64_t>(b) * gm.T);
-    s += trow[(static_cast<int64_t>(b) * gm.H + h) * gm.T + t];
+  if ((per_head & 3) == 0 && (reinterpret_cast<uintptr_t>(trow) & 15) == 0) {
+    const float4* v = reinterpret_cast<const float4*>(src);
+    const int64_t nv = per_head >> 2;
+    int64_t i = threadIdx.x;
+    for (; i + (kInFlight - 1) * kThreads < nv; i += kInFlight * kThreads) {
+      float4 a[kInFlight];
+#pragma unroll
+      for (int j = 0; j < kInFlight; ++j) a[j] = v[i + j * kThreads];
+#pragma unroll
+      for (int j = 0; j < kInFlight; ++j) s = (((s + a[j].x) + a[j].y) + a[j].z) + a[j].w;
+    }
+    for (; i < nv; i += kThreads) {
+      const float4 a = v[i];
+      s = (((s + a.x) + a.y) + a.z) + a.w;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < per_head; i += kThreads) s += src[i];
   }
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) s += __shfl_xor(s, o);
@@ -224,7 +250,7 @@ __global__ __launch_bounds__(kWave * kNpRedWaves) void npci_dtheta_reduce(const 
   if (threadIdx.x == 0) {
     float t = 0.f;
     for (int v = 0; v < kNpRedWaves; ++v) t += s_w[v];
-    dtheta[h] = t;
+    dtheta[blockIdx.x] = t;
   }
 }
 

@@ -87,44 +87,13 @@ __device__ __forceinline__ void store16<float>(float* p, const float* v) {
   store_f32<kPrDims>(p, v);
 }
 
-// The lane's 16 values of one row as raw 16-byte vectors: the next
-// workgroup step's row is requested before the current one is used.
-template <typename T>
-struct RawSlice {
-  uint4 w[kPrDims * sizeof(T) / 16];
-};
-
-template <typename T>
-__device__ __forceinline__ void load_raw(const T* p, RawSlice<T>& r) {
-  const uint4* v = reinterpret_cast<const uint4*>(p);
-#pragma unroll
-  for (int i = 0; i < kPrDims * static_cast<int>(sizeof(T)) / 16; ++i) r.w[i] = v[i];
-}
-
-__device__ __forceinline__ void widen(const RawSlice<bf16>& r, float* x) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    x[8 * i + 0] = bf16_lo(r.w[i].x); x[8 * i + 1] = bf16_hi(r.w[i].x);
-    x[8 * i + 2] = bf16_lo(r.w[i].y); x[8 * i + 3] = bf16_hi(r.w[i].y);
-    x[8 * i + 4] = bf16_lo(r.w[i].z); x[8 * i + 5] = bf16_hi(r.w[i].z);
-    x[8 * i + 6] = bf16_lo(r.w[i].w); x[8 * i + 7] = bf16_hi(r.w[i].w);
-  }
-}
-__device__ __forceinline__ void widen(const RawSlice<float>& r, float* x) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[4 * i + 0] = __uint_as_float(r.w[i].x); x[4 * i + 1] = __uint_as_float(r.w[i].y);
-    x[4 * i + 2] = __uint_as_float(r.w[i].z); x[4 * i + 3] = __uint_as_float(r.w[i].w);
-  }
-}
-
 // One workgroup step of a lane: its row (the same in the four lanes of a
 // quad), whether it exists, and the loads issued for it.
 template <typename T>
 struct PrStep {
   PrRow rw;
   bool ok;
-  RawSlice<T> x;
+  RawSlice16<T> x;
   float gown;   // backward: dout[row][plane g]
 };
 

@@ -7,7 +7,9 @@ a zero delta or a delta parallel to x take the reference's special paths (the
 parallel row is exact in fp32: a delta that is parallel only up to rounding
 sits on the 1e-7 activity threshold in any fp32 evaluation, the reference's
 included).
-dtheta has a fixed summation order: two runs agree bit for bit.
+dtheta has a fixed summation order: two runs agree bit for bit.  The shapes
+cover B*T per head not a multiple of 4 (the reduction's single-entry path),
+a multiple of 4 (16-byte vectors) and 32,800 entries (eight vectors in flight).
 """
 
 import pytest
@@ -50,7 +52,8 @@ def run(pkg, x, d, th, gr, device, tau):
 
 @pytest.mark.parametrize("xdt,ddt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
                                      (torch.bfloat16, torch.float32)])
-@pytest.mark.parametrize("shape,permuted", [((2, 3, 37), False), ((2, 3, 9), False), ((1, 8, 300), True)])
+@pytest.mark.parametrize("shape,permuted", [((2, 3, 37), False), ((2, 3, 9), False), ((1, 8, 300), True),
+                                            ((2, 2, 16400), False)])
 def test_matches_oracle(pkg, device, xdt, ddt, shape, permuted):
     B, H, T = shape
     x, d, th, gr = inputs(B, H, T, xdt, ddt, seed=T + H, permuted=permuted)
