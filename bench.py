@@ -287,6 +287,38 @@ def npci_extra(pkg, device, steps, warmup):
                       "term written and read); timed from HIP-graph replays"}
 
 
+def packet_extra(pkg, device, steps, warmup):
+    """The InterferencePacket pool (three EMA timescales and their mix) fused, fwd and bwd, on the L3
+    block's input at the training microbatch: x [15, 2048, 512] bf16; beside it the same forward as three
+    separate EMA scans and the bf16 mix (the reference's composition, on this build's EMA kernels)."""
+    B, N, D = 15, 2048, 512
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, N, D, generator=g).to(torch.bfloat16).to(device)
+    dp = torch.randn(B, N, D, generator=g).to(torch.bfloat16).to(device)
+    a = torch.tensor([1 / 16, 1 / 64, 1 / 256], device=device)
+    w = torch.softmax(torch.tensor([0.3, -0.2, 0.1]), 0).to(device)
+    packet = importlib.import_module("dwarf-v2_amd.packet")
+    ema = importlib.import_module("dwarf-v2_amd.ema")
+    _, state = packet.pool_forward(x, a, w, 1e-5, 0.5)
+    ms_f = graph_ms(lambda: packet.pool_forward(x, a, w, 1e-5, 0.5), max(steps, 20), warmup)
+    ms_b = graph_ms(lambda: packet.pool_backward(x, a, w, state, dp, 1e-5, 0.5), max(steps, 20), warmup)
+    wb = w.to(torch.bfloat16)
+
+    def composed():
+        scans = [ema.ema_forward(x, a[k:k + 1], 1e-5, 0.5) for k in range(3)]
+        return (wb[0] * scans[0] + wb[1] * scans[1]) + wb[2] * scans[2]
+
+    ms_c = graph_ms(composed, max(steps, 20), warmup)
+    n = B * N * D
+    fb, bb = 4 * n, 6 * n
+    return {"ms_fwd": ms_f, "ms_bwd": ms_b, "ms_fwd_composed": ms_c,
+            "fwd_hbm_frac": fb / (ms_f * 1e-3) / HBM_PEAK, "bwd_hbm_frac": bb / (ms_b * 1e-3) / HBM_PEAK,
+            "fwd_bytes": fb, "bwd_bytes": bb,
+            "config": "x [15,2048,512] bf16, timescales 16/64/256; algorithmic bytes fwd 4 B/element (x read, "
+                      "pooled written), bwd 6 B/element (dpooled and x read, dx written); composed = three EMA "
+                      "scans + bf16 mix; timed from HIP-graph replays"}
+
+
 def long_context_extra(pkg, device, steps, warmup):
     B, H, N = 4, 8, 8192
     t, js, jl = synth(pkg, B, H, N, 4, device)
@@ -320,7 +352,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe", "npci"],
+    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe", "npci", "packet"],
                     help="run only this extra workload and print its JSON (for per-workload profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 10 times (scales HBM byte counters)")
@@ -347,7 +379,7 @@ def main() -> int:
     if args.extra_only:
         fn = {"q6_decode": q6_decode_extra, "q6_prefill": q6_prefill_extra,
               "long_context": long_context_extra, "phase_probe": phase_probe_extra,
-              "npci": npci_extra}[args.extra_only]
+              "npci": npci_extra, "packet": packet_extra}[args.extra_only]
         print(json.dumps({args.extra_only: fn(pkg, device, args.steps, args.warmup)}), flush=True)
         return 0
     B, H, N = 15, 8, 2048
@@ -382,6 +414,7 @@ def main() -> int:
         log("phase-probe features: q of the training microbatch")
         extra["phase_probe"] = phase_probe_extra(pkg, device, args.steps, args.warmup)
         extra["npci"] = npci_extra(pkg, device, args.steps, args.warmup)
+        extra["packet"] = packet_extra(pkg, device, args.steps, args.warmup)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):

@@ -10,13 +10,15 @@ Public surface (reference names, Lanerra/dwarf-v2):
   inverse_bounded_ema_factor                         kernels/causal_ema_scan.py
   phase_probe_features, _PhaseProbeFn                kernels/dsqg_attention_v22.py
   npci_rotate                                        kernels/dsqg_attention_v22.py
+  interference_pool, interference_packet_forward     train/train_dwarf.py (InterferencePacket)
   q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
 """
 
-from . import _lib, lattice, npci, ops, probe, q6
+from . import _lib, lattice, npci, ops, packet, probe, q6
 from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
 from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
 from .npci import npci_rotate
+from .packet import _InterferencePoolFn, interference_packet_forward, interference_pool
 from .probe import _PhaseProbeFn, phase_probe_features
 from .lattice import (
     ALL_OFFSETS,
@@ -34,6 +36,7 @@ __all__ = [
     "GROUPED_MODE_IDS",
     "R_PLANES",
     "_DSQGV18GroupedFn",
+    "_InterferencePoolFn",
     "_PhaseProbeFn",
     "_canonicalize_offsets",
     "_normalize_plane_shift",
@@ -45,6 +48,8 @@ __all__ = [
     "dsqg_attention_v18_grouped",
     "dsqg_backward",
     "dsqg_forward",
+    "interference_packet_forward",
+    "interference_pool",
     "inverse_bounded_ema_factor",
     "npci_rotate",
     "phase_probe_features",

@@ -47,6 +47,11 @@ EXPORTED_SYMBOLS = (
     "dwarf_npci_fwd",
     "dwarf_npci_bwd_workspace_bytes",
     "dwarf_npci_bwd",
+    "dwarf_packet_pool_state_bytes",
+    "dwarf_packet_pool_fwd_workspace_bytes",
+    "dwarf_packet_pool_fwd",
+    "dwarf_packet_pool_bwd_workspace_bytes",
+    "dwarf_packet_pool_bwd",
 )
 
 
@@ -207,6 +212,34 @@ class NpciBwdArgs(ctypes.Structure):
     ]
 
 
+PACKET_MAX_SCALES = 4
+
+
+class PacketPoolFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_int32), ("N", c_int32), ("D", c_int32), ("K", c_int32),
+        ("dtype", c_int32),
+        ("floor_", c_float), ("ceiling", c_float),
+        ("x", c_void_p), ("x_stride", _i64(3)),
+        ("alpha", c_void_p),
+        ("weight", c_void_p),
+        ("pooled", c_void_p), ("pooled_stride", _i64(3)),
+        ("state", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
+class PacketPoolBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", PacketPoolFwdArgs),
+        ("dpooled", c_void_p), ("dpooled_stride", _i64(3)),
+        ("dx", c_void_p), ("dx_stride", _i64(3)),
+        ("dalpha", c_void_p),
+        ("dweight", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The HIP library is missing, stale or failed a call."""
 
@@ -274,6 +307,15 @@ def load() -> ctypes.CDLL:
     lib.dwarf_npci_bwd_workspace_bytes.argtypes = [POINTER(NpciBwdArgs)]
     lib.dwarf_npci_bwd.restype = c_int
     lib.dwarf_npci_bwd.argtypes = [POINTER(NpciBwdArgs), c_void_p]
+    for name in ("dwarf_packet_pool_state_bytes", "dwarf_packet_pool_fwd_workspace_bytes"):
+        getattr(lib, name).restype = c_size_t
+        getattr(lib, name).argtypes = [POINTER(PacketPoolFwdArgs)]
+    lib.dwarf_packet_pool_fwd.restype = c_int
+    lib.dwarf_packet_pool_fwd.argtypes = [POINTER(PacketPoolFwdArgs), c_void_p]
+    lib.dwarf_packet_pool_bwd_workspace_bytes.restype = c_size_t
+    lib.dwarf_packet_pool_bwd_workspace_bytes.argtypes = [POINTER(PacketPoolBwdArgs)]
+    lib.dwarf_packet_pool_bwd.restype = c_int
+    lib.dwarf_packet_pool_bwd.argtypes = [POINTER(PacketPoolBwdArgs), c_void_p]
     version = lib.dwarf_abi_version()
     if version != ABI_VERSION:
         raise NativeLibraryError(f"{LIB_NAME} ABI {version} does not match the binding's ABI {ABI_VERSION}")

@@ -28,6 +28,12 @@ size_t phase_probe_bwd_workspace(const dwarf_phase_probe_bwd_args& a);
 size_t npci_bwd_workspace(const dwarf_npci_bwd_args& a);
 hipError_t launch_npci_fwd(const dwarf_npci_fwd_args& a, hipStream_t stream);
 hipError_t launch_npci_bwd(const dwarf_npci_bwd_args& a, hipStream_t stream);
+size_t packet_state_bytes(int B, int N, int D, int K);
+size_t packet_fwd_workspace(int B, int N, int D, int K);
+size_t packet_bwd_workspace(int B, int N, int D, int K);
+int packet_max_scales();
+hipError_t launch_packet_fwd(const dwarf_packet_pool_fwd_args& a, hipStream_t stream);
+hipError_t launch_packet_bwd(const dwarf_packet_pool_bwd_args& a, hipStream_t stream);
 hipError_t launch_phase_probe_fwd(const dwarf_phase_probe_fwd_args& a, hipStream_t stream);
 hipError_t launch_phase_probe_bwd(const dwarf_phase_probe_bwd_args& a, hipStream_t stream);
 }  // namespace dwarf
@@ -272,6 +278,56 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream) {
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
   return hip_status(dwarf::launch_ema_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_ema_bwd");
+}
+
+// ---- InterferencePacket pool ---------------------------------------------------
+static int check_packet(const dwarf_packet_pool_fwd_args& a, bool need_pooled) {
+  if (a.K < 1 || a.K > dwarf::packet_max_scales() || a.K > DWARF_PACKET_MAX_SCALES)
+    return fail(DWARF_ERR_UNSUPPORTED, "K=%d scales (1..%d are built)", a.K, DWARF_PACKET_MAX_SCALES);
+  int rc = check_ema_common(a.B, a.N, a.D, a.dtype, 0, a.floor_, a.ceiling, a.alpha);
+  if (rc) return rc;
+  if (!a.weight) return fail(DWARF_ERR_INVALID_ARGUMENT, "weight is NULL");
+  if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
+  if (need_pooled && (rc = check_btd("pooled", a.pooled, a.pooled_stride, a.dtype, a.D))) return rc;
+  if (a.B > 0 && a.N > 0 && a.D > 0 && !a.state) return fail(DWARF_ERR_INVALID_ARGUMENT, "state is NULL");
+  return DWARF_OK;
+}
+
+size_t dwarf_packet_pool_state_bytes(const dwarf_packet_pool_fwd_args* a) {
+  return a && a->K >= 1 && a->K <= DWARF_PACKET_MAX_SCALES ? dwarf::packet_state_bytes(a->B, a->N, a->D, a->K) : 0;
+}
+size_t dwarf_packet_pool_fwd_workspace_bytes(const dwarf_packet_pool_fwd_args* a) {
+  return a && a->K >= 1 && a->K <= DWARF_PACKET_MAX_SCALES ? dwarf::packet_fwd_workspace(a->B, a->N, a->D, a->K) : 0;
+}
+size_t dwarf_packet_pool_bwd_workspace_bytes(const dwarf_packet_pool_bwd_args* a) {
+  const dwarf_packet_pool_fwd_args* f = a ? &a->fwd : nullptr;
+  return f && f->K >= 1 && f->K <= DWARF_PACKET_MAX_SCALES ? dwarf::packet_bwd_workspace(f->B, f->N, f->D, f->K) : 0;
+}
+
+int dwarf_packet_pool_fwd(const dwarf_packet_pool_fwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_packet_pool_fwd_args& a = *args;
+  int rc = check_packet(a, true);
+  if (rc) return rc;
+  if (a.B == 0 || a.N == 0 || a.D == 0) return ok();
+  const size_t need = dwarf::packet_fwd_workspace(a.B, a.N, a.D, a.K);
+  if (!a.workspace || a.workspace_bytes < need)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  return hip_status(dwarf::launch_packet_fwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_packet_pool_fwd");
+}
+
+int dwarf_packet_pool_bwd(const dwarf_packet_pool_bwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_packet_pool_bwd_args& a = *args;
+  int rc = check_packet(a.fwd, false);
+  if (rc) return rc;
+  if ((rc = check_btd("dpooled", a.dpooled, a.dpooled_stride, a.fwd.dtype, a.fwd.D))) return rc;
+  if ((rc = check_btd("dx", a.dx, a.dx_stride, a.fwd.dtype, a.fwd.D))) return rc;
+  if (a.fwd.B == 0 || a.fwd.N == 0 || a.fwd.D == 0) return ok();
+  const size_t need = dwarf::packet_bwd_workspace(a.fwd.B, a.fwd.N, a.fwd.D, a.fwd.K);
+  if (!a.workspace || a.workspace_bytes < need)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  return hip_status(dwarf::launch_packet_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_packet_pool_bwd");
 }
 
 // ---- phase-probe features ---------------------------------------------------

@@ -2,15 +2,17 @@
 
 ``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::ema_fwd``,
 ``dwarf::ema_bwd``, ``dwarf::phase_probe_fwd``, ``dwarf::phase_probe_bwd``,
-``dwarf::npci_fwd`` and ``dwarf::npci_bwd`` are custom ops with fake
-(shape-only) implementations, so ``torch.compile`` traces the DSQG, EMA,
-phase-probe and NPCI autograd Functions without graph breaks (the trainer
+``dwarf::npci_fwd``, ``dwarf::npci_bwd``, ``dwarf::packet_pool_fwd`` and
+``dwarf::packet_pool_bwd`` are custom ops with fake (shape-only)
+implementations, so ``torch.compile`` traces the DSQG, EMA, phase-probe, NPCI
+and InterferencePacket-pool autograd Functions without graph breaks (the trainer
 compiles the model, train:1083).  The real
 implementations normalise layouts (unit head-dim stride, 16-byte rows,
 contiguous fp32 tables and plane features, int32 offsets on the device) and
 call the C ABI on the current stream.  The op names follow the drop-in
 boundary of the reference ops (kernels/dsqg_attention_v22.py:2691-2777,
-371-451 and 221-254, kernels/causal_ema_scan.py:263-509).
+371-451 and 221-254, kernels/causal_ema_scan.py:263-509,
+train/train_dwarf.py:260-267).
 """
 
 from __future__ import annotations
@@ -22,6 +24,7 @@ import torch
 from . import dsqg as _dsqg
 from . import ema as _ema
 from . import npci as _npci
+from . import packet as _packet
 from . import probe as _probe
 
 Tensor = torch.Tensor
@@ -147,3 +150,28 @@ def npci_bwd(x: Tensor, x_delta: Tensor, theta_h: Tensor, grad: Tensor, tau: flo
 def _npci_bwd_fake(x, x_delta, theta_h, grad, tau):
     return (x.new_empty(x.shape, dtype=_npci_dtype(x)), x.new_empty(x.shape, dtype=_npci_dtype(x_delta)),
             x.new_empty((theta_h.numel(),), dtype=torch.float32))
+
+
+# ---- InterferencePacket pool -----------------------------------------------------------------
+@torch.library.custom_op("dwarf::packet_pool_fwd", mutates_args=())
+def packet_pool_fwd(x: Tensor, alpha: Tensor, weight: Tensor, floor: float, ceiling: float) -> tuple[Tensor, Tensor]:
+    """(pooled with x's dtype, per-chunk scan states fp32 [B, ceil(N/16), K*D])."""
+    return _packet.pool_forward(x, alpha, weight, floor, ceiling)
+
+
+@packet_pool_fwd.register_fake
+def _packet_pool_fwd_fake(x, alpha, weight, floor, ceiling):
+    return x.new_empty(x.shape), x.new_empty(_packet.state_shape(x, alpha.numel()), dtype=torch.float32)
+
+
+@torch.library.custom_op("dwarf::packet_pool_bwd", mutates_args=())
+def packet_pool_bwd(x: Tensor, alpha: Tensor, weight: Tensor, state: Tensor, dpooled: Tensor, floor: float,
+                    ceiling: float) -> tuple[Tensor, Tensor, Tensor]:
+    """(dx with x's dtype, dalpha [K] fp32 clamp-projected, dweight [K] fp32)."""
+    return _packet.pool_backward(x, alpha, weight, state, dpooled, floor, ceiling)
+
+
+@packet_pool_bwd.register_fake
+def _packet_pool_bwd_fake(x, alpha, weight, state, dpooled, floor, ceiling):
+    return (x.new_empty(x.shape), x.new_empty((alpha.numel(),), dtype=torch.float32),
+            x.new_empty((alpha.numel(),), dtype=torch.float32))

@@ -196,6 +196,62 @@ size_t dwarf_ema_bwd_workspace_bytes(const dwarf_ema_bwd_args* args);
 int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* InterferencePacket pool: K causal EMA scans of one input and their mix    */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * x [B,N,D] of `dtype` (unit stride on D); alpha [K] and weight [K] fp32 on
+ * the device, 1 <= K <= DWARF_PACKET_MAX_SCALES.  Computes
+ *   scan_k = EMA(x, clamp(alpha[k], floor_, ceiling)), stored in dtype,
+ *   pooled = (((w_0 scan_0) + w_1 scan_1) + ...), w_k = weight[k] in dtype,
+ * every product and partial sum rounded to dtype as the reference's tensor
+ * arithmetic rounds them (train:262-267 with K = 3 timescales).  `state`
+ * (dwarf_packet_pool_state_bytes, fp32) receives each 16-token chunk's
+ * incoming scan states; the backward reads it.
+ */
+#define DWARF_PACKET_MAX_SCALES 4
+
+typedef struct {
+  int32_t B, N, D, K;
+  int32_t dtype;
+  float floor_, ceiling;
+  const void* x; int64_t x_stride[3];
+  const float* alpha;
+  const float* weight;
+  void* pooled; int64_t pooled_stride[3];
+  float* state;
+  void* workspace; size_t workspace_bytes;
+} dwarf_packet_pool_fwd_args;
+
+size_t dwarf_packet_pool_state_bytes(const dwarf_packet_pool_fwd_args* args);
+size_t dwarf_packet_pool_fwd_workspace_bytes(const dwarf_packet_pool_fwd_args* args);
+
+/* Replaces InterferencePacket.forward's K causal_ema_scan calls and the
+ * weighted sum of their outputs (train:262-267). */
+int dwarf_packet_pool_fwd(const dwarf_packet_pool_fwd_args* args, dwarf_stream_t stream);
+
+/*
+ * fwd as passed to the forward (pooled and fwd.workspace unused, state
+ * read); dx [B,N,D] of `dtype`; dalpha [K] (projected for each factor's clamp
+ * as ema:357-364 does) and dweight [K] (sum of dpooled * scan_k, rounded to
+ * dtype) are written, each may be NULL.
+ */
+typedef struct {
+  dwarf_packet_pool_fwd_args fwd;
+  const void* dpooled; int64_t dpooled_stride[3];
+  void* dx; int64_t dx_stride[3];
+  float* dalpha;
+  float* dweight;
+  void* workspace; size_t workspace_bytes;
+} dwarf_packet_pool_bwd_args;
+
+size_t dwarf_packet_pool_bwd_workspace_bytes(const dwarf_packet_pool_bwd_args* args);
+
+/* The gradients autograd forms for those K scans and the mix: x (summed over
+ * the scans), each factor, each weight. */
+int dwarf_packet_pool_bwd(const dwarf_packet_pool_bwd_args* args, dwarf_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Phase-probe features  y[b,h,n,r] = <x, p_r> / sqrt(|x|^2 + 1e-6 hd)       */
 /* ------------------------------------------------------------------------ */
 

@@ -6,7 +6,9 @@ y[t] = a x[t] + (1 - a) y[t-1], y[-1] = 0, with float64 state for float64
 inputs and float32 state otherwise.  alpha may be one value or one per
 channel ([D]); ``_reference`` broadcasts a [D] alpha the same way.  An
 optional reset_mask [B,N] zeroes the state before the tokens it marks
-(ema:368-509, 533-535).
+(ema:368-509, 533-535).  ``interference_pool`` and its backward restate the
+InterferencePacket's K scans of one input and their weighted sum
+(train/train_dwarf.py:260-267) on top of these.
 """
 
 from __future__ import annotations
@@ -76,3 +78,39 @@ def ema_adjoint(x: torch.Tensor, y: torch.Tensor, dy: torch.Tensor, alpha: torch
     blocked = ((a_in <= floor) & (da > 0)) | ((a_in >= ceiling) & (da < 0))
     da = torch.where(blocked, torch.zeros_like(da), da)
     return dx, da
+
+
+def interference_pool(x: torch.Tensor, factors: torch.Tensor, weights: torch.Tensor, floor: float = 1e-5,
+                      ceiling: float = 0.5) -> torch.Tensor:
+    """The InterferencePacket's pooled scans (train:262-267): scan_k = ema_scan(x, factor_k) in x's dtype,
+    pooled = ((w_0 scan_0 + w_1 scan_1) + ...) with w_k cast to x's dtype and each product and partial
+    sum evaluated in x's dtype, as the reference's tensor arithmetic does."""
+    dt = x.dtype
+    pooled = None
+    for f, w in zip(factors.reshape(-1), weights.reshape(-1)):
+        term = w.to(dt) * ema_scan(x, f.reshape(1), floor, ceiling)
+        pooled = term if pooled is None else pooled + term
+    return pooled
+
+
+def interference_pool_backward(x: torch.Tensor, factors: torch.Tensor, weights: torch.Tensor,
+                               dpooled: torch.Tensor, floor: float = 1e-5, ceiling: float = 0.5):
+    """(dx, dfactors [K], dweights [K]) of ``interference_pool`` for the output gradient ``dpooled``.
+
+    The gradient of scan_k is dpooled * w_k in x's dtype; each scan's adjoint is ``ema_adjoint`` with
+    its own clamp projection; dx is the sum over the scans in the accumulation dtype, rounded once to
+    x's dtype (the reference's autograd adds the K bf16 gradients one by one: the two differ by bf16
+    rounding only); dweight_k = sum of (dpooled * scan_k) in x's dtype, accumulated in the accumulation
+    dtype and rounded to x's dtype, as a bf16 sum-reduction returns it."""
+    dt = x.dtype
+    acc = torch.float64 if dt == torch.float64 else torch.float32
+    g = dpooled.to(dt)
+    dx = torch.zeros(x.shape, dtype=acc)
+    dfs, dws = [], []
+    for f, w in zip(factors.reshape(-1), weights.reshape(-1)):
+        scan = ema_scan(x, f.reshape(1), floor, ceiling)
+        dxk, dak = ema_adjoint(x, scan, g * w.to(dt), f.reshape(1), floor, ceiling)
+        dx += dxk
+        dfs.append(dak.reshape(()))
+        dws.append((g * scan).to(acc).sum().to(dt).to(acc))
+    return dx.to(dt), torch.stack(dfs), torch.stack(dws)

@@ -29,7 +29,7 @@ def lib(pkg):
 
 def test_exports_every_declared_symbol(pkg, lib):
     names = declared_functions()
-    assert len(names) == 22
+    assert len(names) == 27
     assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
     for name in names:
         assert hasattr(lib, name), name
@@ -47,6 +47,8 @@ STRUCTS = {
     "dwarf_phase_probe_bwd_args": "PhaseProbeBwdArgs",
     "dwarf_npci_fwd_args": "NpciFwdArgs",
     "dwarf_npci_bwd_args": "NpciBwdArgs",
+    "dwarf_packet_pool_fwd_args": "PacketPoolFwdArgs",
+    "dwarf_packet_pool_bwd_args": "PacketPoolBwdArgs",
 }
 
 
@@ -119,3 +121,17 @@ def test_validation_errors_without_gpu(pkg, lib):
     assert lib.dwarf_npci_fwd(ctypes.byref(n), None) == L.DWARF_ERR_INVALID_ARGUMENT   # tau must be positive
     n.strength_tau = 0.25
     assert lib.dwarf_npci_fwd(ctypes.byref(n), None) == L.DWARF_ERR_INVALID_ARGUMENT   # x is NULL
+    k = L.PacketPoolFwdArgs()
+    k.B, k.N, k.D, k.K, k.dtype, k.floor_, k.ceiling = 1, 32, 8, 5, L.DWARF_BF16, 1e-5, 0.5
+    assert lib.dwarf_packet_pool_fwd(ctypes.byref(k), None) == L.DWARF_ERR_UNSUPPORTED   # at most 4 scales
+    assert lib.dwarf_packet_pool_state_bytes(ctypes.byref(k)) == 0
+    k.K = 3
+    assert lib.dwarf_packet_pool_state_bytes(ctypes.byref(k)) == 1 * 2 * 3 * 8 * 4      # [B][N/16][K*D] fp32
+    assert lib.dwarf_packet_pool_fwd(ctypes.byref(k), None) == L.DWARF_ERR_INVALID_ARGUMENT   # alpha is NULL
+    k.floor_, k.ceiling = 0.6, 0.5
+    assert lib.dwarf_packet_pool_fwd(ctypes.byref(k), None) == L.DWARF_ERR_INVALID_ARGUMENT   # bad bounds
+    kb = L.PacketPoolBwdArgs()
+    kb.fwd = k
+    assert lib.dwarf_packet_pool_bwd(ctypes.byref(kb), None) == L.DWARF_ERR_INVALID_ARGUMENT
+    # starts and carries [B][N/16][K*D] fp32, then 2K slots per apply workgroup (one here)
+    assert lib.dwarf_packet_pool_bwd_workspace_bytes(ctypes.byref(kb)) == (2 * 1 * 2 * 3 * 8 + 2 * 3) * 4

@@ -32,7 +32,8 @@ def oracle(x, alpha, dy):
 
 
 @pytest.mark.parametrize("B,N,D,per_channel", [(2, 300, 64, False), (2, 257, 64, True), (2, 9, 7, False),
-                                               (3, 130, 7, True), (1, 64, 512, True)])
+                                               (3, 130, 7, True), (1, 64, 512, True),
+                                               (32, 100, 512, True), (16, 70, 512, False)])   # 64- and 32-wide carry runs
 def test_fp32(pkg, device, B, N, D, per_channel):
     g = torch.Generator().manual_seed(N + D)
     x = torch.randn(B, N, D, generator=g)
@@ -148,7 +149,7 @@ def reset_pattern(B, N, g, kind):
 
 @pytest.mark.parametrize("B,N,D,per_channel,kind", [(2, 300, 64, False, "random"), (2, 257, 64, True, "chunk_edges"),
                                                     (3, 130, 7, True, "random"), (2, 49, 8, False, "chunk_edges"),
-                                                    (1, 1000, 512, True, "random")])
+                                                    (1, 1000, 512, True, "random"), (32, 100, 512, True, "random")])
 def test_reset_fp32(pkg, device, B, N, D, per_channel, kind):
     """Reset-aware scan (ema:368-509) against the float64 oracle: y, dx, dalpha <= 1e-5 relative."""
     g = torch.Generator().manual_seed(N + D + 1)

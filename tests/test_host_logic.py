@@ -92,6 +92,21 @@ def test_ema_errors(pkg):
         pkg.causal_ema_scan(x, torch.full((3,), 0.1))   # per-channel accepted, but no CPU path
 
 
+def test_interference_pool_errors(pkg):
+    x = torch.zeros(2, 5, 3)
+    a, w = torch.tensor([0.1, 0.01, 0.001]), torch.full((3,), 1 / 3)
+    with pytest.raises(ValueError):
+        pkg.interference_pool(torch.zeros(5, 3), a, w)
+    with pytest.raises(ValueError):   # one weight per factor
+        pkg.interference_pool(x, a, w[:2])
+    with pytest.raises(ValueError):   # at most four timescales
+        pkg.interference_pool(x, torch.full((5,), 0.1), torch.full((5,), 0.2))
+    with pytest.raises(ValueError):
+        pkg.interference_pool(x, a, w, floor=0.6, ceiling=0.5)
+    with pytest.raises(RuntimeError):   # no CPU path
+        pkg.interference_pool(x, a, w)
+
+
 def test_q6_errors(pkg):
     with pytest.raises(ValueError):
         pkg.q6.pack_kv(torch.zeros(1, 1, 4, 64), torch.zeros(1, 1, 5, 64))
