@@ -14,8 +14,6 @@ determinism and torch.compile; and ``interference_packet_forward`` against
 the same module composed of separate ``causal_ema_scan`` calls.
 """
 
-import importlib
-
 import pytest
 import torch
 
