@@ -98,3 +98,31 @@ def test_dtheta_deterministic_and_compile(pkg, device):
         results.append((loss.detach(), xx.grad, dd.grad, tt.grad))
     for u, v in zip(*results):
         assert torch.equal(u, v)
+
+
+def test_graph_replay_matches_eager(pkg, device):
+    """Forward and backward launches captured in a HIP graph (as bench.py times them): every replay, with
+    eager work and synchronisations between replays, equals the eager result bit for bit."""
+    npci = pkg.npci
+    x, d, th, gr = inputs(2, 8, 700, torch.bfloat16, torch.bfloat16, seed=12, permuted=True)
+    x, d, th, gr = x.to(device), d.to(device), th.to(device), gr.to(device=device, dtype=torch.bfloat16)
+
+    def step():
+        return (npci.npci_forward(x, d, th, 0.25),) + npci.npci_backward(x, d, th, gr, 0.25)
+
+    ref = [t.clone() for t in step()]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for _ in range(3):
+        npci.npci_forward(d, x, th, 0.25)   # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(u, v) for u, v in zip(outs, ref))

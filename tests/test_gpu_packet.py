@@ -157,3 +157,32 @@ def test_packet_forward_matches_composed_scans(pkg, device):
         assert max_abs(u, v) < 2e-2
     for u, v in zip(*grads):
         assert rel_err(u, v) < 2e-2
+
+
+def test_graph_replay_matches_eager(pkg, device):
+    """The pool's forward and backward launches captured in a HIP graph (as bench.py times them): every
+    replay, with eager work and synchronisations between replays, equals the eager result bit for bit."""
+    packet = pkg.packet
+    x, a, w, dp = inputs(3, 700, 512, 3, torch.bfloat16, seed=11)
+    x, a, w, dp = x.to(device), a.to(device), w.to(device), dp.to(device)
+
+    def step():
+        pooled, state = packet.pool_forward(x, a, w, 1e-5, 0.5)
+        return (pooled,) + packet.pool_backward(x, a, w, state, dp, 1e-5, 0.5)
+
+    ref = [t.clone() for t in step()]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    for _ in range(3):
+        packet.pool_forward(dp, a, w, 1e-5, 0.5)   # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(u, v) for u, v in zip(outs, ref))
