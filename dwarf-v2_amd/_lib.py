@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "dwarf_q6_unpack_kv",
     "dwarf_dsqg_q6_prefill_fwd",
     "dwarf_dsqg_q6_decode",
+    "dwarf_dsqg_q6_decode_workspace_bytes",
     "dwarf_phase_probe_fwd",
     "dwarf_phase_probe_bwd_workspace_bytes",
     "dwarf_phase_probe_bwd",
@@ -162,6 +163,7 @@ class Q6DecodeArgs(ctypes.Structure):
         ("query_probes", c_void_p), ("qprobe_layer_stride", c_int64),
         ("offsets", c_void_p),
         ("out", c_void_p), ("out_stride", _i64(4)),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
     ]
 
 
@@ -310,6 +312,8 @@ def load() -> ctypes.CDLL:
     for name in ("dwarf_packet_pool_state_bytes", "dwarf_packet_pool_fwd_workspace_bytes"):
         getattr(lib, name).restype = c_size_t
         getattr(lib, name).argtypes = [POINTER(PacketPoolFwdArgs)]
+    lib.dwarf_dsqg_q6_decode_workspace_bytes.restype = c_size_t
+    lib.dwarf_dsqg_q6_decode_workspace_bytes.argtypes = [POINTER(Q6DecodeArgs)]
     lib.dwarf_packet_pool_fwd.restype = c_int
     lib.dwarf_packet_pool_fwd.argtypes = [POINTER(PacketPoolFwdArgs), c_void_p]
     lib.dwarf_packet_pool_bwd_workspace_bytes.restype = c_size_t

@@ -22,6 +22,7 @@ hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const i
                             float* vout, hipStream_t stream);
 hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream);
 hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream);
+size_t q6_decode_workspace(const dwarf_dsqg_q6_decode_args& a);
 int q6_max_decode_offsets();
 int q6_max_decode_heads();
 size_t phase_probe_bwd_workspace(const dwarf_phase_probe_bwd_args& a);
@@ -473,6 +474,11 @@ int dwarf_dsqg_q6_prefill_fwd(const dwarf_dsqg_q6_prefill_args* args, dwarf_stre
   return hip_status(dwarf::launch_q6_prefill(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_q6_prefill_fwd");
 }
 
+size_t dwarf_dsqg_q6_decode_workspace_bytes(const dwarf_dsqg_q6_decode_args* args) {
+  if (!args || args->S < 0 || args->L < 0 || args->H < 0 || args->J < 0) return 0;
+  return dwarf::q6_decode_workspace(*args);
+}
+
 int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t stream) {
   if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
   const dwarf_dsqg_q6_decode_args& a = *args;
@@ -491,10 +497,16 @@ int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t s
   if (!a.pos || !a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "positions, a parameter table, probes or offsets is NULL");
   if (a.se_stride[2] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "scale_embed needs unit stride on head_dim");
+  if (!aligned16(a.scale_embed) || a.se_stride[0] % 4 || a.se_stride[1] % 4)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "scale_embed rows must be 16-byte aligned (read as float4)");
   if (a.pbase_stride[1] < 0 || a.pgain_stride[1] < 0 ||
       (a.pbase_stride[1] + a.pgain_stride[1] + DWARF_R_PLANES) * 4 * static_cast<int64_t>(a.J_large) >= (int64_t(1) << 31))
     return fail(DWARF_ERR_UNSUPPORTED, "decode reads a head's phase tables with 32-bit offsets (span below 2 GiB)");
   if (a.S == 0 || a.L == 0) return ok();
+  const size_t need = dwarf::q6_decode_workspace(a);
+  if (!a.workspace || a.workspace_bytes < need)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  if (!aligned16(a.workspace)) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
   return hip_status(dwarf::launch_q6_decode(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_q6_decode");
 }
 

@@ -490,37 +490,138 @@ struct DecBatch {
   uint32_t k0, k1, k2, v0, v1, v2;
   uint32_t ks, vs;   // fp16 scale pairs of the two groups
   float z, base, gain;
+  float t;           // the row's T entry: log2(e) (<q, e_j> / 8 + pb_j)
   int j;
   bool ok;
 };
 
 struct DecLayout {
   int JE, list_len;
-  size_t off_list, bytes;
+  size_t bytes;
 };
 
 __host__ __device__ inline DecLayout dec_layout(int J, int H) {
   DecLayout L;
   L.JE = (J + 1 + 15) / 16 * 16;                                   // offsets, the sentinel column, padding
   L.list_len = (J + 3 * kDecRows + 1) / 2 * 2;
-  L.off_list = static_cast<size_t>(H) * L.JE * 4;                  // s_T[H][JE]
-  L.bytes = L.off_list + static_cast<size_t>(H) * L.list_len * 8;  // s_list[H][list_len] int2
+  L.bytes = static_cast<size_t>(H) * L.list_len * 8;               // s_list[H][list_len] int2
   return L;
+}
+
+// The decode step's T table, T[l][s][h][j] = log2(e) (<q, e_j> / 8 + pb_j)
+// for every (layer, sequence, head) and offset, rows of JE floats with 0 at
+// j >= J (the sentinel column).  A workgroup takes 64 (sequence, head) rows
+// of one layer: it stages the layer's E rows in bf16 (as the GPU path rounds
+// them; hi and lo halves for the fp32 table) and its pos_bias in LDS, then
+// each wave multiplies its 16 q rows (A) by 16 E rows at a time (B).
+constexpr int kTabRows = 64;    // (sequence, head) rows per workgroup
+constexpr int kTabERow = 72;    // bf16 E row stride (elements)
+
+__host__ __device__ inline size_t dec_table_lds(int JE, int H, bool split) {
+  return static_cast<size_t>(JE) * kTabERow * 2 * (split ? 2 : 1) + static_cast<size_t>(JE) * H * 4;
+}
+
+__global__ __launch_bounds__(kBlock) void q6_decode_table(const dwarf_dsqg_q6_decode_args a, float* __restrict__ T,
+                                                          int JE) {
+  constexpr float kC = 0.125f * kLog2e;
+  const int rows = a.S * a.H;
+  const int per_layer = (rows + kTabRows - 1) / kTabRows;
+  const int ly = blockIdx.x / per_layer;
+  const int r0 = (blockIdx.x - ly * per_layer) * kTabRows + (threadIdx.x / kWave) * 16;
+  const int l = threadIdx.x % kWave, lr = l & 15, lc = l >> 4;
+  const int J = a.J, H = a.H;
+  const bool split = !a.se_round_bf16;
+  extern __shared__ float smem[];
+  uint16_t* sEh = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* sEl = sEh + JE * kTabERow;                                  // used when split
+  float* s_pb = reinterpret_cast<float*>(sEh + JE * kTabERow * (split ? 2 : 1));   // [JE][H]
+
+  // this wave's q rows first, so their latency overlaps the staging
+  uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if (r0 + lr < rows) {
+    const int sq = (r0 + lr) / H, h = r0 + lr - sq * H;
+    const bf16* qrow = reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1] + h * a.q_stride[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) xa[ks] = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * lc);
+  }
+  const float* se = a.scale_embed + ly * a.se_stride[0];
+  const float* pbl = a.pos_bias + ly * a.pb_stride[0];
+  // staging: every load of a batch is issued before any is used (4 floats of
+  // one E row per load, 16 loads per row)
+  constexpr int kBatch = 8;
+  for (int i0 = threadIdx.x; i0 < JE * 16; i0 += kBatch * kBlock) {
+    float4 v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + u * kBlock, j = i >> 4;
+      v[u] = i < JE * 16 && j < J ? *reinterpret_cast<const float4*>(se + j * a.se_stride[1] + 4 * (i & 15))
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i < JE * 16) {
+        const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        uint16_t* dh = sEh + (i >> 4) * kTabERow + 4 * (i & 15);
+        uint16_t* dl = sEl + (i >> 4) * kTabERow + 4 * (i & 15);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const __bf16 hi = static_cast<__bf16>(x[e]);
+          dh[e] = __builtin_bit_cast(uint16_t, hi);
+          if (split) dl[e] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x[e] - static_cast<float>(hi)));
+        }
+      }
+    }
+  }
+  for (int i0 = threadIdx.x; i0 < JE * H; i0 += kBatch * kBlock) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + u * kBlock, j = i / H, h = i - j * H;
+      v[u] = i < JE * H && j < J ? pbl[j * a.pb_stride[1] + h * a.pb_stride[2]] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (i0 + u * kBlock < JE * H) s_pb[i0 + u * kBlock] = v[u];
+  }
+  __syncthreads();
+  if (r0 >= rows) return;   // whole wave, after the only barrier
+  for (int tile = 0; tile < JE / 16; ++tile) {
+    const int j = tile * 16 + lr;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const uint4 eh = *reinterpret_cast<const uint4*>(sEh + j * kTabERow + 32 * ks + 8 * lc);
+      acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), bf16x8_from_bits(eh), acc);
+      if (split) {
+        const uint4 el = *reinterpret_cast<const uint4*>(sEl + j * kTabERow + 32 * ks + 8 * lc);
+        acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), bf16x8_from_bits(el), acc);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = r0 + 4 * lc + r;   // (sequence, head) row of the product
+      if (i < rows) {
+        const int sq = i / H, h = i - sq * H;
+        T[(static_cast<int64_t>(ly * a.S + sq) * H + h) * JE + j] = j < J ? (acc[r] + 8.0f * s_pb[j * H + h]) * kC : 0.f;
+      }
+    }
+  }
 }
 
 // Sum over all 64 lanes, in every lane.
 __device__ __forceinline__ float wave_allsum(float x) { return sum_over_queries16(group_sum<4>(x)); }
 
 template <int SHIFT>
-__global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf_dsqg_q6_decode_args a) {
+__global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf_dsqg_q6_decode_args a,
+                                                                    const float* __restrict__ T) {
   constexpr float kC = 0.125f * kLog2e;
   constexpr float kSlack2 = 8.0f * kLog2e;
   static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's chunk");
   const int J = a.J, H = a.H, J_small = a.J_small;
   const DecLayout lay = dec_layout(J, H);
   extern __shared__ float smem[];
-  float* s_T = smem;
-  int2* s_list_all = reinterpret_cast<int2*>(reinterpret_cast<char*>(smem) + lay.off_list);
+  int2* s_list_all = reinterpret_cast<int2*>(smem);
 
   const int sq = blockIdx.x / a.L;
   const int ly = blockIdx.x - sq * a.L;
@@ -528,11 +629,12 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
   const int l = threadIdx.x % kWave;
   const int c = l & 3;        // 16-dim chunk
   const int rr = l >> 2;      // row of the batch
-  const int lr = l & 15, lc = l >> 4;
   const int hk = h / (H / a.H_kv);
   const int t = uniform(a.pos[sq]);
   const int Nc = a.Ncache;
   int2* list = s_list_all + h * lay.list_len;
+  // this (sequence, layer, head)'s row of the T table (q6_decode_table)
+  const float* Th = T + (static_cast<int64_t>(ly * a.S + sq) * H + h) * lay.JE;
   // rows t - delta in [0, Nc); the sentinel (J, t + 1) gives row -1
   const int cnt = build_offset_list<kDecRows>(list, a.offsets, J, t, t, Nc, 1, make_int2(J, t + 1));
   const int cntp = (cnt + kDecRows - 1) / kDecRows * kDecRows;
@@ -568,57 +670,13 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
     const int i = e.x - J_small;
     b.base = buf_load_f32(rpb, far ? static_cast<uint32_t>(i * ph_step + 4 * c) : kOutOfRange);
     b.gain = buf_load_f32(rpg, far ? static_cast<uint32_t>(i * pg_step + 4 * c) : kOutOfRange);
+    b.t = Th[e.x];
   };
 
   DecBatch b0, b1;
   if (cnt > 0) fetch(0, b0);
 
-  // T[i][j] for the workgroup's heads i: A = q rows (head i in row i), B = E^T
   const bf16* qrows = reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1];
-  {
-    uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-    if (lr < H) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        xa[ks] = *reinterpret_cast<const uint4*>(qrows + lr * a.q_stride[2] + 32 * ks + 8 * lc);
-    }
-    const float* se = a.scale_embed + ly * a.se_stride[0];
-    const float* pbl = a.pos_bias + ly * a.pb_stride[0];
-    for (int tile = h; tile < lay.JE / 16; tile += H) {   // wave-uniform
-      const int j = tile * 16 + lr;
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        float e8[8];
-        if (j < J) {
-          const float4* p = reinterpret_cast<const float4*>(se + j * a.se_stride[1] + 32 * ks + 8 * lc);
-          const float4 u0 = p[0], u1 = p[1];
-          e8[0] = u0.x; e8[1] = u0.y; e8[2] = u0.z; e8[3] = u0.w;
-          e8[4] = u1.x; e8[5] = u1.y; e8[6] = u1.z; e8[7] = u1.w;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) e8[e] = 0.f;
-        }
-        if (a.se_round_bf16) {
-          bf16x8 hi;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) hi[e] = static_cast<__bf16>(e8[e]);
-          acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), hi, acc);
-        } else {
-          bf16x8 hi, lo;
-          split_bf16x8(e8, hi, lo);
-          acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), hi, acc);
-          acc = mfma16_bf16(bf16x8_from_bits(xa[ks]), lo, acc);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 4 * lc + r;
-        if (i < H) s_T[i * lay.JE + j] = j < J ? (acc[r] + 8.0f * pbl[j * a.pb_stride[1] + i * a.pb_stride[2]]) * kC : 0.f;
-      }
-    }
-  }
-
   // this head's query: lane c's 16 dims as bf16 pairs, their sum, and y of
   // plane c = <q, probe_c> / sqrt(|q|^2 + 1e-6 hd) (dsqg:3231-3249)
   const bf16* qh = qrows + h * a.q_stride[2];
@@ -643,8 +701,6 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
     for (int r = 0; r < kPlanes; ++r) yp[r] = wave_allsum(qd * qp[r * kHeadDim + l]);
     yg = (c == 0 ? yp[0] : c == 1 ? yp[1] : c == 2 ? yp[2] : yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
   }
-  const float* Th = s_T + h * lay.JE;
-  __syncthreads();   // T complete
 
   float acc[16];
 #pragma unroll
@@ -654,7 +710,7 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
   auto consume = [&](int k0, const DecBatch& b) {
     const float kd = q6_dot16_biased(q32, b.k0, b.k1, b.k2) + qbias;
     const float dot = group_sum<4>(kd * half_lo_or_hi(b.ks, khi));
-    const float s2 = b.ok ? fmaf(dot, kC, Th[b.j]) : -INFINITY;
+    const float s2 = b.ok ? fmaf(dot, kC, b.t) : -INFINITY;
     if (s2 > m + kSlack2) {   // per row group; the groups are put on one scale at the end
       const float f = __builtin_amdgcn_exp2f(m - s2);
 #pragma unroll
@@ -767,11 +823,20 @@ hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t st
   return hipGetLastError();
 }
 
+size_t q6_decode_workspace(const dwarf_dsqg_q6_decode_args& a) {
+  return static_cast<size_t>(a.S) * a.L * a.H * dec_layout(a.J, a.H).JE * sizeof(float);
+}
+
 hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream) {
+  const DecLayout lay = dec_layout(a.J, a.H);
+  float* T = static_cast<float*>(a.workspace);
+  const int table_blocks = a.L * ((a.S * a.H + kTabRows - 1) / kTabRows);
+  hipLaunchKernelGGL(q6_decode_table, dim3(table_blocks), dim3(kBlock), dec_table_lds(lay.JE, a.H, !a.se_round_bf16),
+                     stream, a, T, lay.JE);
   const int blocks = a.S * a.L;
-  const size_t lds = dec_layout(a.J, a.H).bytes;
+  const size_t lds = lay.bytes;
 #define DWARF_Q6D_CASE(S) \
-  case S: hipLaunchKernelGGL(q6_decode_q4<S>, dim3(blocks), dim3(kWave * a.H), lds, stream, a); break;
+  case S: hipLaunchKernelGGL(q6_decode_q4<S>, dim3(blocks), dim3(kWave * a.H), lds, stream, a, T); break;
   switch (a.plane_shift) {
     DWARF_Q6D_CASE(0) DWARF_Q6D_CASE(1) DWARF_Q6D_CASE(2) DWARF_Q6D_CASE(3) DWARF_Q6D_CASE(4)
     DWARF_Q6D_CASE(5) DWARF_Q6D_CASE(6) DWARF_Q6D_CASE(7) DWARF_Q6D_CASE(8) DWARF_Q6D_CASE(9)

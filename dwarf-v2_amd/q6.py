@@ -165,6 +165,9 @@ def q6_decode(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, que
     a.offsets = offsets.data_ptr()
     a.out, a.out_stride = out.data_ptr(), _p64(out.stride())
     lib = _lib.load()
+    ws = torch.empty(max(int(lib.dwarf_dsqg_q6_decode_workspace_bytes(ctypes.byref(a))), 16), device=q.device,
+                     dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check(lib.dwarf_dsqg_q6_decode(ctypes.byref(a), torch.cuda.current_stream(q.device).cuda_stream),
                "dwarf_dsqg_q6_decode")
     return out

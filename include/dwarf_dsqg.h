@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 2
+#define DWARF_ABI_VERSION 3
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
@@ -412,7 +412,12 @@ typedef struct {
   const float* query_probes; int64_t qprobe_layer_stride; /* [L,4,hd] */
   const int32_t* offsets;    /* [J], shared by all layers */
   void* out; int64_t out_stride[4];
+  void* workspace; size_t workspace_bytes;  /* dwarf_dsqg_q6_decode_workspace_bytes, 16-byte aligned */
 } dwarf_dsqg_q6_decode_args;
+
+/* The step's per-(sequence, layer, head) score table: S*L*H*JE fp32,
+ * JE = (J + 16) rounded down to a multiple of 16. */
+size_t dwarf_dsqg_q6_decode_workspace_bytes(const dwarf_dsqg_q6_decode_args* args);
 
 int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args,
                          dwarf_stream_t stream);

@@ -29,7 +29,7 @@ def lib(pkg):
 
 def test_exports_every_declared_symbol(pkg, lib):
     names = declared_functions()
-    assert len(names) == 27
+    assert len(names) == 28
     assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
     for name in names:
         assert hasattr(lib, name), name
@@ -104,6 +104,8 @@ def test_validation_errors_without_gpu(pkg, lib):
     d.J, d.J_small, d.J_large, d.H, d.H_kv = 96, 17, 79, 32, 32
     assert lib.dwarf_dsqg_q6_decode(ctypes.byref(d), None) == L.DWARF_ERR_UNSUPPORTED   # one wave per head, <= 16
     assert b"heads" in lib.dwarf_last_error()
+    d.S, d.L, d.H, d.H_kv = 3, 2, 8, 8   # the T table: S*L*H rows of JE = 112 fp32 at J = 96
+    assert lib.dwarf_dsqg_q6_decode_workspace_bytes(ctypes.byref(d)) == 3 * 2 * 8 * 112 * 4
     p = L.PhaseProbeFwdArgs()
     p.B, p.H, p.N, p.head_dim, p.R, p.end = 1, 1, 8, 32, 4, 8
     assert lib.dwarf_phase_probe_fwd(ctypes.byref(p), None) == L.DWARF_ERR_UNSUPPORTED   # head_dim 64 only
