@@ -291,6 +291,7 @@ static int check_packet(const dwarf_packet_pool_fwd_args& a, bool need_pooled) {
   if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
   if (need_pooled && (rc = check_btd("pooled", a.pooled, a.pooled_stride, a.dtype, a.D))) return rc;
   if (a.B > 0 && a.N > 0 && a.D > 0 && !a.state) return fail(DWARF_ERR_INVALID_ARGUMENT, "state is NULL");
+  if (reinterpret_cast<uintptr_t>(a.state) & 3u) return fail(DWARF_ERR_INVALID_ARGUMENT, "state must be 4-byte aligned");
   return DWARF_OK;
 }
 
@@ -314,6 +315,7 @@ int dwarf_packet_pool_fwd(const dwarf_packet_pool_fwd_args* args, dwarf_stream_t
   const size_t need = dwarf::packet_fwd_workspace(a.B, a.N, a.D, a.K);
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(a.workspace) & 15u) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
   return hip_status(dwarf::launch_packet_fwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_packet_pool_fwd");
 }
 
@@ -328,6 +330,7 @@ int dwarf_packet_pool_bwd(const dwarf_packet_pool_bwd_args* args, dwarf_stream_t
   const size_t need = dwarf::packet_bwd_workspace(a.fwd.B, a.fwd.N, a.fwd.D, a.fwd.K);
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(a.workspace) & 15u) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
   return hip_status(dwarf::launch_packet_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_packet_pool_bwd");
 }
 

@@ -207,7 +207,8 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream);
  * every product and partial sum rounded to dtype as the reference's tensor
  * arithmetic rounds them (train:262-267 with K = 3 timescales).  `state`
  * (dwarf_packet_pool_state_bytes, fp32) receives each 16-token chunk's
- * incoming scan states; the backward reads it.
+ * incoming scan states; the backward reads it.  Workspaces are 16-byte
+ * aligned.
  */
 #define DWARF_PACKET_MAX_SCALES 4
 
