@@ -61,6 +61,21 @@ int hip_status(hipError_t e, const char* what) {
   return fail(DWARF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Zeroes n floats: the parameter gradients of a call with no rows (a sum over
+// nothing).  A kernel rather than a memset, so the call may be captured in a
+// HIP graph.
+__global__ void zero_floats_kernel(float* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+int zero_floats(float* p, int64_t n, hipStream_t stream, const char* what) {
+  if (!p || n <= 0) return ok();
+  hipLaunchKernelGGL(zero_floats_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, p,
+                     static_cast<int>(n));
+  return hip_status(hipGetLastError(), what);
+}
+
 constexpr int kMaxOffsets = 256;  // LDS tables of the DSQG kernels
 
 size_t elem_size(int dtype) { return dtype == DWARF_BF16 ? 2 : 4; }
@@ -254,10 +269,10 @@ int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream) {
   const dwarf_ema_fwd_args& a = *args;
   int rc = check_ema_common(a.B, a.N, a.D, a.dtype, a.alpha_per_channel, a.floor_, a.ceiling, a.alpha);
   if (rc) return rc;
+  if (a.B == 0 || a.N == 0 || a.D == 0) return ok();   // empty x: nothing to read or write
   if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
   if ((rc = check_btd("y", a.y, a.y_stride, a.dtype, a.D))) return rc;
   if ((rc = check_reset(a.reset, a.reset_stride, a.B, a.N))) return rc;
-  if (a.B == 0 || a.N == 0 || a.D == 0) return ok();
   const size_t need = dwarf::ema_fwd_workspace(a.B, a.N, a.D);
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
@@ -269,12 +284,13 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream) {
   const dwarf_ema_bwd_args& a = *args;
   int rc = check_ema_common(a.B, a.N, a.D, a.dtype, a.alpha_per_channel, a.floor_, a.ceiling, a.alpha);
   if (rc) return rc;
+  if (a.B == 0 || a.N == 0 || a.D == 0)   // empty x: dalpha is a sum over nothing
+    return zero_floats(a.dalpha, a.alpha_per_channel ? a.D : 1, reinterpret_cast<hipStream_t>(stream), "dwarf_ema_bwd");
   if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
   if ((rc = check_btd("y", a.y, a.y_stride, a.dtype, a.D))) return rc;
   if ((rc = check_btd("dy", a.dy, a.dy_stride, a.dtype, a.D))) return rc;
   if ((rc = check_btd("dx", a.dx, a.dx_stride, a.dtype, a.D))) return rc;
   if ((rc = check_reset(a.reset, a.reset_stride, a.B, a.N))) return rc;
-  if (a.B == 0 || a.N == 0 || a.D == 0) return ok();
   const size_t need = dwarf::ema_bwd_workspace(a.B, a.N, a.D);
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
@@ -282,12 +298,15 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream) {
 }
 
 // ---- InterferencePacket pool ---------------------------------------------------
+static bool packet_empty(const dwarf_packet_pool_fwd_args& a) { return a.B == 0 || a.N == 0 || a.D == 0; }
+
 static int check_packet(const dwarf_packet_pool_fwd_args& a, bool need_pooled) {
   if (a.K < 1 || a.K > dwarf::packet_max_scales() || a.K > DWARF_PACKET_MAX_SCALES)
     return fail(DWARF_ERR_UNSUPPORTED, "K=%d scales (1..%d are built)", a.K, DWARF_PACKET_MAX_SCALES);
   int rc = check_ema_common(a.B, a.N, a.D, a.dtype, 0, a.floor_, a.ceiling, a.alpha);
   if (rc) return rc;
   if (!a.weight) return fail(DWARF_ERR_INVALID_ARGUMENT, "weight is NULL");
+  if (packet_empty(a)) return DWARF_OK;   // no rows to read or write
   if ((rc = check_btd("x", a.x, a.x_stride, a.dtype, a.D))) return rc;
   if (need_pooled && (rc = check_btd("pooled", a.pooled, a.pooled_stride, a.dtype, a.D))) return rc;
   if (a.B > 0 && a.N > 0 && a.D > 0 && !a.state) return fail(DWARF_ERR_INVALID_ARGUMENT, "state is NULL");
@@ -324,6 +343,11 @@ int dwarf_packet_pool_bwd(const dwarf_packet_pool_bwd_args* args, dwarf_stream_t
   const dwarf_packet_pool_bwd_args& a = *args;
   int rc = check_packet(a.fwd, false);
   if (rc) return rc;
+  if (packet_empty(a.fwd)) {   // the factor and weight gradients are sums over nothing
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if ((rc = zero_floats(a.dalpha, a.fwd.K, s, "dwarf_packet_pool_bwd"))) return rc;
+    return zero_floats(a.dweight, a.fwd.K, s, "dwarf_packet_pool_bwd");
+  }
   if ((rc = check_btd("dpooled", a.dpooled, a.dpooled_stride, a.fwd.dtype, a.fwd.D))) return rc;
   if ((rc = check_btd("dx", a.dx, a.dx_stride, a.fwd.dtype, a.fwd.D))) return rc;
   if (a.fwd.B == 0 || a.fwd.N == 0 || a.fwd.D == 0) return ok();
@@ -343,9 +367,10 @@ static int check_probe_fwd(const dwarf_phase_probe_fwd_args& a, bool need_out) {
   if (a.dtype != DWARF_BF16 && a.dtype != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", a.dtype);
   if (static_cast<int64_t>(a.B) * a.H * a.N >= (int64_t(1) << 31))
     return fail(DWARF_ERR_UNSUPPORTED, "B*H*N must stay below 2^31 rows");
+  if (!a.probes || !aligned16(a.probes)) return fail(DWARF_ERR_INVALID_ARGUMENT, "probes NULL or not 16-byte aligned");
+  if (static_cast<int64_t>(a.B) * a.H * a.N == 0) return DWARF_OK;   // no rows to read or write
   int rc = check_rows("x", a.x, a.x_stride, 3, a.dtype);
   if (rc) return rc;
-  if (!a.probes || !aligned16(a.probes)) return fail(DWARF_ERR_INVALID_ARGUMENT, "probes NULL or not 16-byte aligned");
   if (need_out && !a.out) return fail(DWARF_ERR_INVALID_ARGUMENT, "out is NULL");
   return DWARF_OK;
 }
@@ -367,6 +392,9 @@ int dwarf_phase_probe_bwd(const dwarf_phase_probe_bwd_args* args, dwarf_stream_t
   const dwarf_phase_probe_bwd_args& a = *args;
   int rc = check_probe_fwd(a.fwd, false);
   if (rc) return rc;
+  if (static_cast<int64_t>(a.fwd.B) * a.fwd.H * a.fwd.N == 0)   // dprobes is a sum over nothing
+    return zero_floats(a.dprobes, static_cast<int64_t>(a.fwd.R) * a.fwd.head_dim, reinterpret_cast<hipStream_t>(stream),
+                       "dwarf_phase_probe_bwd");
   if (!a.dout) return fail(DWARF_ERR_INVALID_ARGUMENT, "dout is NULL");
   if ((rc = check_rows("dx", a.dx, a.dx_stride, 3, a.fwd.dtype))) return rc;
   if (a.dprobes) {
@@ -388,10 +416,11 @@ static int check_npci(const dwarf_npci_fwd_args& a, bool need_out) {
     if (dt != DWARF_BF16 && dt != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", dt);
   if (static_cast<int64_t>(a.B) * a.H * a.T >= (int64_t(1) << 31))
     return fail(DWARF_ERR_UNSUPPORTED, "B*H*T must stay below 2^31 rows");
+  if (!a.theta && a.H > 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "theta is NULL");
+  if (static_cast<int64_t>(a.B) * a.H * a.T == 0) return DWARF_OK;   // no rows to read or write
   int rc = check_rows("x", a.x, a.x_stride, 3, a.x_dtype);
   if (rc) return rc;
   if ((rc = check_rows("delta", a.delta, a.delta_stride, 3, a.delta_dtype))) return rc;
-  if (!a.theta) return fail(DWARF_ERR_INVALID_ARGUMENT, "theta is NULL");
   if (need_out && (rc = check_rows("out", a.out, a.out_stride, 3, a.x_dtype))) return rc;
   return DWARF_OK;
 }
@@ -412,10 +441,12 @@ int dwarf_npci_bwd(const dwarf_npci_bwd_args* args, dwarf_stream_t stream) {
   const dwarf_npci_bwd_args& a = *args;
   int rc = check_npci(a.fwd, false);
   if (rc) return rc;
+  if (!a.dtheta && a.fwd.H > 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtheta is NULL");
+  if (static_cast<int64_t>(a.fwd.B) * a.fwd.H * a.fwd.T == 0)   // dtheta is a sum over nothing
+    return zero_floats(a.dtheta, a.fwd.H, reinterpret_cast<hipStream_t>(stream), "dwarf_npci_bwd");
   if ((rc = check_rows("grad", a.grad, a.grad_stride, 3, a.fwd.x_dtype))) return rc;
   if ((rc = check_rows("dx", a.dx, a.dx_stride, 3, a.fwd.x_dtype))) return rc;
   if ((rc = check_rows("ddelta", a.ddelta, a.ddelta_stride, 3, a.fwd.delta_dtype))) return rc;
-  if (!a.dtheta) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtheta is NULL");
   const size_t need = dwarf::npci_bwd_workspace(a);
   if (need && (!a.workspace || a.workspace_bytes < need))
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);

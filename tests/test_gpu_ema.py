@@ -181,3 +181,15 @@ def test_reset_bf16_and_all_false_mask(pkg, device):
     none = torch.zeros(2, 3000, dtype=torch.bool)
     assert all(torch.equal(a, b) for a, b in zip(run_reset(pkg, x, alpha, dy, none, device),
                                                  run(pkg, x, alpha, dy, device)))
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_empty_sequence(pkg, device, per_channel):
+    """x [B,0,D]: an empty scan, dx empty and dalpha exactly 0 (a sum over nothing)."""
+    x = torch.zeros(2, 0, 8, device=device, dtype=torch.bfloat16, requires_grad=True)
+    a = torch.full((8 if per_channel else 1,), 0.1, device=device, requires_grad=True)
+    y = pkg.causal_ema_scan(x, a)
+    assert y.shape == (2, 0, 8)
+    y.float().sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad.shape == (2, 0, 8) and torch.equal(a.grad.cpu(), torch.zeros(a.shape))

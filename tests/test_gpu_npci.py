@@ -126,3 +126,16 @@ def test_graph_replay_matches_eager(pkg, device):
         graph.replay()
         torch.cuda.synchronize()
         assert all(torch.equal(u, v) for u, v in zip(outs, ref))
+
+
+def test_empty_rows(pkg, device):
+    """T = 0: an empty rotation, empty dx and ddelta, and dtheta exactly 0."""
+    x = torch.zeros(2, 3, 0, 64, device=device, dtype=torch.bfloat16, requires_grad=True)
+    d = torch.zeros(2, 3, 0, 64, device=device, dtype=torch.bfloat16, requires_grad=True)
+    th = torch.full((3,), 0.1, device=device, requires_grad=True)
+    out = pkg.npci_rotate(x, d, th)
+    assert out.shape == (2, 3, 0, 64) and out.dtype == torch.bfloat16
+    out.float().sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad.shape == x.shape and d.grad.shape == d.shape
+    assert torch.equal(th.grad.cpu(), torch.zeros(3))

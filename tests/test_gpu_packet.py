@@ -186,3 +186,16 @@ def test_graph_replay_matches_eager(pkg, device):
         graph.replay()
         torch.cuda.synchronize()
         assert all(torch.equal(u, v) for u, v in zip(outs, ref))
+
+
+def test_empty_sequence(pkg, device):
+    """x [B,0,D]: an empty pool, dx empty, and the factor and weight gradients exactly 0."""
+    x = torch.zeros(2, 0, 16, device=device, dtype=torch.bfloat16, requires_grad=True)
+    a = torch.tensor(FACTORS[:3], device=device, requires_grad=True)
+    w = torch.full((3,), 1 / 3, device=device, requires_grad=True)
+    pooled = pkg.interference_pool(x, a, w)
+    assert pooled.shape == (2, 0, 16)
+    pooled.float().sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad.shape == x.shape
+    assert torch.equal(a.grad.cpu(), torch.zeros(3)) and torch.equal(w.grad.cpu(), torch.zeros(3))

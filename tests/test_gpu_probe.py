@@ -91,3 +91,14 @@ def test_torch_compile_traces_without_graph_breaks(pkg, device):
         results.append((loss.detach(), xx.grad, pp.grad))
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+def test_empty_sequence(pkg, device):
+    """N = 0: empty features and dx, and dprobes exactly 0."""
+    x = torch.zeros(2, 3, 0, 64, device=device, dtype=torch.bfloat16, requires_grad=True)
+    p = torch.nn.functional.normalize(torch.randn(4, 64), dim=-1).to(device).requires_grad_(True)
+    y = pkg.phase_probe_features(x, p)
+    assert y.shape == (2, 3, 0, 4)
+    y.sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad.shape == x.shape and torch.equal(p.grad.cpu(), torch.zeros(4, 64))
