@@ -134,6 +134,7 @@ int check_fwd(const dwarf_dsqg_fwd_args& a) {
   int rc = check_lattice(a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, a.query_start);
   if (rc) return rc;
   if (a.dtype != DWARF_BF16 && a.dtype != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", a.dtype);
+  if (a.B == 0 || a.N == 0) return DWARF_OK;   // no rows to read or write
   if ((rc = check_rows("q", a.q, a.q_stride, 3, a.dtype))) return rc;
   if ((rc = check_rows("k", a.k, a.k_stride, 3, a.dtype))) return rc;
   if ((rc = check_rows("v", a.v, a.v_stride, 3, a.dtype))) return rc;
@@ -184,6 +185,16 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
   const dwarf_dsqg_bwd_args& a = *args;
   int rc = check_fwd(a.fwd);
   if (rc) return rc;
+  if (a.fwd.B == 0 || a.fwd.N == 0) {   // the parameter gradients are sums over nothing
+    if (!do_params) return ok();
+    const dwarf_dsqg_fwd_args& f = a.fwd;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t jl = f.J_large > 0 ? f.J_large : 1;
+    if ((rc = zero_floats(a.dpos_bias, static_cast<int64_t>(f.J) * f.H, s, name))) return rc;
+    if ((rc = zero_floats(a.dscale_embed, static_cast<int64_t>(f.J) * f.head_dim, s, name))) return rc;
+    if ((rc = zero_floats(a.dphase_base, jl * f.H * DWARF_R_PLANES, s, name))) return rc;
+    return zero_floats(a.dphase_gain, jl * f.H * DWARF_R_PLANES, s, name);
+  }
   const int dt = a.fwd.dtype;
   if ((rc = check_contig_rows("dout", a.dout, a.dout_stride, dt))) return rc;
   if (dt == DWARF_BF16 && (rc = check_gather_span("dout", a.dout_stride[2], 2, a.fwd.N))) return rc;
@@ -200,7 +211,6 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
     if (!a.dz_pre) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre is NULL");
     if (!aligned16(a.dz_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre must be 16-byte aligned");
   }
-  if (a.fwd.B == 0 || a.fwd.N == 0) return ok();
   const dwarf::BwdWorkspace ws = dwarf::bwd_workspace_layout(a);
   if (!a.workspace || a.workspace_bytes < ws.total)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", ws.total, a.workspace_bytes);

@@ -193,3 +193,22 @@ def test_torch_compile_traces_without_graph_breaks(pkg, device):
         results.append([loss.detach()] + [xd[n].grad for n in NAMES])
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+def test_empty_batch(pkg, device):
+    """B = 0: an empty output, empty dq/dk/dv/dy/dz, and the parameter gradients exactly 0
+    (the reference allocates them zeroed, dsqg:2380-2392)."""
+    offsets = lattice(pkg)
+    x = make_inputs(1, 4, 2, 64, offsets, 17, seed=63, dtype=torch.bfloat16)
+    xd = {n: (t[:0] if t.dim() == 4 else t).to(device).requires_grad_(True) for n, t in x.items()}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.dsqg_attention_v18_grouped(*(xd[n] for n in NAMES), 96, 17, 79, off, None, None, None, None, None, 3,
+                                         0, False, 0, 0, 1)
+    assert out.shape[0] == 0
+    out.float().sum().backward()
+    torch.cuda.synchronize()
+    for n in NAMES:
+        g = xd[n].grad
+        assert g is not None and g.shape == xd[n].shape
+        if xd[n].dim() != 4:   # the parameter tables
+            assert not g.any(), n
