@@ -125,14 +125,15 @@ def q6_prefill(q, cache, pos_bias, scale_embed, phase_base, phase_gain, query_pr
 
 
 def q6_decode(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, query_probes, offsets_dev,
-              j_small, j_large, plane_shift=0):
+              j_small, j_large, plane_shift=0, round_se=True):
     """One decode step over L layers.
 
     q [S,L,H,64] bf16 (one new query per sequence and layer), pos [S] int32
     positions, caches [L,S,Hkv,Ncache,128] uint8, per-layer tables with a
     leading L dimension: pos_bias [L,J,H], scale_embed [L,J,64], phase_base /
     phase_gain [L,J_L,H,4], query_probes [L,4,64] (normalised).  Returns
-    out [S,L,H,64] bf16.
+    out [S,L,H,64] bf16.  round_se rounds scale_embed to bf16 as the GPU path
+    does (dsqg:760-763); False keeps it in fp32 (bf16 hi + lo on the MFMA).
     """
     if not q.is_cuda:
         raise RuntimeError("the q6 HIP kernels require device tensors")
@@ -153,7 +154,7 @@ def q6_decode(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, que
     a.S, a.L, a.H, a.H_kv, a.Ncache, a.head_dim = S, L, H, caches.shape[2], caches.shape[3], HD
     a.J, a.J_small, a.J_large = int(j_small) + int(j_large), int(j_small), int(j_large)
     a.plane_shift = int(plane_shift)
-    a.se_round_bf16 = 1
+    a.se_round_bf16 = int(bool(round_se))
     a.q, a.q_stride = q.data_ptr(), _p64(q.stride())
     a.pos = pos.data_ptr()
     a.cache, a.cache_stride = caches.data_ptr(), _p64(caches.stride()[:4])

@@ -44,7 +44,7 @@ def test_pack_matches_cpu_codec_bit_exact(pkg, device, dtype):
     assert np.allclose(z, rz, rtol=1e-5, atol=1e-6)
 
 
-def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs, return_lse=False):
+def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs, return_lse=False, round_se=True):
     kd, vd, _ = q6_ref.unpack_slots(cache_np)
     inp = dict(x)
     inp["k"] = torch.from_numpy(kd).double()
@@ -52,7 +52,7 @@ def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs, return_lse=Fal
     inp["y_pre"] = features(x["q"].double(), qp).double()
     inp["z_pre"] = features(torch.from_numpy(kd).double(), kp).double()
     return dsqg_ref.dsqg_forward(*(inp[n].double() for n in NAMES), offsets, js, plane_shift=shift,
-                                 query_start=qs, round_se=True, return_lse=return_lse)
+                                 query_start=qs, round_se=round_se, return_lse=return_lse)
 
 
 def test_prefill_matches_oracle(pkg, device):
@@ -97,6 +97,32 @@ def test_decode_matches_oracle(pkg, device):
         for s in range(S):
             t = int(pos[s])
             assert max_abs(out[s, l], ref[s, :, t]) < 2e-2, (s, l)
+
+
+def test_decode_fp32_scale_embed(pkg, device):
+    """round_se=False: the score table takes SE in fp32 (bf16 hi + lo halves on the MFMA), against the
+    oracle without SE rounding; SE scaled up so its rounding would show."""
+    offsets = list(pkg.ALL_OFFSETS)
+    S, L, H, Hkv, N = 2, 2, 4, 2, 400
+    layers = [make_inputs(S, H, Hkv, N, offsets, 17, seed=70 + l, dtype=torch.bfloat16, gain_std=6.0)
+              for l in range(L)]
+    for x in layers:
+        x["scale_embed"] = 40.0 * x["scale_embed"]
+    pos = torch.tensor([399, 130], dtype=torch.int32)
+    qp, kp = orthogonal_probes(64, 0)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    caches = torch.stack([pkg.q6.pack_kv(x["k"].to(device), x["v"].to(device), kp.to(device)) for x in layers])
+    qdec = torch.stack([torch.stack([layers[l]["q"][s, :, int(pos[s])] for l in range(L)]) for s in range(S)])
+    tables = {n: torch.stack([x[n] for x in layers]).to(device) for n in ("pos_bias", "scale_embed", "phase_base",
+                                                                          "phase_gain")}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_decode(qdec.to(device), pos.to(device), caches, tables["pos_bias"], tables["scale_embed"],
+                           tables["phase_base"], tables["phase_gain"], torch.stack([qp] * L).to(device), off,
+                           17, 79, 0, round_se=False).cpu()
+    for l in range(L):
+        ref = _oracle_on_cache(layers[l], caches[l].cpu().numpy(), offsets, 17, 0, qp, kp, 0, round_se=False)
+        for s in range(S):
+            assert max_abs(out[s, l], ref[s, :, int(pos[s])]) < 2e-2, (s, l)
 
 
 def test_decode_full_lattice_eight_heads(pkg, device):
