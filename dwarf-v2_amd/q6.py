@@ -85,8 +85,9 @@ def unpack_kv(cache: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 def q6_prefill(q, cache, pos_bias, scale_embed, phase_base, phase_gain, query_probes, offsets_dev,
-               j_small, j_large, plane_shift=0, query_start=0, *, return_lse=False):
-    """DSQG forward over a q6 cache.  q [B,H,N,64] bf16; returns bf16 out (and lse)."""
+               j_small, j_large, plane_shift=0, query_start=0, *, return_lse=False, round_se=True):
+    """DSQG forward over a q6 cache.  q [B,H,N,64] bf16; returns bf16 out (and lse).  round_se rounds
+    scale_embed to bf16 as the GPU path does (dsqg:760-763); False keeps it in fp32."""
     if not q.is_cuda:
         raise RuntimeError("the q6 HIP kernels require device tensors")
     q = _rows(q.to(torch.bfloat16))
@@ -106,7 +107,7 @@ def q6_prefill(q, cache, pos_bias, scale_embed, phase_base, phase_gain, query_pr
     a.B, a.H, a.H_kv, a.N, a.head_dim = B, H, cache.shape[1], N, HD
     a.J, a.J_small, a.J_large = int(j_small) + int(j_large), int(j_small), int(j_large)
     a.plane_shift, a.query_start = int(plane_shift), max(0, min(int(query_start), N))
-    a.se_round_bf16 = 1
+    a.se_round_bf16 = int(bool(round_se))
     a.q, a.q_stride = q.data_ptr(), _p64(q.stride())
     a.cache, a.cache_stride = cache.data_ptr(), _p64(cache.stride()[:3])
     a.pos_bias, a.pb_stride = pos_bias.data_ptr(), _p64(pos_bias.stride())

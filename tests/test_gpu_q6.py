@@ -74,6 +74,23 @@ def test_prefill_matches_oracle(pkg, device):
     assert (lse.cpu().double()[fin] - rlse[fin]).abs().max().item() < 2e-2
 
 
+def test_prefill_fp32_scale_embed(pkg, device):
+    """round_se=False: the prefill's <q, e_j> table takes SE in fp32, against the oracle without SE
+    rounding; SE scaled up so its rounding would show."""
+    offsets = list(pkg.ALL_OFFSETS)
+    x = make_inputs(1, 4, 2, 260, offsets, 17, seed=5, dtype=torch.bfloat16, gain_std=6.0)
+    x["scale_embed"] = 40.0 * x["scale_embed"]
+    qp, kp = orthogonal_probes(64, 0)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    xd = {n: t.to(device) for n, t in x.items()}
+    cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"], xd["phase_gain"],
+                            qp.to(device), off, 17, 79, 0, 1, round_se=False)
+    ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, 0, qp, kp, 1, round_se=False)
+    assert max_abs(out, ref) < 2e-2
+
+
 def test_decode_matches_oracle(pkg, device):
     offsets = list(pkg.ALL_OFFSETS)
     shift = 0
