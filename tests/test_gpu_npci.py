@@ -51,7 +51,7 @@ def run(pkg, x, d, th, gr, device, tau):
 
 
 @pytest.mark.parametrize("xdt,ddt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
-                                     (torch.bfloat16, torch.float32)])
+                                     (torch.bfloat16, torch.float32), (torch.float32, torch.bfloat16)])
 @pytest.mark.parametrize("shape,permuted", [((2, 3, 37), False), ((2, 3, 9), False), ((1, 8, 300), True),
                                             ((2, 2, 16400), False)])
 def test_matches_oracle(pkg, device, xdt, ddt, shape, permuted):
