@@ -212,3 +212,19 @@ def test_empty_batch(pkg, device):
         assert g is not None and g.shape == xd[n].shape
         if xd[n].dim() != 4:   # the parameter tables
             assert not g.any(), n
+
+
+def test_maximum_offsets_bf16(pkg, device):
+    """J = 256, the most offsets the kernels take (17 near, 239 far: 48..286): LDS tables past 64 KB per
+    workgroup (gfx950 allows 160 KB).  Output and all 9 gradients against the float64 oracle within the
+    bf16 bar (2e-2 max-abs, times the gradient's largest magnitude where that exceeds 1: the table
+    gradients sum over every pair)."""
+    offsets = list(range(1, 18)) + list(range(48, 48 + 239))
+    x = make_inputs(1, 2, 2, 320, offsets, 17, seed=71, dtype=torch.bfloat16)
+    dout = torch.randn(1, 2, 320, 64, generator=torch.Generator().manual_seed(72)).to(torch.bfloat16)
+    out, grads = gpu_fwd_bwd(pkg, x, offsets, 17, 0, 1, dout, device)
+    rout, _, rgrads = oracle_fwd_bwd(x, offsets, 17, 0, 1, dout.float(), True)
+    assert max_abs(out.float(), rout) < BF16_ABS
+    for n in NAMES:
+        scale = max(1.0, rgrads[n].abs().max().item())
+        assert max_abs(grads[n].float(), rgrads[n]) < BF16_ABS * scale, n
