@@ -202,3 +202,23 @@ def test_decode_graph_replay_matches_eager(pkg, device):
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
         del other
+
+
+def test_decode_maximum_sizes(pkg, device):
+    """J = 256 offsets (17 near, 239 far) and H = 16 heads (a 1024-thread workgroup, H_kv = 4): the
+    decode step against the oracle on the dequantised cache."""
+    offsets = list(range(1, 18)) + list(range(48, 48 + 239))
+    S, H, Hkv, N = 2, 16, 4, 320
+    x = make_inputs(S, H, Hkv, N, offsets, 17, seed=81, dtype=torch.bfloat16, gain_std=6.0)
+    pos = torch.tensor([319, 200], dtype=torch.int32)
+    qp, kp = orthogonal_probes(64, 0)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    cache = pkg.q6.pack_kv(x["k"].to(device), x["v"].to(device), kp.to(device))
+    qdec = torch.stack([x["q"][s, :, int(pos[s])] for s in range(S)]).unsqueeze(1)   # [S,1,H,64]
+    tab = {n: x[n].unsqueeze(0).to(device) for n in ("pos_bias", "scale_embed", "phase_base", "phase_gain")}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_decode(qdec.to(device), pos.to(device), cache.unsqueeze(0), tab["pos_bias"], tab["scale_embed"],
+                           tab["phase_base"], tab["phase_gain"], qp.unsqueeze(0).to(device), off, 17, 239, 0).cpu()
+    ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, 0, qp, kp, 0)
+    for s in range(S):
+        assert max_abs(out[s, 0], ref[s, :, int(pos[s])]) < 2e-2, s
