@@ -222,3 +222,18 @@ def test_decode_maximum_sizes(pkg, device):
     ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, 0, qp, kp, 0)
     for s in range(S):
         assert max_abs(out[s, 0], ref[s, :, int(pos[s])]) < 2e-2, s
+
+
+def test_prefill_maximum_offsets(pkg, device):
+    """J = 256 offsets (17 near, 239 far) in the prefill, against the oracle on the dequantised cache."""
+    offsets = list(range(1, 18)) + list(range(48, 48 + 239))
+    x = make_inputs(1, 4, 2, 320, offsets, 17, seed=83, dtype=torch.bfloat16, gain_std=6.0)
+    qp, kp = orthogonal_probes(64, 0)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    xd = {n: t.to(device) for n, t in x.items()}
+    cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"], xd["phase_gain"],
+                            qp.to(device), off, 17, 239, 0, 1)
+    ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, 0, qp, kp, 1)
+    assert max_abs(out, ref) < 2e-2
