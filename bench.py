@@ -413,7 +413,9 @@ def main() -> int:
         extra["long_context"] = long_context_extra(pkg, device, max(3, args.steps // 4), 2)
         log("phase-probe features: q of the training microbatch")
         extra["phase_probe"] = phase_probe_extra(pkg, device, args.steps, args.warmup)
+        log("NPCI rotation: k of the training microbatch")
         extra["npci"] = npci_extra(pkg, device, args.steps, args.warmup)
+        log("InterferencePacket pool: x [15,2048,512], three timescales")
         extra["packet"] = packet_extra(pkg, device, args.steps, args.warmup)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
