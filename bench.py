@@ -141,7 +141,8 @@ def cpu_baseline(pkg):
                        f"runs: {dt:.2f} s each; {cpu}")}
 
 
-def q6_decode_extra(pkg, device, steps, warmup):
+def decode_workload(pkg, device):
+    """The cfg5 decode step's inputs: 256 sequences x 9 layers x H8, q6 caches of length 2048 (seeded)."""
     S, L, H, N = 256, 9, 8, 2048
     offsets = list(pkg.ALL_OFFSETS)
     J, js = len(offsets), 17
@@ -154,17 +155,28 @@ def q6_decode_extra(pkg, device, steps, warmup):
     pgain = (0.64 * torch.randn(L, J - js, H, 4, generator=g)).to(device)
     qp, kp = pkg._orthogonal_phase_probes(4, 64, 0)
     qpn = torch.nn.functional.normalize(qp, dim=-1)
-    kpn = torch.nn.functional.normalize(kp, dim=-1).to(device)
+    kpn = torch.nn.functional.normalize(kp, dim=-1)
     caches = torch.empty((L, S, H, N, 128), dtype=torch.uint8, device=device)
     gd = torch.Generator(device=device).manual_seed(1)
     for l in range(L):
         k = torch.randn(S, H, N, 64, generator=gd, device=device, dtype=torch.bfloat16)
         v = torch.randn(S, H, N, 64, generator=gd, device=device, dtype=torch.bfloat16)
-        caches[l] = pkg.q6.pack_kv(k, v, kpn)
+        caches[l] = pkg.q6.pack_kv(k, v, kpn.to(device))
         del k, v
-    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    return dict(S=S, L=L, H=H, N=N, offsets=offsets, js=js, pos=pos, qdec=qdec, pos_bias=pb, scale_embed=se,
+                phase_base=pbase, phase_gain=pgain, qpn=qpn, kpn=kpn, caches=caches,
+                off=torch.tensor(offsets, dtype=torch.int32, device=device),
+                qps=torch.stack([qpn] * L).to(device))
+
+
+def q6_decode_extra(pkg, device, steps, warmup):
+    w = decode_workload(pkg, device)
+    S, L, H, offsets, js, pos = w["S"], w["L"], w["H"], w["offsets"], w["js"], w["pos"]
+    J = len(offsets)
+    qdec, pb, se, pbase, pgain, caches = (w[n] for n in ("qdec", "pos_bias", "scale_embed", "phase_base",
+                                                         "phase_gain", "caches"))
+    off, qps = w["off"], w["qps"]
     posd = pos.to(device)
-    qps = torch.stack([qpn] * L).to(device)
 
     def run():
         return pkg.q6.q6_decode(qdec, posd, caches, pb, se, pbase, pgain, qps, off, js, J - js, 0)
