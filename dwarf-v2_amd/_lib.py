@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "dwarf_dsqg_q6_prefill_fwd",
     "dwarf_dsqg_q6_decode",
     "dwarf_dsqg_q6_decode_workspace_bytes",
+    "dwarf_dsqg_q6_decode_noalloc",
     "dwarf_phase_probe_fwd",
     "dwarf_phase_probe_bwd_workspace_bytes",
     "dwarf_phase_probe_bwd",
@@ -297,6 +298,8 @@ def load() -> ctypes.CDLL:
     lib.dwarf_dsqg_q6_prefill_fwd.argtypes = [POINTER(Q6PrefillArgs), c_void_p]
     lib.dwarf_dsqg_q6_decode.restype = c_int
     lib.dwarf_dsqg_q6_decode.argtypes = [POINTER(Q6DecodeArgs), c_void_p]
+    lib.dwarf_dsqg_q6_decode_noalloc.restype = c_int
+    lib.dwarf_dsqg_q6_decode_noalloc.argtypes = [POINTER(Q6DecodeArgs), c_void_p]
     lib.dwarf_phase_probe_fwd.restype = c_int
     lib.dwarf_phase_probe_fwd.argtypes = [POINTER(PhaseProbeFwdArgs), c_void_p]
     lib.dwarf_phase_probe_bwd_workspace_bytes.restype = c_size_t

@@ -21,7 +21,8 @@ hipError_t launch_q6_pack(int B, int Hkv, int N, int dtype, const void* k, const
 hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const int64_t* cs, float* kout,
                             float* vout, hipStream_t stream);
 hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream);
-hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream);
+hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, float* table, hipStream_t stream);
+hipError_t q6_decode_scratch(float** ptr);
 size_t q6_decode_workspace(const dwarf_dsqg_q6_decode_args& a);
 int q6_max_decode_offsets();
 int q6_max_decode_heads();
@@ -523,9 +524,8 @@ size_t dwarf_dsqg_q6_decode_workspace_bytes(const dwarf_dsqg_q6_decode_args* arg
   return dwarf::q6_decode_workspace(*args);
 }
 
-int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t stream) {
-  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
-  const dwarf_dsqg_q6_decode_args& a = *args;
+// Shapes and limits of the decode step (no pointer is dereferenced here).
+static int check_decode_shape(const dwarf_dsqg_q6_decode_args& a) {
   if (a.S < 0 || a.L < 0 || a.Ncache < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes");
   int rc = check_lattice(a.H, a.H_kv, a.Ncache, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, 0);
   if (rc) return rc;
@@ -535,6 +535,12 @@ int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t s
     return fail(DWARF_ERR_UNSUPPORTED, "decode runs one wave per head: at most %d heads", dwarf::q6_max_decode_heads());
   if (static_cast<int64_t>(a.Ncache) * DWARF_Q6_SLOT_BYTES >= (int64_t(1) << 31))
     return fail(DWARF_ERR_UNSUPPORTED, "decode gathers with 32-bit offsets: Ncache x 128 B must stay below 2 GiB");
+  return DWARF_OK;
+}
+
+// Pointers, strides and table layouts of the decode step.
+static int check_decode_args(const dwarf_dsqg_q6_decode_args& a) {
+  int rc;
   if ((rc = check_rows("q", a.q, a.q_stride, 3, DWARF_BF16))) return rc;
   if ((rc = check_rows("out", a.out, a.out_stride, 3, DWARF_BF16))) return rc;
   if ((rc = check_cache(a.cache, a.cache_stride, 3))) return rc;
@@ -546,12 +552,41 @@ int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t s
   if (a.pbase_stride[1] < 0 || a.pgain_stride[1] < 0 ||
       (a.pbase_stride[1] + a.pgain_stride[1] + DWARF_R_PLANES) * 4 * static_cast<int64_t>(a.J_large) >= (int64_t(1) << 31))
     return fail(DWARF_ERR_UNSUPPORTED, "decode reads a head's phase tables with 32-bit offsets (span below 2 GiB)");
+  return DWARF_OK;
+}
+
+int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_dsqg_q6_decode_args& a = *args;
+  int rc;
+  if ((rc = check_decode_shape(a)) || (rc = check_decode_args(a))) return rc;
   if (a.S == 0 || a.L == 0) return ok();
   const size_t need = dwarf::q6_decode_workspace(a);
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
   if (!aligned16(a.workspace)) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
-  return hip_status(dwarf::launch_q6_decode(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_q6_decode");
+  return hip_status(dwarf::launch_q6_decode(a, static_cast<float*>(a.workspace), reinterpret_cast<hipStream_t>(stream)),
+                    "dwarf_dsqg_q6_decode");
+}
+
+int dwarf_dsqg_q6_decode_noalloc(const dwarf_dsqg_q6_decode_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_dsqg_q6_decode_args& a = *args;
+  int rc;
+  if ((rc = check_decode_shape(a))) return rc;
+  const size_t need = dwarf::q6_decode_workspace(a);
+  if (need > DWARF_Q6_DECODE_SCRATCH_BYTES)
+    return fail(DWARF_ERR_UNSUPPORTED,
+                "no-allocation decode: the score table needs %zu bytes (S*L*H*JE fp32), above the %zu-byte "
+                "device array; use dwarf_dsqg_q6_decode with a workspace", need,
+                static_cast<size_t>(DWARF_Q6_DECODE_SCRATCH_BYTES));
+  if ((rc = check_decode_args(a))) return rc;
+  if (a.S == 0 || a.L == 0) return ok();
+  float* table = nullptr;
+  const hipError_t e = dwarf::q6_decode_scratch(&table);
+  if (e != hipSuccess) return hip_status(e, "dwarf_dsqg_q6_decode_noalloc (device array address)");
+  return hip_status(dwarf::launch_q6_decode(a, table, reinterpret_cast<hipStream_t>(stream)),
+                    "dwarf_dsqg_q6_decode_noalloc");
 }
 
 }  // extern "C"

@@ -13,6 +13,8 @@
 //   [104,120) z[4] fp32 (key-probe features of the dequantised K row)
 //   [120,128) zero
 // A gathered offset therefore reads exactly one 128-byte line.
+#include <mutex>
+
 #include "common.h"
 #include "dsqg_internal.h"
 #include "gather.h"
@@ -827,9 +829,8 @@ size_t q6_decode_workspace(const dwarf_dsqg_q6_decode_args& a) {
   return static_cast<size_t>(a.S) * a.L * a.H * dec_layout(a.J, a.H).JE * sizeof(float);
 }
 
-hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stream) {
+hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, float* T, hipStream_t stream) {
   const DecLayout lay = dec_layout(a.J, a.H);
-  float* T = static_cast<float*>(a.workspace);
   const int table_blocks = a.L * ((a.S * a.H + kTabRows - 1) / kTabRows);
   hipLaunchKernelGGL(q6_decode_table, dim3(table_blocks), dim3(kBlock), dec_table_lds(lay.JE, a.H, !a.se_round_bf16),
                      stream, a, T, lay.JE);
@@ -849,5 +850,39 @@ hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, hipStream_t stre
 
 int q6_max_decode_offsets() { return 256; }
 int q6_max_decode_heads() { return kMaxDecHeads; }
+
+}  // namespace dwarf
+
+// ---------------------------------------------------------------------------
+// Score table of the no-allocation decode step: a file-scope device array,
+// one copy per GPU, held from module load until the process ends.  In host
+// code `scratch` names a host-side stand-in, not device memory: its device
+// address comes from hipGetSymbolAddress, looked up once per device (with
+// that device current) and kept per device.  Every no-allocation decode on a
+// GPU uses that GPU's one copy, so calls that overlap on one GPU race; each
+// call rewrites every table entry it reads, so nothing needs clearing.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[DWARF_Q6_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+namespace dwarf {
+
+hipError_t q6_decode_scratch(float** ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static float* addr[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev] = static_cast<float*>(p);
+  }
+  *ptr = addr[dev];
+  return hipSuccess;
+}
 
 }  // namespace dwarf

@@ -125,17 +125,10 @@ def q6_prefill(q, cache, pos_bias, scale_embed, phase_base, phase_gain, query_pr
     return (out, lse) if return_lse else out
 
 
-def q6_decode(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, query_probes, offsets_dev,
-              j_small, j_large, plane_shift=0, round_se=True):
-    """One decode step over L layers.
-
-    q [S,L,H,64] bf16 (one new query per sequence and layer), pos [S] int32
-    positions, caches [L,S,Hkv,Ncache,128] uint8, per-layer tables with a
-    leading L dimension: pos_bias [L,J,H], scale_embed [L,J,64], phase_base /
-    phase_gain [L,J_L,H,4], query_probes [L,4,64] (normalised).  Returns
-    out [S,L,H,64] bf16.  round_se rounds scale_embed to bf16 as the GPU path
-    does (dsqg:760-763); False keeps it in fp32 (bf16 hi + lo on the MFMA).
-    """
+def _decode_args(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, query_probes, offsets_dev,
+                 j_small, j_large, plane_shift, round_se, out):
+    """Validated tensors and the filled Q6DecodeArgs of one decode step (the tensors are returned so that
+    they outlive the call)."""
     if not q.is_cuda:
         raise RuntimeError("the q6 HIP kernels require device tensors")
     q = _rows(q.to(torch.bfloat16))
@@ -150,7 +143,10 @@ def q6_decode(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, que
     phase_gain = phase_gain.float().contiguous()
     qp = query_probes.float().contiguous()
     offsets = offsets_dev.to(device=q.device, dtype=torch.int32).contiguous()
-    out = torch.empty((S, L, H, HD), device=q.device, dtype=torch.bfloat16)
+    if out is None:
+        out = torch.empty((S, L, H, HD), device=q.device, dtype=torch.bfloat16)
+    elif out.shape != (S, L, H, HD) or out.dtype != torch.bfloat16 or out.device != q.device:
+        raise ValueError(f"out must be a bf16 [{S},{L},{H},{HD}] tensor on {q.device}")
     a = _lib.Q6DecodeArgs()
     a.S, a.L, a.H, a.H_kv, a.Ncache, a.head_dim = S, L, H, caches.shape[2], caches.shape[3], HD
     a.J, a.J_small, a.J_large = int(j_small) + int(j_large), int(j_small), int(j_large)
@@ -166,10 +162,42 @@ def q6_decode(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, que
     a.query_probes, a.qprobe_layer_stride = qp.data_ptr(), qp.stride(0)
     a.offsets = offsets.data_ptr()
     a.out, a.out_stride = out.data_ptr(), _p64(out.stride())
+    keep = (q, caches, pos, pos_bias, scale_embed, phase_base, phase_gain, qp, offsets)
+    return a, out, keep
+
+
+def q6_decode(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, query_probes, offsets_dev,
+              j_small, j_large, plane_shift=0, round_se=True):
+    """One decode step over L layers.
+
+    q [S,L,H,64] bf16 (one new query per sequence and layer), pos [S] int32
+    positions, caches [L,S,Hkv,Ncache,128] uint8, per-layer tables with a
+    leading L dimension: pos_bias [L,J,H], scale_embed [L,J,64], phase_base /
+    phase_gain [L,J_L,H,4], query_probes [L,4,64] (normalised).  Returns
+    out [S,L,H,64] bf16.  round_se rounds scale_embed to bf16 as the GPU path
+    does (dsqg:760-763); False keeps it in fp32 (bf16 hi + lo on the MFMA).
+    """
+    a, out, keep = _decode_args(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, query_probes,
+                                offsets_dev, j_small, j_large, plane_shift, round_se, None)
     lib = _lib.load()
-    ws = torch.empty(max(int(lib.dwarf_dsqg_q6_decode_workspace_bytes(ctypes.byref(a))), 16), device=q.device,
+    ws = torch.empty(max(int(lib.dwarf_dsqg_q6_decode_workspace_bytes(ctypes.byref(a))), 16), device=out.device,
                      dtype=torch.uint8)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    _lib.check(lib.dwarf_dsqg_q6_decode(ctypes.byref(a), torch.cuda.current_stream(q.device).cuda_stream),
+    _lib.check(lib.dwarf_dsqg_q6_decode(ctypes.byref(a), torch.cuda.current_stream(out.device).cuda_stream),
                "dwarf_dsqg_q6_decode")
+    del keep
+    return out
+
+
+def q6_decode_noalloc(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, query_probes, offsets_dev,
+                      j_small, j_large, plane_shift=0, round_se=True, *, out=None):
+    """q6_decode through dwarf_dsqg_q6_decode_noalloc: the library allocates nothing (its score table is a
+    per-GPU device array of 16 MiB, so S*L*H*JE fp32 must fit; concurrent calls on one GPU race).  Pass
+    ``out`` (bf16 [S,L,H,64]) and already-normalised tensors to keep the whole call free of allocation."""
+    a, out, keep = _decode_args(q, pos, caches, pos_bias, scale_embed, phase_base, phase_gain, query_probes,
+                                offsets_dev, j_small, j_large, plane_shift, round_se, out)
+    lib = _lib.load()
+    _lib.check(lib.dwarf_dsqg_q6_decode_noalloc(ctypes.byref(a), torch.cuda.current_stream(out.device).cuda_stream),
+               "dwarf_dsqg_q6_decode_noalloc")
+    del keep
     return out

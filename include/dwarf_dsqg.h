@@ -23,10 +23,11 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 3
+#define DWARF_ABI_VERSION 4
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
+#define DWARF_Q6_DECODE_SCRATCH_BYTES (16u << 20) /* per-GPU score table of dwarf_dsqg_q6_decode_noalloc */
 
 typedef struct ihipStream_t* dwarf_stream_t; /* == hipStream_t */
 
@@ -422,6 +423,21 @@ size_t dwarf_dsqg_q6_decode_workspace_bytes(const dwarf_dsqg_q6_decode_args* arg
 
 int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args,
                          dwarf_stream_t stream);
+
+/*
+ * The decode step without allocation: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments and results
+ * as dwarf_dsqg_q6_decode, except that args->workspace is ignored: the score
+ * table lives in a file-scope device array of DWARF_Q6_DECODE_SCRATCH_BYTES
+ * (16 MiB) per GPU, held until the process ends.  Returns DWARF_ERR_UNSUPPORTED
+ * when dwarf_dsqg_q6_decode_workspace_bytes(args) exceeds that size (S*L*H*JE
+ * fp32 <= 4 Mi floats, e.g. 512 sequences x 9 layers x 8 heads at J = 96).
+ * Calls no allocating routine.  All calls on one GPU share its array: calls
+ * that overlap on one GPU (two streams, two threads) race.
+ */
+int dwarf_dsqg_q6_decode_noalloc(const dwarf_dsqg_q6_decode_args* args,
+                                 dwarf_stream_t stream);
 
 #ifdef __cplusplus
 }

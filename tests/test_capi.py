@@ -29,7 +29,7 @@ def lib(pkg):
 
 def test_exports_every_declared_symbol(pkg, lib):
     names = declared_functions()
-    assert len(names) == 28
+    assert len(names) == 29
     assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
     for name in names:
         assert hasattr(lib, name), name
@@ -106,6 +106,14 @@ def test_validation_errors_without_gpu(pkg, lib):
     assert b"heads" in lib.dwarf_last_error()
     d.S, d.L, d.H, d.H_kv = 3, 2, 8, 8   # the T table: S*L*H rows of JE = 112 fp32 at J = 96
     assert lib.dwarf_dsqg_q6_decode_workspace_bytes(ctypes.byref(d)) == 3 * 2 * 8 * 112 * 4
+    # the no-allocation decode keeps the table in a 16 MiB device array: 4,681 x 1 x 8 x 112 fp32 fit
+    # (16,776,704 bytes), one sequence more does not; rejected before any pointer or HIP call
+    d.S, d.L = 4682, 1
+    assert lib.dwarf_dsqg_q6_decode_noalloc(ctypes.byref(d), None) == L.DWARF_ERR_UNSUPPORTED
+    assert b"16777216-byte device array" in lib.dwarf_last_error()
+    d.S = 4681
+    assert lib.dwarf_dsqg_q6_decode_noalloc(ctypes.byref(d), None) == L.DWARF_ERR_INVALID_ARGUMENT   # q is NULL
+    assert lib.dwarf_dsqg_q6_decode_noalloc(None, None) == L.DWARF_ERR_INVALID_ARGUMENT
     p = L.PhaseProbeFwdArgs()
     p.B, p.H, p.N, p.head_dim, p.R, p.end = 1, 1, 8, 32, 4, 8
     assert lib.dwarf_phase_probe_fwd(ctypes.byref(p), None) == L.DWARF_ERR_UNSUPPORTED   # head_dim 64 only

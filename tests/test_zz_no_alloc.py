@@ -1,0 +1,53 @@
+"""The no-allocation decode entry point (dwarf_dsqg_q6_decode_noalloc) against the decode step with a
+workspace (dwarf_dsqg_q6_decode), through the C ABI on an MI355X.
+
+Both run the same two kernels on the same inputs; only where the score table lives differs (a per-GPU
+device array instead of the caller's workspace), so the outputs must be equal bit for bit.  Two calls in a
+row, the second with fewer sequences and a different lattice, check that the array keeps no state that
+leaks from one call into the next.
+"""
+
+import pytest
+import torch
+
+from tests.dsqg_cases import make_inputs, orthogonal_probes
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(pkg, device, S, L, H, Hkv, N, offsets, j_small, seed, shift):
+    layers = [make_inputs(S, H, Hkv, N, offsets, j_small, seed=seed + l, dtype=torch.bfloat16, plane_shift=shift,
+                          gain_std=6.0) for l in range(L)]
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.randint(0, N, (S,), generator=g, dtype=torch.int32)
+    qp, kp = orthogonal_probes(64, shift)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    caches = torch.stack([pkg.q6.pack_kv(x["k"].to(device), x["v"].to(device), kp.to(device)) for x in layers])
+    qdec = torch.stack([torch.stack([layers[l]["q"][s, :, int(pos[s])] for l in range(L)]) for s in range(S)])
+    tabs = {n: torch.stack([x[n] for x in layers]).to(device)
+            for n in ("pos_bias", "scale_embed", "phase_base", "phase_gain")}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    return (qdec.to(device), pos.to(device), caches, tabs["pos_bias"], tabs["scale_embed"], tabs["phase_base"],
+            tabs["phase_gain"], torch.stack([qp] * L).to(device), off, j_small, len(offsets) - j_small, shift)
+
+
+def test_noalloc_decode_matches_workspace_decode(pkg, device):
+    lattice = list(pkg.ALL_OFFSETS)
+    cases = [
+        # (S, L, H, Hkv, N, offsets, j_small, seed, shift): the second call is smaller
+        (6, 3, 8, 2, 700, lattice, 17, 11, 3),
+        (3, 2, 4, 4, 300, lattice[:40], 17, 29, 0),
+    ]
+    for S, L, H, Hkv, N, offsets, js, seed, shift in cases:
+        args = _case(pkg, device, S, L, H, Hkv, N, offsets, js, seed, shift)
+        ref = pkg.q6.q6_decode(*args)
+        out = torch.full_like(ref, float("nan"))
+        got = pkg.q6.q6_decode_noalloc(*args, out=out)
+        torch.cuda.synchronize()
+        assert got.data_ptr() == out.data_ptr()
+        assert torch.equal(got, ref), (S, L, H, N)
+        # fp32 scale embeddings (a second MFMA pass over the table) through the same array
+        ref32 = pkg.q6.q6_decode(*args, round_se=False)
+        got32 = pkg.q6.q6_decode_noalloc(*args, round_se=False)
+        torch.cuda.synchronize()
+        assert torch.equal(got32, ref32), (S, L, H, N)
