@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -79,7 +79,12 @@ class DsqgFwdArgs(ctypes.Structure):
         ("offsets", c_void_p),
         ("out", c_void_p), ("out_stride", _i64(4)),
         ("lse", c_void_p), ("lse_stride", _i64(3)),
+        ("schedule", c_int32),
     ]
+
+
+DWARF_SCHED_BAND = 1
+DWARF_SCHED_TWO_PASS = 2
 
 
 class DsqgBwdArgs(ctypes.Structure):

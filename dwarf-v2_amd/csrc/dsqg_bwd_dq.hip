@@ -546,23 +546,37 @@ constexpr int kGatherWgsPerCu = 3;
 __host__ __device__ constexpr int dse_blocks_per_wave(int J) { return (J + 1 + 15) / 16 <= 8 ? 2 : 5; }
 __host__ __device__ constexpr int dse_wgs_per_cu(int mbw) { return mbw <= 2 ? 4 : 2; }
 
+// Near band: the leading small offsets j < JB (ascending, unique, at most
+// kBandMax) are served from a K window [n0 - kBandMax, n0 + 64) in LDS on the
+// matrix cores (dsqg_bwd_dq_bf16_g4); the gather loop takes the others.
+constexpr int kBandMax = 32;                    // largest band offset; the window's look-back
+constexpr int kWinRows = kQT + kBandMax;        // 96 K rows of 128 bytes
+constexpr int kBandSlots = 32;                  // band scratch columns per query
+
 struct DqG4Layout {
-  int JE, JL4, list_len;
-  size_t off_ph, off_list, off_dph, off_e, off_st, bytes;
+  int JE, JL4, list_len, dphw;
+  size_t off_ph, off_list, off_dph, off_e, off_jn, off_st, bytes;
 };
 
-// JE >= J + 1 keeps a sentinel row J of zeros in the E table.
+// JE >= J + 1 keeps a sentinel row J of zeros in the E table.  A wave's dPhase
+// table doubles as its band scratch [16][32] fp32 at the start of a tile (it
+// is cleared after the band); the last region holds the K window [96][128 B]
+// at the start of a tile and the dQe staging [4][16][36] fp32 at its end.
 __host__ __device__ inline DqG4Layout dq_g4_layout(int J, int J_large) {
   DqG4Layout L;
   L.JE = (J + 1 + 15) / 16 * 16;
   L.JL4 = (J_large + 1) / 2 * 2;
   L.list_len = (L.JE + 2 * kStepDq + 1) / 2 * 2;   // list + padding for the last step and its prefetch
+  L.dphw = L.JL4 * 8 > kQPW * kBandSlots ? L.JL4 * 8 : kQPW * kBandSlots;
   L.off_ph = static_cast<size_t>(2 * L.JE) * 4;                       // s_pb2[JE], s_off[JE]
   L.off_list = L.off_ph + static_cast<size_t>(L.JL4) * 4 * 8;         // s_ph[JL4][4] float2
   L.off_dph = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;   // s_list[4][list_len] int2
-  L.off_e = L.off_dph + static_cast<size_t>(4 * L.JL4) * 8 * 4;       // s_dph[4][JL4][8]
-  L.off_st = L.off_e + static_cast<size_t>(L.JE) * kERowT * 2;        // sE[JE][72] bf16
-  L.bytes = L.off_st + static_cast<size_t>(4 * kQPW * kStRow) * 4;    // dQe staging [4][16][36]
+  L.off_e = L.off_dph + static_cast<size_t>(4 * L.dphw) * 4;          // s_dph[4][dphw]
+  L.off_jn = L.off_e + static_cast<size_t>(L.JE) * kERowT * 2;        // sE[JE][72] bf16
+  L.off_st = L.off_jn + 16 * 9;                                        // s_jn[kBandMax + 1] int (+ pad)
+  const size_t st = static_cast<size_t>(4 * kQPW * kStRow) * 4;
+  const size_t win = static_cast<size_t>(kWinRows) * 128;
+  L.bytes = L.off_st + (st > win ? st : win);
   return L;
 }
 
@@ -619,9 +633,24 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
   float* s_dph_all = reinterpret_cast<float*>(sm + lay.off_dph);
   uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
   float* s_st_all = reinterpret_cast<float*>(sm + lay.off_st);
+  int* s_jn = reinterpret_cast<int*>(sm + lay.off_jn);       // [0]: JB; [d]: band slot of offset d, or -1
+  char* s_win = sm + lay.off_st;                              // K window [96][128 B] (aliases the dQe staging)
 
   stage_se_bf16(f.scale_embed, f.se_stride, J, lay.JE, sE, kERowT);
   for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // the band: the leading small offsets while they ascend and stay <= kBandMax
+    for (int d = 1; d <= kBandMax; ++d) s_jn[d] = -1;
+    int jb = 0;
+    while ((f.schedule & DWARF_SCHED_BAND) && jb < J_small && jb < kBandSlots) {
+      const int d = s_off[jb];
+      if (d < 1 || d > kBandMax || (jb > 0 && d <= s_off[jb - 1])) break;
+      s_jn[d] = jb++;
+    }
+    s_jn[0] = jb;
+  }
+  __syncthreads();   // s_jn is read in every tile's prologue
 
   const int lane = threadIdx.x;
   const int w = lane / kWave;
@@ -630,7 +659,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
   const int qi = l >> 2;
   const int lr = l & 15, lc = l >> 4;
   int2* s_list = s_list_all + w * lay.list_len;
-  float* s_dph = s_dph_all + w * lay.JL4 * 8;
+  float* s_dph = s_dph_all + w * lay.dphw;
   float* s_st = s_st_all + w * kQPW * kStRow;
   const int ks_b = static_cast<int>(f.k_stride[2]) * 2, vs_b = static_cast<int>(f.v_stride[2]) * 2;
   const int zs_b = static_cast<int>(f.z_stride[2]) * 4;
@@ -707,8 +736,21 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     const int zb_lane = n_eff * zs_b + 4 * g;
     const uint32_t ds_lane = row_ok ? static_cast<uint32_t>(4 * n) : kOutOfRange;
 
-    __syncthreads();   // the previous tile's dPhase tables have been read
-    for (int i = lane; i < 4 * lay.JL4 * 8; i += kBlock) s_dph_all[i] = 0.f;
+    __syncthreads();   // the previous tile's dPhase tables and dQe staging have been read
+    const int JB = s_jn[0];
+    if (JB > 0) {
+      // K rows [n0 - kBandMax, n0 + 64) into the window: three 1 KB DMA loads per wave; LDS chunk
+      // (i & 7) of row i >> 3 holds the row's 16-byte chunk (i & 7) ^ (row & 7) (bank spread)
+      typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        const int i = kBlock * u + lane;
+        const int row = i >> 3, c = (i & 7) ^ (row & 7);
+        const int key = t * kQT - kBandMax + row;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(void*)(s_win + 4096 * u + 1024 * w), 16,
+                                                 static_cast<uint32_t>(key * ks_b + 16 * c), 0, 0, 0);
+      }
+    }
     if (h != cur_h) {
       cur_h = h;
       for (int j = lane; j < lay.JE; j += kBlock)
@@ -721,12 +763,156 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     }
     int cnt = 0;
     // padded with the sentinel to a multiple of 4 plus 4: every step's reads and the next prefetch
-    if (n0w < N) cnt = build_offset_list<kStepDq / 2>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N));
-    __syncthreads();   // tables staged, dPhase tables cleared
+    if (n0w < N)
+      cnt = build_offset_list<kStepDq / 2>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N), JB);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's window loads have landed
+    __syncthreads();   // tables and the K window staged
+
+    // ---- near band (offsets j < JB) on the matrix cores ----
+    // Band lane (lc, lr) serves query n0w + lr; in the MFMA C layout it holds
+    // keys 16 t + 4 lc + r of the wave's key blocks t = 0..2 (keys
+    // [n0w - 32, n0w + 16)), and its dQ result dims 16 lc + [0, 16).
+    //   S^T  = K_win Q^T, dP^T = V dO^T     (v_mfma_f32_16x16x32_bf16)
+    //   P = exp2(S' - lse), dS = P (dP - delta) on the band's diagonals
+    //   dQ^T += K_win^T dS^T + E^T dS^T     (v_mfma_f32_16x16x16_bf16, dS as bf16 hi + lo)
+    float* scr = s_dph;   // this wave's band scratch [16 queries][32 slots] (cleared below)
+    float bandq[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) bandq[i] = 0.f;
+    if (JB > 0 && n0w < N) {
+      const int src4 = 4 * (4 * lr);                     // gather-layout lane of query n0w + lr
+      const float dl_b = __int_as_float(__builtin_amdgcn_ds_bpermute(src4, __float_as_int(dlt)));
+      const float ls_b = __int_as_float(
+          __builtin_amdgcn_ds_bpermute(src4, __float_as_int(row_ok && mass ? lse2 : INFINITY)));
+      uint4 xd[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+      if (n0w + lr < N) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          xd[ks] = *reinterpret_cast<const uint4*>(dob + static_cast<int64_t>(n0w + lr) * a.dout_stride[2] + 32 * ks +
+                                                   8 * lc);
+      }
+      auto win16 = [&](int row, int c) { return s_win + row * 128 + 16 * (c ^ (row & 7)); };
+      // band slot of the pair (query n0w + lr, key n0w - 32 + 16 tb + 4 lc + r), or -1
+      auto band_slot = [&](int tb, int r) {
+        const int delta = lr + kBandMax - 16 * tb - 4 * lc - r;
+        const int slot = delta >= 1 && delta <= kBandMax ? s_jn[delta] : -1;
+        return n0w - kBandMax + 16 * tb + 4 * lc + r >= 0 ? slot : -1;
+      };
+      // <q, e_slot> of the band slots, into the scratch as [query][slot]
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        if (16 * bb < JB) {
+          f32x4 qe = zero4();
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const uint4 ea = *reinterpret_cast<const uint4*>(sE + (16 * bb + lr) * kERowT + 32 * ks + 8 * lc);
+            qe = mfma16_bf16(bf16x8_from_bits(ea), bf16x8_from_bits(xq[ks]), qe);
+          }
+          *reinterpret_cast<f32x4*>(scr + lr * kBandSlots + 16 * bb + 4 * lc) = qe;
+        }
+      }
+      float dsv[3][4];
+#pragma unroll
+      for (int tb = 0; tb < 3; ++tb) {
+        const int wr = 16 * (w + tb) + lr;               // window row of key n0w - 32 + 16 tb + lr
+        const uint4 ka0 = *reinterpret_cast<const uint4*>(win16(wr, lc));
+        const uint4 ka1 = *reinterpret_cast<const uint4*>(win16(wr, 4 + lc));
+        f32x4 S = mfma16_bf16(bf16x8_from_bits(ka0), bf16x8_from_bits(xq[0]), zero4());
+        S = mfma16_bf16(bf16x8_from_bits(ka1), bf16x8_from_bits(xq[1]), S);
+        const int key = n0w - kBandMax + 16 * tb + lr;   // before 0: out of range, zeros
+        const uint32_t vo = static_cast<uint32_t>(key * vs_b + 16 * lc);
+        const uint4 va0 = buf_load16(rv, vo), va1 = buf_load16(rv, vo + 64);
+        f32x4 Dp = mfma16_bf16(bf16x8_from_bits(va0), bf16x8_from_bits(xd[0]), zero4());
+        Dp = mfma16_bf16(bf16x8_from_bits(va1), bf16x8_from_bits(xd[1]), Dp);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int slot = band_slot(tb, r);
+          float ds = 0.f;
+          if (slot >= 0) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(S[r] + scr[lr * kBandSlots + slot], kC, s_pb2[slot]) - ls_b);
+            ds = p * (Dp[r] - dl_b);
+          }
+          dsv[tb][r] = ds;
+        }
+      }
+      // dS of the band into the scratch as [query][slot] (zeros where no pair)
+      __builtin_amdgcn_wave_barrier();
+      *reinterpret_cast<f32x4*>(scr + lr * kBandSlots + 8 * lc) = zero4();
+      *reinterpret_cast<f32x4*>(scr + lr * kBandSlots + 8 * lc + 4) = zero4();
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int tb = 0; tb < 3; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int slot = band_slot(tb, r);
+          if (slot >= 0) scr[lr * kBandSlots + slot] = dsv[tb][r];
+        }
+      __builtin_amdgcn_wave_barrier();
+      f32x4 acch[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acch[db] = zero4();
+      // dQ^T += K^T (c dS^T): K^T read transposed from the window (rows 16 (w + tb) + 4 lc + e, dims
+      // 16 (lr / 4) + 4 db + lr % 4 of MFMA row lr), c dS^T from the C layout of S^T as bf16 hi + lo
+#pragma unroll
+      for (int tb = 0; tb < 3; ++tb) {
+        float cd[4], cl[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          cd[r] = kScale * dsv[tb][r];
+          cl[r] = cd[r] - round_bf16(cd[r]);
+        }
+        const i16x4 bh = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(cd[0], cd[1]), pack_bf16x2(cd[2], cd[3])));
+        const i16x4 bl = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(cl[0], cl[1]), pack_bf16x2(cl[2], cl[3])));
+        const int R = 16 * (w + tb) + 4 * lc + (lr >> 2);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const i16x4 ak = lds_read_tr16(win16(R, 2 * (lr & 3) + (db >> 1)) + 8 * (db & 1));
+          acch[db] = mfma16k16_bf16(ak, bh, acch[db]);
+          acch[db] = mfma16k16_bf16(ak, bl, acch[db]);
+        }
+      }
+      // dQe of the band: E^T (c dS^T), E^T read transposed from the bf16 E table
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        if (16 * bb < JB) {
+          const f32x4 dsr = *reinterpret_cast<const f32x4*>(scr + lr * kBandSlots + 16 * bb + 4 * lc);
+          float cd[4], cl[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            cd[r] = kScale * dsr[r];
+            cl[r] = cd[r] - round_bf16(cd[r]);
+          }
+          const i16x4 bh = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(cd[0], cd[1]), pack_bf16x2(cd[2], cd[3])));
+          const i16x4 bl = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(cl[0], cl[1]), pack_bf16x2(cl[2], cl[3])));
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            const i16x4 ae = lds_read_tr16(sE + (16 * bb + 4 * lc + (lr >> 2)) * kERowT + 16 * (lr & 3) + 4 * db);
+            acch[db] = mfma16k16_bf16(ae, bh, acch[db]);
+            acch[db] = mfma16k16_bf16(ae, bl, acch[db]);
+          }
+        }
+      }
+      // the band's dS into the workspace matrix (query column n0w + lr, rows j = lc + 4 k)
+      for (int j = lc; j < JB; j += 4) {
+        const uint32_t off = n0w + lr < N ? static_cast<uint32_t>(4 * (j * N + n0w + lr)) : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(scr[lr * kBandSlots + j]), rds, off, 0, 0);
+      }
+      // into the gather layout: query qi, dims 16 g + i <- band lane (lc = g, lr = qi)
+      const int srcq = 4 * (qi + 16 * g);
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          bandq[4 * db + r] = __int_as_float(
+              __builtin_amdgcn_ds_bpermute(srcq, __float_as_int(acch[db][r])));
+      __builtin_amdgcn_wave_barrier();
+    }
+    for (int i = l; i < lay.dphw; i += kWave) scr[i] = 0.f;   // this wave's dPhase table
+    __builtin_amdgcn_wave_barrier();
 
     float dq[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) dq[i] = 0.f;
+    for (int i = 0; i < 16; ++i) dq[i] = bandq[i];
     float dy = 0.f;
     f32x4 dqe[4];
 #pragma unroll
@@ -880,8 +1066,8 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     __syncthreads();   // every wave's dPhase table is complete
     // dPhase of this tile: the four waves' sums in a fixed order
     for (int i = lane; i < JL * 8; i += kBlock)
-      part_ph[prow * JL * 8 + i] = ((s_dph_all[i] + s_dph_all[lay.JL4 * 8 + i]) + s_dph_all[2 * lay.JL4 * 8 + i]) +
-                                   s_dph_all[3 * lay.JL4 * 8 + i];
+      part_ph[prow * JL * 8 + i] = ((s_dph_all[i] + s_dph_all[lay.dphw + i]) + s_dph_all[2 * lay.dphw + i]) +
+                                   s_dph_all[3 * lay.dphw + i];
     // dQe rows move from the MFMA layout (query 4 lc + r, dim 16 nb + lr) to
     // the lane layout through the wave's staging area, half a row at a time
 #pragma unroll

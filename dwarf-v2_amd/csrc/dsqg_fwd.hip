@@ -23,7 +23,7 @@ namespace {
 
 constexpr float kRescaleSlack = 8.0f;
 
-template <typename T, int SHIFT, int L, bool FAST>
+template <typename T, int SHIFT, int L, bool FAST, bool TWO_PASS>
 __global__ __launch_bounds__(kBlock) void dsqg_fwd_kernel(const dwarf_dsqg_fwd_args a, int tiles, int total) {
   constexpr int HD = kHeadDim;
   constexpr int DPL = HD / L;     // head dims held by one lane
@@ -81,6 +81,25 @@ __global__ __launch_bounds__(kBlock) void dsqg_fwd_kernel(const dwarf_dsqg_fwd_a
     const float* zbase = a.z_pre + b * a.z_stride[0] + hk * a.z_stride[1];
     const float scale = 0.125f;  // 1/sqrt(64)
 
+    if constexpr (TWO_PASS) {
+      // offline softmax (dsqg:863-1044): the row maximum first, so the weighted sum never rescales
+      for (int j = 0; j < a.J; ++j) {
+        const int delta = s_off[j];
+        if (wave_n_last < delta) continue;
+        const int s = n - delta;
+        if (s < 0 || s >= a.N) continue;
+        float kv[DPL];
+        load_f32<T, DPL>(kbase + static_cast<int64_t>(s) * a.k_stride[2], kv);
+        const float* e = s_se + j * HD + g * DPL;
+        float dot = 0.f;
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) dot = fmaf(q[d], kv[d] + e[d], dot);
+        dot = group_sum<L>(dot);
+        const float score = fmaf(dot, scale, s_pb[j]);
+        if (score > m) m = score;
+      }
+    }
+
     for (int j = 0; j < a.J; ++j) {
       const int delta = s_off[j];
       if (wave_n_last < delta) continue;  // no lane of this wave has a source
@@ -116,7 +135,7 @@ __global__ __launch_bounds__(kBlock) void dsqg_fwd_kernel(const dwarf_dsqg_fwd_a
         }
       }
 
-      if (score > m + kRescaleSlack) {
+      if (!TWO_PASS && score > m + kRescaleSlack) {
         const float c = dexp<FAST>(m - score);  // 0 on the first valid offset
 #pragma unroll
         for (int d = 0; d < DPL; ++d) acc[d] *= c;
@@ -200,7 +219,7 @@ struct FwdChunk {
   int j[CJ];
 };
 
-template <int SHIFT, int CJ>
+template <int SHIFT, int CJ, bool TWO_PASS>
 __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_fwd_args a, int tiles, int total) {
   constexpr float kC = 0.125f * kLog2e;           // 1/sqrt(64) in base-2 score units
   constexpr float kSlack2 = 8.0f * kLog2e;        // kRescaleSlack in base 2
@@ -353,7 +372,7 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
       sc[jj] = c.ok[jj] ? s2 : -INFINITY;
       cmax = fmaxf(cmax, sc[jj]);
     }
-    if (cmax > m + kSlack2) {
+    if (!TWO_PASS && cmax > m + kSlack2) {
       const float f = __builtin_amdgcn_exp2f(m - cmax);   // 0 on the first valid chunk
 #pragma unroll
       for (int d = 0; d < 16; ++d) acc[d] *= f;
@@ -385,6 +404,25 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
     }
   };
 
+  if (TWO_PASS && cnt > 0) {
+    // offline softmax (dsqg:863-1044): each row's score maximum over the list first, so the
+    // weighted sum below never rescales (m stays the maximum; -3e38 for a row without sources)
+    float mx = -3.0e38f;
+    for (int k0 = 0; k0 < cnt; ++k0) {
+      const int2 e = s_list[k0];
+      const int j = uniform(e.x), d = uniform(e.y);
+      const uint32_t ko = static_cast<uint32_t>(kb_lane - d * ks_b);
+      const uint4 k0v = buf_load16(rk, ko), k1v = buf_load16(rk, ko + 16);
+      const uint32_t kw[8] = {k0v.x, k0v.y, k0v.z, k0v.w, k1v.x, k1v.y, k1v.z, k1v.w};
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dot = dot2bf(q32[i], kw[i], dot);
+      dot = group_sum<4>(dot);
+      const float s2 = fmaf(dot, kC, s_qe[qi * lay.qe_row + j]);
+      if (static_cast<uint32_t>(n_eff - d) < static_cast<uint32_t>(N)) mx = fmaxf(mx, s2);
+    }
+    m = mx;
+  }
   if (cnt > 0) {
     FwdChunk<CJ> c0, c1;
     fetch(0, c0);
@@ -416,14 +454,17 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
         lsum > 0.f ? (m + __builtin_amdgcn_logf(lsum)) * kLn2 : -INFINITY;
 }
 
-template <int CJ>
+template <int CJ, bool TWO_PASS>
 hipError_t launch_fwd_bf16_q4(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
   const int tiles = (a.N + kQPB - 1) / kQPB;
   const int total = tiles * a.B * a.H;
   if (total == 0) return hipSuccess;
   const size_t lds = fwd_layout(a.J, a.J_large, CJ).bytes;
-#define DWARF_FWDQ4_CASE(S) \
-  case S: hipLaunchKernelGGL((dsqg_fwd_bf16_q4<S, CJ>), dim3(total), dim3(kBlock), lds, stream, a, tiles, total); break;
+#define DWARF_FWDQ4_CASE(S)                                                                                     \
+  case S:                                                                                                       \
+    hipLaunchKernelGGL((dsqg_fwd_bf16_q4<S, CJ, TWO_PASS>), dim3(total), dim3(kBlock), lds, stream, a, tiles,   \
+                       total);                                                                                  \
+    break;
   switch (a.plane_shift) {
     DWARF_FWDQ4_CASE(0) DWARF_FWDQ4_CASE(1) DWARF_FWDQ4_CASE(2) DWARF_FWDQ4_CASE(3) DWARF_FWDQ4_CASE(4)
     DWARF_FWDQ4_CASE(5) DWARF_FWDQ4_CASE(6) DWARF_FWDQ4_CASE(7) DWARF_FWDQ4_CASE(8) DWARF_FWDQ4_CASE(9)
@@ -434,7 +475,7 @@ hipError_t launch_fwd_bf16_q4(const dwarf_dsqg_fwd_args& a, hipStream_t stream) 
   return hipGetLastError();
 }
 
-template <typename T, int L, bool FAST>
+template <typename T, int L, bool FAST, bool TWO_PASS>
 hipError_t launch_shift(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
   constexpr int QPB = kBlock / L;
   const int tiles = (a.N + QPB - 1) / QPB;
@@ -442,7 +483,7 @@ hipError_t launch_shift(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(a.J) * (kHeadDim + 2) * sizeof(float);
 #define DWARF_FWD_CASE(S)                                                                        \
   case S:                                                                                        \
-    hipLaunchKernelGGL((dsqg_fwd_kernel<T, S, L, FAST>), dim3(total), dim3(kBlock), lds, \
+    hipLaunchKernelGGL((dsqg_fwd_kernel<T, S, L, FAST, TWO_PASS>), dim3(total), dim3(kBlock), lds, \
                        stream, a, tiles, total);                                                 \
     break;
   switch (a.plane_shift) {
@@ -459,8 +500,10 @@ hipError_t launch_shift(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_dsqg_fwd(const dwarf_dsqg_fwd_args& a, hipStream_t stream) {
-  if (a.dtype == DWARF_BF16) return launch_fwd_bf16_q4<kChunkFwd>(a, stream);
-  return launch_shift<float, 2, false>(a, stream);
+  const bool two_pass = (a.schedule & DWARF_SCHED_TWO_PASS) != 0;
+  if (a.dtype == DWARF_BF16)
+    return two_pass ? launch_fwd_bf16_q4<kChunkFwd, true>(a, stream) : launch_fwd_bf16_q4<kChunkFwd, false>(a, stream);
+  return two_pass ? launch_shift<float, 2, false, true>(a, stream) : launch_shift<float, 2, false, false>(a, stream);
 }
 
 }  // namespace dwarf

@@ -71,18 +71,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, in
 // Appends to `list` (wave-private LDS) the (index, offset) pairs of the
 // offsets that give some position in [lo, hi] a partner position inside
 // [0, N): partner = position - dir * offset, dir = +1 for queries looking
-// back at keys, -1 for keys looking forward at queries.  Pads with `pad`
-// up to a multiple of CJ plus two chunks.  Returns the (uniform) count.
+// back at keys, -1 for keys looking forward at queries.  Offsets j < j_skip
+// are left out (served elsewhere).  Pads with `pad` up to a multiple of CJ
+// plus two chunks.  Returns the (uniform) count.
 template <int CJ>
 __device__ __forceinline__ int build_offset_list(int2* list, const int* s_off, int J, int lo, int hi, int N, int dir,
-                                                 int2 pad) {
+                                                 int2 pad, int j_skip = 0) {
   const int l = threadIdx.x % kWave;
   int cnt = 0;
   for (int base = 0; base < J; base += kWave) {
     const int j = base + l;
     const int d = j < J ? s_off[j] : 0;
     const int sd = dir * d;
-    const bool need = j < J && sd <= hi && sd >= lo - (N - 1);
+    const bool need = j < J && j >= j_skip && sd <= hi && sd >= lo - (N - 1);
     const uint64_t mask = __ballot(need);
     const int pos = cnt + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));

@@ -29,6 +29,22 @@ from .lattice import GROUPED_MODE_IDS, R_PLANES
 
 HEAD_DIM = 64
 _SLAB_MODES = (GROUPED_MODE_IDS["overlap_slab"], GROUPED_MODE_IDS["overlap_slab_bwd"])
+# Schedule of the baseline mode: the near band of the dQ launch on the matrix
+# cores (DWARF_SCHED_BAND) measured faster than the gather loop alone (0.252 vs
+# 0.258 ms for the dQ launch at B15 H8 T2048), so it is the default.  The
+# overlap-slab modes always set it; online_softmax=False adds
+# DWARF_SCHED_TWO_PASS (the offline-softmax forward).
+DEFAULT_SCHEDULE = 1
+
+
+def schedule_for(grouped_mode_id: int, online_softmax: bool) -> int:
+    """DWARF_SCHED_* flags for the reference's mode arguments (dsqg:2271-2314, 2394, 2470)."""
+    sched = DEFAULT_SCHEDULE
+    if int(grouped_mode_id) in _SLAB_MODES:
+        sched |= _lib.DWARF_SCHED_BAND
+    if not online_softmax:
+        sched |= _lib.DWARF_SCHED_TWO_PASS
+    return sched
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -61,7 +77,7 @@ def _planes(t: torch.Tensor) -> torch.Tensor:
 
 
 def _fill_fwd(a: _lib.DsqgFwdArgs, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
-              offsets, j_small, j_large, plane_shift, query_start, out, lse, se_round) -> None:
+              offsets, j_small, j_large, plane_shift, query_start, out, lse, se_round, schedule=0) -> None:
     B, H, N, HD = q.shape
     a.B, a.H, a.H_kv, a.N, a.head_dim = B, H, k.shape[1], N, HD
     a.J, a.J_small, a.J_large = int(j_small) + int(j_large), int(j_small), int(j_large)
@@ -80,6 +96,7 @@ def _fill_fwd(a: _lib.DsqgFwdArgs, q, k, v, pos_bias, scale_embed, phase_base, p
     a.offsets = offsets.data_ptr()
     a.out, a.out_stride = out.data_ptr(), _lib.i64_array(out.stride())
     a.lse, a.lse_stride = lse.data_ptr(), _lib.i64_array(lse.stride())
+    a.schedule = int(schedule)
 
 
 def _device_offsets(offsets_dev: torch.Tensor, device: torch.device, j_val: int) -> torch.Tensor:
@@ -104,11 +121,12 @@ def normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_p
 
 
 def dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
-                 j_small, j_large, plane_shift=0, query_start=0, *, events=None):
+                 j_small, j_large, plane_shift=0, query_start=0, *, events=None, schedule=None):
     """Raw forward launch: returns (out, lse).  q/k/v share one dtype (bf16 or fp32).
 
     ``events``: optional (start, end) torch.cuda.Event pair recorded around the
-    launch on the current stream.
+    launch on the current stream.  ``schedule``: DWARF_SCHED_* flags (None: the
+    default schedule, ``DEFAULT_SCHEDULE``).
     """
     lib = _lib.load()
     B, H, N, _ = q.shape
@@ -116,7 +134,8 @@ def dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, 
     lse = torch.empty((B, H, N), device=q.device, dtype=torch.float32)
     args = _lib.DsqgFwdArgs()
     _fill_fwd(args, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
-              j_small, j_large, plane_shift, query_start, out, lse, se_round=q.dtype != torch.float32)
+              j_small, j_large, plane_shift, query_start, out, lse, se_round=q.dtype != torch.float32,
+              schedule=DEFAULT_SCHEDULE if schedule is None else schedule)
     if events:
         events[0].record()
     _lib.check(lib.dwarf_dsqg_fwd(ctypes.byref(args), _stream(q.device)), "dwarf_dsqg_fwd")
@@ -126,7 +145,7 @@ def dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, 
 
 
 def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
-                  out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None):
+                  out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None, schedule=None):
     """Raw backward: the dq, params and dkdv stages on the current stream.
 
     Returns (dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz).  ``events``:
@@ -150,7 +169,8 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     dz = torch.empty(z_pre.shape, device=dev, dtype=torch.float32)
     args = _lib.DsqgBwdArgs()
     _fill_fwd(args.fwd, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
-              j_small, j_large, plane_shift, query_start, out, lse, se_round=q.dtype != torch.float32)
+              j_small, j_large, plane_shift, query_start, out, lse, se_round=q.dtype != torch.float32,
+              schedule=DEFAULT_SCHEDULE if schedule is None else schedule)
     args.dout, args.dout_stride = dout.data_ptr(), _lib.i64_array(dout.stride())
     args.dq, args.dq_stride = dq.data_ptr(), _lib.i64_array(dq.stride())
     args.dk, args.dk_stride = dk.data_ptr(), _lib.i64_array(dk.stride())
@@ -215,12 +235,15 @@ class _DSQGV18GroupedFn(torch.autograd.Function):
             raise ValueError(f"j_val={j_val} != j_small={j_small} + j_large={j_large}")
         if offsets_dev.numel() != int(j_val):
             raise ValueError(f"offsets_dev has {offsets_dev.numel()} entries, expected j_val={j_val}")
+        schedule = schedule_for(grouped_mode_id, bool(online_softmax))
         out, lse = torch.ops.dwarf.dsqg_fwd(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
-                                            offsets_dev, int(j_small), int(j_large), int(plane_shift), query_start)
+                                            offsets_dev, int(j_small), int(j_large), int(plane_shift), query_start,
+                                            schedule)
         ctx.save_for_backward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre,
                               out, lse, offsets_dev)
         ctx.j_small, ctx.j_large = int(j_small), int(j_large)
         ctx.plane_shift, ctx.query_start = int(plane_shift), query_start
+        ctx.schedule = schedule
         return out
 
     @staticmethod
@@ -229,7 +252,7 @@ class _DSQGV18GroupedFn(torch.autograd.Function):
          out, lse, offsets) = ctx.saved_tensors
         grads = torch.ops.dwarf.dsqg_bwd(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre,
                                          z_pre, offsets, out, lse, ctx.j_small, ctx.j_large, ctx.plane_shift,
-                                         ctx.query_start)
+                                         ctx.query_start, ctx.schedule)
         dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz = grads
         return (dq, dk.to(k.dtype), dv.to(v.dtype), dpb.to(pos_bias.dtype), dse.to(scale_embed.dtype),
                 dpbase.to(phase_base.dtype), dpgain.to(phase_gain.dtype), dy.to(y_pre.dtype),
@@ -249,12 +272,15 @@ def dsqg_attention_v18_grouped(
     the HIP kernels here; "hip" is an alias) and "eager", which the reference
     maps to its CPU oracle.  This library ships no CPU path, so "eager" and
     non-device tensors raise instead of falling back.  ``online_softmax`` and
-    the overlap-slab ``grouped_mode_id`` values select schedules of the same
-    mathematics in the reference; they are accepted and run the one HIP
-    schedule.  The five sparse-plan buffers are unused, as in the baseline mode.
+    ``grouped_mode_id`` select schedules of the same mathematics, as in the
+    reference (``schedule_for``): the overlap-slab modes (1, 3) serve the near
+    offsets of the dQ launch as a dense band on the matrix cores, and
+    online_softmax=False runs the two-pass (offline) softmax forward.  The
+    reference's slab planner buffers (sparse order, groups) describe its own
+    tiling of the far offsets and are not used.
     """
     del verify_mode, sparse_order_dev, group_start_dev, group_len_dev, group_dmin_dev, group_dmax_dev
-    del k_group_size, max_group_spread_observed, online_softmax
+    del k_group_size, max_group_spread_observed
     backend = str(backend).lower()
     if backend not in {"auto", "triton", "hip", "eager"}:
         raise ValueError("backend must be auto, triton, hip, or eager")
@@ -271,6 +297,6 @@ def dsqg_attention_v18_grouped(
         pos_bias.float(), scale_embed.float(), phase_base.float(), phase_gain.float(),
         y_pre.float(), z_pre.float(),
         int(j_val), int(j_small), int(j_large), offsets_dev, None, None, None, None, None,
-        0, int(grouped_mode_id), False, 0, int(plane_shift), int(query_start), True,
+        0, int(grouped_mode_id), False, 0, int(plane_shift), int(query_start), bool(online_softmax),
     )
     return output if output.dtype == original_dtype else output.to(original_dtype)

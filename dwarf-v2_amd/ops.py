@@ -34,16 +34,16 @@ Tensor = torch.Tensor
 @torch.library.custom_op("dwarf::dsqg_fwd", mutates_args=())
 def dsqg_fwd(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, scale_embed: Tensor, phase_base: Tensor,
              phase_gain: Tensor, y_pre: Tensor, z_pre: Tensor, offsets: Tensor, j_small: int, j_large: int,
-             plane_shift: int, query_start: int) -> tuple[Tensor, Tensor]:
-    """Forward launch; returns (out like q, lse [B,H,N] fp32)."""
+             plane_shift: int, query_start: int, schedule: int = 0) -> tuple[Tensor, Tensor]:
+    """Forward launch; returns (out like q, lse [B,H,N] fp32).  schedule: DWARF_SCHED_* flags."""
     t = _dsqg.normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets,
                                j_small + j_large)
-    return _dsqg.dsqg_forward(*t, j_small, j_large, plane_shift, query_start)
+    return _dsqg.dsqg_forward(*t, j_small, j_large, plane_shift, query_start, schedule=schedule)
 
 
 @dsqg_fwd.register_fake
 def _dsqg_fwd_fake(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets, j_small, j_large,
-                   plane_shift, query_start):
+                   plane_shift, query_start, schedule=0):
     B, H, N, HD = q.shape
     return q.new_empty((B, H, N, HD)), q.new_empty((B, H, N), dtype=torch.float32)
 
@@ -51,17 +51,18 @@ def _dsqg_fwd_fake(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre
 @torch.library.custom_op("dwarf::dsqg_bwd", mutates_args=())
 def dsqg_bwd(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, scale_embed: Tensor,
              phase_base: Tensor, phase_gain: Tensor, y_pre: Tensor, z_pre: Tensor, offsets: Tensor, out: Tensor,
-             lse: Tensor, j_small: int, j_large: int, plane_shift: int,
-             query_start: int) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+             lse: Tensor, j_small: int, j_large: int, plane_shift: int, query_start: int,
+             schedule: int = 0) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Backward launches; returns (dq, dk, dv, dpos_bias, dscale_embed, dphase_base, dphase_gain, dy, dz)."""
     t = _dsqg.normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets,
                                j_small + j_large)
-    return _dsqg.dsqg_backward(dout, *t, out, lse.contiguous(), j_small, j_large, plane_shift, query_start)
+    return _dsqg.dsqg_backward(dout, *t, out, lse.contiguous(), j_small, j_large, plane_shift, query_start,
+                               schedule=schedule)
 
 
 @dsqg_bwd.register_fake
 def _dsqg_bwd_fake(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets, out, lse,
-                   j_small, j_large, plane_shift, query_start):
+                   j_small, j_large, plane_shift, query_start, schedule=0):
     f32 = torch.float32
     return (q.new_empty(q.shape), q.new_empty(k.shape), q.new_empty(v.shape),
             q.new_empty(pos_bias.shape, dtype=f32), q.new_empty(scale_embed.shape, dtype=f32),

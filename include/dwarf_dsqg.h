@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 4
+#define DWARF_ABI_VERSION 5
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
@@ -81,7 +81,24 @@ typedef struct {
   const int32_t* offsets;
   void* out;  int64_t out_stride[4];
   float* lse; int64_t lse_stride[3];
+  int32_t schedule;       /* DWARF_SCHED_* bit flags: which schedule of the same mathematics runs */
 } dwarf_dsqg_fwd_args;
+
+/*
+ * Schedules (dwarf_dsqg_fwd_args.schedule).  They compute the same function;
+ * results differ only by fp32 summation order.
+ *   DWARF_SCHED_BAND: the bf16 dQ launch serves the leading small offsets
+ *     (ascending, <= 32) as a dense band on the matrix cores from a K window
+ *     in LDS, the reference's overlap-slab formulation of the near offsets
+ *     (grouped_mode overlap_slab / overlap_slab_bwd, dsqg:1047-1256,
+ *     1491-1727); fp32 launches ignore it.
+ *   DWARF_SCHED_TWO_PASS: the forward takes each row's score maximum first and
+ *     then forms the softmax and the weighted sum without rescaling: the
+ *     reference's offline-softmax kernel (online_softmax=False,
+ *     _fwd_v18_grouped dsqg:863-1044).
+ */
+#define DWARF_SCHED_BAND 1
+#define DWARF_SCHED_TWO_PASS 2
 
 /*
  * Replaces the forward launch of _DSQGV18GroupedFn.forward (dsqg:2300-2314,

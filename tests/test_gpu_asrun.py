@@ -49,19 +49,19 @@ def excess(got: torch.Tensor, ref: torch.Tensor, bf16: bool) -> float:
     return float(((g - r).abs() - bar).max())
 
 
-def run_gpu(pkg, t, offsets, js, shift, qs, device):
+def run_gpu(pkg, t, offsets, js, shift, qs, device, mode=0):
     xd = {n: t[n].to(device).detach().clone().requires_grad_(True) for n in NAMES}
     off = torch.tensor(offsets, dtype=torch.int32, device=device)
     out = pkg.dsqg_attention_v18_grouped(*(xd[n] for n in NAMES), len(offsets), js, len(offsets) - js, off,
-                                         None, None, None, None, None, 3, 0, False, 0, shift, qs)
+                                         None, None, None, None, None, 3, mode, False, 0, shift, qs)
     out.backward(t["dout"].to(device=device, dtype=out.dtype))
     torch.cuda.synchronize()
     return out.detach().cpu(), {n: xd[n].grad.cpu() for n in NAMES}
 
 
-def check_rows(pkg, t, offsets, js, shift, qs, device, head_chunk=None):
+def check_rows(pkg, t, offsets, js, shift, qs, device, head_chunk=None, mode=0):
     """GPU fwd+bwd on the whole batch, oracle per batch row (and head chunk): returns nothing, asserts."""
-    out, grads = run_gpu(pkg, t, offsets, js, shift, qs, device)
+    out, grads = run_gpu(pkg, t, offsets, js, shift, qs, device, mode)
     cpu = {n: t[n].detach().cpu() for n in list(NAMES) + ["dout"]}
     B, H, N, _ = cpu["q"].shape
     Hkv = cpu["k"].shape[1]
@@ -103,11 +103,13 @@ def check_rows(pkg, t, offsets, js, shift, qs, device, head_chunk=None):
     note("worst excess over the bar: " + ", ".join(f"{n} {v:+.2e}" for n, v in worst.items()))
 
 
-def test_cfg2_training_microbatch_as_benched(pkg, device):
-    """B15 H8 T2048 bf16 fwd+bwd on bench.py's seed-0 inputs (3,840 query tiles)."""
-    note("cfg2 B15 H8 T2048 bf16 fwd+bwd")
+@pytest.mark.parametrize("mode", [0, 3])
+def test_cfg2_training_microbatch_as_benched(pkg, device, mode):
+    """B15 H8 T2048 bf16 fwd+bwd on bench.py's seed-0 inputs (3,840 query tiles), in the baseline and the
+    overlap-slab schedule."""
+    note(f"cfg2 B15 H8 T2048 bf16 fwd+bwd, grouped mode {mode}")
     t, js, jl = bench.synth(pkg, 15, 8, 2048, 0, torch.device("cpu"))
-    check_rows(pkg, t, list(pkg.ALL_OFFSETS), js, 0, 1, device)
+    check_rows(pkg, t, list(pkg.ALL_OFFSETS), js, 0, 1, device, mode=mode)
 
 
 def test_cfg4_long_context_as_benched(pkg, device):

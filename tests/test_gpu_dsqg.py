@@ -24,12 +24,12 @@ FP32_REL = 1e-5
 BF16_ABS = 2e-2
 
 
-def gpu_fwd_bwd(pkg, x, offsets, js, shift, qs, dout, device):
+def gpu_fwd_bwd(pkg, x, offsets, js, shift, qs, dout, device, mode=0, online=True):
     xd = {n: t.to(device).requires_grad_(True) for n, t in x.items()}
     off = torch.tensor(offsets, dtype=torch.int32, device=device)
     out = pkg.dsqg_attention_v18_grouped(
         *(xd[n] for n in NAMES), len(offsets), js, len(offsets) - js, off,
-        None, None, None, None, None, 3, 0, False, 0, shift, qs,
+        None, None, None, None, None, 3, mode, False, 0, shift, qs, online_softmax=online,
     )
     out.backward(dout.to(device=device, dtype=out.dtype))
     torch.cuda.synchronize()
@@ -228,3 +228,44 @@ def test_maximum_offsets_bf16(pkg, device):
     for n in NAMES:
         scale = max(1.0, rgrads[n].abs().max().item())
         assert max_abs(grads[n].float(), rgrads[n]) < BF16_ABS * scale, n
+
+
+@pytest.mark.parametrize("mode,online", [(1, True), (3, True), (0, False), (3, False)])
+def test_bf16_schedules_match_oracle(pkg, device, mode, online):
+    """The overlap-slab modes (near band of the dQ launch on the matrix cores) and the offline-softmax
+    (two-pass) forward: bf16 output and all 9 gradients against the oracle, at a ragged N with query_start 2,
+    hot MOVT angles and plane shift 9."""
+    offsets = lattice(pkg)
+    x = make_inputs(2, 4, 4, 301, offsets, 17, seed=88 + mode, dtype=torch.bfloat16, plane_shift=9, gain_std=6.0)
+    dout = torch.randn(2, 4, 301, 64, generator=torch.Generator().manual_seed(89)).to(torch.bfloat16)
+    out, grads = gpu_fwd_bwd(pkg, x, offsets, 17, 9, 2, dout, device, mode=mode, online=online)
+    ro, _, rg = oracle_fwd_bwd(x, offsets, 17, 9, 2, dout.float(), round_se=True)
+    assert max_abs(out, ro) < BF16_ABS
+    for n in NAMES:
+        assert max_abs(grads[n], rg[n]) < BF16_ABS, (n, max_abs(grads[n], rg[n]))
+
+
+def test_fp32_two_pass_forward(pkg, device):
+    """online_softmax=False in fp32: the two-pass forward and the gradients within 1e-5 relative."""
+    offsets = lattice(pkg)
+    x = make_inputs(1, 3, 3, 260, offsets, 17, seed=93, dtype=torch.float32, plane_shift=3, gain_std=6.0)
+    dout = torch.randn(1, 3, 260, 64, generator=torch.Generator().manual_seed(94))
+    out, grads = gpu_fwd_bwd(pkg, x, offsets, 17, 3, 1, dout, device, mode=0, online=False)
+    ro, _, rg = oracle_fwd_bwd(x, offsets, 17, 3, 1, dout, round_se=False)
+    assert rel_err(out, ro) < FP32_REL
+    for n in NAMES:
+        assert rel_err(grads[n], rg[n]) < FP32_REL, (n, rel_err(grads[n], rg[n]))
+
+
+def test_band_lattice_edges(pkg, device):
+    """Lattices whose small offsets the band takes only in part: a small offset above 32 (stays in the
+    gather loop) and unsorted small offsets (the band stops at the first descent); mode 3 against the
+    oracle."""
+    for offsets, js in (([1, 2, 3, 5, 8, 13, 21, 40, 48, 64, 96], 8), ([2, 1, 4, 3, 48, 96], 4)):
+        x = make_inputs(1, 2, 2, 200, offsets, js, seed=95, dtype=torch.bfloat16, gain_std=4.0)
+        dout = torch.randn(1, 2, 200, 64, generator=torch.Generator().manual_seed(96)).to(torch.bfloat16)
+        out, grads = gpu_fwd_bwd(pkg, x, offsets, js, 0, 1, dout, device, mode=3)
+        ro, _, rg = oracle_fwd_bwd(x, offsets, js, 0, 1, dout.float(), round_se=True)
+        assert max_abs(out, ro) < BF16_ABS
+        for n in NAMES:
+            assert max_abs(grads[n], rg[n]) < BF16_ABS, (offsets, n, max_abs(grads[n], rg[n]))
