@@ -197,6 +197,16 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
     return zero_floats(a.dphase_gain, jl * f.H * DWARF_R_PLANES, s, name);
   }
   const int dt = a.fwd.dtype;
+  if (dt == DWARF_BF16) {
+    // the dS matrix of one (b, h) is addressed with 32-bit offsets 4 (j N + n)
+    if (4 * static_cast<int64_t>(a.fwd.J) * a.fwd.N >= (int64_t(1) << 31))
+      return fail(DWARF_ERR_UNSUPPORTED, "bf16 backward: 4 x J x N bytes of dS per (b, h) must stay below 2 GiB");
+    // the dK/dV launch stages every head of a GQA group's tables in LDS
+    const size_t lds = dwarf::dkdv_lds_bytes(a.fwd.J, a.fwd.J_large, a.fwd.H / a.fwd.H_kv);
+    if (do_dkdv && lds > dwarf::kMaxLdsBytes)
+      return fail(DWARF_ERR_UNSUPPORTED, "bf16 dK/dV: %zu bytes of LDS tables for J=%d and %d query heads per KV head "
+                  "exceed the %zu bytes of a workgroup", lds, a.fwd.J, a.fwd.H / a.fwd.H_kv, dwarf::kMaxLdsBytes);
+  }
   if ((rc = check_contig_rows("dout", a.dout, a.dout_stride, dt))) return rc;
   if (dt == DWARF_BF16 && (rc = check_gather_span("dout", a.dout_stride[2], 2, a.fwd.N))) return rc;
   if (do_dq) {
@@ -513,6 +523,7 @@ int dwarf_dsqg_q6_prefill_fwd(const dwarf_dsqg_q6_prefill_args* args, dwarf_stre
   if ((rc = check_rows("q", a.q, a.q_stride, 3, DWARF_BF16))) return rc;
   if ((rc = check_rows("out", a.out, a.out_stride, 3, DWARF_BF16))) return rc;
   if ((rc = check_cache(a.cache, a.cache_stride, 2))) return rc;
+  if ((rc = check_gather_span("cache", DWARF_Q6_SLOT_BYTES, 1, a.N))) return rc;
   if (!a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter table, probe table or offsets is NULL");
   if (a.B == 0 || a.N == 0) return ok();

@@ -600,6 +600,8 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
   return w;
 }
 
+size_t dkdv_lds_bytes(int J, int J_large, int group) { return kv_layout(J, J_large, group, kChunkKv).bytes; }
+
 hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
                            bool do_params, bool do_dkdv) {
   if (do_dq) {

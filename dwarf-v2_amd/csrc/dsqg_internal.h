@@ -63,6 +63,8 @@ hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws,
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
 hipError_t launch_dsqg_bwd_dse(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
 size_t dq_lds_bytes(int J, int J_large, int dtype);
+size_t dkdv_lds_bytes(int J, int J_large, int group);   // bf16 dK/dV launch, per workgroup
+constexpr size_t kMaxLdsBytes = 160 * 1024;             // LDS per workgroup on gfx950
 int dq_tile_queries(int dtype);   // queries per tile of the dQ launch
 int dq_gather_wgs_per_cu();       // resident workgroups per CU of the bf16 dQ gather launch
 int dq_dse_wgs_per_cu(int J);     // resident workgroups per CU of the bf16 dSE launch

@@ -180,7 +180,9 @@ def causal_ema_scan(x: torch.Tensor, ema_factor: torch.Tensor, floor: float = 1e
         raise ValueError(f"reset_mask must have shape {tuple(x.shape[:2])}")
     if not x.is_cuda:
         raise RuntimeError("the EMA HIP kernels require device tensors")
-    xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.bfloat16)
+    # bf16 runs the bf16 kernels; every other dtype computes in fp32 (the reference's state and
+    # arithmetic, ema:272-278) and the result is cast back to x's dtype
+    xin = x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.float32)
     if reset_mask is not None:
         out = _CausalEMAResetFn.apply(xin, ema_factor, reset_mask, float(floor), float(ceiling))
     else:

@@ -145,3 +145,50 @@ def test_validation_errors_without_gpu(pkg, lib):
     assert lib.dwarf_packet_pool_bwd(ctypes.byref(kb), None) == L.DWARF_ERR_INVALID_ARGUMENT
     # starts and carries [B][N/16][K*D] fp32, then 2K slots per apply workgroup (one here)
     assert lib.dwarf_packet_pool_bwd_workspace_bytes(ctypes.byref(kb)) == (2 * 1 * 2 * 3 * 8 + 2 * 3) * 4
+
+
+def _fake_fwd(L, B, H, H_kv, N, J, J_small):
+    """Forward args with aligned placeholder pointers (validation never dereferences them)."""
+    a = L.DsqgFwdArgs()
+    a.B, a.H, a.H_kv, a.N, a.head_dim = B, H, H_kv, N, 64
+    a.J, a.J_small, a.J_large = J, J_small, J - J_small
+    a.dtype = L.DWARF_BF16
+    p = 0x10000
+    for name in ("q", "k", "v", "out"):
+        setattr(a, name, p)
+    for name, rows in (("q", H), ("out", H), ("k", H_kv), ("v", H_kv)):
+        setattr(a, name + "_stride", L.i64_array((rows * N * 64, N * 64, 64, 1)))
+    a.pos_bias = a.scale_embed = a.phase_base = a.phase_gain = a.lse = p
+    a.y_pre, a.z_pre, a.offsets = p, p, p
+    a.y_stride = L.i64_array((H * N * 4, N * 4, 4))
+    a.z_stride = L.i64_array((H_kv * N * 4, N * 4, 4))
+    a.lse_stride = L.i64_array((H * N, N, 1))
+    return a
+
+
+def test_backward_limits_without_gpu(pkg, lib):
+    """bf16 backward shapes the kernels cannot address or stage are refused before any launch: the dS
+    matrix's 32-bit offsets (4 J N bytes per (b, h)) and the dK/dV launch's LDS tables of a GQA group."""
+    L = pkg._lib
+    b = L.DsqgBwdArgs()
+    b.fwd = _fake_fwd(L, 1, 1, 1, 2_100_000, 256, 17)         # 4 x 256 x 2.1M bytes of dS
+    b.dout, b.dout_stride = 0x10000, L.i64_array((2_100_000 * 64, 2_100_000 * 64, 64, 1))
+    assert lib.dwarf_dsqg_bwd_dq(ctypes.byref(b), None) == L.DWARF_ERR_UNSUPPORTED
+    assert b"dS" in lib.dwarf_last_error()
+    b.fwd = _fake_fwd(L, 1, 16, 1, 512, 256, 17)              # 16 heads' tables per KV head at J = 256
+    b.dout_stride = L.i64_array((16 * 512 * 64, 512 * 64, 64, 1))
+    assert lib.dwarf_dsqg_bwd_dkdv(ctypes.byref(b), None) == L.DWARF_ERR_UNSUPPORTED
+    assert b"LDS" in lib.dwarf_last_error()
+
+
+def test_prefill_gather_span_without_gpu(pkg, lib):
+    """The q6 prefill gathers cache rows with 32-bit offsets: (2N + 128) x 128 B must stay below 2 GiB."""
+    L = pkg._lib
+    a = L.Q6PrefillArgs()
+    N = 8_400_000
+    a.B, a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large = 1, 1, 1, N, 64, 96, 17, 79
+    a.q = a.out = a.cache = 0x10000
+    a.q_stride = a.out_stride = L.i64_array((N * 64, N * 64, 64, 1))
+    a.cache_stride = L.i64_array((N * 128, N * 128, 128))
+    assert lib.dwarf_dsqg_q6_prefill_fwd(ctypes.byref(a), None) == L.DWARF_ERR_UNSUPPORTED
+    assert b"cache" in lib.dwarf_last_error()

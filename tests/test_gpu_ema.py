@@ -61,6 +61,24 @@ def test_bf16_long_context(pkg, device):
     assert rel_err(da, rda) < 1e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float64])
+def test_other_dtypes_compute_in_fp32(pkg, device, dtype):
+    """fp16 and fp64 inputs run the fp32 kernels and come back in their own dtype: y and dx match the
+    oracle on the fp32-cast inputs to fp32 accuracy, plus the output dtype's rounding for fp16."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 300, 64, generator=g).to(dtype)
+    alpha = torch.rand(64, generator=g) * 0.2 + 0.01
+    dy = torch.randn(2, 300, 64, generator=g).to(dtype)
+    y, dx, da = run(pkg, x, alpha, dy, device)
+    assert y.dtype == dtype and dx.dtype == dtype
+    ry = ema_ref.ema_scan(x.double(), alpha.double())
+    rdx, rda = ema_ref.ema_adjoint(x.double(), ry, dy.double(), alpha.double())
+    tol = 1e-3 if dtype == torch.float16 else 1e-5
+    assert rel_err(y, ry) < tol
+    assert rel_err(dx, rdx) < tol
+    assert rel_err(da, rda) < (1e-5 if dtype == torch.float64 else 1e-3)
+
+
 def test_clamped_alpha_and_projection(pkg, device):
     x = torch.randn(1, 50, 8)
     dy = torch.ones(1, 50, 8)
