@@ -71,6 +71,17 @@ def synth(pkg, B, H, N, seed, device, dtype=torch.bfloat16, plane_shift=0):
     return t, js, J - js
 
 
+class CacheFlush:
+    """Evicts every cache level (L2, the 256 MB MALL) by READING 1 GiB: a write would leave dirty lines
+    behind, and the timed kernel would then pay for their write-back."""
+
+    def __init__(self, device):
+        self.buf = torch.ones(1 << 28, dtype=torch.float32, device=device)
+
+    def __call__(self):
+        self.buf.sum()
+
+
 def time_dsqg_step(pkg, t, js, jl, steps, warmup, flush=None):
     """Returns (ms_per_step, per-launch average ms dict)."""
     ops = pkg.dsqg if hasattr(pkg, "dsqg") else importlib.import_module("dwarf-v2_amd.dsqg")
@@ -111,34 +122,89 @@ def time_dsqg_step(pkg, t, js, jl, steps, warmup, flush=None):
     return total_ms / steps, per
 
 
-def cpu_baseline(pkg):
-    """The CPU restatement of the reference eager path (oracle/), fp32 fwd+bwd on
-    batch row 0 of the training microbatch (B=1 of 15: 2,048 of 30,720 tokens)."""
-    from oracle import dsqg_ref
+def cpu_cores() -> tuple[int, int, int | None]:
+    """(threads used, affinity cores, cgroup quota cores or None): every core the process may run on,
+    i.e. the affinity set, capped by the cgroup's CPU quota where one is set (more threads than the
+    quota only queue behind it)."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, int(q) // int(per))
+    except (OSError, ValueError):
+        pass
+    return (min(aff, quota) if quota else aff), aff, quota
 
-    threads = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(threads)
-    t, js, jl = synth(pkg, 1, 8, 2048, 0, torch.device("cpu"), dtype=torch.float32)
-    names = ("q", "k", "v", "pos_bias", "scale_embed", "phase_base", "phase_gain", "y_pre", "z_pre")
-    inputs = {n: t[n] for n in names}
-    offsets = t["offsets"].tolist()
-    times = []
-    budget_end = time.perf_counter() + 12.0     # about 10-30 s of CPU work, at least 3 repeats
-    while len(times) < 3 or (time.perf_counter() < budget_end and len(times) < 50):
-        t0 = time.perf_counter()
-        dsqg_ref.dsqg_forward_backward(inputs, offsets, js, t["dout"], query_start=1)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    dt = times[len(times) // 2]
-    cpu = ""
+
+def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with family/model/stepping (the name alone can be generic)."""
+    want = ("model name", "cpu family", "model", "stepping")
+    got: dict[str, str] = {}
     try:
         with open("/proc/cpuinfo") as f:
-            cpu = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+            for ln in f:
+                k, _, v = ln.partition(":")
+                k = k.strip()
+                if k in want and k not in got:
+                    got[k] = v.strip()
+                if len(got) == len(want):
+                    break
     except OSError:
-        pass
-    return {"value": 2048 / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle/dsqg_ref fp32 fwd+bwd of batch row 0 (B=1,H=8,T=2048,J=96), median of {len(times)} "
-                       f"runs: {dt:.2f} s each; {cpu}")}
+        return "unknown CPU"
+    return (f"{got.get('model name', 'unknown CPU')} (family {got.get('cpu family', '?')}, "
+            f"model {got.get('model', '?')}, stepping {got.get('stepping', '?')})")
+
+
+def median_seconds(fn, budget_s: float, min_reps: int = 3, max_reps: int = 50) -> tuple[float, int]:
+    times: list[float] = []
+    end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline(pkg):
+    """The CPU restatements of the reference's eager paths (oracle/), timed on this host's cores.
+
+    value: cfg2's fwd+bwd in its own dtype (bf16 inputs) on batch row 0 (B=1 of 15, the rows are
+    independent, so tokens/s scales to the whole microbatch).  Also timed: the same in fp32, cfg1's
+    forward (fp32 B1 H8 T2048, the whole config) and the EMA restatement of ``_reference``
+    (ema:511-538) at cfg4's x [4,8192,512] bf16.  The DSQG restatement computes in fp32 for bf16
+    inputs, as the reference eager computes its scores (dsqg:2658-2662).  Medians of >= 3 runs."""
+    from oracle import dsqg_ref, ema_ref
+
+    threads, aff, quota = cpu_cores()
+    torch.set_num_threads(threads)
+    cpu = torch.device("cpu")
+    names = ("q", "k", "v", "pos_bias", "scale_embed", "phase_base", "phase_gain", "y_pre", "z_pre")
+    res = {}
+    for tag, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        t, js, _ = synth(pkg, 1, 8, 2048, 0, cpu, dtype=dt)
+        inputs = {n: t[n] for n in names}
+        offsets = t["offsets"].tolist()
+        sec, reps = median_seconds(
+            lambda: dsqg_ref.dsqg_forward_backward(inputs, offsets, js, t["dout"], query_start=1), 5.0)
+        res[f"cfg2_fwd_bwd_{tag}"] = {"tokens_per_s": 2048 / sec, "s_per_row": sec, "runs": reps}
+        if tag == "fp32":
+            sec, reps = median_seconds(lambda: dsqg_ref.dsqg_forward(*(inputs[n] for n in names), offsets, js,
+                                                                     query_start=1), 3.0)
+            res["cfg1_fwd_fp32"] = {"tokens_per_s": 2048 / sec, "s_per_call": sec, "runs": reps}
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4, 8192, 512, generator=g).to(torch.bfloat16)
+    alpha = 1.0 - (0.90 + 0.099 * torch.rand(512, generator=g))
+    sec, reps = median_seconds(lambda: ema_ref.ema_scan(x, alpha), 3.0)
+    res["cfg4_ema_fwd_bf16"] = {"tokens_per_s": 4 * 8192 / sec, "s_per_call": sec, "runs": reps}
+    head = res["cfg2_fwd_bwd_bf16"]
+    return {"value": head["tokens_per_s"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle/dsqg_ref fwd+bwd of batch row 0 of cfg2 (B=1 of 15, H=8, T=2048, J=96), bf16 "
+                       f"inputs, median of {head['runs']} runs of {head['s_per_row']:.2f} s; {threads} threads "
+                       f"(affinity {aff} cores, cgroup quota {quota if quota else 'none'}); {cpu_model()}"),
+            "breakdown": res}
 
 
 def decode_workload(pkg, device):
@@ -169,17 +235,31 @@ def decode_workload(pkg, device):
                 qps=torch.stack([qpn] * L).to(device))
 
 
+def decode_bytes(pos, offsets, js, L, H) -> int:
+    """Algorithmic bytes of one decode step: per (sequence, layer, head) the bf16 query and output
+    (256 B), 104 B of q6 K+V per valid cache row and 16 B of stored z per valid far row, plus the
+    per-layer tables."""
+    nv = [sum(1 for d in offsets if int(t) - d >= 0) for t in pos]
+    nf = [sum(1 for d in offsets[js:] if int(t) - d >= 0) for t in pos]
+    return sum(L * H * (256 + 104 * a + 16 * b) for a, b in zip(nv, nf)) + L * TABLE_BYTES
+
+
 def q6_decode_extra(pkg, device, steps, warmup):
+    """The cfg5 decode step timed three ways: HIP-graph replays at fixed positions (warm: the 109 MB
+    working set stays in the 256 MB MALL), graph replays of ten steps whose positions advance by one
+    per step, and single steps after a 1 GiB read that evicts the caches (cold), positions advancing."""
     w = decode_workload(pkg, device)
-    S, L, H, offsets, js, pos = w["S"], w["L"], w["H"], w["offsets"], w["js"], w["pos"]
+    S, L, H, N, offsets, js, pos = w["S"], w["L"], w["H"], w["N"], w["offsets"], w["js"], w["pos"]
     J = len(offsets)
     qdec, pb, se, pbase, pgain, caches = (w[n] for n in ("qdec", "pos_bias", "scale_embed", "phase_base",
                                                          "phase_gain", "caches"))
     off, qps = w["off"], w["qps"]
     posd = pos.to(device)
+    adv = [(pos + i).clamp(max=N - 1).to(torch.int32) for i in range(10)]
+    advd = [p.to(device) for p in adv]
 
-    def run():
-        return pkg.q6.q6_decode(qdec, posd, caches, pb, se, pbase, pgain, qps, off, js, J - js, 0)
+    def run(p=posd):
+        return pkg.q6.q6_decode(qdec, p, caches, pb, se, pbase, pgain, qps, off, js, J - js, 0)
 
     for _ in range(warmup):
         run()
@@ -192,17 +272,40 @@ def q6_decode_extra(pkg, device, steps, warmup):
     torch.cuda.synchronize()
     ms_eager = a.elapsed_time(b) / steps
     ms = graph_ms(run, max(steps, 20), warmup)
-    nv = [sum(1 for d in offsets if int(t) - d >= 0) for t in pos]
-    nf = [sum(1 for d in offsets[js:] if int(t) - d >= 0) for t in pos]
-    bytes_ = sum(L * H * (256 + 104 * a_ + 16 * b_) for a_, b_ in zip(nv, nf)) + L * TABLE_BYTES
-    del caches
+    turn = [0]
+
+    def run_adv():
+        p = advd[turn[0] % len(advd)]
+        turn[0] += 1
+        return run(p)
+
+    ms_adv = graph_ms(run_adv, max(steps, 20), warmup)
+    flush = CacheFlush(device)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+    for i, (ea, eb) in enumerate(evs):
+        flush()
+        ea.record()
+        run(advd[i % len(advd)])
+        eb.record()
+    torch.cuda.synchronize()
+    ms_cold = sum(ea.elapsed_time(eb) for ea, eb in evs) / len(evs)
+    del flush
+    bytes_ = decode_bytes(pos.tolist(), offsets, js, L, H)
+    bytes_adv = sum(decode_bytes(p.tolist(), offsets, js, L, H) for p in adv) / len(adv)
+    del caches, w
     torch.cuda.empty_cache()
     return {"tokens_per_s": S / (ms * 1e-3), "ms_per_step": ms, "ms_per_step_eager": ms_eager,
-            "algorithmic_bytes": bytes_,
+            "ms_per_step_advancing": ms_adv, "ms_per_step_cold_advancing": ms_cold,
+            "algorithmic_bytes": bytes_, "algorithmic_bytes_advancing": bytes_adv,
             "achieved_GBps": bytes_ / (ms * 1e-3) / 1e9, "hbm_frac": bytes_ / (ms * 1e-3) / HBM_PEAK,
+            "hbm_frac_advancing": bytes_adv / (ms_adv * 1e-3) / HBM_PEAK,
+            "hbm_frac_cold_advancing": bytes_adv / (ms_cold * 1e-3) / HBM_PEAK,
             "config": "S=256 seqs x L=9 layers x H=8, cache 2048, positions U{96..2047} seed 0; "
                       "bytes count 104 B q6 K+V per valid row + 16 B stored z per valid far row; "
-                      "timed from HIP-graph replays (10 steps per graph), eager launch loop in ms_per_step_eager"}
+                      "ms_per_step from HIP-graph replays (10 steps per graph) at fixed positions, "
+                      "ms_per_step_advancing from replays of 10 steps at positions t..t+9, "
+                      "ms_per_step_cold_advancing per step after a 1 GiB read (caches evicted, clean), "
+                      "eager launch loop in ms_per_step_eager"}
 
 
 def q6_prefill_extra(pkg, device, steps, warmup):
@@ -398,10 +501,9 @@ def main() -> int:
     log("training microbatch: DSQG fwd+bwd B15 H8 T2048 bf16")
     t, js, jl = synth(pkg, B, H, N, 0, device)
     ms, per = time_dsqg_step(pkg, t, js, jl, args.steps, args.warmup)
-    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=device)
-    ms_cold, per_cold = time_dsqg_step(pkg, t, js, jl, max(5, args.steps // 2), 1,
-                                       flush=lambda: flush_buf.fill_(1))
-    del flush_buf
+    flush = CacheFlush(device)
+    ms_cold, per_cold = time_dsqg_step(pkg, t, js, jl, max(5, args.steps // 2), 1, flush=flush)
+    del flush
     th = B * H * N
     bytes_launch = {"fwd": th * FWD_BYTES_PER_TH + TABLE_BYTES,
                     "bwd_dq": th * DQ_BYTES_PER_TH + TABLE_BYTES,
@@ -454,7 +556,7 @@ def main() -> int:
         "extra": extra,
     }
     if not args.no_cpu_baseline:
-        log("cpu baseline: oracle fp32 fwd+bwd, B=1 sample")
+        log("cpu baseline: oracle cfg2 bf16/fp32 fwd+bwd rows, cfg1 forward, cfg4 EMA")
         line["cpu_baseline"] = cpu_baseline(pkg)
     print(json.dumps(line), flush=True)
     return 0

@@ -10,15 +10,18 @@ Public surface (reference names, Lanerra/dwarf-v2):
   inverse_bounded_ema_factor                         kernels/causal_ema_scan.py
   phase_probe_features, _PhaseProbeFn                kernels/dsqg_attention_v22.py
   npci_rotate                                        kernels/dsqg_attention_v22.py
+  _plan_sparse_groups, _verify_sparse_plan,
+  _normalize_grouping_args (planner module)          kernels/dsqg_attention_v22.py
   interference_pool, interference_packet_forward     train/train_dwarf.py (InterferencePacket)
   q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
 """
 
-from . import _lib, lattice, npci, ops, packet, probe, q6
+from . import _lib, lattice, npci, ops, packet, planner, probe, q6
 from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
 from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
 from .npci import npci_rotate
 from .packet import _InterferencePoolFn, interference_packet_forward, interference_pool
+from .planner import _normalize_grouping_args, _plan_sparse_groups, _verify_sparse_plan
 from .probe import _PhaseProbeFn, phase_probe_features
 from .lattice import (
     ALL_OFFSETS,
@@ -39,9 +42,12 @@ __all__ = [
     "_InterferencePoolFn",
     "_PhaseProbeFn",
     "_canonicalize_offsets",
+    "_normalize_grouping_args",
     "_normalize_plane_shift",
     "_orthogonal_phase_probes",
     "_phase_plane_channels",
+    "_plan_sparse_groups",
+    "_verify_sparse_plan",
     "bounded_ema_factor",
     "build_offset_groups",
     "causal_ema_scan",

@@ -276,8 +276,10 @@ def dsqg_attention_v18_grouped(
     reference (``schedule_for``): the overlap-slab modes (1, 3) serve the near
     offsets of the dQ launch as a dense band on the matrix cores, and
     online_softmax=False runs the two-pass (offline) softmax forward.  The
-    reference's slab planner buffers (sparse order, groups) describe its own
-    tiling of the far offsets and are not used.
+    slab plan buffers (sparse order, groups; built by ``planner.plan_sparse_groups``
+    as the reference's module builds them, dsqg:2888-2923) describe a slab
+    tiling of the far offsets, which these kernels gather per offset instead:
+    they are accepted and not read.
     """
     del verify_mode, sparse_order_dev, group_start_dev, group_len_dev, group_dmin_dev, group_dmax_dev
     del k_group_size, max_group_spread_observed
