@@ -403,13 +403,16 @@ def npci_extra(pkg, device, steps, warmup):
 
 
 def packet_extra(pkg, device, steps, warmup):
-    """The InterferencePacket pool (three EMA timescales and their mix) fused, fwd and bwd, on the L3
-    block's input at the training microbatch: x [15, 2048, 512] bf16; beside it the same forward as three
-    separate EMA scans and the bf16 mix (the reference's composition, on this build's EMA kernels)."""
+    """The InterferencePacket at the training microbatch, x [15, 2048, 512] bf16 and gate logits of the same
+    shape: the fused pool (three EMA timescales and their mix) fwd and bwd; the fused packet (pool + RMS
+    direction, confidence and gate, train:262-273) fwd and bwd; beside them the reference's composition on
+    this build's kernels (three separate EMA scans and the bf16 mix; the pool followed by PyTorch's
+    elementwise packet)."""
     B, N, D = 15, 2048, 512
     g = torch.Generator().manual_seed(0)
     x = torch.randn(B, N, D, generator=g).to(torch.bfloat16).to(device)
     dp = torch.randn(B, N, D, generator=g).to(torch.bfloat16).to(device)
+    gate = (1.5 * torch.randn(B, N, D, generator=g)).to(torch.bfloat16).to(device)
     a = torch.tensor([1 / 16, 1 / 64, 1 / 256], device=device)
     w = torch.softmax(torch.tensor([0.3, -0.2, 0.1]), 0).to(device)
     packet = importlib.import_module("dwarf-v2_amd.packet")
@@ -417,21 +420,40 @@ def packet_extra(pkg, device, steps, warmup):
     _, state = packet.pool_forward(x, a, w, 1e-5, 0.5)
     ms_f = graph_ms(lambda: packet.pool_forward(x, a, w, 1e-5, 0.5), max(steps, 20), warmup)
     ms_b = graph_ms(lambda: packet.pool_backward(x, a, w, state, dp, 1e-5, 0.5), max(steps, 20), warmup)
+    _, pooled, pstate, ms_rows = packet.packet_forward(x, a, w, gate, 1e-5, 0.5)
+    ms_pf = graph_ms(lambda: packet.packet_forward(x, a, w, gate, 1e-5, 0.5), max(steps, 20), warmup)
+    ms_pb = graph_ms(lambda: packet.packet_backward(x, a, w, gate, pooled, pstate, ms_rows, dp, 1e-5, 0.5),
+                     max(steps, 20), warmup)
     wb = w.to(torch.bfloat16)
 
     def composed():
         scans = [ema.ema_forward(x, a[k:k + 1], 1e-5, 0.5) for k in range(3)]
         return (wb[0] * scans[0] + wb[1] * scans[1]) + wb[2] * scans[2]
 
+    def composed_packet():
+        pf = packet.pool_forward(x, a, w, 1e-5, 0.5)[0].float()
+        rms = pf.square().mean(-1, keepdim=True).sqrt()
+        direction = pf * torch.rsqrt(pf.square().mean(-1, keepdim=True) + 1e-6)
+        return (direction * torch.tanh(rms / 0.25) * torch.sigmoid(gate.float())).to(torch.bfloat16)
+
     ms_c = graph_ms(composed, max(steps, 20), warmup)
+    ms_cp = graph_ms(composed_packet, max(steps, 20), warmup)
     n = B * N * D
     fb, bb = 4 * n, 6 * n
+    pfb, pbb = 8 * n + 4 * B * N, 12 * n + 4 * B * N
     return {"ms_fwd": ms_f, "ms_bwd": ms_b, "ms_fwd_composed": ms_c,
             "fwd_hbm_frac": fb / (ms_f * 1e-3) / HBM_PEAK, "bwd_hbm_frac": bb / (ms_b * 1e-3) / HBM_PEAK,
             "fwd_bytes": fb, "bwd_bytes": bb,
-            "config": "x [15,2048,512] bf16, timescales 16/64/256; algorithmic bytes fwd 4 B/element (x read, "
-                      "pooled written), bwd 6 B/element (dpooled and x read, dx written); composed = three EMA "
-                      "scans + bf16 mix; timed from HIP-graph replays"}
+            "packet_ms_fwd": ms_pf, "packet_ms_bwd": ms_pb, "packet_ms_fwd_composed": ms_cp,
+            "packet_fwd_bytes": pfb, "packet_bwd_bytes": pbb,
+            "packet_fwd_hbm_frac": pfb / (ms_pf * 1e-3) / HBM_PEAK,
+            "packet_bwd_hbm_frac": pbb / (ms_pb * 1e-3) / HBM_PEAK,
+            "config": "x and gate logits [15,2048,512] bf16, timescales 16/64/256; algorithmic bytes: pool fwd "
+                      "4 B/element (x read, pooled written), pool bwd 6 B/element (dpooled and x read, dx "
+                      "written); packet fwd 8 B/element (x and gate read, pooled and packet written) + 4 B/token "
+                      "(ms), packet bwd 12 B/element (dpacket, gate, pooled, x read; dgate, dx written) + 4 B/token; "
+                      "composed = three EMA scans + bf16 mix, composed packet = fused pool + PyTorch elementwise "
+                      "packet; timed from HIP-graph replays"}
 
 
 def long_context_extra(pkg, device, steps, warmup):

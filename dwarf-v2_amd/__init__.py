@@ -12,7 +12,8 @@ Public surface (reference names, Lanerra/dwarf-v2):
   npci_rotate                                        kernels/dsqg_attention_v22.py
   _plan_sparse_groups, _verify_sparse_plan,
   _normalize_grouping_args (planner module)          kernels/dsqg_attention_v22.py
-  interference_pool, interference_packet_forward     train/train_dwarf.py (InterferencePacket)
+  interference_pool, interference_packet,
+  interference_packet_forward                        train/train_dwarf.py (InterferencePacket)
   q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
 """
 
@@ -20,7 +21,7 @@ from . import _lib, lattice, npci, ops, packet, planner, probe, q6
 from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
 from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
 from .npci import npci_rotate
-from .packet import _InterferencePoolFn, interference_packet_forward, interference_pool
+from .packet import _InterferencePacketFn, _InterferencePoolFn, interference_packet, interference_packet_forward, interference_pool
 from .planner import _normalize_grouping_args, _plan_sparse_groups, _verify_sparse_plan
 from .probe import _PhaseProbeFn, phase_probe_features
 from .lattice import (
@@ -39,6 +40,7 @@ __all__ = [
     "GROUPED_MODE_IDS",
     "R_PLANES",
     "_DSQGV18GroupedFn",
+    "_InterferencePacketFn",
     "_InterferencePoolFn",
     "_PhaseProbeFn",
     "_canonicalize_offsets",
@@ -54,6 +56,7 @@ __all__ = [
     "dsqg_attention_v18_grouped",
     "dsqg_backward",
     "dsqg_forward",
+    "interference_packet",
     "interference_packet_forward",
     "interference_pool",
     "inverse_bounded_ema_factor",

@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -54,6 +54,9 @@ EXPORTED_SYMBOLS = (
     "dwarf_packet_pool_fwd",
     "dwarf_packet_pool_bwd_workspace_bytes",
     "dwarf_packet_pool_bwd",
+    "dwarf_packet_fwd",
+    "dwarf_packet_bwd_workspace_bytes",
+    "dwarf_packet_bwd",
 )
 
 
@@ -248,6 +251,28 @@ class PacketPoolBwdArgs(ctypes.Structure):
     ]
 
 
+class PacketFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("pool", PacketPoolFwdArgs),
+        ("packet_dtype", c_int32),
+        ("gate", c_void_p), ("gate_stride", _i64(3)),
+        ("packet", c_void_p), ("packet_stride", _i64(3)),
+        ("ms", c_void_p),
+    ]
+
+
+class PacketBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", PacketFwdArgs),
+        ("dpacket", c_void_p), ("dpacket_stride", _i64(3)),
+        ("dgate", c_void_p), ("dgate_stride", _i64(3)),
+        ("dx", c_void_p), ("dx_stride", _i64(3)),
+        ("dalpha", c_void_p),
+        ("dweight", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
+    ]
+
+
 class NativeLibraryError(RuntimeError):
     """The HIP library is missing, stale or failed a call."""
 
@@ -328,6 +353,12 @@ def load() -> ctypes.CDLL:
     lib.dwarf_packet_pool_bwd_workspace_bytes.argtypes = [POINTER(PacketPoolBwdArgs)]
     lib.dwarf_packet_pool_bwd.restype = c_int
     lib.dwarf_packet_pool_bwd.argtypes = [POINTER(PacketPoolBwdArgs), c_void_p]
+    lib.dwarf_packet_fwd.restype = c_int
+    lib.dwarf_packet_fwd.argtypes = [POINTER(PacketFwdArgs), c_void_p]
+    lib.dwarf_packet_bwd_workspace_bytes.restype = c_size_t
+    lib.dwarf_packet_bwd_workspace_bytes.argtypes = [POINTER(PacketBwdArgs)]
+    lib.dwarf_packet_bwd.restype = c_int
+    lib.dwarf_packet_bwd.argtypes = [POINTER(PacketBwdArgs), c_void_p]
     version = lib.dwarf_abi_version()
     if version != ABI_VERSION:
         raise NativeLibraryError(f"{LIB_NAME} ABI {version} does not match the binding's ABI {ABI_VERSION}")

@@ -36,6 +36,10 @@ size_t packet_bwd_workspace(int B, int N, int D, int K);
 int packet_max_scales();
 hipError_t launch_packet_fwd(const dwarf_packet_pool_fwd_args& a, hipStream_t stream);
 hipError_t launch_packet_bwd(const dwarf_packet_pool_bwd_args& a, hipStream_t stream);
+size_t interference_packet_bwd_workspace(int B, int N, int D, int K, int dtype);
+int packet_max_row_channels(int D);
+hipError_t launch_interference_packet_fwd(const dwarf_packet_fwd_args& a, hipStream_t stream);
+hipError_t launch_interference_packet_bwd(const dwarf_packet_bwd_args& a, hipStream_t stream);
 hipError_t launch_phase_probe_fwd(const dwarf_phase_probe_fwd_args& a, hipStream_t stream);
 hipError_t launch_phase_probe_bwd(const dwarf_phase_probe_bwd_args& a, hipStream_t stream);
 }  // namespace dwarf
@@ -357,6 +361,66 @@ int dwarf_packet_pool_fwd(const dwarf_packet_pool_fwd_args* args, dwarf_stream_t
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
   if (reinterpret_cast<uintptr_t>(a.workspace) & 15u) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
   return hip_status(dwarf::launch_packet_fwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_packet_pool_fwd");
+}
+
+static int check_packet_rows(const dwarf_packet_fwd_args& p, bool fwd) {
+  const dwarf_packet_pool_fwd_args& a = p.pool;
+  if (p.packet_dtype != DWARF_BF16 && p.packet_dtype != DWARF_F32)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "packet_dtype=%d", p.packet_dtype);
+  if (a.D > dwarf::packet_max_row_channels(a.D))
+    return fail(DWARF_ERR_UNSUPPORTED, "D=%d: a row's channels are one workgroup's lanes (D <= %d)", a.D,
+                dwarf::packet_max_row_channels(a.D));
+  int rc = check_packet(a, fwd);
+  if (rc) return rc;
+  if (packet_empty(a)) return DWARF_OK;
+  if ((rc = check_btd("gate", p.gate, p.gate_stride, p.packet_dtype, a.D))) return rc;
+  if (fwd && (rc = check_btd("packet", p.packet, p.packet_stride, p.packet_dtype, a.D))) return rc;
+  if (!fwd && (rc = check_btd("pooled", a.pooled, a.pooled_stride, a.dtype, a.D))) return rc;
+  if (!p.ms) return fail(DWARF_ERR_INVALID_ARGUMENT, "ms is NULL");
+  if (reinterpret_cast<uintptr_t>(p.ms) & 3u) return fail(DWARF_ERR_INVALID_ARGUMENT, "ms must be 4-byte aligned");
+  return DWARF_OK;
+}
+
+int dwarf_packet_fwd(const dwarf_packet_fwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_packet_fwd_args& p = *args;
+  int rc = check_packet_rows(p, true);
+  if (rc) return rc;
+  const dwarf_packet_pool_fwd_args& a = p.pool;
+  if (packet_empty(a)) return ok();
+  const size_t need = dwarf::packet_fwd_workspace(a.B, a.N, a.D, a.K);
+  if (!a.workspace || a.workspace_bytes < need)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(a.workspace) & 15u) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+  return hip_status(dwarf::launch_interference_packet_fwd(p, reinterpret_cast<hipStream_t>(stream)), "dwarf_packet_fwd");
+}
+
+size_t dwarf_packet_bwd_workspace_bytes(const dwarf_packet_bwd_args* a) {
+  const dwarf_packet_pool_fwd_args* f = a ? &a->fwd.pool : nullptr;
+  return f && f->K >= 1 && f->K <= DWARF_PACKET_MAX_SCALES && f->B >= 0 && f->N >= 0 && f->D >= 0
+             ? dwarf::interference_packet_bwd_workspace(f->B, f->N, f->D, f->K, f->dtype)
+             : 0;
+}
+
+int dwarf_packet_bwd(const dwarf_packet_bwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_packet_bwd_args& p = *args;
+  int rc = check_packet_rows(p.fwd, false);
+  if (rc) return rc;
+  const dwarf_packet_pool_fwd_args& f = p.fwd.pool;
+  if (packet_empty(f)) {   // the factor and weight gradients are sums over nothing
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if ((rc = zero_floats(p.dalpha, f.K, s, "dwarf_packet_bwd"))) return rc;
+    return zero_floats(p.dweight, f.K, s, "dwarf_packet_bwd");
+  }
+  if ((rc = check_btd("dpacket", p.dpacket, p.dpacket_stride, p.fwd.packet_dtype, f.D))) return rc;
+  if ((rc = check_btd("dgate", p.dgate, p.dgate_stride, p.fwd.packet_dtype, f.D))) return rc;
+  if ((rc = check_btd("dx", p.dx, p.dx_stride, f.dtype, f.D))) return rc;
+  const size_t need = dwarf::interference_packet_bwd_workspace(f.B, f.N, f.D, f.K, f.dtype);
+  if (!p.workspace || p.workspace_bytes < need)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, p.workspace_bytes);
+  if (reinterpret_cast<uintptr_t>(p.workspace) & 255u) return fail(DWARF_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return hip_status(dwarf::launch_interference_packet_bwd(p, reinterpret_cast<hipStream_t>(stream)), "dwarf_packet_bwd");
 }
 
 int dwarf_packet_pool_bwd(const dwarf_packet_pool_bwd_args* args, dwarf_stream_t stream) {

@@ -364,10 +364,221 @@ __global__ __launch_bounds__(kPkRedThreads) void packet_param_reduce(const float
   }
 }
 
+// ---- packet: RMS direction, confidence and gate (train:268-273) -----------
+// Per token, with u the stored pooled values and s = sigmoid(gate logit):
+//   ms = mean_d u^2,   r = rsqrt(ms + 1e-6),   conf = tanh(sqrt(ms) / 0.25)
+//   packet = G(((u r) conf) s)                 (G: the packet's dtype)
+// packet_fwd_rows is the pool's apply stage laid out by rows: one workgroup
+// per (batch row, 16-token chunk) with its lanes over all D channels (VEC
+// each), so after the chunk's scans are rescanned and pooled is stored, the
+// 16 tokens' ms are one two-level LDS sum (fixed order) away.
+constexpr int kPkRowMaxThreads = 1024;
+constexpr float kPkEps = 1e-6f;
+constexpr float kPkConfScale = 0.25f;
+
+__device__ __forceinline__ float pk_sigmoid(float z) { return 1.f / (1.f + __expf(-z)); }
+
+// Sum of row r of s_red ([16][nt]) in a fixed order: level 1 adds 16 entries
+// per (row, quarter-block), level 2 adds the nt / 16 partials of each row.
+// Every thread of the block calls it; returns the 16 sums in s_out.
+__device__ __forceinline__ void pk_rows_sum(float* s_red, float* s_mid, float* s_out) {
+  const int nt = blockDim.x, q = nt / 16;
+  __syncthreads();
+  {
+    const int r = threadIdx.x & 15, part = threadIdx.x >> 4;
+    const float* src = s_red + r * nt + part * 16;
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sum += src[e];
+    s_mid[r * q + part] = sum;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float sum = 0.f;
+    for (int part = 0; part < q; ++part) sum += s_mid[threadIdx.x * q + part];
+    s_out[threadIdx.x] = sum;
+  }
+  __syncthreads();
+}
+
+template <typename T, typename G, int VEC, int K>
+__global__ __launch_bounds__(kPkRowMaxThreads) void packet_fwd_rows(
+    const T* __restrict__ x, int64_t sxb, int64_t sxn, T* __restrict__ pooled, int64_t spb, int64_t spn,
+    const G* __restrict__ gate, int64_t sgb, int64_t sgn, G* __restrict__ packet, int64_t sqb, int64_t sqn,
+    float* __restrict__ ms, const float* __restrict__ alpha, const float* __restrict__ weight,
+    const float* __restrict__ state, EmaGeom g) {
+  extern __shared__ float s_pk[];
+  float* s_red = s_pk;                          // [16][nt]
+  float* s_mid = s_red + kChunkT * blockDim.x;  // [16][nt / 16]
+  float* s_ms = s_mid + blockDim.x;             // [16]
+  const int c = blockIdx.x % g.NC, b = blockIdx.x / g.NC;
+  const int dv = threadIdx.x;
+  const bool live = dv < g.DV;
+  const int d0 = dv * VEC;
+  const int t0 = c * kChunkT;
+  const int len = min(kChunkT, g.N - t0);
+  float u[kChunkT][VEC];
+#pragma unroll
+  for (int t = 0; t < kChunkT; ++t)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) u[t][i] = 0.f;
+  if (live) {
+    float a[K], wk[K], st[K][VEC];
+    const float* cr = state + (static_cast<int64_t>(b) * g.NC + c) * (K * g.D) + d0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      a[k] = pk_alpha(alpha, k, g);
+      wk[k] = rnd<T>(weight[k]);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) st[k][i] = cr[k * g.D + i];
+    }
+    const T* px = x + b * sxb + static_cast<int64_t>(t0) * sxn + d0;
+    T* po = pooled + b * spb + static_cast<int64_t>(t0) * spn + d0;
+    float xv[kChunkT][VEC];
+#pragma unroll
+    for (int t = 0; t < kChunkT; ++t)
+      if (t < len) ldv<T, VEC>(px + static_cast<int64_t>(t) * sxn, xv[t]);
+#pragma unroll
+    for (int t = 0; t < kChunkT; ++t)
+      if (t < len) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          float acc = 0.f;
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            st[k][i] = fmaf(a[k], xv[t][i], (1.f - a[k]) * st[k][i]);
+            const float term = rnd<T>(wk[k] * rnd<T>(st[k][i]));
+            acc = k == 0 ? term : rnd<T>(acc + term);
+          }
+          u[t][i] = acc;
+        }
+        stv<T, VEC>(po + static_cast<int64_t>(t) * spn, u[t]);
+      }
+  }
+#pragma unroll
+  for (int t = 0; t < kChunkT; ++t) {
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) sq = fmaf(u[t][i], u[t][i], sq);
+    s_red[t * blockDim.x + threadIdx.x] = sq;
+  }
+  pk_rows_sum(s_red, s_mid, s_ms);
+  const float inv_d = 1.f / static_cast<float>(g.D);
+  if (threadIdx.x < 16 && threadIdx.x < len) ms[static_cast<int64_t>(b) * g.N + t0 + threadIdx.x] = s_ms[threadIdx.x] * inv_d;
+  if (!live) return;
+  const G* pg = gate + b * sgb + static_cast<int64_t>(t0) * sgn + d0;
+  G* pq = packet + b * sqb + static_cast<int64_t>(t0) * sqn + d0;
+#pragma unroll
+  for (int t = 0; t < kChunkT; ++t)
+    if (t < len) {
+      const float m = s_ms[t] * inv_d;
+      const float r = rsqrtf(m + kPkEps);
+      const float conf = tanhf(sqrtf(m) / kPkConfScale);
+      float gl[VEC], out[VEC];
+      ldv<G, VEC>(pg + static_cast<int64_t>(t) * sgn, gl);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) out[i] = ((u[t][i] * r) * conf) * pk_sigmoid(gl[i]);
+      stv<G, VEC>(pq + static_cast<int64_t>(t) * sqn, out);
+    }
+}
+
+// Backward of the packet for KPB tokens per workgroup, lanes over channels.
+// With A = u r conf and S = sum_d G_d s_d u_d (G = dpacket):
+//   dgate = G(dpacket A s (1 - s))
+//   dms   = -0.5 r^3 conf S  +  r S (1 - conf^2) / 0.25 / (2 sqrt(ms))
+//   dpooled = T(dpacket s r conf + dms 2 u / D)
+// (the chain autograd forms for train:268-273; sqrt(ms) = 0 gives NaN there
+// as it does in the reference).  dpooled goes to the pool's backward.
+constexpr int kPkBwdTokens = 4;
+
+template <typename T, typename G, int VEC>
+__global__ __launch_bounds__(kPkRowMaxThreads) void packet_bwd_rows(
+    const T* __restrict__ pooled, int64_t spb, int64_t spn, const float* __restrict__ ms,
+    const G* __restrict__ gate, int64_t sgb, int64_t sgn, const G* __restrict__ dpacket, int64_t sdb, int64_t sdn,
+    T* __restrict__ dpooled, int64_t sab, int64_t san, G* __restrict__ dgate, int64_t seb, int64_t sen, EmaGeom g) {
+  __shared__ float s_red[kPkBwdTokens][kPkRowMaxThreads / kWave];
+  __shared__ float s_sum[kPkBwdTokens];
+  const int groups = (g.N + kPkBwdTokens - 1) / kPkBwdTokens;
+  const int tg = blockIdx.x % groups, b = blockIdx.x / groups;
+  const int t0 = tg * kPkBwdTokens;
+  const int len = min(kPkBwdTokens, g.N - t0);
+  const int dv = threadIdx.x;
+  const bool live = dv < g.DV;
+  const int d0 = dv * VEC;
+  float u[kPkBwdTokens][VEC], dp[kPkBwdTokens][VEC], sg[kPkBwdTokens][VEC];
+  float part[kPkBwdTokens];
+#pragma unroll
+  for (int t = 0; t < kPkBwdTokens; ++t) {
+    part[t] = 0.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) u[t][i] = dp[t][i] = sg[t][i] = 0.f;
+    if (live && t < len) {
+      const int64_t n = t0 + t;
+      float gl[VEC];
+      ldv<T, VEC>(pooled + b * spb + n * spn + d0, u[t]);
+      ldv<G, VEC>(gate + b * sgb + n * sgn + d0, gl);
+      ldv<G, VEC>(dpacket + b * sdb + n * sdn + d0, dp[t]);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        sg[t][i] = pk_sigmoid(gl[i]);
+        part[t] = fmaf(dp[t][i] * sg[t][i], u[t][i], part[t]);
+      }
+    }
+  }
+  // S per token: wave sums (fixed butterfly), then the waves in order
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+#pragma unroll
+  for (int t = 0; t < kPkBwdTokens; ++t) {
+    float v = part[t];
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o);
+    if (l == 0) s_red[t][w] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < kPkBwdTokens) {
+    float sum = 0.f;
+    for (int v = 0; v < static_cast<int>(blockDim.x) / kWave; ++v) sum += s_red[threadIdx.x][v];
+    s_sum[threadIdx.x] = sum;
+  }
+  __syncthreads();
+  if (!live) return;
+  const float two_over_d = 2.f / static_cast<float>(g.D);
+#pragma unroll
+  for (int t = 0; t < kPkBwdTokens; ++t)
+    if (t < len) {
+      const int64_t n = t0 + t;
+      const float m = ms[static_cast<int64_t>(b) * g.N + n];
+      const float r = rsqrtf(m + kPkEps);
+      const float rms = sqrtf(m);
+      const float conf = tanhf(rms / kPkConfScale);
+      const float S = s_sum[t];
+      const float dconf = r * S, dr = conf * S;
+      const float dms = dr * (-0.5f * r * r * r) + (dconf * (1.f - conf * conf) / kPkConfScale) / (2.f * rms);
+      float du[VEC], dgl[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float A = (u[t][i] * r) * conf;
+        du[i] = ((dp[t][i] * sg[t][i]) * conf) * r + dms * two_over_d * u[t][i];
+        dgl[i] = ((dp[t][i] * A) * (1.f - sg[t][i])) * sg[t][i];
+      }
+      stv<T, VEC>(dpooled + b * sab + n * san + d0, du);
+      stv<G, VEC>(dgate + b * seb + n * sen + d0, dgl);
+    }
+}
+
 inline int pk_nc(int N) { return (N + kChunkT - 1) / kChunkT; }
 
 inline size_t pk_state_floats(int B, int N, int D, int K) {
   return static_cast<size_t>(B) * pk_nc(N) * D * K;
+}
+
+// The pool backward's workspace: starts and carries (K*D per chunk each),
+// then 2K slots per apply workgroup (a lane takes at least one (chunk,
+// channel) pair, so at most ceil(B*NC*D / 256) workgroups).
+inline size_t pk_pool_bwd_ws(int B, int N, int D, int K) {
+  const size_t pairs = static_cast<size_t>(B) * pk_nc(N) * D;
+  return (2 * pk_state_floats(B, N, D, K) + 2 * static_cast<size_t>(K) * ((pairs + kEmaBlock - 1) / kEmaBlock)) *
+         sizeof(float);
 }
 
 // The geometry of the x-shaped stages (D channels, VEC per lane).
@@ -386,20 +597,43 @@ inline EmaGeom pk_carry_geom(int B, int N, int D, int K, float lo, float hi) {
   return g;
 }
 
+// The forward's local and carry stages: each chunk's incoming scan states in `state`.
 template <typename T, int VEC, int K>
-void pk_fwd_typed(const dwarf_packet_pool_fwd_args& a, hipStream_t stream) {
-  const EmaGeom g = pk_geom(a.B, a.N, a.D, VEC, a.floor_, a.ceiling);
+void pk_fwd_states(const dwarf_packet_pool_fwd_args& a, const EmaGeom& g, hipStream_t stream) {
   float* ends = static_cast<float*>(a.workspace);
   const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
-  const T* x = static_cast<const T*>(a.x);
-  hipLaunchKernelGGL((packet_fwd_local<T, VEC, K>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
-                     a.x_stride[1], a.alpha, ends, g);
+  hipLaunchKernelGGL((packet_fwd_local<T, VEC, K>), dim3(blocks), dim3(kEmaBlock), 0, stream,
+                     static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], a.alpha, ends, g);
   const EmaGeom gc = pk_carry_geom(a.B, a.N, a.D, K, a.floor_, a.ceiling);
   launch_carry<false, false>(ends, a.state, a.alpha, gc, a.B, K * a.D, stream);
-  hipLaunchKernelGGL((packet_fwd_apply<T, VEC, K>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
-                     a.x_stride[1], static_cast<T*>(a.pooled), a.pooled_stride[0], a.pooled_stride[1], a.alpha,
-                     a.weight, a.state, g);
+}
+
+template <typename T, int VEC, int K>
+void pk_fwd_typed(const dwarf_packet_pool_fwd_args& a, hipStream_t stream) {
+  const EmaGeom g = pk_geom(a.B, a.N, a.D, VEC, a.floor_, a.ceiling);
+  pk_fwd_states<T, VEC, K>(a, g, stream);
+  const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
+  const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
+  hipLaunchKernelGGL((packet_fwd_apply<T, VEC, K>), dim3(blocks), dim3(kEmaBlock), 0, stream,
+                     static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<T*>(a.pooled),
+                     a.pooled_stride[0], a.pooled_stride[1], a.alpha, a.weight, a.state, g);
+}
+
+inline int pk_row_threads(int DV) { return (DV + kWave - 1) / kWave * kWave; }
+
+template <typename T, typename G, int VEC, int K>
+void pkt_fwd_typed(const dwarf_packet_fwd_args& p, hipStream_t stream) {
+  const dwarf_packet_pool_fwd_args& a = p.pool;
+  const EmaGeom g = pk_geom(a.B, a.N, a.D, VEC, a.floor_, a.ceiling);
+  pk_fwd_states<T, VEC, K>(a, g, stream);
+  const int nt = pk_row_threads(g.DV);
+  const size_t lds = static_cast<size_t>(kChunkT * nt + nt + 16) * sizeof(float);
+  hipLaunchKernelGGL((packet_fwd_rows<T, G, VEC, K>), dim3(a.B * g.NC), dim3(nt), lds, stream,
+                     static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<T*>(a.pooled),
+                     a.pooled_stride[0], a.pooled_stride[1], static_cast<const G*>(p.gate), p.gate_stride[0],
+                     p.gate_stride[1], static_cast<G*>(p.packet), p.packet_stride[0], p.packet_stride[1], p.ms,
+                     a.alpha, a.weight, a.state, g);
 }
 
 template <typename T, int VEC, int VA, int K>
@@ -449,18 +683,57 @@ void pk_bwd_k(const dwarf_packet_pool_bwd_args& a, hipStream_t s) {
   }
 }
 
+template <typename T, typename G, int VEC, int VA>
+void pkt_fwd_k(const dwarf_packet_fwd_args& a, hipStream_t s) {
+  switch (a.pool.K) {
+    case 1: pkt_fwd_typed<T, G, VEC, 1>(a, s); break;
+    case 2: pkt_fwd_typed<T, G, VEC, 2>(a, s); break;
+    case 3: pkt_fwd_typed<T, G, VEC, 3>(a, s); break;
+    default: pkt_fwd_typed<T, G, VEC, 4>(a, s); break;
+  }
+}
+
+// The packet's backward: dpooled (into the workspace after the pool's part)
+// and dgate from the rows kernel, then the pool's backward on that dpooled.
+template <typename T, typename G, int VEC, int VA>
+void pkt_bwd_k(const dwarf_packet_bwd_args& p, hipStream_t s) {
+  const dwarf_packet_pool_fwd_args& f = p.fwd.pool;
+  const EmaGeom g = pk_geom(f.B, f.N, f.D, VEC, f.floor_, f.ceiling);
+  const size_t pool_ws = (pk_pool_bwd_ws(f.B, f.N, f.D, f.K) + 255) / 256 * 256;
+  T* dpooled = reinterpret_cast<T*>(static_cast<char*>(p.workspace) + pool_ws);
+  const int64_t dsn = f.D, dsb = static_cast<int64_t>(f.N) * f.D;
+  const int nt = pk_row_threads(g.DV);
+  const int groups = (f.N + kPkBwdTokens - 1) / kPkBwdTokens;
+  hipLaunchKernelGGL((packet_bwd_rows<T, G, VEC>), dim3(f.B * groups), dim3(nt), 0, s,
+                     static_cast<const T*>(f.pooled), f.pooled_stride[0], f.pooled_stride[1], p.fwd.ms,
+                     static_cast<const G*>(p.fwd.gate), p.fwd.gate_stride[0], p.fwd.gate_stride[1],
+                     static_cast<const G*>(p.dpacket), p.dpacket_stride[0], p.dpacket_stride[1], dpooled, dsb, dsn,
+                     static_cast<G*>(p.dgate), p.dgate_stride[0], p.dgate_stride[1], g);
+  dwarf_packet_pool_bwd_args pb{};
+  pb.fwd = f;
+  pb.dpooled = dpooled;
+  pb.dpooled_stride[0] = dsb; pb.dpooled_stride[1] = dsn; pb.dpooled_stride[2] = 1;
+  pb.dx = p.dx;
+  for (int i = 0; i < 3; ++i) pb.dx_stride[i] = p.dx_stride[i];
+  pb.dalpha = p.dalpha;
+  pb.dweight = p.dweight;
+  pb.workspace = p.workspace;
+  pb.workspace_bytes = pool_ws;
+  pk_bwd_k<T, VEC, VA>(pb, s);
+}
+
 }  // namespace
 
 size_t packet_state_bytes(int B, int N, int D, int K) { return pk_state_floats(B, N, D, K) * sizeof(float); }
 size_t packet_fwd_workspace(int B, int N, int D, int K) { return pk_state_floats(B, N, D, K) * sizeof(float); }
-// starts and carries (K*D per chunk each), then 2K slots per apply workgroup
-// (a lane takes at least one (chunk, channel) pair, so at most
-// ceil(B*NC*D / 256) workgroups).
-size_t packet_bwd_workspace(int B, int N, int D, int K) {
-  const size_t pairs = static_cast<size_t>(B) * pk_nc(N) * D;
-  return (2 * pk_state_floats(B, N, D, K) + 2 * static_cast<size_t>(K) * ((pairs + kEmaBlock - 1) / kEmaBlock)) *
-         sizeof(float);
+size_t packet_bwd_workspace(int B, int N, int D, int K) { return pk_pool_bwd_ws(B, N, D, K); }
+// The pool's backward workspace, then dpooled [B,N,D] of the pool dtype.
+size_t interference_packet_bwd_workspace(int B, int N, int D, int K, int dtype) {
+  return (pk_pool_bwd_ws(B, N, D, K) + 255) / 256 * 256 +
+         static_cast<size_t>(B) * N * D * (dtype == DWARF_BF16 ? 2 : 4);
 }
+// A row's channels are the lanes of one workgroup: 4 per lane when D % 4 == 0.
+int packet_max_row_channels(int D) { return D % 4 == 0 ? kPkRowMaxThreads * 4 : kPkRowMaxThreads; }
 int packet_max_scales() { return kMaxScales; }
 
 // Lanes take 4 channels in the streaming stages when D % 4 == 0 (rows are
@@ -487,6 +760,44 @@ hipError_t launch_packet_bwd(const dwarf_packet_pool_bwd_args& a, hipStream_t st
     if (vec4) pk_bwd_k<float, 4, 1>(a, stream);
     else pk_bwd_k<float, 1, 1>(a, stream);
   }
+  return hipGetLastError();
+}
+
+// The packet kernels take 4 channels per lane when D % 4 == 0, else 1; the
+// pool's backward as above.
+template <typename G>
+void ipk_fwd_pool(const dwarf_packet_fwd_args& a, hipStream_t stream) {
+  const bool vec4 = (a.pool.D % 4) == 0;
+  if (a.pool.dtype == DWARF_BF16) {
+    if (vec4) pkt_fwd_k<bf16, G, 4, 2>(a, stream);
+    else pkt_fwd_k<bf16, G, 1, 1>(a, stream);
+  } else {
+    if (vec4) pkt_fwd_k<float, G, 4, 1>(a, stream);
+    else pkt_fwd_k<float, G, 1, 1>(a, stream);
+  }
+}
+
+template <typename G>
+void ipk_bwd_pool(const dwarf_packet_bwd_args& a, hipStream_t stream) {
+  const bool vec4 = (a.fwd.pool.D % 4) == 0;
+  if (a.fwd.pool.dtype == DWARF_BF16) {
+    if (vec4) pkt_bwd_k<bf16, G, 4, 2>(a, stream);
+    else pkt_bwd_k<bf16, G, 1, 1>(a, stream);
+  } else {
+    if (vec4) pkt_bwd_k<float, G, 4, 1>(a, stream);
+    else pkt_bwd_k<float, G, 1, 1>(a, stream);
+  }
+}
+
+hipError_t launch_interference_packet_fwd(const dwarf_packet_fwd_args& a, hipStream_t stream) {
+  if (a.packet_dtype == DWARF_BF16) ipk_fwd_pool<bf16>(a, stream);
+  else ipk_fwd_pool<float>(a, stream);
+  return hipGetLastError();
+}
+
+hipError_t launch_interference_packet_bwd(const dwarf_packet_bwd_args& a, hipStream_t stream) {
+  if (a.fwd.packet_dtype == DWARF_BF16) ipk_bwd_pool<bf16>(a, stream);
+  else ipk_bwd_pool<float>(a, stream);
   return hipGetLastError();
 }
 

@@ -2,10 +2,11 @@
 
 ``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::ema_fwd``,
 ``dwarf::ema_bwd``, ``dwarf::phase_probe_fwd``, ``dwarf::phase_probe_bwd``,
-``dwarf::npci_fwd``, ``dwarf::npci_bwd``, ``dwarf::packet_pool_fwd`` and
-``dwarf::packet_pool_bwd`` are custom ops with fake (shape-only)
-implementations, so ``torch.compile`` traces the DSQG, EMA, phase-probe, NPCI
-and InterferencePacket-pool autograd Functions without graph breaks (the trainer
+``dwarf::npci_fwd``, ``dwarf::npci_bwd``, ``dwarf::packet_pool_fwd``,
+``dwarf::packet_pool_bwd``, ``dwarf::packet_fwd`` and ``dwarf::packet_bwd`` are
+custom ops with fake (shape-only) implementations, so ``torch.compile`` traces
+the DSQG, EMA, phase-probe, NPCI and InterferencePacket autograd Functions
+without graph breaks (the trainer
 compiles the model, train:1083).  The real
 implementations normalise layouts (unit head-dim stride, 16-byte rows,
 contiguous fp32 tables and plane features, int32 offsets on the device) and
@@ -176,3 +177,31 @@ def packet_pool_bwd(x: Tensor, alpha: Tensor, weight: Tensor, state: Tensor, dpo
 def _packet_pool_bwd_fake(x, alpha, weight, state, dpooled, floor, ceiling):
     return (x.new_empty(x.shape), x.new_empty((alpha.numel(),), dtype=torch.float32),
             x.new_empty((alpha.numel(),), dtype=torch.float32))
+
+
+# ---- InterferencePacket packet ---------------------------------------------------------------
+@torch.library.custom_op("dwarf::packet_fwd", mutates_args=())
+def packet_fwd(x: Tensor, alpha: Tensor, weight: Tensor, gate: Tensor, floor: float,
+               ceiling: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(packet with gate's dtype, pooled with x's dtype, per-chunk scan states fp32, ms [B,N] fp32)."""
+    return _packet.packet_forward(x, alpha, weight, gate, floor, ceiling)
+
+
+@packet_fwd.register_fake
+def _packet_fwd_fake(x, alpha, weight, gate, floor, ceiling):
+    return (x.new_empty(x.shape, dtype=gate.dtype), x.new_empty(x.shape),
+            x.new_empty(_packet.state_shape(x, alpha.numel()), dtype=torch.float32),
+            x.new_empty(x.shape[:2], dtype=torch.float32))
+
+
+@torch.library.custom_op("dwarf::packet_bwd", mutates_args=())
+def packet_bwd(x: Tensor, alpha: Tensor, weight: Tensor, gate: Tensor, pooled: Tensor, state: Tensor, ms: Tensor,
+               dpacket: Tensor, floor: float, ceiling: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(dx with x's dtype, dalpha [K] fp32 clamp-projected, dweight [K] fp32, dgate with gate's dtype)."""
+    return _packet.packet_backward(x, alpha, weight, gate, pooled, state, ms, dpacket, floor, ceiling)
+
+
+@packet_bwd.register_fake
+def _packet_bwd_fake(x, alpha, weight, gate, pooled, state, ms, dpacket, floor, ceiling):
+    return (x.new_empty(x.shape), x.new_empty((alpha.numel(),), dtype=torch.float32),
+            x.new_empty((alpha.numel(),), dtype=torch.float32), x.new_empty(x.shape, dtype=gate.dtype))

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 5
+#define DWARF_ABI_VERSION 6
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
@@ -269,6 +269,51 @@ size_t dwarf_packet_pool_bwd_workspace_bytes(const dwarf_packet_pool_bwd_args* a
 /* The gradients autograd forms for those K scans and the mix: x (summed over
  * the scans), each factor, each weight. */
 int dwarf_packet_pool_bwd(const dwarf_packet_pool_bwd_args* args, dwarf_stream_t stream);
+
+/*
+ * InterferencePacket packet (train:262-273): the pool above, then per token,
+ * with u the pooled values as stored,
+ *   ms = mean_d u^2                      (written to ms[b*N + n], fp32)
+ *   packet = P(((u rsqrt(ms + 1e-6)) tanh(sqrt(ms) / 0.25)) sigmoid(gate))
+ * where gate [B,N,D] holds gate_proj's output (the logits) and P is
+ * packet_dtype, the dtype of gate and packet (the reference casts the packet
+ * to the block input's dtype).  pool.pooled is written (the backward reads
+ * it); pool.workspace and pool.state as for the pool.  D <= 4096 (D <= 1024
+ * when D % 4 != 0): a row's channels are the lanes of one workgroup.
+ */
+typedef struct {
+  dwarf_packet_pool_fwd_args pool;
+  int32_t packet_dtype;
+  const void* gate; int64_t gate_stride[3];
+  void* packet; int64_t packet_stride[3];
+  float* ms;  /* [B*N] */
+} dwarf_packet_fwd_args;
+
+/* Replaces InterferencePacket.forward up to the packet (train:262-273): the
+ * K scans, their mix, the RMS direction, the confidence and the gate. */
+int dwarf_packet_fwd(const dwarf_packet_fwd_args* args, dwarf_stream_t stream);
+
+/*
+ * fwd as passed to the forward (pool.x, pool.pooled, pool.state, gate and ms
+ * read); dpacket [B,N,D] and dgate [B,N,D] (the gradient of the logits) of
+ * packet_dtype; dx, dalpha, dweight as for the pool's backward.
+ */
+typedef struct {
+  dwarf_packet_fwd_args fwd;
+  const void* dpacket; int64_t dpacket_stride[3];
+  void* dgate; int64_t dgate_stride[3];
+  void* dx; int64_t dx_stride[3];
+  float* dalpha;
+  float* dweight;
+  void* workspace; size_t workspace_bytes;
+} dwarf_packet_bwd_args;
+
+/* The pool backward's workspace plus B*N*D values of pool.dtype (dpooled). */
+size_t dwarf_packet_bwd_workspace_bytes(const dwarf_packet_bwd_args* args);
+
+/* The gradients autograd forms for train:262-273: x, each factor, each
+ * weight and the gate logits.  sqrt(ms) = 0 gives NaN as in the reference. */
+int dwarf_packet_bwd(const dwarf_packet_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Phase-probe features  y[b,h,n,r] = <x, p_r> / sqrt(|x|^2 + 1e-6 hd)       */

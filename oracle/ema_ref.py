@@ -8,7 +8,9 @@ channel ([D]); ``_reference`` broadcasts a [D] alpha the same way.  An
 optional reset_mask [B,N] zeroes the state before the tokens it marks
 (ema:368-509, 533-535).  ``interference_pool`` and its backward restate the
 InterferencePacket's K scans of one input and their weighted sum
-(train/train_dwarf.py:260-267) on top of these.
+(train/train_dwarf.py:260-267) on top of these, and ``packet_from_pooled``
+the packet that InterferencePacket.forward forms from the pool
+(train:268-273), differentiable so its gradients come from autograd.
 """
 
 from __future__ import annotations
@@ -114,3 +116,17 @@ def interference_pool_backward(x: torch.Tensor, factors: torch.Tensor, weights: 
         dfs.append(dak.reshape(()))
         dws.append((g * scan).to(acc).sum().to(dt).to(acc))
     return dx.to(dt), torch.stack(dfs), torch.stack(dws)
+
+
+def packet_from_pooled(pooled: torch.Tensor, gate_logits: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    """train:268-273: with u = pooled in fp32 (fp64 for fp64 input), rms = sqrt(mean u^2),
+    direction = u rsqrt(mean u^2 + 1e-6), confidence = tanh(rms / 0.25), gate = sigmoid(logits),
+    packet = (direction * confidence * gate) cast to out_dtype."""
+    acc = torch.float64 if pooled.dtype == torch.float64 else torch.float32
+    u = pooled.to(acc)
+    rms = u.square().mean(-1, keepdim=True).sqrt()
+    direction = u * torch.rsqrt(u.square().mean(-1, keepdim=True) + 1e-6)
+    confidence = torch.tanh(rms / 0.25)
+    gate = torch.sigmoid(gate_logits.to(acc))
+    return (direction * confidence * gate).to(out_dtype)
+

@@ -29,7 +29,7 @@ def lib(pkg):
 
 def test_exports_every_declared_symbol(pkg, lib):
     names = declared_functions()
-    assert len(names) == 29
+    assert len(names) == 32
     assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
     for name in names:
         assert hasattr(lib, name), name
@@ -49,6 +49,8 @@ STRUCTS = {
     "dwarf_npci_bwd_args": "NpciBwdArgs",
     "dwarf_packet_pool_fwd_args": "PacketPoolFwdArgs",
     "dwarf_packet_pool_bwd_args": "PacketPoolBwdArgs",
+    "dwarf_packet_fwd_args": "PacketFwdArgs",
+    "dwarf_packet_bwd_args": "PacketBwdArgs",
 }
 
 
@@ -145,6 +147,21 @@ def test_validation_errors_without_gpu(pkg, lib):
     assert lib.dwarf_packet_pool_bwd(ctypes.byref(kb), None) == L.DWARF_ERR_INVALID_ARGUMENT
     # starts and carries [B][N/16][K*D] fp32, then 2K slots per apply workgroup (one here)
     assert lib.dwarf_packet_pool_bwd_workspace_bytes(ctypes.byref(kb)) == (2 * 1 * 2 * 3 * 8 + 2 * 3) * 4
+    pf = L.PacketFwdArgs()
+    pf.pool = k
+    pf.pool.floor_, pf.pool.ceiling = 1e-5, 0.5
+    pf.pool.alpha = pf.pool.weight = 0x10000
+    pf.packet_dtype = 7
+    assert lib.dwarf_packet_fwd(ctypes.byref(pf), None) == L.DWARF_ERR_INVALID_ARGUMENT   # packet dtype
+    assert b"packet_dtype" in lib.dwarf_last_error()
+    pf.packet_dtype, pf.pool.D = L.DWARF_BF16, 4100
+    assert lib.dwarf_packet_fwd(ctypes.byref(pf), None) == L.DWARF_ERR_UNSUPPORTED       # D above 4096
+    pbk = L.PacketBwdArgs()
+    pbk.fwd = pf
+    pbk.fwd.pool.D = 8
+    # the pool's backward workspace (256-byte aligned), then dpooled [B,N,D] bf16
+    assert lib.dwarf_packet_bwd_workspace_bytes(ctypes.byref(pbk)) == 512 + 1 * 32 * 8 * 2   # 408 -> 512
+    assert lib.dwarf_packet_bwd(ctypes.byref(pbk), None) == L.DWARF_ERR_INVALID_ARGUMENT  # x is NULL
 
 
 def _fake_fwd(L, B, H, H_kv, N, J, J_small):

@@ -12,6 +12,14 @@ join many chunks, B*K*D wide enough for the 64- and 32-channel carry runs, a
 strided x view, a factor outside [floor, ceiling];
 determinism and torch.compile; and ``interference_packet_forward`` against
 the same module composed of separate ``causal_ema_scan`` calls.
+
+The packet (``interference_packet``, train:262-273): the packet against
+oracle/ema_ref.py's packet_from_pooled of the kernel's own pooled values
+(fp32 within 1e-5 relative; bf16 within one bf16 ulp (2^-7 |value|) plus 1e-6,
+the cast's own rounding on both sides), pooled against the pool oracle as
+above; the gradients against autograd through packet_from_pooled (dgate:
+fp32 1e-5 relative, bf16 the same one-ulp bar; dpooled as autograd rounds it to
+the pool dtype) followed by interference_pool_backward, at the pool's bars.
 """
 
 import pytest
@@ -199,3 +207,110 @@ def test_empty_sequence(pkg, device):
     torch.cuda.synchronize()
     assert x.grad.shape == x.shape
     assert torch.equal(a.grad.cpu(), torch.zeros(3)) and torch.equal(w.grad.cpu(), torch.zeros(3))
+
+
+def packet_inputs(B, N, D, K, dtype, gdtype, seed):
+    x, a, w, dp = inputs(B, N, D, K, dtype, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    gate = (1.5 * torch.randn(B, N, D, generator=g)).to(gdtype)
+    dpk = torch.randn(B, N, D, generator=g).to(gdtype)
+    return x, a, w, gate, dpk
+
+
+def packet_oracle(x, a, w, gate, pooled, dpk):
+    """(packet from the kernel's pooled, dx, dalpha, dweight, dgate): autograd through packet_from_pooled
+    (fp64 for fp32 tensors), then interference_pool_backward on the pooled gradient autograd forms."""
+    wide = x.dtype == torch.float32
+    u = (pooled.double() if wide else pooled).clone().requires_grad_(True)
+    gl = (gate.double() if gate.dtype == torch.float32 else gate).clone().requires_grad_(True)
+    out = ema_ref.packet_from_pooled(u, gl, gl.dtype)
+    out.backward(dpk.to(out.dtype))
+    xs, av, wv = (x.double(), a.double(), w.double()) if wide else (x, a, w)
+    rdx, rda, rdw = ema_ref.interference_pool_backward(xs, av, wv, u.grad)
+    return out.detach(), rdx, rda, rdw, gl.grad
+
+
+def bf16_close(got, ref, floor=1e-6, rel=2.0 ** -7):
+    g, r = got.double(), ref.double()
+    return float(((g - r).abs() - (floor + rel * r.abs())).max()) <= 0
+
+
+@pytest.mark.parametrize("dtype,gdtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                          (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("B,N,D,K", [(2, 37, 64, 3), (1, 9, 12, 2), (2, 300, 512, 3), (1, 50, 1000, 4),
+                                     (1, 20, 4096, 1)])
+def test_packet_matches_oracle(pkg, device, dtype, gdtype, B, N, D, K):
+    x, a, w, gate, dpk = packet_inputs(B, N, D, K, dtype, gdtype, seed=N + D + K)
+    packet_mod = pkg.packet
+    xd, ad, wd, gd = x.to(device), a.to(device), w.to(device), gate.to(device)
+    pk, pooled, state, ms = packet_mod.packet_forward(xd, ad, wd, gd, 1e-5, 0.5)
+    dx, da, dw, dg = packet_mod.packet_backward(xd, ad, wd, gd, pooled, state, ms, dpk.to(device), 1e-5, 0.5)
+    torch.cuda.synchronize()
+    pk, pooled, ms, dx, da, dw, dg = (t.cpu() for t in (pk, pooled, ms, dx, da, dw, dg))
+    assert pk.dtype == gdtype and dg.dtype == gdtype and pooled.dtype == dtype
+    wide = dtype == torch.float32
+    ref_pool = ema_ref.interference_pool(*((x.double(), a.double(), w.double()) if wide else (x, a, w)))
+    rpk, rdx, rda, rdw, rdg = packet_oracle(x, a, w, gate, pooled, dpk)
+    assert torch.allclose(ms.double(), pooled.double().square().mean(-1), rtol=1e-5, atol=1e-12)
+    if dtype == torch.float32:
+        assert rel_err(pooled, ref_pool) < 1e-5
+        assert rel_err(pk, rpk) < 1e-5
+        assert rel_err(dg, rdg) < 1e-5
+        assert rel_err(dx, rdx) < 1e-5
+        assert rel_err(da, rda) < 1e-4
+        assert rel_err(dw, rdw) < 1e-4
+    else:
+        assert max_abs(pooled.float(), ref_pool.float()) < 2e-2
+        if gdtype == torch.float32:
+            assert rel_err(pk, rpk) < 1e-5
+            assert rel_err(dg, rdg) < 1e-5
+        else:
+            assert bf16_close(pk, rpk)
+            assert bf16_close(dg, rdg)
+        assert max_abs(dx.float(), rdx.float()) < 2e-2
+        assert rel_err(da, rda) < 1e-3
+        assert rel_err(dw, rdw) < 1e-2
+
+
+def test_packet_deterministic_compile_and_graph(pkg, device):
+    """interference_packet twice bit-equal, under torch.compile (fullgraph) bit-equal to eager, and its raw
+    forward + backward launches replayed from a HIP graph equal to eager on every replay."""
+    x, a, w, gate, dpk = packet_inputs(2, 300, 512, 3, torch.bfloat16, torch.bfloat16, seed=21)
+    x, a, w, gate, dpk = (t.to(device) for t in (x, a, w, gate, dpk))
+
+    def step(xx, aa, ww, gg):
+        return (pkg.interference_packet(xx, aa, ww, gg).float() * dpk.float()).sum()
+
+    results = []
+    for fn in (step, step, torch.compile(step, backend="aot_eager", fullgraph=True)):
+        leaves = [t.clone().requires_grad_(True) for t in (x, a, w, gate)]
+        loss = fn(*leaves)
+        loss.backward()
+        torch.cuda.synchronize()
+        results.append([loss.detach()] + [t.grad for t in leaves])
+    for other in results[1:]:
+        assert all(torch.equal(u, v) for u, v in zip(results[0], other))
+
+    packet = pkg.packet
+
+    def launches():
+        pk, pooled, state, ms = packet.packet_forward(x, a, w, gate, 1e-5, 0.5)
+        return (pk, pooled, ms) + packet.packet_backward(x, a, w, gate, pooled, state, ms, dpk, 1e-5, 0.5)
+
+    ref = [t.clone() for t in launches()]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launches()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = launches()
+    for _ in range(3):
+        packet.packet_forward(dpk, a, w, gate, 1e-5, 0.5)   # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(u, v) for u, v in zip(outs, ref))
+

@@ -6,6 +6,7 @@ ema:7-11 must equal autograd through the recurrence.
 """
 
 import importlib
+import math
 
 import pytest
 import torch
@@ -103,3 +104,37 @@ def test_reset_adjoint_equals_autograd(per_channel):
     dx, da = ema_ref.ema_adjoint(x.detach(), y.detach(), dy, alpha.detach(), reset_mask=reset)
     assert float((dx - gx).abs().max()) < 1e-12
     assert float((da - ga).abs().max()) < 1e-11
+
+
+def test_packet_known_answers():
+    """Rows with closed-form packets (train:268-273): a constant row c gives rms |c|, direction
+    c / sqrt(c^2 + 1e-6) and confidence tanh(|c| / 0.25); tanh(1) and sigmoid(0) = 1/2, sigmoid(ln 3) = 3/4
+    are textbook values."""
+    D = 64
+    tanh1 = 0.7615941559557649
+    u = torch.full((1, 3, D), 0.25, dtype=torch.float64)
+    u[0, 1] = -0.25
+    u[0, 2, : D // 2], u[0, 2, D // 2:] = 0.5, -0.5           # rms 0.5: tanh(2)
+    logits = torch.zeros(1, 3, D, dtype=torch.float64)
+    logits[0, 1] = math.log(3.0)
+    got = ema_ref.packet_from_pooled(u, logits, torch.float64)
+    d = 0.25 / math.sqrt(0.0625 + 1e-6)
+    assert torch.allclose(got[0, 0], torch.full((D,), d * tanh1 * 0.5, dtype=torch.float64), rtol=1e-15)
+    assert torch.allclose(got[0, 1], torch.full((D,), -d * tanh1 * 0.75, dtype=torch.float64), rtol=1e-15)
+    d2 = 0.5 / math.sqrt(0.25 + 1e-6)
+    want = torch.tensor([d2] * (D // 2) + [-d2] * (D // 2), dtype=torch.float64) * math.tanh(2.0) * 0.5
+    assert torch.allclose(got[0, 2], want, rtol=1e-15)
+
+
+def test_packet_direction_has_unit_rms_and_gradcheck():
+    g = torch.Generator().manual_seed(3)
+    u = torch.randn(2, 5, 16, generator=g, dtype=torch.float64)
+    logits = torch.randn(2, 5, 16, generator=g, dtype=torch.float64)
+    big = torch.full_like(logits, 60.0)                         # sigmoid -> 1
+    p = ema_ref.packet_from_pooled(u, big, torch.float64)
+    ms = u.square().mean(-1, keepdim=True)
+    conf = torch.tanh(ms.sqrt() / 0.25)
+    assert torch.allclose((p / conf).square().mean(-1, keepdim=True), ms / (ms + 1e-6), rtol=1e-12)
+    u.requires_grad_(True)
+    logits.requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda a, b: ema_ref.packet_from_pooled(a, b, torch.float64), (u, logits))
