@@ -87,13 +87,19 @@ def test_fp32_gqa_and_query_start(pkg, device):
 
 @pytest.mark.parametrize("case", ["movt_small", "gqa", "lattice96"])
 def test_fp32_matches_reference_golden(pkg, device, case):
-    """The reference's own eager outputs and gradients (float64 fixtures)."""
+    """The reference's own eager outputs and gradients (float64 fixtures).  The kernels see the inputs
+    rounded to fp32: against the oracle on those same inputs (float64 evaluation) they meet the fp32 bar,
+    1e-5 relative; against the fixtures, which saw the unrounded inputs, 1e-5 plus that rounding (2e-5)."""
     data = np.load(os.path.join(GOLDEN, f"dsqg_eager_{case}.npz"))
     B, H, Hkv, N, hd, js, jl, shift = [int(v) for v in data["meta"]]
     x = {n: torch.from_numpy(data[f"in_{n}"]).float() for n in NAMES}
     offsets = data["offsets"].tolist()
-    out, grads = gpu_fwd_bwd(pkg, x, offsets, js, shift, 0, torch.from_numpy(data["dout"]).float(), device)
-    # inputs were rounded from float64 to fp32, so compare at 1e-5 relative plus that rounding
+    dout = torch.from_numpy(data["dout"]).float()
+    out, grads = gpu_fwd_bwd(pkg, x, offsets, js, shift, 0, dout, device)
+    ro, _, rg = oracle_fwd_bwd(x, offsets, js, shift, 0, dout, round_se=False)
+    assert rel_err(out, ro) < FP32_REL
+    for n in NAMES:
+        assert rel_err(grads[n], rg[n]) < FP32_REL, n
     assert rel_err(out, torch.from_numpy(data["out"])) < 2e-5
     for n in NAMES:
         assert rel_err(grads[n], torch.from_numpy(data[f"grad_{n}"])) < 2e-5, n
@@ -217,8 +223,7 @@ def test_empty_batch(pkg, device):
 def test_maximum_offsets_bf16(pkg, device):
     """J = 256, the most offsets the kernels take (17 near, 239 far: 48..286): LDS tables past 64 KB per
     workgroup (gfx950 allows 160 KB).  Output and all 9 gradients against the float64 oracle within the
-    bf16 bar (2e-2 max-abs, times the gradient's largest magnitude where that exceeds 1: the table
-    gradients sum over every pair)."""
+    plain bf16 bar, 2e-2 max-abs (the largest error measured is 7.6e-3, on dv)."""
     offsets = list(range(1, 18)) + list(range(48, 48 + 239))
     x = make_inputs(1, 2, 2, 320, offsets, 17, seed=71, dtype=torch.bfloat16)
     dout = torch.randn(1, 2, 320, 64, generator=torch.Generator().manual_seed(72)).to(torch.bfloat16)
@@ -226,8 +231,7 @@ def test_maximum_offsets_bf16(pkg, device):
     rout, _, rgrads = oracle_fwd_bwd(x, offsets, 17, 0, 1, dout.float(), True)
     assert max_abs(out.float(), rout) < BF16_ABS
     for n in NAMES:
-        scale = max(1.0, rgrads[n].abs().max().item())
-        assert max_abs(grads[n].float(), rgrads[n]) < BF16_ABS * scale, n
+        assert max_abs(grads[n].float(), rgrads[n]) < BF16_ABS, n
 
 
 @pytest.mark.parametrize("mode,online", [(1, True), (3, True), (0, False), (3, False)])
