@@ -14,6 +14,7 @@
 #include "common.h"
 #include "dsqg_internal.h"
 #include "gather.h"
+#include "mfma.h"
 
 namespace dwarf {
 namespace {
@@ -172,10 +173,16 @@ constexpr int kKPB = 64;       // keys per workgroup
 constexpr int kChunkKv = 1;    // offsets per prefetch chunk
 constexpr int kMinWgKv = 3;    // workgroups per CU the register budget is sized for
 constexpr int kERowKv = 72;    // bf16 E row stride (elements)
+// Near band: the leading small offsets j < JB (ascending, unique, at most
+// kBandMaxKv) are served on the matrix cores from Q / dO windows of the
+// queries [m0, m0 + 96) of the workgroup's 64 keys; the gather loop takes the
+// other offsets.
+constexpr int kBandMaxKv = 32;
+constexpr int kWinRowsKv = kKPB + kBandMaxKv;   // 96 query rows of 128 bytes per window
 
 struct KvLayout {
   int JE, JL4, list_len, group;
-  size_t off_ph, off_list, off_e, bytes;
+  size_t off_ph, off_list, off_e, off_jn, off_win, off_dl, bytes;
 };
 
 __host__ __device__ inline KvLayout kv_layout(int J, int J_large, int group, int CJ) {
@@ -187,7 +194,10 @@ __host__ __device__ inline KvLayout kv_layout(int J, int J_large, int group, int
   L.off_ph = static_cast<size_t>(group + 1) * L.JE * 4;                  // s_pb2[group][JE], s_off[JE]
   L.off_list = L.off_ph + static_cast<size_t>(group) * L.JL4 * 4 * 8;    // s_ph[group][JL4][4] float2
   L.off_e = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;        // s_list[4][list_len] int2
-  L.bytes = L.off_e + static_cast<size_t>(L.JE) * kERowKv * 2;           // sE[JE][72] bf16
+  L.off_jn = L.off_e + static_cast<size_t>(L.JE) * kERowKv * 2;          // sE[JE][72] bf16
+  L.off_win = L.off_jn + 144;                                             // s_jn[kBandMaxKv + 1] int (+ pad)
+  L.off_dl = L.off_win + static_cast<size_t>(2 * kWinRowsKv) * 128;      // Q window, dO window [96][128 B]
+  L.bytes = L.off_dl + static_cast<size_t>(kWinRowsKv) * 8;              // s_dl[96] (delta, log2 lse)
   return L;
 }
 
@@ -217,6 +227,10 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   float2* s_ph = reinterpret_cast<float2*>(sm + lay.off_ph);
   int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
   uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
+  int* s_jn = reinterpret_cast<int*>(sm + lay.off_jn);  // [0]: JB; [d]: band slot of offset d, or -1
+  char* s_qw = sm + lay.off_win;                         // Q rows m0 .. m0 + 95 (16-byte chunks swizzled)
+  char* s_dw = s_qw + kWinRowsKv * 128;                  // dO rows, same layout
+  float2* s_dl = reinterpret_cast<float2*>(sm + lay.off_dl);
 
   const int work = xcd_remap(blockIdx.x, total);
   const int bhk = work / tiles;
@@ -231,17 +245,19 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   const int l = lane % kWave;
   const int g = l & 3;
   const int ki = l >> 2;
-  const int m0w = tile * kKPB + w * kKPW;
+  const int lr = l & 15, lc = l >> 4;
+  const int m0 = tile * kKPB;
+  const int m0w = m0 + w * kKPW;
   const int m = m0w + ki;
   const bool key_ok = m < N;
   const int64_t mm = m;
   uint4 kx0 = {0u, 0u, 0u, 0u}, kx1 = {0u, 0u, 0u, 0u}, vx0 = {0u, 0u, 0u, 0u}, vx1 = {0u, 0u, 0u, 0u};
   float zg = 0.f;
+  const bf16* kbase = reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1];
+  const bf16* vbase = reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] + hk * f.v_stride[1];
   if (key_ok) {
-    const uint4* k4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] +
-                                                     hk * f.k_stride[1] + mm * f.k_stride[2] + 16 * g);
-    const uint4* v4 = reinterpret_cast<const uint4*>(reinterpret_cast<const bf16*>(f.v) + b * f.v_stride[0] +
-                                                     hk * f.v_stride[1] + mm * f.v_stride[2] + 16 * g);
+    const uint4* k4 = reinterpret_cast<const uint4*>(kbase + mm * f.k_stride[2] + 16 * g);
+    const uint4* v4 = reinterpret_cast<const uint4*>(vbase + mm * f.v_stride[2] + 16 * g);
     kx0 = k4[0]; kx1 = k4[1]; vx0 = v4[0]; vx1 = v4[1];
     zg = f.z_pre[b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2] + g];
   }
@@ -261,14 +277,27 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
         make_float2(f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r],
                     f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r]);
   }
+  if (threadIdx.x == 0) {
+    // the band: the leading small offsets while they ascend and stay <= kBandMaxKv
+    for (int d = 1; d <= kBandMaxKv; ++d) s_jn[d] = -1;
+    int jb = 0;
+    while ((f.schedule & DWARF_SCHED_BAND) && jb < J_small) {
+      const int d = f.offsets[jb];
+      if (d < 1 || d > kBandMaxKv || (jb > 0 && d <= f.offsets[jb - 1])) break;
+      s_jn[d] = jb++;
+    }
+    s_jn[0] = jb;
+  }
   __syncthreads();
+  const int JB = s_jn[0];
+  const bool wave_live = m0w < N;   // waves past the end still reach every barrier
 
-  if (m0w >= N) return;                       // whole wave past the end (no block barriers below)
   const int m_hi = min(m0w + kKPW - 1, N - 1);
   int2* s_list = s_list_all + w * lay.list_len;
-  // offsets giving some key m0w..m_hi a query m + delta in [0, N); the
-  // sentinel offset N + 16 - m0w puts every key's query past the end.
-  const int cnt = build_offset_list<CJ>(s_list, s_off, J, m0w, m_hi, N, -1, make_int2(J, N + 16 - m0w));
+  // offsets giving some key m0w..m_hi a query m + delta in [0, N), the band's
+  // left out; the sentinel offset N + 16 - m0w puts every key's query past the end.
+  const int cnt = wave_live ? build_offset_list<CJ>(s_list, s_off, J, m0w, m_hi, N, -1, make_int2(J, N + 16 - m0w), JB)
+                            : 0;
   const int cntp = (cnt + CJ - 1) / CJ * CJ;
 
   const uint32_t k32[8] = {kx0.x, kx0.y, kx0.z, kx0.w, kx1.x, kx1.y, kx1.z, kx1.w};
@@ -276,6 +305,15 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   // own V pair of plane g (dims 16g + SHIFT, +1)
   const float va = (SHIFT & 1) ? bf16_hi(v32[SHIFT >> 1]) : bf16_lo(v32[SHIFT >> 1]);
   const float vb = ((SHIFT + 1) & 1) ? bf16_hi(v32[(SHIFT + 1) >> 1]) : bf16_lo(v32[(SHIFT + 1) >> 1]);
+  // the wave's keys as MFMA B operands for the band: key m0w + lr, dims 32 ks + 8 lc + [0, 8)
+  uint4 kB[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}}, vB[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if (JB > 0 && m0w + lr < N) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      kB[ks] = *reinterpret_cast<const uint4*>(kbase + static_cast<int64_t>(m0w + lr) * f.k_stride[2] + 32 * ks + 8 * lc);
+      vB[ks] = *reinterpret_cast<const uint4*>(vbase + static_cast<int64_t>(m0w + lr) * f.v_stride[2] + 32 * ks + 8 * lc);
+    }
+  }
 
   float dk[16], dv[16];
 #pragma unroll
@@ -300,6 +338,28 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
     const __amdgpu_buffer_rsrc_t ry = rows_rsrc(f.y_pre + b * f.y_stride[0] + h * f.y_stride[1], ys_b, N, 16);
     const float* pb2 = s_pb2 + hh * lay.JE;
     const float2* ph_h = s_ph + hh * lay.JL4 * kPlanes;
+
+    // the near band's windows for this head: query rows m0 .. m0 + 95 of q and dO (three 1 KB DMA
+    // loads per wave and window; LDS chunk (i & 7) of row i >> 3 holds the row's 16-byte chunk
+    // (i & 7) ^ (row & 7), a bank spread) and their (delta, log2 lse) pairs (4-byte DMA loads).  They
+    // land while the gather loop runs; the band follows it.
+    typedef __attribute__((address_space(3))) void lds_void;
+    if (JB > 0) {   // uniform over the workgroup
+      if (hh > 0) __syncthreads();   // every wave is done with the previous head's windows
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        const int i = kBlock * u + lane;
+        const int row = i >> 3, c = (i & 7) ^ (row & 7);
+        const int nq = m0 + row;   // past N: out of range, zeros
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(void*)(s_qw + 4096 * u + 1024 * w), 16,
+                                                 static_cast<uint32_t>(nq * qs_b + 16 * c), 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(void*)(s_dw + 4096 * u + 1024 * w), 16,
+                                                 static_cast<uint32_t>(nq * ds_b + 16 * c), 0, 0, 0);
+      }
+      if (w < 3)   // dwords 64 w + l of the (delta, log2 lse) rows m0 ..; past N: zeros (masked below)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rdl, (lds_void*)(void*)(reinterpret_cast<char*>(s_dl) + 256 * w), 4,
+                                                 static_cast<uint32_t>(8 * m0 + 4 * lane), 0, 0, 0);
+    }
 
     auto fetch = [&](int k0, KvChunk<CJ>& c) {
 #pragma unroll
@@ -389,6 +449,98 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
         consume(c1);
       }
     }
+    // ---- near band (offsets j < JB) on the matrix cores ----
+    // Band lane (lc, lr) serves key m0w + lr; in the MFMA C layout it holds
+    // queries m0w + 16 tb + 4 lc + r of the wave's query blocks tb = 0..2
+    // (queries [m0w, m0w + 48)), and its dK / dV results dims 16 lc + [0, 16).
+    //   S^T = Q K^T, dP^T = dO V^T, <q, e_slot> = Q E^T   (v_mfma_f32_16x16x32_bf16)
+    //   P = exp2(S' - lse), dS = P (dP - delta) on the band's diagonals
+    //   dK^T += Q^T (c dS^T), dV^T += dO^T P^T            (v_mfma_f32_16x16x16_bf16, bf16 hi + lo)
+    if (JB > 0) {   // uniform over the workgroup
+      __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's window loads have landed
+      __syncthreads();
+      auto win16 = [&](char* wb, int row, int c) { return wb + row * 128 + 16 * (c ^ (row & 7)); };
+      const bool key_band = m0w + lr < N;
+      f32x4 acck[4], accv[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) { acck[db] = zero4(); accv[db] = zero4(); }
+#pragma unroll
+      for (int tb = 0; tb < 3; ++tb) {
+        const int wr = 16 * (w + tb) + lr;   // window row of query m0w + 16 tb + lr
+        const uint4 qa0 = *reinterpret_cast<const uint4*>(win16(s_qw, wr, lc));
+        const uint4 qa1 = *reinterpret_cast<const uint4*>(win16(s_qw, wr, 4 + lc));
+        const uint4 da0 = *reinterpret_cast<const uint4*>(win16(s_dw, wr, lc));
+        const uint4 da1 = *reinterpret_cast<const uint4*>(win16(s_dw, wr, 4 + lc));
+        f32x4 S = mfma16_bf16(bf16x8_from_bits(qa0), bf16x8_from_bits(kB[0]), zero4());
+        S = mfma16_bf16(bf16x8_from_bits(qa1), bf16x8_from_bits(kB[1]), S);
+        f32x4 Dp = mfma16_bf16(bf16x8_from_bits(da0), bf16x8_from_bits(vB[0]), zero4());
+        Dp = mfma16_bf16(bf16x8_from_bits(da1), bf16x8_from_bits(vB[1]), Dp);
+        // <q, e_slot> of this block's queries: C[query 4 lc + r][slot 16 bb + lr]
+        f32x4 qe[2];
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb) {
+          qe[bb] = zero4();
+          if (16 * bb < JB) {
+            const uint4 e0 = *reinterpret_cast<const uint4*>(sE + (16 * bb + lr) * kERowKv + 8 * lc);
+            const uint4 e1 = *reinterpret_cast<const uint4*>(sE + (16 * bb + lr) * kERowKv + 32 + 8 * lc);
+            qe[bb] = mfma16_bf16(bf16x8_from_bits(qa0), bf16x8_from_bits(e0), qe[bb]);
+            qe[bb] = mfma16_bf16(bf16x8_from_bits(qa1), bf16x8_from_bits(e1), qe[bb]);
+          }
+        }
+        float pv[4], cds[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qq = 16 * tb + 4 * lc + r;   // query m0w + qq, key m0w + lr
+          const int delta = qq - lr;
+          const int slot = delta >= 1 && delta <= kBandMaxKv ? s_jn[delta] : -1;
+          // <q, e_slot> of this lane's query lives in lane (slot % 16, lc), register r of block slot / 16
+          const int src = 4 * ((slot & 15) + 16 * lc);
+          const float q0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(qe[0][r])));
+          const float q1 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(qe[1][r])));
+          float p = 0.f, ds = 0.f;
+          if (slot >= 0 && key_band && m0w + qq < N) {
+            const float2 dl = s_dl[16 * (w + tb) + 4 * lc + r];
+            const float qev = slot < 16 ? q0 : q1;
+            p = __builtin_amdgcn_exp2f(fmaf(S[r] + qev, kC, pb2[slot]) - dl.y);
+            ds = p * (Dp[r] - dl.x);
+          }
+          pv[r] = p;
+          cds[r] = kScale * ds;
+        }
+        float cl[4], pl[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          cl[r] = cds[r] - round_bf16(cds[r]);
+          pl[r] = pv[r] - round_bf16(pv[r]);
+        }
+        const i16x4 dsh = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(cds[0], cds[1]), pack_bf16x2(cds[2], cds[3])));
+        const i16x4 dsl = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(cl[0], cl[1]), pack_bf16x2(cl[2], cl[3])));
+        const i16x4 ph = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])));
+        const i16x4 plo = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(pl[0], pl[1]), pack_bf16x2(pl[2], pl[3])));
+        // Q^T and dO^T read transposed from the windows: rows 16 (w + tb) + 4 lc + e, dims
+        // 16 (lr / 4) + 4 db + lr % 4 of MFMA row lr
+        const int R = 16 * (w + tb) + 4 * lc + (lr >> 2);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const i16x4 aq = lds_read_tr16(win16(s_qw, R, 2 * (lr & 3) + (db >> 1)) + 8 * (db & 1));
+          const i16x4 ad = lds_read_tr16(win16(s_dw, R, 2 * (lr & 3) + (db >> 1)) + 8 * (db & 1));
+          acck[db] = mfma16k16_bf16(aq, dsh, acck[db]);
+          acck[db] = mfma16k16_bf16(aq, dsl, acck[db]);
+          accv[db] = mfma16k16_bf16(ad, ph, accv[db]);
+          accv[db] = mfma16k16_bf16(ad, plo, accv[db]);
+        }
+      }
+      // into the gather layout: key ki, dims 16 g + i <- band lane (lc = g, lr = ki)
+      const int srck = 4 * (ki + 16 * g);
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          dk[4 * db + r] += __int_as_float(__builtin_amdgcn_ds_bpermute(srck, __float_as_int(acck[db][r])));
+          dv[4 * db + r] += __int_as_float(__builtin_amdgcn_ds_bpermute(srck, __float_as_int(accv[db][r])));
+        }
+    }
+
   }
 
   if (!key_ok) return;
