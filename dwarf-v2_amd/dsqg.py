@@ -29,9 +29,10 @@ from .lattice import GROUPED_MODE_IDS, R_PLANES
 
 HEAD_DIM = 64
 _SLAB_MODES = (GROUPED_MODE_IDS["overlap_slab"], GROUPED_MODE_IDS["overlap_slab_bwd"])
-# Schedule of the baseline mode: the near band of the dQ launch on the matrix
-# cores (DWARF_SCHED_BAND) measured faster than the gather loop alone (0.252 vs
-# 0.258 ms for the dQ launch at B15 H8 T2048), so it is the default.  The
+# Schedule of the baseline mode: the near band of the dQ and dK/dV launches on
+# the matrix cores (DWARF_SCHED_BAND) measured faster than the gather loops
+# alone at B15 H8 T2048 (dQ 271 vs 280-284 us, dK/dV 241 vs 262-265 us on one
+# box), so it is the default; 0 selects the gather loops alone.  The
 # overlap-slab modes always set it; online_softmax=False adds
 # DWARF_SCHED_TWO_PASS (the offline-softmax forward).
 DEFAULT_SCHEDULE = 1
