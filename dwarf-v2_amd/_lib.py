@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "dwarf_ema_bwd",
     "dwarf_q6_pack_kv",
     "dwarf_q6_unpack_kv",
+    "dwarf_dsqg_q6_prefill_workspace_bytes",
     "dwarf_dsqg_q6_prefill_fwd",
     "dwarf_dsqg_q6_decode",
     "dwarf_dsqg_q6_decode_workspace_bytes",
@@ -152,6 +153,7 @@ class Q6PrefillArgs(ctypes.Structure):
         ("offsets", c_void_p),
         ("out", c_void_p), ("out_stride", _i64(4)),
         ("lse", c_void_p), ("lse_stride", _i64(3)),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
     ]
 
 
@@ -324,6 +326,8 @@ def load() -> ctypes.CDLL:
         c_int32, c_int32, c_int32, c_int32,
         POINTER(c_uint8), POINTER(c_int64), c_void_p, c_void_p, c_void_p,
     ]
+    lib.dwarf_dsqg_q6_prefill_workspace_bytes.restype = c_size_t
+    lib.dwarf_dsqg_q6_prefill_workspace_bytes.argtypes = [POINTER(Q6PrefillArgs)]
     lib.dwarf_dsqg_q6_prefill_fwd.restype = c_int
     lib.dwarf_dsqg_q6_prefill_fwd.argtypes = [POINTER(Q6PrefillArgs), c_void_p]
     lib.dwarf_dsqg_q6_decode.restype = c_int

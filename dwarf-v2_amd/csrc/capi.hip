@@ -21,6 +21,7 @@ hipError_t launch_q6_pack(int B, int Hkv, int N, int dtype, const void* k, const
 hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const int64_t* cs, float* kout,
                             float* vout, hipStream_t stream);
 hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream);
+size_t q6_prefill_workspace(const dwarf_dsqg_q6_prefill_args& a);
 hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, float* table, hipStream_t stream);
 hipError_t q6_decode_scratch(float** ptr);
 size_t q6_decode_workspace(const dwarf_dsqg_q6_decode_args& a);
@@ -578,6 +579,11 @@ int dwarf_q6_unpack_kv(int32_t B, int32_t H_kv, int32_t N, int32_t head_dim, con
                     "dwarf_q6_unpack_kv");
 }
 
+size_t dwarf_dsqg_q6_prefill_workspace_bytes(const dwarf_dsqg_q6_prefill_args* args) {
+  if (!args || args->B < 0 || args->H_kv < 0 || args->N < 0) return 0;
+  return dwarf::q6_prefill_workspace(*args);
+}
+
 int dwarf_dsqg_q6_prefill_fwd(const dwarf_dsqg_q6_prefill_args* args, dwarf_stream_t stream) {
   if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
   const dwarf_dsqg_q6_prefill_args& a = *args;
@@ -590,6 +596,14 @@ int dwarf_dsqg_q6_prefill_fwd(const dwarf_dsqg_q6_prefill_args* args, dwarf_stre
   if ((rc = check_gather_span("cache", DWARF_Q6_SLOT_BYTES, 1, a.N))) return rc;
   if (!a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter table, probe table or offsets is NULL");
+  if (a.workspace) {   // the widened-row schedule: 160-byte rows gathered with 32-bit offsets
+    if ((rc = check_gather_span("widened cache rows", 160, 1, a.N))) return rc;
+    const size_t need = dwarf::q6_prefill_workspace(a);
+    if (a.workspace_bytes < need)
+      return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+    if (reinterpret_cast<uintptr_t>(a.workspace) & 255u)
+      return fail(DWARF_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  }
   if (a.B == 0 || a.N == 0) return ok();
   return hip_status(dwarf::launch_q6_prefill(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_q6_prefill_fwd");
 }

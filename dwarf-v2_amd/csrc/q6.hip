@@ -13,7 +13,13 @@
 //   [104,120) z[4] fp32 (key-probe features of the dequantised K row)
 //   [120,128) zero
 // A gathered offset therefore reads exactly one 128-byte line.
+//
+// Widened row (the prefill's workspace), one per cache slot, 160 bytes:
+//   [0,64) K codes as bytes c + 32   [64,128) V codes as bytes c + 32
+//   [128,160) per 16-dim chunk g: the fp16 K and V scales of its group and z[g]
+// Byte c + 32 is the 6-bit field with its sign bit flipped (1..63).
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "dsqg_internal.h"
@@ -256,8 +262,68 @@ struct PfSlot {
   int j;
 };
 
-template <int SHIFT>
-__global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_prefill_args a, int tiles, int total) {
+constexpr int kXRow = 160;                       // widened row bytes
+constexpr int kXK = 0, kXV = 64, kXMeta = 128;   // K bytes, V bytes, per-chunk (scales, z)
+
+// A slot read from the widened rows: the lane's 16 K and 16 V code bytes and
+// (K scale | V scale << 16, z of its plane).
+struct PxSlot {
+  uint4 k, v;
+  uint2 meta;
+  bool ok;
+  int j;
+};
+
+// Sixteen 6-bit fields of a 12-byte chunk as bytes with the sign bit flipped
+// (c + 32), four per dword in element order.
+__device__ __forceinline__ uint4 q6_code_bytes16(uint32_t w0, uint32_t w1, uint32_t w2) {
+  const uint64_t lo = (static_cast<uint64_t>(w1) << 32) | w0;
+  const uint64_t hi = (static_cast<uint64_t>(w2) << 32) | w1;
+  uint32_t o[4];
+#pragma unroll
+  for (int qd = 0; qd < 4; ++qd) {
+    uint32_t x = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int bit = 6 * (4 * qd + e);
+      const uint32_t f = static_cast<uint32_t>(bit < 32 ? lo >> bit : hi >> (bit - 32)) & 63u;
+      x |= (f ^ 0x20u) << (8 * e);
+    }
+    o[qd] = x;
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Widens every cache row of the prefill once: one thread per (row, 16-dim
+// chunk); the four threads of a row write its 160 bytes.
+__global__ __launch_bounds__(kBlock) void q6_widen_rows(int Hkv, int N, int64_t rows, const uint8_t* __restrict__ cache,
+                                                        int64_t cs0, int64_t cs1, int64_t cs2, uint8_t* __restrict__ xr) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= rows * 4) return;
+  const int c = static_cast<int>(i & 3);
+  const int64_t r = i >> 2;
+  const int t = static_cast<int>(r % N);
+  const int64_t bh = r / N;
+  const int hk = static_cast<int>(bh % Hkv);
+  const int64_t b = bh / Hkv;
+  const uint8_t* s = cache + b * cs0 + hk * cs1 + t * cs2;
+  const uint32_t* k32 = reinterpret_cast<const uint32_t*>(s + kKCodes + 12 * c);
+  const uint32_t* v32 = reinterpret_cast<const uint32_t*>(s + kVCodes + 12 * c);
+  const uint4 kb = q6_code_bytes16(k32[0], k32[1], k32[2]);
+  const uint4 vb = q6_code_bytes16(v32[0], v32[1], v32[2]);
+  const uint32_t ks = *reinterpret_cast<const uint32_t*>(s + kKScales);
+  const uint32_t vs = *reinterpret_cast<const uint32_t*>(s + kVScales);
+  const uint32_t z = *reinterpret_cast<const uint32_t*>(s + kZ + 4 * c);
+  const int sh = c >= 2 ? 16 : 0;   // chunks 2, 3 are in group 1
+  uint8_t* o = xr + r * kXRow;
+  *reinterpret_cast<uint4*>(o + kXK + 16 * c) = kb;
+  *reinterpret_cast<uint4*>(o + kXV + 16 * c) = vb;
+  *reinterpret_cast<uint2*>(o + kXMeta + 8 * c) = make_uint2(((ks >> sh) & 0xffffu) | (((vs >> sh) & 0xffffu) << 16), z);
+}
+
+template <int SHIFT, bool WIDE>
+__global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_prefill_args a,
+                                                           const uint8_t* __restrict__ xr, int tiles, int total) {
   constexpr float kC = 0.125f * kLog2e;
   constexpr float kSlack2 = 8.0f * kLog2e;
   static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
@@ -377,64 +443,108 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
   }
 
   const int n_eff = live ? n : n0w - 2 * N;   // no source for a query that is not live
-  const uint8_t* cb = a.cache + b * a.cache_stride[0] + hk * a.cache_stride[1];
-  const int sstride = static_cast<int>(a.cache_stride[2]);
-  const __amdgpu_buffer_rsrc_t rc = rows_rsrc(cb, sstride, N, kSlot);
+  // rows of this (b, kv head): the cache slots, or their widened copies
+  const int sstride = WIDE ? kXRow : static_cast<int>(a.cache_stride[2]);
+  const __amdgpu_buffer_rsrc_t rc =
+      WIDE ? rows_rsrc(xr + static_cast<int64_t>(b * a.H_kv + hk) * N * kXRow, kXRow, N, kXRow)
+           : rows_rsrc(a.cache + b * a.cache_stride[0] + hk * a.cache_stride[1], sstride, N, kSlot);
   const int sb_lane = n_eff * sstride;
   const bool khi = g >= 2;   // this lane's 16 dims are in group g / 2: scale in the high half
+  using Slot = typename std::conditional<WIDE, PxSlot, PfSlot>::type;
 
   float acc[16];
 #pragma unroll
   for (int d = 0; d < 16; ++d) acc[d] = 0.f;
   float m = -3.0e38f, lsum = 0.f;
+  float wsum = 0.f;   // widened rows: sum of the V weights, for the +32 carried by the V code bytes
 
-  auto fetch = [&](int k0, PfSlot& s) {
+  auto fetch = [&](int k0, Slot& s) {
     const int2 e = s_list[k0];
     const int j = uniform(e.x), d = uniform(e.y);
     s.j = j;
     s.ok = static_cast<uint32_t>(n_eff - d) < static_cast<uint32_t>(N);
     const uint32_t base = static_cast<uint32_t>(sb_lane - d * sstride);
-    const auto kx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kKCodes + 12 * g, 0, 0);
-    const auto vx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kVCodes + 12 * g, 0, 0);
-    s.k0 = kx[0]; s.k1 = kx[1]; s.k2 = kx[2];
-    s.v0 = vx[0]; s.v1 = vx[1]; s.v2 = vx[2];
-    s.ks = cache_dword(rc, base + kKScales);
-    s.vs = cache_dword(rc, base + kVScales);
-    const bool far = j >= J_small && j < J;
-    s.z = __uint_as_float(cache_dword(rc, far ? base + kZ + 4 * g : kOutOfRange));
+    if constexpr (WIDE) {
+      s.k = buf_load16(rc, base + kXK + 16 * g);
+      s.v = buf_load16(rc, base + kXV + 16 * g);
+      const auto mt = __builtin_amdgcn_raw_buffer_load_b64(rc, base + kXMeta + 8 * g, 0, 0);
+      s.meta = make_uint2(mt[0], mt[1]);
+    } else {
+      const auto kx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kKCodes + 12 * g, 0, 0);
+      const auto vx = __builtin_amdgcn_raw_buffer_load_b96(rc, base + kVCodes + 12 * g, 0, 0);
+      s.k0 = kx[0]; s.k1 = kx[1]; s.k2 = kx[2];
+      s.v0 = vx[0]; s.v1 = vx[1]; s.v2 = vx[2];
+      s.ks = cache_dword(rc, base + kKScales);
+      s.vs = cache_dword(rc, base + kVScales);
+      const bool far = j >= J_small && j < J;
+      s.z = __uint_as_float(cache_dword(rc, far ? base + kZ + 4 * g : kOutOfRange));
+    }
   };
 
-  auto consume = [&](const PfSlot& s) {
+  auto consume = [&](const Slot& s) {
     float cf[16];
-    const float kd = q6_dot16_biased(q32, s.k0, s.k1, s.k2) + qbias;
-    const float dot = group_sum<4>(kd * half_lo_or_hi(s.ks, khi));
+    float kd, ksc, vsc, zf;
+    if constexpr (WIDE) {
+      // K: v_perm puts two code bytes under the bf16 high byte 0x43, i.e. the
+      // pair (128 + byte) = (160 + c); sum_d q_d (160 + c_d) as in the slot path
+      const uint32_t kw[4] = {s.k.x, s.k.y, s.k.z, s.k.w};
+      kd = qbias;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kd = dot2bf(q32[2 * i], __builtin_amdgcn_perm(0x43434343u, kw[i], 0x04010400u), kd);
+        kd = dot2bf(q32[2 * i + 1], __builtin_amdgcn_perm(0x43434343u, kw[i], 0x04030402u), kd);
+      }
+      ksc = half_bits_to_f32(static_cast<uint16_t>(s.meta.x));
+      vsc = half_bits_to_f32(static_cast<uint16_t>(s.meta.x >> 16));
+      zf = __uint_as_float(s.meta.y);
+    } else {
+      kd = q6_dot16_biased(q32, s.k0, s.k1, s.k2) + qbias;
+      ksc = half_lo_or_hi(s.ks, khi);
+      vsc = half_lo_or_hi(s.vs, khi);
+      zf = s.z;
+    }
+    const float dot = group_sum<4>(kd * ksc);
     const float s2 = s.ok ? fmaf(dot, kC, s_qe[qi * lay.qe_row + s.j]) : -INFINITY;
     if (s2 > m + kSlack2) {
       const float f = __builtin_amdgcn_exp2f(m - s2);   // 0 on the first valid offset
 #pragma unroll
       for (int d = 0; d < 16; ++d) acc[d] *= f;
       lsum *= f;
+      if constexpr (WIDE) wsum *= f;
       m = s2;
     }
     const float p = __builtin_amdgcn_exp2f(s2 - m);   // m is finite: 0 without a source
     lsum += p;
-    q6_codes16(s.v0, s.v1, s.v2, cf);
+    if constexpr (WIDE) {
+      // V: each code byte to fp32 (v_cvt_f32_ubyte*): c + 32; the MOVT pair
+      // drops the +32 here, the other dims when the row ends
+      const uint32_t vw[4] = {s.v.x, s.v.y, s.v.z, s.v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cf[4 * i + e] = static_cast<float>((vw[i] >> (8 * e)) & 0xffu);
+      cf[SHIFT] -= 32.f;
+      cf[SHIFT + 1] -= 32.f;
+    } else {
+      q6_codes16(s.v0, s.v1, s.v2, cf);
+    }
     if (s.j >= J_small && s.j < J) {   // wave-uniform
       const float2 ph = s_ph[(s.j - J_small) * kPlanes + g];
       float sn, cs;
-      dsincos<true>(fmaf(ph.y * yg, s.z, ph.x), &sn, &cs);
+      dsincos<true>(fmaf(ph.y * yg, zf, ph.x), &sn, &cs);
       const float va = cf[SHIFT], vb = cf[SHIFT + 1];
       cf[SHIFT] = cs * va - sn * vb;
       cf[SHIFT + 1] = sn * va + cs * vb;
     }
-    const float wgt = p * half_lo_or_hi(s.vs, khi);
+    const float wgt = p * vsc;
+    if constexpr (WIDE) wsum += wgt;
 #pragma unroll
     for (int d = 0; d < 16; ++d) acc[d] = fmaf(wgt, cf[d], acc[d]);
     pin_regs<16>(acc);
   };
 
   if (cnt > 0) {
-    PfSlot s0, s1;
+    Slot s0, s1;
     fetch(0, s0);
     for (int k0 = 0; k0 < cnt; k0 += 2) {
       fetch(k0 + 1, s1);   // past the list end this reads the sentinel: zeros
@@ -445,6 +555,11 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
   }
 
   if (!row_ok) return;
+  if constexpr (WIDE) {
+#pragma unroll
+    for (int d = 0; d < 16; ++d)
+      if (d != SHIFT && d != SHIFT + 1) acc[d] = fmaf(-32.f, wsum, acc[d]);
+  }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.out) + b * a.out_stride[0] + h * a.out_stride[1] +
                                        nn * a.out_stride[2] + 16 * g);
@@ -808,13 +923,18 @@ hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const i
   return hipGetLastError();
 }
 
-hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream) {
-  const int tiles = (a.N + kPfQPB - 1) / kPfQPB;
-  const int total = tiles * a.B * a.H;
-  if (total == 0) return hipSuccess;
+size_t q6_prefill_workspace(const dwarf_dsqg_q6_prefill_args& a) {
+  return static_cast<size_t>(a.B) * a.H_kv * a.N * kXRow;
+}
+
+template <bool WIDE>
+hipError_t launch_prefill_rows(const dwarf_dsqg_q6_prefill_args& a, const uint8_t* xr, int tiles, int total,
+                               hipStream_t stream) {
   const size_t lds = pf_layout(a.J, a.J_large).bytes;
-#define DWARF_Q6P_CASE(S) \
-  case S: hipLaunchKernelGGL(q6_prefill_q4<S>, dim3(total), dim3(kBlock), lds, stream, a, tiles, total); break;
+#define DWARF_Q6P_CASE(S)                                                                                    \
+  case S:                                                                                                    \
+    hipLaunchKernelGGL((q6_prefill_q4<S, WIDE>), dim3(total), dim3(kBlock), lds, stream, a, xr, tiles, total); \
+    break;
   switch (a.plane_shift) {
     DWARF_Q6P_CASE(0) DWARF_Q6P_CASE(1) DWARF_Q6P_CASE(2) DWARF_Q6P_CASE(3) DWARF_Q6P_CASE(4)
     DWARF_Q6P_CASE(5) DWARF_Q6P_CASE(6) DWARF_Q6P_CASE(7) DWARF_Q6P_CASE(8) DWARF_Q6P_CASE(9)
@@ -823,6 +943,20 @@ hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t st
   }
 #undef DWARF_Q6P_CASE
   return hipGetLastError();
+}
+
+hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream) {
+  const int tiles = (a.N + kPfQPB - 1) / kPfQPB;
+  const int total = tiles * a.B * a.H;
+  if (total == 0) return hipSuccess;
+  if (!a.workspace) return launch_prefill_rows<false>(a, nullptr, tiles, total, stream);
+  uint8_t* xr = static_cast<uint8_t*>(a.workspace);
+  const int64_t rows = static_cast<int64_t>(a.B) * a.H_kv * a.N;
+  hipLaunchKernelGGL(q6_widen_rows, dim3(static_cast<unsigned>((rows * 4 + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                     stream, a.H_kv, a.N, rows, a.cache, a.cache_stride[0], a.cache_stride[1], a.cache_stride[2], xr);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_prefill_rows<true>(a, xr, tiles, total, stream);
 }
 
 size_t q6_decode_workspace(const dwarf_dsqg_q6_decode_args& a) {

@@ -85,9 +85,13 @@ def unpack_kv(cache: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 def q6_prefill(q, cache, pos_bias, scale_embed, phase_base, phase_gain, query_probes, offsets_dev,
-               j_small, j_large, plane_shift=0, query_start=0, *, return_lse=False, round_se=True):
+               j_small, j_large, plane_shift=0, query_start=0, *, return_lse=False, round_se=True, widen=True):
     """DSQG forward over a q6 cache.  q [B,H,N,64] bf16; returns bf16 out (and lse).  round_se rounds
-    scale_embed to bf16 as the GPU path does (dsqg:760-763); False keeps it in fp32."""
+    scale_embed to bf16 as the GPU path does (dsqg:760-763); False keeps it in fp32.
+
+    widen=True widens every cache row once into a workspace (160 bytes per row: the codes as bytes, the
+    scales and z) and gathers those; widen=False gathers the 128-byte slots and widens each code at every
+    use, with no workspace.  Both compute the same math."""
     if not q.is_cuda:
         raise RuntimeError("the q6 HIP kernels require device tensors")
     q = _rows(q.to(torch.bfloat16))
@@ -120,6 +124,11 @@ def q6_prefill(q, cache, pos_bias, scale_embed, phase_base, phase_gain, query_pr
     if lse is not None:
         a.lse, a.lse_stride = lse.data_ptr(), _p64(lse.stride())
     lib = _lib.load()
+    workspace = None
+    if widen:
+        nbytes = int(lib.dwarf_dsqg_q6_prefill_workspace_bytes(ctypes.byref(a)))
+        workspace = torch.empty(max(nbytes, 256), device=q.device, dtype=torch.uint8)
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
     _lib.check(lib.dwarf_dsqg_q6_prefill_fwd(ctypes.byref(a), torch.cuda.current_stream(q.device).cuda_stream),
                "dwarf_dsqg_q6_prefill_fwd")
     return (out, lse) if return_lse else out

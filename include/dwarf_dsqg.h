@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 6
+#define DWARF_ABI_VERSION 7
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
@@ -434,6 +434,14 @@ int dwarf_q6_unpack_kv(int32_t B, int32_t H_kv, int32_t N, int32_t head_dim,
  * query_probes [4,hd] fp32 (dsqg:3234-3249); z is read from the slot (written
  * by dwarf_q6_pack_kv from the dequantised K).  q [B,H,N,hd] bf16; out like q;
  * lse may be NULL.
+ *
+ * workspace: NULL gathers the 128-byte slots directly and widens every code
+ * at each of its uses (no allocation).  Otherwise it must hold
+ * dwarf_dsqg_q6_prefill_workspace_bytes() bytes, 256-byte aligned: the
+ * launch first widens each cache row once into it (the 6-bit codes as bytes,
+ * with the row's scales and z beside them, 160 bytes per row) and the
+ * attention gathers those rows.  Both give the same math: codes and scales
+ * are exact either way and only the fp32 summation order differs.
  */
 typedef struct {
   int32_t B, H, H_kv, N, head_dim;
@@ -450,7 +458,11 @@ typedef struct {
   const int32_t* offsets;
   void* out; int64_t out_stride[4];
   float* lse; int64_t lse_stride[3];
+  void* workspace; size_t workspace_bytes;
 } dwarf_dsqg_q6_prefill_args;
+
+/* Bytes of the widened-row workspace: B * H_kv * N * 160 (0 for bad sizes). */
+size_t dwarf_dsqg_q6_prefill_workspace_bytes(const dwarf_dsqg_q6_prefill_args* args);
 
 int dwarf_dsqg_q6_prefill_fwd(const dwarf_dsqg_q6_prefill_args* args,
                               dwarf_stream_t stream);

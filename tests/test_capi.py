@@ -29,7 +29,7 @@ def lib(pkg):
 
 def test_exports_every_declared_symbol(pkg, lib):
     names = declared_functions()
-    assert len(names) == 32
+    assert len(names) == 33
     assert sorted(pkg._lib.EXPORTED_SYMBOLS) == names
     for name in names:
         assert hasattr(lib, name), name
@@ -209,3 +209,32 @@ def test_prefill_gather_span_without_gpu(pkg, lib):
     a.cache_stride = L.i64_array((N * 128, N * 128, 128))
     assert lib.dwarf_dsqg_q6_prefill_fwd(ctypes.byref(a), None) == L.DWARF_ERR_UNSUPPORTED
     assert b"cache" in lib.dwarf_last_error()
+
+
+def test_prefill_workspace_without_gpu(pkg, lib):
+    """The widened-row prefill: its workspace size, and a short, misaligned or unaddressable workspace refused
+    before any launch (a NULL workspace keeps the direct slot schedule)."""
+    L = pkg._lib
+    a = L.Q6PrefillArgs()
+    a.B, a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large = 2, 6, 3, 100, 64, 96, 17, 79
+    assert lib.dwarf_dsqg_q6_prefill_workspace_bytes(ctypes.byref(a)) == 2 * 3 * 100 * 160
+    assert lib.dwarf_dsqg_q6_prefill_workspace_bytes(None) == 0
+    N = a.N
+    a.q = a.out = a.cache = 0x10000
+    a.q_stride = a.out_stride = L.i64_array((6 * N * 64, N * 64, 64, 1))
+    a.cache_stride = L.i64_array((3 * N * 128, N * 128, 128))
+    a.pos_bias = a.scale_embed = a.phase_base = a.phase_gain = a.offsets = a.query_probes = 0x10000
+    a.workspace, a.workspace_bytes = 0x10000, 2 * 3 * 100 * 160 - 1
+    assert lib.dwarf_dsqg_q6_prefill_fwd(ctypes.byref(a), None) == L.DWARF_ERR_WORKSPACE
+    assert b"needs 96000 bytes" in lib.dwarf_last_error()
+    a.workspace, a.workspace_bytes = 0x10010, 2 * 3 * 100 * 160
+    assert lib.dwarf_dsqg_q6_prefill_fwd(ctypes.byref(a), None) == L.DWARF_ERR_WORKSPACE
+    assert b"256-byte aligned" in lib.dwarf_last_error()
+    # 160-byte rows reach 2 GiB of 32-bit gather offsets sooner than the 128-byte slots do
+    N = 6_800_000
+    a.B, a.H, a.H_kv, a.N = 1, 1, 1, N
+    a.q_stride = a.out_stride = L.i64_array((N * 64, N * 64, 64, 1))
+    a.cache_stride = L.i64_array((N * 128, N * 128, 128))
+    a.workspace, a.workspace_bytes = 0x10000, N * 160
+    assert lib.dwarf_dsqg_q6_prefill_fwd(ctypes.byref(a), None) == L.DWARF_ERR_UNSUPPORTED
+    assert b"widened" in lib.dwarf_last_error()

@@ -55,9 +55,12 @@ def _oracle_on_cache(x, cache_np, offsets, js, shift, qp, kp, qs, return_lse=Fal
                                  query_start=qs, round_se=round_se, return_lse=return_lse)
 
 
-def test_prefill_matches_oracle(pkg, device):
+@pytest.mark.parametrize("widen,shift", [(True, 2), (False, 2), (True, 7), (True, 14)])
+def test_prefill_matches_oracle(pkg, device, widen, shift):
+    """Both prefill schedules (cache rows widened once into a workspace, or slots gathered directly), GQA, a
+    ragged N, query_start 1 and hot MOVT angles; odd and last plane shifts on the widened rows, whose MOVT
+    pair is the one accumulated without the code bytes' +32."""
     offsets = list(pkg.ALL_OFFSETS)
-    shift = 2
     x = make_inputs(2, 4, 2, 300, offsets, 17, seed=3, dtype=torch.bfloat16, plane_shift=shift, gain_std=6.0)
     qp, kp = orthogonal_probes(64, shift)
     qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
@@ -65,7 +68,8 @@ def test_prefill_matches_oracle(pkg, device):
     cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
     off = torch.tensor(offsets, dtype=torch.int32, device=device)
     out, lse = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"],
-                                 xd["phase_gain"], qp.to(device), off, 17, 79, shift, 1, return_lse=True)
+                                 xd["phase_gain"], qp.to(device), off, 17, 79, shift, 1, return_lse=True,
+                                 widen=widen)
     ref, rlse = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, shift, qp, kp, 1, return_lse=True)
     assert max_abs(out, ref) < 2e-2
     # lse (natural log, -inf before query_start) within the bf16 bar
@@ -74,7 +78,8 @@ def test_prefill_matches_oracle(pkg, device):
     assert (lse.cpu().double()[fin] - rlse[fin]).abs().max().item() < 2e-2
 
 
-def test_prefill_fp32_scale_embed(pkg, device):
+@pytest.mark.parametrize("widen", [True, False])
+def test_prefill_fp32_scale_embed(pkg, device, widen):
     """round_se=False: the prefill's <q, e_j> table takes SE in fp32, against the oracle without SE
     rounding; SE scaled up so its rounding would show."""
     offsets = list(pkg.ALL_OFFSETS)
@@ -86,7 +91,7 @@ def test_prefill_fp32_scale_embed(pkg, device):
     cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
     off = torch.tensor(offsets, dtype=torch.int32, device=device)
     out = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"], xd["phase_gain"],
-                            qp.to(device), off, 17, 79, 0, 1, round_se=False)
+                            qp.to(device), off, 17, 79, 0, 1, round_se=False, widen=widen)
     ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, 0, qp, kp, 1, round_se=False)
     assert max_abs(out, ref) < 2e-2
 
@@ -224,7 +229,8 @@ def test_decode_maximum_sizes(pkg, device):
         assert max_abs(out[s, 0], ref[s, :, int(pos[s])]) < 2e-2, s
 
 
-def test_prefill_maximum_offsets(pkg, device):
+@pytest.mark.parametrize("widen", [True, False])
+def test_prefill_maximum_offsets(pkg, device, widen):
     """J = 256 offsets (17 near, 239 far) in the prefill, against the oracle on the dequantised cache."""
     offsets = list(range(1, 18)) + list(range(48, 48 + 239))
     x = make_inputs(1, 4, 2, 320, offsets, 17, seed=83, dtype=torch.bfloat16, gain_std=6.0)
@@ -234,6 +240,6 @@ def test_prefill_maximum_offsets(pkg, device):
     cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
     off = torch.tensor(offsets, dtype=torch.int32, device=device)
     out = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"], xd["phase_gain"],
-                            qp.to(device), off, 17, 239, 0, 1)
+                            qp.to(device), off, 17, 239, 0, 1, widen=widen)
     ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, 0, qp, kp, 1)
     assert max_abs(out, ref) < 2e-2
