@@ -997,9 +997,9 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     // lane (lr, lc) supplies dS of query lr at offset lc (from the lane of
     // query lr with g = lc) and E[j_lc][16 nb + lr].
     auto dqe_step = [&](const float* ds4, const int* j4) {
-      const float sel = g == 0 ? ds4[0] : g == 1 ? ds4[1] : g == 2 ? ds4[2] : ds4[3];
+      const float sel = pick4(g, ds4[0], ds4[1], ds4[2], ds4[3]);
       const float av = __shfl(sel, 4 * lr + lc);
-      const int jsel = lc == 0 ? j4[0] : lc == 1 ? j4[1] : lc == 2 ? j4[2] : j4[3];
+      const int jsel = pick4(lc, j4[0], j4[1], j4[2], j4[3]);
       const uint16_t* er = sE + jsel * kERowT + lr;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
@@ -1021,7 +1021,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
       u0 += dpp_f<0x128>(u0);   // row_ror:8
       u1 += dpp_f<0x128>(u1);
       const int k = l >> 4;
-      const int jk = k == 0 ? j4[0] : k == 1 ? j4[1] : k == 2 ? j4[2] : j4[3];
+      const int jk = pick4(k, j4[0], j4[1], j4[2], j4[3]);
       if (((l >> 2) & 3) == 0 && jk >= J_small && jk < J)
         *reinterpret_cast<float2*>(s_dph + (jk - J_small) * 8 + 2 * g) = make_float2(u0, u1);
     };

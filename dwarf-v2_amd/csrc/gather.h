@@ -11,6 +11,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every tensor (spans are < 2^31)
 
+// The i-th of four values for a lane-varying i in [0, 4), as three selects on
+// the bits of i.  A chained `i == 0 ? a : i == 1 ? b : ...` is lowered as a
+// switch, i.e. nested exec-mask branches around empty blocks.
+template <typename T>
+__device__ __forceinline__ T pick4(int i, T a, T b, T c, T d) {
+  const T lo = (i & 1) ? b : a;
+  const T hi = (i & 1) ? d : c;
+  return (i & 2) ? hi : lo;
+}
+
 __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);

@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kBlock, kPrWgsPerCu) void phase_probe_fwd_kernel(
       widen(cur.x, xv);
       float ss, raw[kPlanes];
       row_sums(xv, p, ss, raw);
-      y = (g == 0 ? raw[0] : g == 1 ? raw[1] : g == 2 ? raw[2] : raw[3]) * rsqrtf(ss + eps);
+      y = pick4(g, raw[0], raw[1], raw[2], raw[3]) * rsqrtf(ss + eps);
     }
     out[cur.rw.b * so0 + cur.rw.h * so1 + static_cast<int64_t>(cur.rw.n) * so2 + g * so3] = y;
   }

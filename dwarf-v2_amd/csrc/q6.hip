@@ -439,7 +439,7 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
     ss = group_sum<4>(ss);
 #pragma unroll
     for (int r = 0; r < kPlanes; ++r) yp[r] = group_sum<4>(yp[r]);
-    yg = (g == 0 ? yp[0] : g == 1 ? yp[1] : g == 2 ? yp[2] : yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
+    yg = pick4(g, yp[0], yp[1], yp[2], yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
   }
 
   const int n_eff = live ? n : n0w - 2 * N;   // no source for a query that is not live
@@ -816,7 +816,7 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
     float yp[kPlanes];
 #pragma unroll
     for (int r = 0; r < kPlanes; ++r) yp[r] = wave_allsum(qd * qp[r * kHeadDim + l]);
-    yg = (c == 0 ? yp[0] : c == 1 ? yp[1] : c == 2 ? yp[2] : yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
+    yg = pick4(c, yp[0], yp[1], yp[2], yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
   }
 
   float acc[16];
