@@ -195,7 +195,7 @@ __host__ __device__ inline KvLayout kv_layout(int J, int J_large, int group, int
   L.off_list = L.off_ph + static_cast<size_t>(group) * L.JL4 * 4 * 8;    // s_ph[group][JL4][4] float2
   L.off_e = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;        // s_list[4][list_len] int2
   L.off_jn = L.off_e + static_cast<size_t>(L.JE) * kERowKv * 2;          // sE[JE][72] bf16
-  L.off_win = L.off_jn + 144;                                             // s_jn[kBandMaxKv + 1] int (+ pad)
+  L.off_win = L.off_jn + kJnSize * 4;                                    // s_jn[kJnSize] int
   L.off_dl = L.off_win + static_cast<size_t>(2 * kWinRowsKv) * 128;      // Q window, dO window [96][128 B]
   L.bytes = L.off_dl + static_cast<size_t>(kWinRowsKv) * 8;              // s_dl[96] (delta, log2 lse)
   return L;
@@ -277,17 +277,8 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
         make_float2(f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r],
                     f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r]);
   }
-  if (threadIdx.x == 0) {
-    // the band: the leading small offsets while they ascend and stay <= kBandMaxKv
-    for (int d = 1; d <= kBandMaxKv; ++d) s_jn[d] = -1;
-    int jb = 0;
-    while ((f.schedule & DWARF_SCHED_BAND) && jb < J_small) {
-      const int d = f.offsets[jb];
-      if (d < 1 || d > kBandMaxKv || (jb > 0 && d <= f.offsets[jb - 1])) break;
-      s_jn[d] = jb++;
-    }
-    s_jn[0] = jb;
-  }
+  if (threadIdx.x == 0)
+    build_band_slots(s_jn, f.offsets, J_small, kBandMaxKv, kBandMaxKv, (f.schedule & DWARF_SCHED_BAND) != 0);
   __syncthreads();
   const int JB = s_jn[0];
   const bool wave_live = m0w < N;   // waves past the end still reach every barrier
@@ -492,7 +483,7 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
         for (int r = 0; r < 4; ++r) {
           const int qq = 16 * tb + 4 * lc + r;   // query m0w + qq, key m0w + lr
           const int delta = qq - lr;
-          const int slot = delta >= 1 && delta <= kBandMaxKv ? s_jn[delta] : -1;
+          const int slot = delta >= 1 && delta <= kBandMaxKv ? s_jn[kJnBias + delta] : -1;
           // <q, e_slot> of this lane's query lives in lane (slot % 16, lc), register r of block slot / 16
           const int src = 4 * ((slot & 15) + 16 * lc);
           const float q0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(qe[0][r])));

@@ -552,6 +552,7 @@ __host__ __device__ constexpr int dse_wgs_per_cu(int mbw) { return mbw <= 2 ? 4 
 constexpr int kBandMax = 32;                    // largest band offset; the window's look-back
 constexpr int kWinRows = kQT + kBandMax;        // 96 K rows of 128 bytes
 constexpr int kBandSlots = 32;                  // band scratch columns per query
+constexpr int kBandDummy = kQPW * kBandSlots;   // a scratch word that takes the band's masked-off stores
 
 struct DqG4Layout {
   int JE, JL4, list_len, dphw;
@@ -559,21 +560,22 @@ struct DqG4Layout {
 };
 
 // JE >= J + 1 keeps a sentinel row J of zeros in the E table.  A wave's dPhase
-// table doubles as its band scratch [16][32] fp32 at the start of a tile (it
-// is cleared after the band); the last region holds the K window [96][128 B]
+// table doubles as its band scratch [16][32] fp32 (and the word after it, which
+// takes the band's masked-off stores) at the start of a tile (it is cleared
+// after the band); the last region holds the K window [96][128 B]
 // at the start of a tile and the dQe staging [4][16][36] fp32 at its end.
 __host__ __device__ inline DqG4Layout dq_g4_layout(int J, int J_large) {
   DqG4Layout L;
   L.JE = (J + 1 + 15) / 16 * 16;
   L.JL4 = (J_large + 1) / 2 * 2;
   L.list_len = (L.JE + 2 * kStepDq + 1) / 2 * 2;   // list + padding for the last step and its prefetch
-  L.dphw = L.JL4 * 8 > kQPW * kBandSlots ? L.JL4 * 8 : kQPW * kBandSlots;
+  L.dphw = L.JL4 * 8 > kBandDummy + 4 ? L.JL4 * 8 : kBandDummy + 4;
   L.off_ph = static_cast<size_t>(2 * L.JE) * 4;                       // s_pb2[JE], s_off[JE]
   L.off_list = L.off_ph + static_cast<size_t>(L.JL4) * 4 * 8;         // s_ph[JL4][4] float2
   L.off_dph = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;   // s_list[4][list_len] int2
   L.off_e = L.off_dph + static_cast<size_t>(4 * L.dphw) * 4;          // s_dph[4][dphw]
   L.off_jn = L.off_e + static_cast<size_t>(L.JE) * kERowT * 2;        // sE[JE][72] bf16
-  L.off_st = L.off_jn + 16 * 9;                                        // s_jn[kBandMax + 1] int (+ pad)
+  L.off_st = L.off_jn + kJnSize * 4;                                   // s_jn[kJnSize] int
   const size_t st = static_cast<size_t>(4 * kQPW * kStRow) * 4;
   const size_t win = static_cast<size_t>(kWinRows) * 128;
   L.bytes = L.off_st + (st > win ? st : win);
@@ -633,23 +635,14 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
   float* s_dph_all = reinterpret_cast<float*>(sm + lay.off_dph);
   uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_e);
   float* s_st_all = reinterpret_cast<float*>(sm + lay.off_st);
-  int* s_jn = reinterpret_cast<int*>(sm + lay.off_jn);       // [0]: JB; [d]: band slot of offset d, or -1
+  int* s_jn = reinterpret_cast<int*>(sm + lay.off_jn);       // [0]: JB; [kJnBias + d]: band slot of delta d, or -1
   char* s_win = sm + lay.off_st;                              // K window [96][128 B] (aliases the dQe staging)
 
   stage_se_bf16(f.scale_embed, f.se_stride, J, lay.JE, sE, kERowT);
   for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    // the band: the leading small offsets while they ascend and stay <= kBandMax
-    for (int d = 1; d <= kBandMax; ++d) s_jn[d] = -1;
-    int jb = 0;
-    while ((f.schedule & DWARF_SCHED_BAND) && jb < J_small && jb < kBandSlots) {
-      const int d = s_off[jb];
-      if (d < 1 || d > kBandMax || (jb > 0 && d <= s_off[jb - 1])) break;
-      s_jn[d] = jb++;
-    }
-    s_jn[0] = jb;
-  }
+  if (threadIdx.x == 0)
+    build_band_slots(s_jn, s_off, J_small, kBandMax, kBandSlots, (f.schedule & DWARF_SCHED_BAND) != 0);
   __syncthreads();   // s_jn is read in every tile's prologue
 
   const int lane = threadIdx.x;
@@ -792,10 +785,10 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
                                                    8 * lc);
       }
       auto win16 = [&](int row, int c) { return s_win + row * 128 + 16 * (c ^ (row & 7)); };
-      // band slot of the pair (query n0w + lr, key n0w - 32 + 16 tb + 4 lc + r), or -1
+      // band slot of the pair (query n0w + lr, key n0w - 32 + 16 tb + 4 lc + r), or -1;
+      // the delta lies in [-15, 47], inside the table
       auto band_slot = [&](int tb, int r) {
-        const int delta = lr + kBandMax - 16 * tb - 4 * lc - r;
-        const int slot = delta >= 1 && delta <= kBandMax ? s_jn[delta] : -1;
+        const int slot = s_jn[kJnBias + lr + kBandMax - 16 * tb - 4 * lc - r];
         return n0w - kBandMax + 16 * tb + 4 * lc + r >= 0 ? slot : -1;
       };
       // <q, e_slot> of the band slots, into the scratch as [query][slot]
@@ -826,13 +819,11 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
         Dp = mfma16_bf16(bf16x8_from_bits(va1), bf16x8_from_bits(xd[1]), Dp);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+          // computed for every lane (slot 0 stands in off the band) and masked, with no branch
           const int slot = band_slot(tb, r);
-          float ds = 0.f;
-          if (slot >= 0) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(S[r] + scr[lr * kBandSlots + slot], kC, s_pb2[slot]) - ls_b);
-            ds = p * (Dp[r] - dl_b);
-          }
-          dsv[tb][r] = ds;
+          const int sl = slot >= 0 ? slot : 0;
+          const float p = __builtin_amdgcn_exp2f(fmaf(S[r] + scr[lr * kBandSlots + sl], kC, s_pb2[sl]) - ls_b);
+          dsv[tb][r] = slot >= 0 ? p * (Dp[r] - dl_b) : 0.f;
         }
       }
       // dS of the band into the scratch as [query][slot] (zeros where no pair)
@@ -845,7 +836,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int slot = band_slot(tb, r);
-          if (slot >= 0) scr[lr * kBandSlots + slot] = dsv[tb][r];
+          scr[slot >= 0 ? lr * kBandSlots + slot : kBandDummy] = dsv[tb][r];
         }
       __builtin_amdgcn_wave_barrier();
       f32x4 acch[4];

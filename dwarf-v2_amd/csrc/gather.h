@@ -11,6 +11,25 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr uint32_t kOutOfRange = 0x80000000u;  // buffer offset past every tensor (spans are < 2^31)
 
+// Near-band slot table in LDS, kJnSize ints: entry 0 holds the band's offset
+// count JB, entry kJnBias + d the band slot of delta d, and -1 for every other
+// delta in [1 - kJnBias, kJnSize - 1 - kJnBias].  The band kernels look up
+// deltas in [-15, 47] without a range check (a range check around the LDS
+// read becomes an exec-mask branch per lookup).  The band is the leading
+// small offsets while they ascend and stay <= max_delta.  Thread 0 only.
+constexpr int kJnBias = 16, kJnSize = 64;
+__device__ __forceinline__ void build_band_slots(int* s_jn, const int* offsets, int J_small, int max_delta,
+                                                 int max_slots, bool band) {
+  for (int i = 1; i < kJnSize; ++i) s_jn[i] = -1;
+  int jb = 0;
+  while (band && jb < J_small && jb < max_slots) {
+    const int d = offsets[jb];
+    if (d < 1 || d > max_delta || (jb > 0 && d <= offsets[jb - 1])) break;
+    s_jn[kJnBias + d] = jb++;
+  }
+  s_jn[0] = jb;
+}
+
 // The i-th of four values for a lane-varying i in [0, 4), as three selects on
 // the bits of i.  A chained `i == 0 ? a : i == 1 ? b : ...` is lowered as a
 // switch, i.e. nested exec-mask branches around empty blocks.
