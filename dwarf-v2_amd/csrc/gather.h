@@ -45,31 +45,6 @@ __device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-// E (scale_embed [J][64] fp32) into LDS as bf16 rows of `row` elements, rows
-// J..JE-1 zero, rounded to nearest even (the reference GPU path's bf16 SE,
-// dsqg:760-763).  Four values per thread step: one 16-byte load, one 8-byte
-// LDS store when the rows are unit-stride and 16-byte aligned.
-__device__ __forceinline__ void stage_se_bf16(const float* se, const int64_t* se_stride, int J, int JE,
-                                              uint16_t* sE, int row) {
-  const bool vec = se_stride[1] == 1 && (se_stride[0] & 3) == 0 && (reinterpret_cast<uintptr_t>(se) & 15) == 0;
-  for (int i = threadIdx.x; i < JE * 16; i += blockDim.x) {
-    const int j = i >> 4, d = 4 * (i & 15);
-    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (j < J) {
-      const float* p = se + j * se_stride[0] + d * se_stride[1];
-      if (vec) {
-        x = *reinterpret_cast<const float4*>(p);
-      } else {
-        x = make_float4(p[0], p[se_stride[1]], p[2 * se_stride[1]], p[3 * se_stride[1]]);
-      }
-    }
-    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-    const bf16x4_t h = {static_cast<__bf16>(x.x), static_cast<__bf16>(x.y), static_cast<__bf16>(x.z),
-                        static_cast<__bf16>(x.w)};
-    *reinterpret_cast<bf16x4_t*>(sE + j * row + d) = h;
-  }
-}
-
 // Zero-instruction barrier on register values: the computations that produce
 // them stay before this point (the compiler may not sink them into a later block).
 template <int CNT>
@@ -96,6 +71,60 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, in
   const int64_t span = rows > 0 ? (rows - 1) * row_bytes + tail : 0;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(span), 0x00020000);
 }
+
+// E (scale_embed [J][64] fp32) into LDS as bf16 rows of `row` elements, rows
+// J..JE-1 zero, rounded to nearest even (the reference GPU path's bf16 SE,
+// dsqg:760-763).  Four values per thread step.  With unit-stride, 16-byte
+// aligned rows (the usual layout) every load is an unconditional 16-byte
+// buffer load, rows >= J reading zeros past the end of the buffer, and a
+// thread issues all its loads before the first conversion: one memory round
+// trip.  (A load under a branch with a zero default forces a wait for it at
+// the join, which had turned the staging into one round trip per step.)
+// Other layouts take a scalar path.
+constexpr int kSeBatch = 8;
+__device__ __forceinline__ void stage_se_bf16(const float* se, const int64_t* se_stride, int J, int JE,
+                                              uint16_t* sE, int row) {
+  // the vector path addresses rows with 32-bit offsets: row stride <= 2^20 elements keeps JE rows below 2 GiB
+  const bool vec = se_stride[1] == 1 && (se_stride[0] & 3) == 0 && se_stride[0] <= (int64_t(1) << 20) &&
+                   (reinterpret_cast<uintptr_t>(se) & 15) == 0;
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  const int n = JE * 16;
+  const int nt = static_cast<int>(blockDim.x);
+  if (vec) {
+    const int rb = static_cast<int>(se_stride[0]) * 4;   // row bytes
+    const __amdgpu_buffer_rsrc_t r = rows_rsrc(se, rb, J, 256);
+    for (int i0 = threadIdx.x; i0 < n; i0 += kSeBatch * nt) {
+      uint4 x[kSeBatch];
+#pragma unroll
+      for (int u = 0; u < kSeBatch; ++u) {
+        const int i = i0 + u * nt;
+        x[u] = buf_load16(r, i < n ? static_cast<uint32_t>((i >> 4) * rb + 16 * (i & 15)) : kOutOfRange);
+      }
+#pragma unroll
+      for (int u = 0; u < kSeBatch; ++u) {
+        const int i = i0 + u * nt;
+        if (i < n) {
+          const bf16x4_t h = {static_cast<__bf16>(__uint_as_float(x[u].x)), static_cast<__bf16>(__uint_as_float(x[u].y)),
+                              static_cast<__bf16>(__uint_as_float(x[u].z)), static_cast<__bf16>(__uint_as_float(x[u].w))};
+          *reinterpret_cast<bf16x4_t*>(sE + (i >> 4) * row + 4 * (i & 15)) = h;
+        }
+      }
+    }
+    return;
+  }
+  for (int i = threadIdx.x; i < n; i += nt) {
+    const int j = i >> 4, d = 4 * (i & 15);
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (j < J) {
+      const float* p = se + j * se_stride[0] + d * se_stride[1];
+      x = make_float4(p[0], p[se_stride[1]], p[2 * se_stride[1]], p[3 * se_stride[1]]);
+    }
+    const bf16x4_t h = {static_cast<__bf16>(x.x), static_cast<__bf16>(x.y), static_cast<__bf16>(x.z),
+                        static_cast<__bf16>(x.w)};
+    *reinterpret_cast<bf16x4_t*>(sE + j * row + d) = h;
+  }
+}
+
 
 // Appends to `list` (wave-private LDS) the (index, offset) pairs of the
 // offsets that give some position in [lo, hi] a partner position inside
