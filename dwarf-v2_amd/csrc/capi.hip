@@ -635,9 +635,14 @@ static int check_decode_args(const dwarf_dsqg_q6_decode_args& a) {
   if ((rc = check_cache(a.cache, a.cache_stride, 3))) return rc;
   if (!a.pos || !a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.query_probes)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "positions, a parameter table, probes or offsets is NULL");
+  if (a.pb_stride[1] < 0 || a.pb_stride[2] < 0 ||
+      ((static_cast<int64_t>(a.J) - 1) * a.pb_stride[1] + (a.H - 1) * a.pb_stride[2] + 1) * 4 >= (int64_t(1) << 31))
+    return fail(DWARF_ERR_UNSUPPORTED, "decode reads a layer's pos_bias with 32-bit offsets (span below 2 GiB)");
   if (a.se_stride[2] != 1) return fail(DWARF_ERR_INVALID_ARGUMENT, "scale_embed needs unit stride on head_dim");
   if (!aligned16(a.scale_embed) || a.se_stride[0] % 4 || a.se_stride[1] % 4)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "scale_embed rows must be 16-byte aligned (read as float4)");
+  if (a.se_stride[1] > (int64_t(1) << 20))
+    return fail(DWARF_ERR_UNSUPPORTED, "decode reads a layer's scale_embed with 32-bit offsets (row stride <= 2^20)");
   if (a.pbase_stride[1] < 0 || a.pgain_stride[1] < 0 ||
       (a.pbase_stride[1] + a.pgain_stride[1] + DWARF_R_PLANES) * 4 * static_cast<int64_t>(a.J_large) >= (int64_t(1) << 31))
     return fail(DWARF_ERR_UNSUPPORTED, "decode reads a head's phase tables with 32-bit offsets (span below 2 GiB)");

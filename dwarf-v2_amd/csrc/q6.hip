@@ -653,31 +653,47 @@ __global__ __launch_bounds__(kBlock) void q6_decode_table(const dwarf_dsqg_q6_de
   uint16_t* sEl = sEh + JE * kTabERow;                                  // used when split
   float* s_pb = reinterpret_cast<float*>(sEh + JE * kTabERow * (split ? 2 : 1));   // [JE][H]
 
-  // this wave's q rows first, so their latency overlaps the staging
-  uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-  if (r0 + lr < rows) {
-    const int sq = (r0 + lr) / H, h = r0 + lr - sq * H;
+  // this wave's q rows first, so their latency overlaps the staging; a row past the end loads
+  // the last row instead (its products are never stored), so the load needs no condition
+  uint4 xa[2];
+  {
+    const int rr = r0 + lr < rows ? r0 + lr : rows - 1;
+    const int sq = rr / H, h = rr - sq * H;
     const bf16* qrow = reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1] + h * a.q_stride[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) xa[ks] = *reinterpret_cast<const uint4*>(qrow + 32 * ks + 8 * lc);
   }
   const float* se = a.scale_embed + ly * a.se_stride[0];
   const float* pbl = a.pos_bias + ly * a.pb_stride[0];
-  // staging: every load of a batch is issued before any is used (4 floats of
-  // one E row per load, 16 loads per row)
+  // Staging, one memory round trip per round of kBatch steps: a round issues
+  // every load before the first use, E rows (4 floats per load, 16 loads per
+  // row) and the layer's pos_bias [J][H] alike.  Both come through buffer
+  // loads, entries past a table (j >= J) reading zeros with no condition
+  // around the load (a conditional load with a default value is waited for at
+  // its join, one round trip each); the host bounds both spans below 2 GiB.
   constexpr int kBatch = 8;
-  for (int i0 = threadIdx.x; i0 < JE * 16; i0 += kBatch * kBlock) {
+  const int pb1 = static_cast<int>(a.pb_stride[1]), pb2 = static_cast<int>(a.pb_stride[2]);
+  const __amdgpu_buffer_rsrc_t rpbl = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(pbl), 0, ((J - 1) * pb1 + (H - 1) * pb2 + 1) * 4, 0x00020000);
+  const int se1 = static_cast<int>(a.se_stride[1]) * 4;   // E row bytes
+  const __amdgpu_buffer_rsrc_t rse = rows_rsrc(se, se1, J, 256);
+  const int ne = JE * 16, np = JE * H;
+  // one round (the first is peeled off the loop: a loop header waits for every load in flight)
+  auto stage_round = [&](int i0) {
     float4 v[kBatch];
+    float pv[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int i = i0 + u * kBlock, j = i >> 4;
-      v[u] = i < JE * 16 && j < J ? *reinterpret_cast<const float4*>(se + j * a.se_stride[1] + 4 * (i & 15))
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+      const uint4 ev = buf_load16(rse, i < ne && j < J ? static_cast<uint32_t>(j * se1 + 16 * (i & 15)) : kOutOfRange);
+      v[u] = make_float4(__uint_as_float(ev.x), __uint_as_float(ev.y), __uint_as_float(ev.z), __uint_as_float(ev.w));
+      const int jp = i / H, hp = i - jp * H;
+      pv[u] = buf_load_f32(rpbl, i < np && jp < J ? static_cast<uint32_t>((jp * pb1 + hp * pb2) * 4) : kOutOfRange);
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int i = i0 + u * kBlock;
-      if (i < JE * 16) {
+      if (i < ne) {
         const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
         uint16_t* dh = sEh + (i >> 4) * kTabERow + 4 * (i & 15);
         uint16_t* dl = sEl + (i >> 4) * kTabERow + 4 * (i & 15);
@@ -688,19 +704,11 @@ __global__ __launch_bounds__(kBlock) void q6_decode_table(const dwarf_dsqg_q6_de
           if (split) dl[e] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x[e] - static_cast<float>(hi)));
         }
       }
+      if (i < np) s_pb[i] = pv[u];
     }
-  }
-  for (int i0 = threadIdx.x; i0 < JE * H; i0 += kBatch * kBlock) {
-    float v[kBatch];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int i = i0 + u * kBlock, j = i / H, h = i - j * H;
-      v[u] = i < JE * H && j < J ? pbl[j * a.pb_stride[1] + h * a.pb_stride[2]] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (i0 + u * kBlock < JE * H) s_pb[i0 + u * kBlock] = v[u];
-  }
+  };
+  stage_round(threadIdx.x);
+  for (int i0 = threadIdx.x + kBatch * kBlock; i0 < (ne > np ? ne : np); i0 += kBatch * kBlock) stage_round(i0);
   __syncthreads();
   if (r0 >= rows) return;   // whole wave, after the only barrier
   for (int tile = 0; tile < JE / 16; ++tile) {
