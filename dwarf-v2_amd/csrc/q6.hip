@@ -576,6 +576,420 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
 }
 
 // ---------------------------------------------------------------------------
+// Prefill on widened rows with the near band on the matrix cores (used when a
+// workspace is given and the lattice has small offsets).  As in the bf16
+// forward (dsqg_fwd_bf16_win): the far offsets j >= JB are walked first,
+// gathering widened rows as q6_prefill_q4 does, with the far q.E columns in
+// the shared LDS region; then the tile's window of keys [n0 - 32, n0 + 64)
+// goes over them, its K and V codes as exact bf16 integers c (16-byte chunks
+// XOR-swizzled by row) and its group scales as fp32, and the leading small
+// offsets j < JB are served on the matrix cores:
+//   S_g^T = C_K,g Q_g^T per 32-dim group g   (v_mfma_f32_16x16x32_bf16)
+//   score = sum_g sK_g(key) S_g
+//   O^T  += C_V^T (P sV_g)^T                  (v_mfma_f32_16x16x16_bf16, P sV_g as bf16 hi + lo)
+// A block of O^T rows spans both groups, so each block is formed with both
+// groups' weights and each lane keeps the group of its own dims.
+// ---------------------------------------------------------------------------
+constexpr int kPfWinBack = 32;
+constexpr int kPfWinRows = kPfQPB + kPfWinBack;   // 96 keys
+
+struct PfWinLayout {
+  int JE, JL4, JBh, near_row, far_row, list_len;
+  size_t off_ph, off_qp, off_list, off_near, off_jn, off_big, off_vwin, off_scl, bytes;
+};
+
+__host__ __device__ inline int pf_pad_words(int n) { return (n + 11) / 16 * 16 + 4; }   // >= n, 4 mod 16
+
+__host__ __device__ inline PfWinLayout pf_win_layout(int J, int J_small, int J_large) {
+  PfWinLayout L;
+  L.JE = (J + 1 + 15) / 16 * 16;
+  L.JL4 = (J_large + 1) / 2 * 2;
+  L.JBh = J_small < kPfWinBack ? J_small : kPfWinBack;
+  L.near_row = pf_pad_words(L.JBh);
+  L.far_row = pf_pad_words(L.JE - L.JBh);
+  L.list_len = (L.JE + 4 + 1) / 2 * 2;
+  L.off_ph = static_cast<size_t>(2 * L.JE) * 4;                          // s_pb[JE], s_off[JE]
+  L.off_qp = L.off_ph + static_cast<size_t>(L.JL4) * 4 * 8;              // s_ph[JL4][4] float2
+  L.off_list = L.off_qp + static_cast<size_t>(kPlanes * kHeadDim) * 4;   // s_qp[4][64]
+  L.off_near = L.off_list + static_cast<size_t>(4 * L.list_len) * 8;     // s_list[4][list_len] int2
+  L.off_jn = L.off_near + static_cast<size_t>(kPfQPB * L.near_row) * 4;  // s_near[64][near_row]
+  L.off_big = L.off_jn + kJnSize * 4;                                    // s_jn[kJnSize]
+  // shared region: sE[JE][72] bf16, then s_far[64][far_row] f32, then the window
+  // (K codes [96][64] bf16, V codes [96][64] bf16, scales [96] float4)
+  L.off_vwin = L.off_big + static_cast<size_t>(kPfWinRows) * 128;
+  L.off_scl = L.off_vwin + static_cast<size_t>(kPfWinRows) * 128;
+  const size_t e_bytes = static_cast<size_t>(L.JE) * kPfERow * 2;
+  const size_t far_bytes = static_cast<size_t>(kPfQPB * L.far_row) * 4;
+  const size_t win_bytes = static_cast<size_t>(kPfWinRows) * (128 + 128 + 16);
+  size_t big = e_bytes > far_bytes ? e_bytes : far_bytes;
+  big = big > win_bytes ? big : win_bytes;
+  L.bytes = L.off_big + big;
+  return L;
+}
+
+// Eight code bytes (c + 32) as eight bf16 values c (exact).
+__device__ __forceinline__ uint4 code_bytes_to_bf16x8(uint32_t w0, uint32_t w1) {
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = i < 2 ? w0 : w1;
+    const int sh = 16 * (i & 1);
+    o[i] = pack_bf16x2(static_cast<float>((w >> sh) & 0xffu) - 32.f, static_cast<float>((w >> (sh + 8)) & 0xffu) - 32.f);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <int SHIFT>
+__global__ __launch_bounds__(kBlock, 2) void q6_prefill_win(const dwarf_dsqg_q6_prefill_args a,
+                                                            const uint8_t* __restrict__ xr, int tiles, int total) {
+  constexpr float kC = 0.125f * kLog2e;
+  constexpr float kSlack2 = 8.0f * kLog2e;
+  static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
+  const int J = a.J, N = a.N, J_small = a.J_small;
+  const PfWinLayout lay = pf_win_layout(J, J_small, a.J_large);
+  const int JE = lay.JE, JBh = lay.JBh, near_row = lay.near_row, far_row = lay.far_row, list_len = lay.list_len;
+  extern __shared__ float smem[];
+  char* sm = reinterpret_cast<char*>(smem);
+  float* s_pb = smem;
+  int* s_off = reinterpret_cast<int*>(smem + JE);
+  float2* s_ph = reinterpret_cast<float2*>(sm + lay.off_ph);
+  float* s_qp = reinterpret_cast<float*>(sm + lay.off_qp);
+  int2* s_list_all = reinterpret_cast<int2*>(sm + lay.off_list);
+  float* s_near = reinterpret_cast<float*>(sm + lay.off_near);
+  int* s_jn = reinterpret_cast<int*>(sm + lay.off_jn);             // [0]: JB; [kJnBias + d]: band slot of d, or -1
+  uint16_t* sE = reinterpret_cast<uint16_t*>(sm + lay.off_big);   // until the q.E tables are written
+  float* s_far = reinterpret_cast<float*>(sm + lay.off_big);      // during the far walk
+  char* s_kwin = sm + lay.off_big;                                 // during the band
+  char* s_vwin = sm + lay.off_vwin;
+  float4* s_scl = reinterpret_cast<float4*>(sm + lay.off_scl);    // (sK0, sK1, sV0, sV1) per window row
+
+  const int work = xcd_remap(blockIdx.x, total);
+  const int bh = work / tiles;
+  const int tile = tiles - 1 - (work - bh * tiles);   // late query tiles first
+  const int b = bh / a.H;
+  const int h = bh - b * a.H;
+  const int hk = h / (a.H / a.H_kv);
+
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int qi = l >> 2;
+  const int lr = l & 15, lc = l >> 4;
+  const int n0 = tile * kPfQPB;
+  const int n0w = n0 + w * kPfQPW;
+  const int n = n0w + qi;
+  const int n_hi = min(n0w + kPfQPW - 1, N - 1);
+  const bool row_ok = n < N;
+  const bool live = row_ok && n >= a.query_start;
+  const int64_t nn = n;
+  int2* s_list = s_list_all + w * list_len;
+  // output addresses now, in vector registers, so the argument fields they come from do not
+  // stay live in scalar registers through both walks
+  uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.out) + b * a.out_stride[0] + h * a.out_stride[1] +
+                                       nn * a.out_stride[2] + 16 * g);
+  float* lse_p = a.lse ? a.lse + b * a.lse_stride[0] + h * a.lse_stride[1] + nn * a.lse_stride[2] : nullptr;
+  asm volatile("" : "+v"(o4), "+v"(lse_p));
+
+  // the wave's q rows (MFMA layout) and this lane's slice, requested first
+  const bf16* qbase = reinterpret_cast<const bf16*>(a.q) + b * a.q_stride[0] + h * a.q_stride[1];
+  uint4 xa[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  if (n0w + lr < N) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      xa[ks] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(n0w + lr) * a.q_stride[2] + 32 * ks + 8 * lc);
+  }
+  uint4 qx0 = {0u, 0u, 0u, 0u}, qx1 = {0u, 0u, 0u, 0u};
+  if (live) {
+    const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * a.q_stride[2] + 16 * g);
+    qx0 = q4[0];
+    qx1 = q4[1];
+  }
+
+  stage_se_bf16(a.scale_embed, a.se_stride, J, JE, sE, kPfERow);
+  for (int j = threadIdx.x; j < JE; j += kBlock) {
+    s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
+    s_off[j] = j < J ? a.offsets[j] : 0;
+  }
+  for (int t = threadIdx.x; t < a.J_large * kPlanes; t += kBlock) {
+    const int i = t / kPlanes, r = t - i * kPlanes;
+    s_ph[t] = make_float2(a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r],
+                          a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r]);
+  }
+  for (int i = threadIdx.x; i < kPlanes * kHeadDim; i += kBlock) s_qp[i] = a.query_probes[i];
+  __syncthreads();
+
+  if (threadIdx.x == 0) build_band_slots(s_jn, s_off, J_small, kPfWinBack, JBh, true);
+  // q.E tables: products into registers, a barrier (every wave is done
+  // reading sE), then the near columns into s_near and the far ones over sE
+  {
+    f32x4 c[kPfMaxBlocks];
+#pragma unroll
+    for (int bi = 0; bi < kPfMaxBlocks; ++bi) {
+      c[bi] = zero4();
+      if (bi * 16 < JE) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const uint4 xb = *reinterpret_cast<const uint4*>(sE + (bi * 16 + lr) * kPfERow + 32 * ks + 8 * lc);
+          c[bi] = mfma16_bf16(bf16x8_from_bits(xa[ks]), bf16x8_from_bits(xb), c[bi]);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int bi = 0; bi < kPfMaxBlocks; ++bi) {
+      if (bi * 16 < JE) {
+        const int j = bi * 16 + lr;
+        const float pb8 = 8.0f * s_pb[j];
+        float* dst = j < JBh ? s_near + (w * kPfQPW + 4 * lc) * near_row + j
+                                 : s_far + (w * kPfQPW + 4 * lc) * far_row + (j - JBh);
+        const int stride = j < JBh ? near_row : far_row;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[r * stride] = (c[bi][r] + pb8) * kC;
+      }
+    }
+  }
+  const int JB = uniform(s_jn[0]);
+
+  // this lane's q slice (bf16 pairs and fp32), 160 * sum(q) for the biased
+  // code pairs, and y of plane g = <q, probe_g> / sqrt(|q|^2 + 1e-6 hd)
+  const uint32_t q32[8] = {qx0.x, qx0.y, qx0.z, qx0.w, qx1.x, qx1.y, qx1.z, qx1.w};
+  float qf[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { qf[2 * i] = bf16_lo(q32[i]); qf[2 * i + 1] = bf16_hi(q32[i]); }
+  float qbias = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qbias = dot2bf(q32[i], 0x3f803f80u, qbias);   // (1, 1) in bf16
+  qbias *= -160.f;
+  float yg;
+  {
+    float ss = 0.f, yp[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+      ss = fmaf(qf[d], qf[d], ss);
+#pragma unroll
+      for (int r = 0; r < kPlanes; ++r) yp[r] = fmaf(qf[d], s_qp[r * kHeadDim + 16 * g + d], yp[r]);
+    }
+    ss = group_sum<4>(ss);
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) yp[r] = group_sum<4>(yp[r]);
+    yg = pick4(g, yp[0], yp[1], yp[2], yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
+  }
+
+  const int n_eff = live ? n : n0w - 2 * N;   // no source for a query that is not live
+  const __amdgpu_buffer_rsrc_t rc = rows_rsrc(xr + static_cast<int64_t>(b * a.H_kv + hk) * N * kXRow, kXRow, N, kXRow);
+  const int sb_lane = n_eff * kXRow;
+  const float* qe_near = s_near + (w * kPfQPW + qi) * near_row;
+  const float* qe_far = s_far + (w * kPfQPW + qi) * far_row - JBh;
+
+  float acc[16];
+#pragma unroll
+  for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+  float m = -3.0e38f, lsum = 0.f;
+  float wsum = 0.f;   // sum of the walk's V weights, for the +32 carried by the V code bytes
+
+  // ---- 1. far walk: the listed offsets j >= JB, gathering widened rows ----
+  if (n0w < N) {
+    const int cnt = build_offset_list<1>(s_list, s_off, J, n0w, n_hi, N, 1, make_int2(J, n0w - N), JB);
+    const bool all_far = JB == JBh;
+    auto fetch = [&](int k0, PxSlot& s) {
+      const int2 e = s_list[k0];
+      const int j = uniform(e.x), d = uniform(e.y);
+      s.j = j;
+      s.ok = static_cast<uint32_t>(n_eff - d) < static_cast<uint32_t>(N);
+      const uint32_t base = static_cast<uint32_t>(sb_lane - d * kXRow);
+      s.k = buf_load16(rc, base + kXK + 16 * g);
+      s.v = buf_load16(rc, base + kXV + 16 * g);
+      const auto mt = __builtin_amdgcn_raw_buffer_load_b64(rc, base + kXMeta + 8 * g, 0, 0);
+      s.meta = make_uint2(mt[0], mt[1]);
+    };
+    auto consume = [&](const PxSlot& s, const float* qe_row) {
+      // K: v_perm puts two code bytes under the bf16 high byte 0x43, i.e. the
+      // pair (128 + byte) = (160 + c); sum_d q_d (160 + c_d) - 160 sum_d q_d
+      const uint32_t kw[4] = {s.k.x, s.k.y, s.k.z, s.k.w};
+      float kd = qbias;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kd = dot2bf(q32[2 * i], __builtin_amdgcn_perm(0x43434343u, kw[i], 0x04010400u), kd);
+        kd = dot2bf(q32[2 * i + 1], __builtin_amdgcn_perm(0x43434343u, kw[i], 0x04030402u), kd);
+      }
+      const float ksc = half_bits_to_f32(static_cast<uint16_t>(s.meta.x));
+      const float vsc = half_bits_to_f32(static_cast<uint16_t>(s.meta.x >> 16));
+      const float zf = __uint_as_float(s.meta.y);
+      const float dot = group_sum<4>(kd * ksc);
+      const float s2 = s.ok ? fmaf(dot, kC, qe_row[s.j]) : -INFINITY;
+      if (s2 > m + kSlack2) {
+        const float f = __builtin_amdgcn_exp2f(m - s2);   // 0 on the first valid offset
+#pragma unroll
+        for (int d = 0; d < 16; ++d) acc[d] *= f;
+        lsum *= f;
+        wsum *= f;
+        m = s2;
+      }
+      const float p = __builtin_amdgcn_exp2f(s2 - m);   // m is finite: 0 without a source
+      lsum += p;
+      // V: each code byte to fp32 (v_cvt_f32_ubyte*): c + 32; the MOVT pair
+      // drops the +32 here, the other dims when the row ends
+      float cf[16];
+      const uint32_t vw[4] = {s.v.x, s.v.y, s.v.z, s.v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cf[4 * i + e] = static_cast<float>((vw[i] >> (8 * e)) & 0xffu);
+      cf[SHIFT] -= 32.f;
+      cf[SHIFT + 1] -= 32.f;
+      if (s.j >= J_small && s.j < J) {   // wave-uniform
+        const float2 ph = s_ph[(s.j - J_small) * kPlanes + g];
+        float sn, cs;
+        dsincos<true>(fmaf(ph.y * yg, zf, ph.x), &sn, &cs);
+        const float va = cf[SHIFT], vb = cf[SHIFT + 1];
+        cf[SHIFT] = cs * va - sn * vb;
+        cf[SHIFT + 1] = sn * va + cs * vb;
+      }
+      const float wgt = p * vsc;
+      wsum += wgt;
+#pragma unroll
+      for (int d = 0; d < 16; ++d) acc[d] = fmaf(wgt, cf[d], acc[d]);
+      pin_regs<16>(acc);
+    };
+    if (cnt > 0) {
+      PxSlot s0, s1;
+      fetch(0, s0);
+      for (int k0 = 0; k0 < cnt; k0 += 2) {
+        fetch(k0 + 1, s1);   // past the list end this reads the sentinel: zeros
+        consume(s0, all_far || s0.j >= JBh ? qe_far : qe_near);
+        fetch(k0 + 2, s0);
+        consume(s1, all_far || s1.j >= JBh ? qe_far : qe_near);
+      }
+    }
+  }
+  // the walk's +32 on the V codes of the dims outside the MOVT pair
+#pragma unroll
+  for (int d = 0; d < 16; ++d)
+    if (d != SHIFT && d != SHIFT + 1) acc[d] = fmaf(-32.f, wsum, acc[d]);
+
+  // ---- 2. near band: offsets j < JB on the matrix cores, from the window in LDS ----
+  __syncthreads();   // every wave is done with the far table: the window goes over it
+  if (JB > 0) {
+    // keys [n0 - 32, n0 + 64), one (row, 16-dim chunk) per unit: codes to bf16
+    // c (keys outside [0, N) read zeros: their scores are masked), 16-byte
+    // chunk cc of a row at position cc ^ (row & 7); the group scales of the
+    // row from chunks 0 and 2
+    for (int u = threadIdx.x; u < kPfWinRows * 4; u += kBlock) {
+      const int row = u >> 2, ch = u & 3;
+      const int key = n0 - kPfWinBack + row;
+      const uint32_t base = static_cast<uint32_t>(key * kXRow);
+      const uint4 kb = buf_load16(rc, base + kXK + 16 * ch);
+      const uint4 vb = buf_load16(rc, base + kXV + 16 * ch);
+      const uint32_t mt = __builtin_amdgcn_raw_buffer_load_b32(rc, base + kXMeta + 8 * ch, 0, 0);
+      const int sw = row & 7;
+      *reinterpret_cast<uint4*>(s_kwin + row * 128 + 16 * ((2 * ch) ^ sw)) = code_bytes_to_bf16x8(kb.x, kb.y);
+      *reinterpret_cast<uint4*>(s_kwin + row * 128 + 16 * ((2 * ch + 1) ^ sw)) = code_bytes_to_bf16x8(kb.z, kb.w);
+      *reinterpret_cast<uint4*>(s_vwin + row * 128 + 16 * ((2 * ch) ^ sw)) = code_bytes_to_bf16x8(vb.x, vb.y);
+      *reinterpret_cast<uint4*>(s_vwin + row * 128 + 16 * ((2 * ch + 1) ^ sw)) = code_bytes_to_bf16x8(vb.z, vb.w);
+      if ((ch & 1) == 0) {
+        float* sc = reinterpret_cast<float*>(s_scl + row) + (ch >> 1);
+        sc[0] = half_bits_to_f32(static_cast<uint16_t>(mt));          // K scale of group ch / 2
+        sc[2] = half_bits_to_f32(static_cast<uint16_t>(mt >> 16));    // V scale of group ch / 2
+      }
+    }
+  }
+  __syncthreads();   // the window is staged
+  if (n0w < N && JB > 0) {
+    // Band lane (lc, lr) serves query n0w + lr; in the MFMA C layout it holds
+    // keys n0w - 32 + 16 tb + 4 lc + r of the wave's key blocks tb = 0..2.
+    const int nq = n0w + lr;
+    const bool live_b = nq < N && nq >= a.query_start;
+    auto win16 = [&](const char* base, int row, int c) { return base + row * 128 + 16 * (c ^ (row & 7)); };
+    const float* qe_b = s_near + (w * kPfQPW + lr) * near_row;
+    // the far walk's running maximum of this query (gather lane 4 lr)
+    const float m_q = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * lr), __float_as_int(m)));
+    float sb[3][4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int tb = 0; tb < 3; ++tb) {
+      const int wr = 16 * (w + tb) + lr;               // window row of key n0w - 32 + 16 tb + lr
+      const uint4 ka0 = *reinterpret_cast<const uint4*>(win16(s_kwin, wr, lc));       // dims 8 lc + [0, 8): group 0
+      const uint4 ka1 = *reinterpret_cast<const uint4*>(win16(s_kwin, wr, 4 + lc));   // group 1
+      const f32x4 S0 = mfma16_bf16(bf16x8_from_bits(ka0), bf16x8_from_bits(xa[0]), zero4());
+      const f32x4 S1 = mfma16_bf16(bf16x8_from_bits(ka1), bf16x8_from_bits(xa[1]), zero4());
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kr = 16 * (w + tb) + 4 * lc + r;     // window row of the entry's key
+        const float4 scl = s_scl[kr];
+        const int slot = s_jn[kJnBias + lr + kPfWinBack - 16 * tb - 4 * lc - r];
+        const bool ok = slot >= 0 && live_b && n0w - kPfWinBack + 16 * tb + 4 * lc + r >= 0;
+        const float sc2 = fmaf(fmaf(scl.x, S0[r], scl.y * S1[r]), kC, qe_b[slot >= 0 ? slot : 0]);
+        sb[tb][r] = ok ? sc2 : -INFINITY;
+        cmax = fmaxf(cmax, sb[tb][r]);
+      }
+    }
+    cmax = max_xor32(max_xor16(cmax));                 // over the four lanes of query lr
+    const float m_use = cmax > m_q + kSlack2 ? cmax : m_q;
+    f32x4 acc0[4], acc1[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) { acc0[db] = zero4(); acc1[db] = zero4(); }
+    float lb = 0.f;
+#pragma unroll
+    for (int tb = 0; tb < 3; ++tb) {
+      float p0h[4], p0l[4], p1h[4], p1l[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float4 scl = s_scl[16 * (w + tb) + 4 * lc + r];
+        const float p = __builtin_amdgcn_exp2f(sb[tb][r] - m_use);   // 0 off the band
+        lb += p;
+        const float w0 = p * scl.z, w1 = p * scl.w;
+        p0h[r] = w0; p0l[r] = w0 - round_bf16(w0);
+        p1h[r] = w1; p1l[r] = w1 - round_bf16(w1);
+      }
+      const i16x4 b0h = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(p0h[0], p0h[1]), pack_bf16x2(p0h[2], p0h[3])));
+      const i16x4 b0l = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(p0l[0], p0l[1]), pack_bf16x2(p0l[2], p0l[3])));
+      const i16x4 b1h = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(p1h[0], p1h[1]), pack_bf16x2(p1h[2], p1h[3])));
+      const i16x4 b1l = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(p1l[0], p1l[1]), pack_bf16x2(p1l[2], p1l[3])));
+      // V code rows read transposed from the window (rows 16 (w + tb) + 4 lc + e,
+      // dims 16 (lr / 4) + 4 db + lr % 4 of MFMA row lr)
+      const int R = 16 * (w + tb) + 4 * lc + (lr >> 2);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const i16x4 av = lds_read_tr16(win16(s_vwin, R, 2 * (lr & 3) + (db >> 1)) + 8 * (db & 1));
+        acc0[db] = mfma16k16_bf16(av, b0h, acc0[db]);
+        acc0[db] = mfma16k16_bf16(av, b0l, acc0[db]);
+        acc1[db] = mfma16k16_bf16(av, b1h, acc1[db]);
+        acc1[db] = mfma16k16_bf16(av, b1l, acc1[db]);
+      }
+    }
+    lb = add_xor32(add_xor16(lb));
+    // into the gather layout: query qi, dims 16 g + 4 db + r <- band lane (lr = qi, lc = g),
+    // whose dims lie in group lc / 2
+    const int srcq = 4 * (qi + 16 * g);
+    const float m_new = __int_as_float(__builtin_amdgcn_ds_bpermute(srcq, __float_as_int(m_use)));
+    const float l_new = __int_as_float(__builtin_amdgcn_ds_bpermute(srcq, __float_as_int(lb)));
+    const float f = __builtin_amdgcn_exp2f(m - m_new);   // 1 when the maximum stays; 0 with no far pair
+    const bool grp1 = lc >= 2;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ob = grp1 ? acc1[db][r] : acc0[db][r];
+        acc[4 * db + r] = fmaf(acc[4 * db + r], f, __int_as_float(__builtin_amdgcn_ds_bpermute(srcq, __float_as_int(ob))));
+      }
+    lsum = fmaf(lsum, f, l_new);
+    m = m_new;
+  }
+
+  if (!row_ok) return;
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  uint4 x0, x1;
+  x0.x = pack_bf16x2(acc[0] * inv, acc[1] * inv);   x0.y = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+  x0.z = pack_bf16x2(acc[4] * inv, acc[5] * inv);   x0.w = pack_bf16x2(acc[6] * inv, acc[7] * inv);
+  x1.x = pack_bf16x2(acc[8] * inv, acc[9] * inv);   x1.y = pack_bf16x2(acc[10] * inv, acc[11] * inv);
+  x1.z = pack_bf16x2(acc[12] * inv, acc[13] * inv); x1.w = pack_bf16x2(acc[14] * inv, acc[15] * inv);
+  o4[0] = x0;
+  o4[1] = x1;
+  if (lse_p && g == 0) *lse_p = lsum > 0.f ? (m + __builtin_amdgcn_logf(lsum)) * kLn2 : -INFINITY;
+}
+
+// ---------------------------------------------------------------------------
 // Decode.  One workgroup per (sequence, layer), one wave per head.
 //
 // A slot's codes come in 12-byte chunks of 16 head dims (K at 12c, V at
@@ -964,6 +1378,21 @@ hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t st
                      stream, a.H_kv, a.N, rows, a.cache, a.cache_stride[0], a.cache_stride[1], a.cache_stride[2], xr);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (a.J_small > 0) {
+    const size_t lds = pf_win_layout(a.J, a.J_small, a.J_large).bytes;
+#define DWARF_Q6W_CASE(S)                                                                                  \
+  case S:                                                                                                  \
+    hipLaunchKernelGGL((q6_prefill_win<S>), dim3(total), dim3(kBlock), lds, stream, a, xr, tiles, total);   \
+    break;
+    switch (a.plane_shift) {
+      DWARF_Q6W_CASE(0) DWARF_Q6W_CASE(1) DWARF_Q6W_CASE(2) DWARF_Q6W_CASE(3) DWARF_Q6W_CASE(4)
+      DWARF_Q6W_CASE(5) DWARF_Q6W_CASE(6) DWARF_Q6W_CASE(7) DWARF_Q6W_CASE(8) DWARF_Q6W_CASE(9)
+      DWARF_Q6W_CASE(10) DWARF_Q6W_CASE(11) DWARF_Q6W_CASE(12) DWARF_Q6W_CASE(13) DWARF_Q6W_CASE(14)
+      default: return hipErrorInvalidValue;
+    }
+#undef DWARF_Q6W_CASE
+    return hipGetLastError();
+  }
   return launch_prefill_rows<true>(a, xr, tiles, total, stream);
 }
 
