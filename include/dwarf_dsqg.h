@@ -87,11 +87,12 @@ typedef struct {
 /*
  * Schedules (dwarf_dsqg_fwd_args.schedule).  They compute the same function;
  * results differ only by fp32 summation order.
- *   DWARF_SCHED_BAND: the bf16 dQ launch serves the leading small offsets
- *     (ascending, <= 32) as a dense band on the matrix cores from a K window
- *     in LDS, the reference's overlap-slab formulation of the near offsets
- *     (grouped_mode overlap_slab / overlap_slab_bwd, dsqg:1047-1256,
- *     1491-1727); fp32 launches ignore it.
+ *   DWARF_SCHED_BAND: the bf16 forward, dQ and dK/dV launches serve the
+ *     leading small offsets (ascending, <= 32) as a dense band on the matrix
+ *     cores from K/V (forward, dQ) or q/dO (dK/dV) windows in LDS, the
+ *     reference's overlap-slab formulation of the near offsets (grouped_mode
+ *     overlap_slab / overlap_slab_bwd, dsqg:1047-1256, 1491-1727, 1957-2187);
+ *     the two-pass forward and fp32 launches ignore it.
  *   DWARF_SCHED_TWO_PASS: the forward takes each row's score maximum first and
  *     then forms the softmax and the weighted sum without rescaling: the
  *     reference's offline-softmax kernel (online_softmax=False,
