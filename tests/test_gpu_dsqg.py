@@ -263,9 +263,11 @@ def test_fp32_two_pass_forward(pkg, device):
 
 def test_band_lattice_edges(pkg, device):
     """Lattices whose small offsets the band takes only in part: a small offset above 32 (stays in the
-    gather loop) and unsorted small offsets (the band stops at the first descent); mode 3 against the
+    gather loop), unsorted small offsets (the band stops at the first descent) and small offsets all
+    above 32 (no band; the forward's walk reads their q.E from the near table); mode 3 against the
     oracle."""
-    for offsets, js in (([1, 2, 3, 5, 8, 13, 21, 40, 48, 64, 96], 8), ([2, 1, 4, 3, 48, 96], 4)):
+    for offsets, js in (([1, 2, 3, 5, 8, 13, 21, 40, 48, 64, 96], 8), ([2, 1, 4, 3, 48, 96], 4),
+                        ([40, 33, 64, 96], 2)):
         x = make_inputs(1, 2, 2, 200, offsets, js, seed=95, dtype=torch.bfloat16, gain_std=4.0)
         dout = torch.randn(1, 2, 200, 64, generator=torch.Generator().manual_seed(96)).to(torch.bfloat16)
         out, grads = gpu_fwd_bwd(pkg, x, offsets, js, 0, 1, dout, device, mode=3)

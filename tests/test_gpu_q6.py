@@ -78,6 +78,27 @@ def test_prefill_matches_oracle(pkg, device, widen, shift):
     assert (lse.cpu().double()[fin] - rlse[fin]).abs().max().item() < 2e-2
 
 
+@pytest.mark.parametrize("offsets,js", [
+    ([1, 2, 3, 5, 8, 13, 21, 40, 48, 64, 96], 8),   # a small offset above 32: the band takes 7 of 8
+    ([2, 1, 4, 3, 48, 96], 4),                      # unsorted small offsets: the band stops at the descent
+    ([40, 33, 64, 96], 2),                          # small offsets all above 32: no band, near table read by the walk
+    ([48, 64, 96], 0),                              # no small offsets: the widened-row gather alone
+])
+def test_prefill_band_lattice_edges(pkg, device, offsets, js):
+    """Widened rows with lattices whose small offsets the near band takes only in part or not at
+    all; against the oracle on the dequantised cache, ragged N, query_start 1."""
+    x = make_inputs(1, 2, 2, 200, offsets, js, seed=97, dtype=torch.bfloat16, gain_std=4.0)
+    qp, kp = orthogonal_probes(64, 0)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    xd = {n: t.to(device) for n, t in x.items()}
+    cache = pkg.q6.pack_kv(xd["k"], xd["v"], kp.to(device))
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_prefill(xd["q"], cache, xd["pos_bias"], xd["scale_embed"], xd["phase_base"], xd["phase_gain"],
+                            qp.to(device), off, js, len(offsets) - js, 0, 1, widen=True)
+    ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, js, 0, qp, kp, 1)
+    assert max_abs(out, ref) < 2e-2, (offsets, max_abs(out, ref))
+
+
 @pytest.mark.parametrize("widen", [True, False])
 def test_prefill_fp32_scale_embed(pkg, device, widen):
     """round_se=False: the prefill's <q, e_j> table takes SE in fp32, against the oracle without SE
