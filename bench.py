@@ -83,7 +83,15 @@ class CacheFlush:
 
 
 def time_dsqg_step(pkg, t, js, jl, steps, warmup, flush=None):
-    """Returns (ms_per_step, per-launch average ms dict)."""
+    """Returns (ms_per_step, per-launch average ms dict).
+
+    The step time comes from K steps bracketed by two events only.  The
+    per-launch durations come from a second run of K steps with an event
+    between launches: each event record costs the stream a gap of several µs
+    between launches, so those events stay out of the step's clock.  With
+    ``flush`` (cold clock) every step is preceded by a cache-evicting read and
+    timed by its own two events.
+    """
     ops = pkg.dsqg if hasattr(pkg, "dsqg") else importlib.import_module("dwarf-v2_amd.dsqg")
     args = (t["q"], t["k"], t["v"], t["pos_bias"], t["scale_embed"], t["phase_base"], t["phase_gain"],
             t["y_pre"], t["z_pre"], t["offsets"])
@@ -92,27 +100,36 @@ def time_dsqg_step(pkg, t, js, jl, steps, warmup, flush=None):
         out, lse = ops.dsqg_forward(*args, js, jl, 0, 1, events=ev_f)
         ops.dsqg_backward(t["dout"], *args, out, lse, js, jl, 0, 1, events=ev_b)
 
+    def ev(n):
+        return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    evs = [([torch.cuda.Event(enable_timing=True) for _ in range(2)],
-            [torch.cuda.Event(enable_timing=True) for _ in range(4)]) for _ in range(steps)]
-    total_ms = 0.0
     if flush is None:
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start, end = ev(2)
         torch.cuda.synchronize()
         start.record()
-        for ef, eb in evs:
-            step(ef, eb)
+        for _ in range(steps):
+            step()
         end.record()
         torch.cuda.synchronize()
         total_ms = start.elapsed_time(end)
     else:
-        for ef, eb in evs:
+        marks = [ev(2) for _ in range(steps)]
+        for s, e in marks:
             flush()
-            step(ef, eb)
+            s.record()
+            step()
+            e.record()
         torch.cuda.synchronize()
-        total_ms = sum(ef[0].elapsed_time(eb[3]) for ef, eb in evs)
+        total_ms = sum(s.elapsed_time(e) for s, e in marks)
+    evs = [(ev(2), ev(4)) for _ in range(steps)]
+    for ef, eb in evs:
+        if flush is not None:
+            flush()
+        step(ef, eb)
+    torch.cuda.synchronize()
     per = {
         "fwd": sum(ef[0].elapsed_time(ef[1]) for ef, _ in evs) / steps,
         "bwd_dq": sum(eb[0].elapsed_time(eb[1]) for _, eb in evs) / steps,
