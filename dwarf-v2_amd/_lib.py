@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "dwarf_dsqg_bwd_dq",
     "dwarf_dsqg_bwd_params",
     "dwarf_dsqg_bwd_dkdv",
+    "dwarf_dsqg_bwd_delta",
     "dwarf_ema_fwd_workspace_bytes",
     "dwarf_ema_fwd",
     "dwarf_ema_bwd_workspace_bytes",
@@ -89,6 +90,7 @@ class DsqgFwdArgs(ctypes.Structure):
 
 DWARF_SCHED_BAND = 1
 DWARF_SCHED_TWO_PASS = 2
+DWARF_SCHED_DELTA_STAGE = 4
 
 
 class DsqgBwdArgs(ctypes.Structure):
@@ -304,7 +306,7 @@ def load() -> ctypes.CDLL:
     lib.dwarf_dsqg_bwd_workspace_bytes.argtypes = [POINTER(DsqgBwdArgs)]
     lib.dwarf_dsqg_bwd.restype = c_int
     lib.dwarf_dsqg_bwd.argtypes = [POINTER(DsqgBwdArgs), c_void_p]
-    for name in ("dwarf_dsqg_bwd_dq", "dwarf_dsqg_bwd_params", "dwarf_dsqg_bwd_dkdv"):
+    for name in ("dwarf_dsqg_bwd_dq", "dwarf_dsqg_bwd_params", "dwarf_dsqg_bwd_dkdv", "dwarf_dsqg_bwd_delta"):
         getattr(lib, name).restype = c_int
         getattr(lib, name).argtypes = [POINTER(DsqgBwdArgs), c_void_p]
     lib.dwarf_ema_fwd_workspace_bytes.restype = c_size_t

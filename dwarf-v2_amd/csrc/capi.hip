@@ -252,6 +252,24 @@ int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) 
   return bwd_stage(args, stream, false, false, true, "dwarf_dsqg_bwd_dkdv");
 }
 
+int dwarf_dsqg_bwd_delta(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
+  if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
+  const dwarf_dsqg_bwd_args& a = *args;
+  int rc = check_fwd(a.fwd);
+  if (rc) return rc;
+  if (a.fwd.dtype != DWARF_BF16)
+    return fail(DWARF_ERR_UNSUPPORTED, "dwarf_dsqg_bwd_delta: bf16 only (the fp32 dQ launch forms delta itself)");
+  if (a.fwd.B == 0 || a.fwd.N == 0) return ok();
+  if ((rc = check_contig_rows("dout", a.dout, a.dout_stride, a.fwd.dtype))) return rc;
+  const dwarf::BwdWorkspace ws = dwarf::bwd_workspace_layout(a);
+  if (!a.workspace || a.workspace_bytes < ws.total)
+    return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", ws.total, a.workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(a.workspace) & 255u) != 0)
+    return fail(DWARF_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return hip_status(dwarf::launch_dsqg_bwd_delta(a, ws, reinterpret_cast<hipStream_t>(stream)),
+                    "dwarf_dsqg_bwd_delta");
+}
+
 // ---- EMA --------------------------------------------------------------------
 static int check_ema_common(int B, int N, int D, int dtype, int per_channel, float lo, float hi, const float* alpha) {
   if (B < 0 || N < 0 || D < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "bad sizes B=%d N=%d D=%d", B, N, D);

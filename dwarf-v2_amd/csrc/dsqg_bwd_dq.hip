@@ -712,7 +712,8 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
     dlt = group_sum<4>(dlt);
     // (delta, lse in log2 units) for the dK/dV launch; +inf makes P = 0 for a
     // query without softmax mass or before query_start
-    if (row_ok && g == 0)
+    // (under DWARF_SCHED_DELTA_STAGE dsqg_bwd_delta_bf16 writes them, the same bits)
+    if (row_ok && g == 0 && !(f.schedule & DWARF_SCHED_DELTA_STAGE))
       *reinterpret_cast<float2*>(delta_ws + 2 * (static_cast<int64_t>(bh) * N + n)) =
           make_float2(dlt, mass ? lse2 : INFINITY);
     // the wave's q rows as the B operand of the per-step <q, e_j> MFMA: lane
@@ -1096,6 +1097,53 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
   }
 }
 
+// The delta stage on its own (DWARF_SCHED_DELTA_STAGE): the (delta, lse in
+// log2 units) pairs of the dQ prologue, with the same lane layout and the same
+// arithmetic (delta = <dO, O_bf16> as v_dot2 over the lane's 16 dims, then the
+// four lanes' sum by DPP), so the pairs equal bit for bit those the dQ launch
+// forms (reference: _compute_D_v18_grouped, dsqg:1263-1289).  One 64-query
+// tile per workgroup.
+__global__ __launch_bounds__(kBlock) void dsqg_bwd_delta_bf16(const dwarf_dsqg_bwd_args a, float* __restrict__ delta_ws,
+                                                             int tiles) {
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  const int N = f.N;
+  const int T = xcd_remap(blockIdx.x, static_cast<int>(gridDim.x));
+  const int bh = T / tiles;
+  const int t = T - bh * tiles;
+  const int b = bh / f.H;
+  const int h = bh - b * f.H;
+  const int lane = threadIdx.x;
+  const int w = lane / kWave;
+  const int l = lane % kWave;
+  const int g = l & 3;
+  const int qi = l >> 2;
+  const int n = t * kQT + kQPW * w + qi;
+  const bool row_ok = n < N;
+  const bool live = row_ok && n >= f.query_start;
+  const int64_t nn = n;
+  float dlt = 0.f, lse2 = 0.f;
+  bool mass = false;
+  if (live) {
+    const bf16* dob = reinterpret_cast<const bf16*>(a.dout) + b * a.dout_stride[0] + h * a.dout_stride[1];
+    const bf16* ob = reinterpret_cast<const bf16*>(f.out) + b * f.out_stride[0] + h * f.out_stride[1];
+    const uint4* d4 = reinterpret_cast<const uint4*>(dob + nn * a.dout_stride[2] + 16 * g);
+    const uint4* o4 = reinterpret_cast<const uint4*>(ob + nn * f.out_stride[2] + 16 * g);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 y = d4[i], o = o4[i];
+      dlt = dot2bf(y.x, o.x, dlt); dlt = dot2bf(y.y, o.y, dlt);
+      dlt = dot2bf(y.z, o.z, dlt); dlt = dot2bf(y.w, o.w, dlt);
+    }
+    const float lse = f.lse[b * f.lse_stride[0] + h * f.lse_stride[1] + nn * f.lse_stride[2]];
+    mass = lse > -INFINITY;
+    lse2 = mass ? lse * kLog2e : 0.f;
+  }
+  dlt = group_sum<4>(dlt);
+  if (row_ok && g == 0)
+    *reinterpret_cast<float2*>(delta_ws + 2 * (static_cast<int64_t>(bh) * N + n)) =
+        make_float2(dlt, mass ? lse2 : INFINITY);
+}
+
 template <int MBW>
 __global__ __launch_bounds__(kBlock, dse_wgs_per_cu(MBW)) void dsqg_bwd_dse_bf16(const dwarf_dsqg_bwd_args a,
                                                                const float* __restrict__ ds_ws,
@@ -1280,6 +1328,15 @@ hipError_t launch_dq_typed(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws,
 }
 
 }  // namespace
+
+hipError_t launch_dsqg_bwd_delta(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  const int total = ws.dq_tiles * f.B * f.H;
+  if (total == 0) return hipSuccess;
+  float* delta = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + ws.delta_off);
+  hipLaunchKernelGGL(dsqg_bwd_delta_bf16, dim3(total), dim3(kBlock), 0, stream, a, delta, ws.dq_tiles);
+  return hipGetLastError();
+}
 
 size_t dq_lds_bytes(int J, int J_large, int dtype) {
   return dtype == DWARF_BF16 ? dq_g4_layout(J, J_large).bytes : dq_lds<float>(J).bytes;

@@ -61,6 +61,7 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a);
 hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
                            bool do_params, bool do_dkdv);
 hipError_t launch_dsqg_bwd_dq(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
+hipError_t launch_dsqg_bwd_delta(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
 hipError_t launch_dsqg_bwd_dse(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream);
 size_t dq_lds_bytes(int J, int J_large, int dtype);
 size_t dkdv_lds_bytes(int J, int J_large, int group);   // bf16 dK/dV launch, per workgroup

@@ -145,13 +145,30 @@ def dsqg_forward(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, 
     return out, lse
 
 
-def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
-                  out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None, schedule=None):
-    """Raw backward: the dq, params and dkdv stages on the current stream.
+_SIDE_STREAMS: dict = {}
 
-    Returns (dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz).  ``events``:
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """This device's second stream for the overlapped backward (default priority)."""
+    key = torch.cuda._utils._get_device_index(device, optional=True)
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+    return _SIDE_STREAMS[key]
+
+
+def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
+                  out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None, schedule=None,
+                  overlap=None):
+    """Raw backward.  Returns (dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz).
+
+    bf16 (``overlap`` None or True, no ``events``): the delta stage and dK/dV
+    run on a second stream beside dQ and the parameter gradients on the
+    current stream, which waits for both (DWARF_SCHED_DELTA_STAGE); the two
+    gather launches then share the CUs.  Otherwise, and for fp32, the dq,
+    params and dkdv stages run in turn on the current stream.  ``events``:
     optional four torch.cuda.Events recorded before dq, after dq, after params
-    and after dkdv.
+    and after dkdv (serial stages, so each interval is one stage).  Either way
+    the results are the same bits.
     """
     lib = _lib.load()
     dev = q.device
@@ -179,10 +196,28 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     args.dpos_bias, args.dscale_embed = dpb.data_ptr(), dse.data_ptr()
     args.dphase_base, args.dphase_gain = dpbase.data_ptr(), dpgain.data_ptr()
     args.dy_pre, args.dz_pre = dy.data_ptr(), dz.data_ptr()
+    overlap = q.dtype == torch.bfloat16 and not events and (overlap is None or overlap)
+    if overlap:
+        args.fwd.schedule |= _lib.DWARF_SCHED_DELTA_STAGE
     nbytes = lib.dwarf_dsqg_bwd_workspace_bytes(ctypes.byref(args))
     workspace = torch.empty(max(int(nbytes), 256), device=dev, dtype=torch.uint8)
     args.workspace, args.workspace_bytes = workspace.data_ptr(), workspace.numel()
     stream = _stream(dev)
+    if overlap:
+        main = torch.cuda.current_stream(dev)
+        side = _side_stream(dev)
+        side.wait_stream(main)
+        _lib.check(lib.dwarf_dsqg_bwd_delta(ctypes.byref(args), side.cuda_stream), "dwarf_dsqg_bwd_delta")
+        _lib.check(lib.dwarf_dsqg_bwd_dkdv(ctypes.byref(args), side.cuda_stream), "dwarf_dsqg_bwd_dkdv")
+        _lib.check(lib.dwarf_dsqg_bwd_dq(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dq")
+        _lib.check(lib.dwarf_dsqg_bwd_params(ctypes.byref(args), stream), "dwarf_dsqg_bwd_params")
+        main.wait_stream(side)
+        # memory the second stream used must not be handed out again before it is done
+        for t in (workspace, dk, dv, dz, dout, q, k, v, out, lse, y_pre, z_pre, pos_bias, scale_embed, phase_base,
+                  phase_gain, offsets_dev):
+            if t.is_cuda:
+                t.record_stream(side)
+        return dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz
     if events:
         events[0].record()
     _lib.check(lib.dwarf_dsqg_bwd_dq(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dq")

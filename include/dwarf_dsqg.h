@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 7
+#define DWARF_ABI_VERSION 8
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
@@ -97,9 +97,15 @@ typedef struct {
  *     then forms the softmax and the weighted sum without rescaling: the
  *     reference's offline-softmax kernel (online_softmax=False,
  *     _fwd_v18_grouped dsqg:863-1044).
+ *   DWARF_SCHED_DELTA_STAGE: the backward's (delta, lse) pairs come from
+ *     dwarf_dsqg_bwd_delta (bf16): the dQ launch forms delta for itself but
+ *     does not write the pairs, and runs two workgroups per CU so that a
+ *     dK/dV launch on another stream can run beside it (the overlapped
+ *     backward: delta then dK/dV on one stream, dQ then params on another).
  */
 #define DWARF_SCHED_BAND 1
 #define DWARF_SCHED_TWO_PASS 2
+#define DWARF_SCHED_DELTA_STAGE 4
 
 /*
  * Replaces the forward launch of _DSQGV18GroupedFn.forward (dsqg:2300-2314,
@@ -158,6 +164,16 @@ int dwarf_dsqg_bwd(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 int dwarf_dsqg_bwd_dq(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 int dwarf_dsqg_bwd_params(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
+
+/*
+ * The delta stage alone (bf16): replaces _compute_D_v18_grouped
+ * (dsqg:1263-1289, launched at dsqg:2380-2386), delta = <dO, O> from the
+ * stored bf16 O, and writes the (delta, lse) pairs that dwarf_dsqg_bwd_dkdv
+ * reads, bit for bit as dwarf_dsqg_bwd_dq forms them.  With
+ * DWARF_SCHED_DELTA_STAGE in args->fwd.schedule the stages may run as
+ * delta -> dkdv on one stream beside dq -> params on another.
+ */
+int dwarf_dsqg_bwd_delta(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Causal EMA scan  y[t] = a*x[t] + (1-a)*y[t-1],  a = clamp(alpha, fl, ce)  */
