@@ -277,33 +277,35 @@ def test_band_lattice_edges(pkg, device):
             assert max_abs(grads[n], rg[n]) < BF16_ABS, (offsets, n, max_abs(grads[n], rg[n]))
 
 
-def _raw_step(pkg, d, off, dout, overlap):
+def _raw_step(pkg, d, off, dout, overlap, qs=1):
     out, lse = pkg.dsqg_forward(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"], d["phase_base"],
-                                d["phase_gain"], d["y_pre"], d["z_pre"], off, 17, 79, 2, 1)
+                                d["phase_gain"], d["y_pre"], d["z_pre"], off, 17, 79, 2, qs)
     grads = pkg.dsqg_backward(dout, d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"], d["phase_base"],
-                              d["phase_gain"], d["y_pre"], d["z_pre"], off, out, lse, 17, 79, 2, 1,
+                              d["phase_gain"], d["y_pre"], d["z_pre"], off, out, lse, 17, 79, 2, qs,
                               overlap=overlap)
     return (out, lse) + tuple(grads)
 
 
-def test_overlapped_backward_matches_serial_bitwise(pkg, device):
+@pytest.mark.parametrize("h,h_kv,qs", [(4, 4, 1), (4, 2, 3)])
+def test_overlapped_backward_matches_serial_bitwise(pkg, device, h, h_kv, qs):
     """bf16 backward with the delta stage and dK/dV on a second stream beside dQ and the parameter
     gradients: all nine gradients equal the serial schedule's bit for bit (same kernels, same
-    summation order), at a ragged N, and the result is the oracle's within the bf16 bar."""
+    summation order), at a ragged N, with and without grouped K/V heads, and the result is the
+    oracle's within the bf16 bar."""
     offsets = lattice(pkg)
-    x = make_inputs(2, 4, 4, 517, offsets, 17, seed=97, dtype=torch.bfloat16, plane_shift=2, gain_std=4.0)
-    dout = torch.randn(2, 4, 517, 64, generator=torch.Generator().manual_seed(98)).to(torch.bfloat16)
+    x = make_inputs(2, h, h_kv, 517, offsets, 17, seed=97, dtype=torch.bfloat16, plane_shift=2, gain_std=4.0)
+    dout = torch.randn(2, h, 517, 64, generator=torch.Generator().manual_seed(98)).to(torch.bfloat16)
     d = to_device(x, device)
     off = torch.tensor(offsets, dtype=torch.int32, device=device)
     dd = dout.to(device)
-    serial = _raw_step(pkg, d, off, dd, False)
+    serial = _raw_step(pkg, d, off, dd, False, qs)
     torch.cuda.synchronize()
     for _ in range(2):
-        over = _raw_step(pkg, d, off, dd, True)
+        over = _raw_step(pkg, d, off, dd, True, qs)
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(over, serial)):
             assert torch.equal(a, b), i
-    ro, _, rg = oracle_fwd_bwd(x, offsets, 17, 2, 1, dout.float(), round_se=True)
+    ro, _, rg = oracle_fwd_bwd(x, offsets, 17, 2, qs, dout.float(), round_se=True)
     assert max_abs(over[0], ro) < BF16_ABS
     for n, g in zip(NAMES, over[2:]):
         assert max_abs(g, rg[n]) < BF16_ABS, n
