@@ -748,6 +748,12 @@ size_t dkdv_lds_bytes(int J, int J_large, int group) { return kv_layout(J, J_lar
 
 hipError_t launch_dsqg_bwd(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream, bool do_dq,
                            bool do_params, bool do_dkdv) {
+  // all stages on one stream with the delta stage requested: the dQ launch then
+  // skips the (delta, lse) pairs, so the delta launch writes them first
+  if (do_dq && do_dkdv && a.fwd.dtype == DWARF_BF16 && (a.fwd.schedule & DWARF_SCHED_DELTA_STAGE)) {
+    const hipError_t e = launch_dsqg_bwd_delta(a, ws, stream);
+    if (e != hipSuccess) return e;
+  }
   if (do_dq) {
     const hipError_t e = launch_dsqg_bwd_dq(a, ws, stream);
     if (e != hipSuccess) return e;

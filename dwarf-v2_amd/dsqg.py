@@ -158,7 +158,7 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 
 def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
                   out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None, schedule=None,
-                  overlap=None):
+                  overlap=None, one_call=False):
     """Raw backward.  Returns (dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz).
 
     bf16 (``overlap`` None or True, no ``events``): the delta stage and dK/dV
@@ -168,7 +168,10 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     params and dkdv stages run in turn on the current stream.  ``events``:
     optional four torch.cuda.Events recorded before dq, after dq, after params
     and after dkdv (serial stages, so each interval is one stage).  Either way
-    the results are the same bits.
+    the results are the same bits.  ``one_call``: every stage through the
+    single entry point ``dwarf_dsqg_bwd`` on the current stream (with the
+    delta-stage flag when ``overlap`` is True; the library then launches the
+    delta stage first), the same bits again.
     """
     lib = _lib.load()
     dev = q.device
@@ -196,13 +199,19 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     args.dpos_bias, args.dscale_embed = dpb.data_ptr(), dse.data_ptr()
     args.dphase_base, args.dphase_gain = dpbase.data_ptr(), dpgain.data_ptr()
     args.dy_pre, args.dz_pre = dy.data_ptr(), dz.data_ptr()
-    overlap = q.dtype == torch.bfloat16 and not events and (overlap is None or overlap)
+    if one_call:
+        overlap = bool(overlap) and q.dtype == torch.bfloat16
+    else:
+        overlap = q.dtype == torch.bfloat16 and not events and (overlap is None or overlap)
     if overlap:
         args.fwd.schedule |= _lib.DWARF_SCHED_DELTA_STAGE
     nbytes = lib.dwarf_dsqg_bwd_workspace_bytes(ctypes.byref(args))
     workspace = torch.empty(max(int(nbytes), 256), device=dev, dtype=torch.uint8)
     args.workspace, args.workspace_bytes = workspace.data_ptr(), workspace.numel()
     stream = _stream(dev)
+    if one_call:
+        _lib.check(lib.dwarf_dsqg_bwd(ctypes.byref(args), stream), "dwarf_dsqg_bwd")
+        return dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz
     if overlap:
         main = torch.cuda.current_stream(dev)
         side = _side_stream(dev)

@@ -102,6 +102,8 @@ typedef struct {
  *     does not write the pairs, and runs two workgroups per CU so that a
  *     dK/dV launch on another stream can run beside it (the overlapped
  *     backward: delta then dK/dV on one stream, dQ then params on another).
+ *     dwarf_dsqg_bwd, which runs every stage on one stream, then launches the
+ *     delta stage first by itself.
  */
 #define DWARF_SCHED_BAND 1
 #define DWARF_SCHED_TWO_PASS 2

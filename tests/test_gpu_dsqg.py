@@ -277,12 +277,12 @@ def test_band_lattice_edges(pkg, device):
             assert max_abs(grads[n], rg[n]) < BF16_ABS, (offsets, n, max_abs(grads[n], rg[n]))
 
 
-def _raw_step(pkg, d, off, dout, overlap, qs=1):
+def _raw_step(pkg, d, off, dout, overlap, qs=1, one_call=False):
     out, lse = pkg.dsqg_forward(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"], d["phase_base"],
                                 d["phase_gain"], d["y_pre"], d["z_pre"], off, 17, 79, 2, qs)
     grads = pkg.dsqg_backward(dout, d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"], d["phase_base"],
                               d["phase_gain"], d["y_pre"], d["z_pre"], off, out, lse, 17, 79, 2, qs,
-                              overlap=overlap)
+                              overlap=overlap, one_call=one_call)
     return (out, lse) + tuple(grads)
 
 
@@ -305,6 +305,12 @@ def test_overlapped_backward_matches_serial_bitwise(pkg, device, h, h_kv, qs):
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(over, serial)):
             assert torch.equal(a, b), i
+    # the single entry point dwarf_dsqg_bwd, without and with the delta-stage flag
+    for flag in (False, True):
+        one = _raw_step(pkg, d, off, dd, flag, qs, one_call=True)
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(one, serial)):
+            assert torch.equal(a, b), (flag, i)
     ro, _, rg = oracle_fwd_bwd(x, offsets, 17, 2, qs, dout.float(), round_se=True)
     assert max_abs(over[0], ro) < BF16_ABS
     for n, g in zip(NAMES, over[2:]):
