@@ -215,10 +215,15 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     if overlap:
         main = torch.cuda.current_stream(dev)
         side = _side_stream(dev)
-        side.wait_stream(main)
+        fork = torch.cuda.Event()
+        fork.record(main)
+        # dQ goes first: its persistent workgroups take their two slots per CU before
+        # dK/dV's thousands of workgroups fill the rest (the other way round dQ waits
+        # for dK/dV to drain and the two barely overlap)
+        _lib.check(lib.dwarf_dsqg_bwd_dq(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dq")
+        side.wait_event(fork)
         _lib.check(lib.dwarf_dsqg_bwd_delta(ctypes.byref(args), side.cuda_stream), "dwarf_dsqg_bwd_delta")
         _lib.check(lib.dwarf_dsqg_bwd_dkdv(ctypes.byref(args), side.cuda_stream), "dwarf_dsqg_bwd_dkdv")
-        _lib.check(lib.dwarf_dsqg_bwd_dq(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dq")
         _lib.check(lib.dwarf_dsqg_bwd_params(ctypes.byref(args), stream), "dwarf_dsqg_bwd_params")
         main.wait_stream(side)
         # memory the second stream used must not be handed out again before it is done
