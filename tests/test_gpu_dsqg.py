@@ -346,3 +346,18 @@ def test_graph_replay_of_overlapped_step_matches_eager(pkg, device):
         for i, (o, r) in enumerate(zip(outs, ref)):
             assert torch.equal(o, r), i
         del other
+
+
+def test_single_backward_entry_point_fp32(pkg, device):
+    """fp32: every stage through dwarf_dsqg_bwd in one call equals the three stage calls bit for bit."""
+    offsets = lattice(pkg)
+    x = make_inputs(1, 3, 3, 261, offsets, 17, seed=101, dtype=torch.float32, plane_shift=2)
+    dout = torch.randn(1, 3, 261, 64, generator=torch.Generator().manual_seed(102))
+    d = to_device(x, device)
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    dd = dout.to(device)
+    staged = _raw_step(pkg, d, off, dd, False)
+    one = _raw_step(pkg, d, off, dd, False, one_call=True)
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(one, staged)):
+        assert torch.equal(a, b), i
