@@ -238,3 +238,24 @@ def test_prefill_workspace_without_gpu(pkg, lib):
     a.workspace, a.workspace_bytes = 0x10000, N * 160
     assert lib.dwarf_dsqg_q6_prefill_fwd(ctypes.byref(a), None) == L.DWARF_ERR_UNSUPPORTED
     assert b"widened" in lib.dwarf_last_error()
+
+
+def test_delta_stage_validation_without_gpu(pkg, lib):
+    """dwarf_dsqg_bwd_delta refuses a NULL argument block, fp32 (the fp32 dQ launch forms delta itself)
+    and a missing or short workspace before any launch; an empty batch is a no-op."""
+    L = pkg._lib
+    assert lib.dwarf_dsqg_bwd_delta(None, None) == L.DWARF_ERR_INVALID_ARGUMENT
+    b = L.DsqgBwdArgs()
+    b.fwd = _fake_fwd(L, 1, 2, 2, 256, 96, 17)
+    b.fwd.schedule = L.DWARF_SCHED_DELTA_STAGE
+    b.dout, b.dout_stride = 0x10000, L.i64_array((2 * 256 * 64, 256 * 64, 64, 1))
+    assert lib.dwarf_dsqg_bwd_delta(ctypes.byref(b), None) == L.DWARF_ERR_WORKSPACE
+    need = lib.dwarf_dsqg_bwd_workspace_bytes(ctypes.byref(b))
+    assert need > 0
+    b.workspace, b.workspace_bytes = 0x10000, need - 256
+    assert lib.dwarf_dsqg_bwd_delta(ctypes.byref(b), None) == L.DWARF_ERR_WORKSPACE
+    b.fwd.dtype = L.DWARF_F32
+    assert lib.dwarf_dsqg_bwd_delta(ctypes.byref(b), None) == L.DWARF_ERR_UNSUPPORTED
+    b.fwd.dtype = L.DWARF_BF16
+    b.fwd.B = 0
+    assert lib.dwarf_dsqg_bwd_delta(ctypes.byref(b), None) == L.DWARF_OK
