@@ -200,6 +200,8 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     args.dphase_base, args.dphase_gain = dpbase.data_ptr(), dpgain.data_ptr()
     args.dy_pre, args.dz_pre = dy.data_ptr(), dz.data_ptr()
     if one_call:
+        if events:
+            raise ValueError("events time the stages of separate calls; one_call runs them in one")
         overlap = bool(overlap) and q.dtype == torch.bfloat16
     else:
         overlap = q.dtype == torch.bfloat16 and not events and (overlap is None or overlap)
