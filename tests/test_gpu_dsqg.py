@@ -361,3 +361,26 @@ def test_single_backward_entry_point_fp32(pkg, device):
     torch.cuda.synchronize()
     for i, (a, b) in enumerate(zip(one, staged)):
         assert torch.equal(a, b), i
+
+
+def test_overlapped_backward_repeated_at_training_shape(pkg, device):
+    """B15 H8 T2048 (the training microbatch): 20 overlapped backward calls in a row, with forward
+    launches on the stream between some of them, each equal bit for bit to the serial schedule's
+    gradients (the second stream's launches never read the delta pairs before they are written)."""
+    offsets = lattice(pkg)
+    x = make_inputs(15, 8, 8, 2048, offsets, 17, seed=103, dtype=torch.bfloat16)
+    dout = torch.randn(15, 8, 2048, 64, generator=torch.Generator().manual_seed(104)).to(torch.bfloat16)
+    d = to_device(x, device)
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    dd = dout.to(device)
+    serial = [t.clone() for t in _raw_step(pkg, d, off, dd, False)]
+    torch.cuda.synchronize()
+    out, lse = serial[0], serial[1]
+    names = ("q", "k", "v", "pos_bias", "scale_embed", "phase_base", "phase_gain", "y_pre", "z_pre")
+    for it in range(20):
+        grads = pkg.dsqg_backward(dd, *(d[n] for n in names), off, out, lse, 17, 79, 2, 1, overlap=True)
+        if it % 3 == 0:
+            pkg.dsqg_forward(*(d[n] for n in names), off, 17, 79, 2, 1)
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(grads, serial[2:])):
+            assert torch.equal(a, b), (it, i)
