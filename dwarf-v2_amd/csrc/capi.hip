@@ -23,7 +23,7 @@ hipError_t launch_q6_unpack(int B, int Hkv, int N, const uint8_t* cache, const i
 hipError_t launch_q6_prefill(const dwarf_dsqg_q6_prefill_args& a, hipStream_t stream);
 size_t q6_prefill_workspace(const dwarf_dsqg_q6_prefill_args& a);
 hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, float* table, hipStream_t stream);
-hipError_t q6_decode_scratch(float** ptr);
+hipError_t q6_decode_scratch(hipStream_t stream, float** ptr);
 size_t q6_decode_workspace(const dwarf_dsqg_q6_decode_args& a);
 int q6_max_decode_offsets();
 int q6_max_decode_heads();
@@ -140,6 +140,10 @@ int check_fwd(const dwarf_dsqg_fwd_args& a) {
   int rc = check_lattice(a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, a.query_start);
   if (rc) return rc;
   if (a.dtype != DWARF_BF16 && a.dtype != DWARF_F32) return fail(DWARF_ERR_INVALID_ARGUMENT, "dtype=%d", a.dtype);
+  constexpr int32_t kKnownSchedule = DWARF_SCHED_BAND | DWARF_SCHED_TWO_PASS | DWARF_SCHED_DELTA_STAGE;
+  if (a.schedule & ~kKnownSchedule)
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "schedule=%d holds bits outside DWARF_SCHED_BAND | TWO_PASS | DELTA_STAGE",
+                a.schedule);
   if (a.B == 0 || a.N == 0) return DWARF_OK;   // no rows to read or write
   if ((rc = check_rows("q", a.q, a.q_stride, 3, a.dtype))) return rc;
   if ((rc = check_rows("k", a.k, a.k_stride, 3, a.dtype))) return rc;
@@ -695,7 +699,7 @@ int dwarf_dsqg_q6_decode_noalloc(const dwarf_dsqg_q6_decode_args* args, dwarf_st
   if ((rc = check_decode_args(a))) return rc;
   if (a.S == 0 || a.L == 0) return ok();
   float* table = nullptr;
-  const hipError_t e = dwarf::q6_decode_scratch(&table);
+  const hipError_t e = dwarf::q6_decode_scratch(reinterpret_cast<hipStream_t>(stream), &table);
   if (e != hipSuccess) return hip_status(e, "dwarf_dsqg_q6_decode_noalloc (device array address)");
   return hip_status(dwarf::launch_q6_decode(a, table, reinterpret_cast<hipStream_t>(stream)),
                     "dwarf_dsqg_q6_decode_noalloc");

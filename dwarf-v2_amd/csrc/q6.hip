@@ -1437,18 +1437,31 @@ static __device__ __align__(256) float scratch[DWARF_Q6_DECODE_SCRATCH_BYTES / s
 
 namespace dwarf {
 
-hipError_t q6_decode_scratch(float** ptr) {
+// The array of the GPU that `stream` belongs to (the current GPU for the null
+// stream).  Its address is looked up with that GPU current, once per GPU.
+hipError_t q6_decode_scratch(hipStream_t stream, float** ptr) {
   constexpr int kMaxDevices = 64;
   static std::mutex mu;
   static float* addr[kMaxDevices] = {};
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return e;
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd = -1;
+    if ((e = hipStreamGetDevice(stream, &sd)) != hipSuccess) return e;
+    dev = static_cast<int>(sd);
+  }
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(mu);
   if (!addr[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return e;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
     if (e != hipSuccess) return e;
     addr[dev] = static_cast<float*>(p);
   }

@@ -158,7 +158,7 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 
 def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
                   out, lse, j_small, j_large, plane_shift=0, query_start=0, *, events=None, schedule=None,
-                  overlap=None, one_call=False):
+                  overlap=None, one_call=False, overlap_events=None):
     """Raw backward.  Returns (dq, dk, dv, dpb, dse, dpbase, dpgain, dy, dz).
 
     bf16 (``overlap`` None or True, no ``events``): the delta stage and dK/dV
@@ -171,7 +171,10 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     the results are the same bits.  ``one_call``: every stage through the
     single entry point ``dwarf_dsqg_bwd`` on the current stream (with the
     delta-stage flag when ``overlap`` is True; the library then launches the
-    delta stage first), the same bits again.
+    delta stage first), the same bits again.  ``overlap_events``: optional six
+    torch.cuda.Events for the overlapped schedule, recorded on the stream each
+    stage runs on: before dq, after dq, after params (current stream), before
+    delta, after delta, after dkdv (second stream).
     """
     lib = _lib.load()
     dev = q.device
@@ -188,10 +191,13 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
     dpgain = alloc(phase_gain.shape, device=dev, dtype=torch.float32)
     dy = torch.empty(y_pre.shape, device=dev, dtype=torch.float32)
     dz = torch.empty(z_pre.shape, device=dev, dtype=torch.float32)
+    # the delta-stage flag is this function's to set: it only holds when the delta launch runs
+    # below, and on its own it would leave dK/dV reading (delta, lse) pairs no stage wrote
+    schedule = (DEFAULT_SCHEDULE if schedule is None else int(schedule)) & ~_lib.DWARF_SCHED_DELTA_STAGE
     args = _lib.DsqgBwdArgs()
     _fill_fwd(args.fwd, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets_dev,
               j_small, j_large, plane_shift, query_start, out, lse, se_round=q.dtype != torch.float32,
-              schedule=DEFAULT_SCHEDULE if schedule is None else schedule)
+              schedule=schedule)
     args.dout, args.dout_stride = dout.data_ptr(), _lib.i64_array(dout.stride())
     args.dq, args.dq_stride = dq.data_ptr(), _lib.i64_array(dq.stride())
     args.dk, args.dk_stride = dk.data_ptr(), _lib.i64_array(dk.stride())
@@ -205,6 +211,8 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
         overlap = bool(overlap) and q.dtype == torch.bfloat16
     else:
         overlap = q.dtype == torch.bfloat16 and not events and (overlap is None or overlap)
+    if overlap_events and (one_call or not overlap):
+        raise ValueError("overlap_events time the stages of the overlapped two-stream schedule")
     if overlap:
         args.fwd.schedule |= _lib.DWARF_SCHED_DELTA_STAGE
     nbytes = lib.dwarf_dsqg_bwd_workspace_bytes(ctypes.byref(args))
@@ -222,11 +230,24 @@ def dsqg_backward(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, 
         # dQ goes first: its persistent workgroups take their two slots per CU before
         # dK/dV's thousands of workgroups fill the rest (the other way round dQ waits
         # for dK/dV to drain and the two barely overlap)
+        ev = overlap_events
+        if ev:
+            ev[0].record(main)
         _lib.check(lib.dwarf_dsqg_bwd_dq(ctypes.byref(args), stream), "dwarf_dsqg_bwd_dq")
+        if ev:
+            ev[1].record(main)
         side.wait_event(fork)
+        if ev:
+            ev[3].record(side)
         _lib.check(lib.dwarf_dsqg_bwd_delta(ctypes.byref(args), side.cuda_stream), "dwarf_dsqg_bwd_delta")
+        if ev:
+            ev[4].record(side)
         _lib.check(lib.dwarf_dsqg_bwd_dkdv(ctypes.byref(args), side.cuda_stream), "dwarf_dsqg_bwd_dkdv")
+        if ev:
+            ev[5].record(side)
         _lib.check(lib.dwarf_dsqg_bwd_params(ctypes.byref(args), stream), "dwarf_dsqg_bwd_params")
+        if ev:
+            ev[2].record(main)
         main.wait_stream(side)
         # memory the second stream used must not be handed out again before it is done
         for t in (workspace, dk, dv, dz, dout, q, k, v, out, lse, y_pre, z_pre, pos_bias, scale_embed, phase_base,

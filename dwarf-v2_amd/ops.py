@@ -35,7 +35,8 @@ Tensor = torch.Tensor
 @torch.library.custom_op("dwarf::dsqg_fwd", mutates_args=())
 def dsqg_fwd(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, scale_embed: Tensor, phase_base: Tensor,
              phase_gain: Tensor, y_pre: Tensor, z_pre: Tensor, offsets: Tensor, j_small: int, j_large: int,
-             plane_shift: int, query_start: int, schedule: int = 0) -> tuple[Tensor, Tensor]:
+             plane_shift: int, query_start: int,
+             schedule: int = _dsqg.DEFAULT_SCHEDULE) -> tuple[Tensor, Tensor]:
     """Forward launch; returns (out like q, lse [B,H,N] fp32).  schedule: DWARF_SCHED_* flags."""
     t = _dsqg.normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets,
                                j_small + j_large)
@@ -44,7 +45,7 @@ def dsqg_fwd(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, scale_embed: Ten
 
 @dsqg_fwd.register_fake
 def _dsqg_fwd_fake(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets, j_small, j_large,
-                   plane_shift, query_start, schedule=0):
+                   plane_shift, query_start, schedule=_dsqg.DEFAULT_SCHEDULE):
     B, H, N, HD = q.shape
     return q.new_empty((B, H, N, HD)), q.new_empty((B, H, N), dtype=torch.float32)
 
@@ -53,7 +54,8 @@ def _dsqg_fwd_fake(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre
 def dsqg_bwd(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, scale_embed: Tensor,
              phase_base: Tensor, phase_gain: Tensor, y_pre: Tensor, z_pre: Tensor, offsets: Tensor, out: Tensor,
              lse: Tensor, j_small: int, j_large: int, plane_shift: int, query_start: int,
-             schedule: int = 0) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+             schedule: int = _dsqg.DEFAULT_SCHEDULE
+             ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Backward launches; returns (dq, dk, dv, dpos_bias, dscale_embed, dphase_base, dphase_gain, dy, dz)."""
     t = _dsqg.normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets,
                                j_small + j_large)
@@ -63,7 +65,7 @@ def dsqg_bwd(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, sc
 
 @dsqg_bwd.register_fake
 def _dsqg_bwd_fake(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets, out, lse,
-                   j_small, j_large, plane_shift, query_start, schedule=0):
+                   j_small, j_large, plane_shift, query_start, schedule=_dsqg.DEFAULT_SCHEDULE):
     f32 = torch.float32
     return (q.new_empty(q.shape), q.new_empty(k.shape), q.new_empty(v.shape),
             q.new_empty(pos_bias.shape, dtype=f32), q.new_empty(scale_embed.shape, dtype=f32),

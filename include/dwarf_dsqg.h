@@ -5,10 +5,12 @@
  * The ABI carries plain device pointers, element strides and a hipStream_t;
  * no framework types cross it.  The caller owns every buffer: outputs,
  * gradients and the workspaces whose sizes the *_workspace_bytes queries
- * report.  Every entry point is stateless and re-entrant, launches on the
- * stream it is given, never allocates device memory and never throws.  It
- * returns a dwarf_status; dwarf_last_error() describes the most recent
- * failure on the calling thread.
+ * report.  Every entry point launches on the stream it is given, never
+ * allocates device memory and never throws.  Every entry point but one is
+ * stateless and re-entrant: dwarf_dsqg_q6_decode_noalloc keeps its score
+ * table in one device array per GPU, so its calls that overlap on one GPU
+ * race (see its declaration).  Each returns a dwarf_status;
+ * dwarf_last_error() describes the most recent failure on the calling thread.
  *
  * Reference interfaces replaced (Lanerra/dwarf-v2):
  *   dsqg = kernels/dsqg_attention_v22.py, ema = kernels/causal_ema_scan.py
@@ -526,8 +528,10 @@ int dwarf_dsqg_q6_decode(const dwarf_dsqg_q6_decode_args* args,
  * (16 MiB) per GPU, held until the process ends.  Returns DWARF_ERR_UNSUPPORTED
  * when dwarf_dsqg_q6_decode_workspace_bytes(args) exceeds that size (S*L*H*JE
  * fp32 <= 4 Mi floats, e.g. 512 sequences x 9 layers x 8 heads at J = 96).
- * Calls no allocating routine.  All calls on one GPU share its array: calls
- * that overlap on one GPU (two streams, two threads) race.
+ * Calls no allocating routine.  The array used is that of the GPU `stream`
+ * belongs to (the current GPU for the null stream).  All calls on one GPU
+ * share its array: calls that overlap on one GPU (two streams, two threads)
+ * race.
  */
 int dwarf_dsqg_q6_decode_noalloc(const dwarf_dsqg_q6_decode_args* args,
                                  dwarf_stream_t stream);

@@ -259,3 +259,25 @@ def test_delta_stage_validation_without_gpu(pkg, lib):
     b.fwd.dtype = L.DWARF_BF16
     b.fwd.B = 0
     assert lib.dwarf_dsqg_bwd_delta(ctypes.byref(b), None) == L.DWARF_OK
+
+
+def test_unknown_schedule_bits_refused_without_gpu(pkg, lib):
+    """Schedule bits outside DWARF_SCHED_BAND | TWO_PASS | DELTA_STAGE are refused by the forward and by
+    every backward stage before any launch; each known flag alone passes validation up to the workspace."""
+    L = pkg._lib
+    a = _fake_fwd(L, 1, 2, 2, 256, 96, 17)
+    for bad in (8, 16, 1 << 30, -1):
+        a.schedule = bad
+        assert lib.dwarf_dsqg_fwd(ctypes.byref(a), None) == L.DWARF_ERR_INVALID_ARGUMENT
+        assert b"schedule" in lib.dwarf_last_error()
+    b = L.DsqgBwdArgs()
+    b.fwd = _fake_fwd(L, 1, 2, 2, 256, 96, 17)
+    b.dout, b.dout_stride = 0x10000, L.i64_array((2 * 256 * 64, 256 * 64, 64, 1))
+    for fn in (lib.dwarf_dsqg_bwd, lib.dwarf_dsqg_bwd_dq, lib.dwarf_dsqg_bwd_params, lib.dwarf_dsqg_bwd_dkdv,
+               lib.dwarf_dsqg_bwd_delta):
+        b.fwd.schedule = L.DWARF_SCHED_BAND | 32
+        assert fn(ctypes.byref(b), None) == L.DWARF_ERR_INVALID_ARGUMENT
+        assert b"schedule" in lib.dwarf_last_error()
+    for good in (0, L.DWARF_SCHED_BAND, L.DWARF_SCHED_TWO_PASS, L.DWARF_SCHED_DELTA_STAGE, 7):
+        b.fwd.schedule = good
+        assert lib.dwarf_dsqg_bwd_delta(ctypes.byref(b), None) == L.DWARF_ERR_WORKSPACE   # got past the flags

@@ -119,6 +119,53 @@ def test_cfg4_long_context_as_benched(pkg, device):
     check_rows(pkg, t, list(pkg.ALL_OFFSETS), js, 0, 1, device, head_chunk=4)
 
 
+@pytest.mark.parametrize("gain_scale", [1.0, 40.0])
+def test_cfg1_fp32_full_lattice_as_benched(pkg, device, gain_scale):
+    """cfg1's shape in fp32: B1 H8 T2048 on bench.py's seed-0 inputs, all 96 offsets (92 with a source, 75
+    of them far), forward and backward through the fp32 kernels, against the float64 oracle one head at a
+    time.  gain_scale 40 multiplies phase_gain (std 0.64 -> 25.6) so the MOVT angles are O(1) rather than
+    O(0.01).  Bar: 1e-5 relative (||a-b||_inf / ||b||_inf) for out and all nine gradients, per head for
+    out/dq/dk/dv/dy/dz and over the head-summed parameter gradients."""
+    note(f"cfg1 B1 H8 T2048 fp32 fwd+bwd, phase_gain x{gain_scale}")
+    t, js, jl = bench.synth(pkg, 1, 8, 2048, 0, torch.device("cpu"), dtype=torch.float32)
+    t["phase_gain"] = t["phase_gain"] * gain_scale
+    offsets = list(pkg.ALL_OFFSETS)
+    out, grads = run_gpu(pkg, t, offsets, js, 0, 1, device)
+    assert out.dtype == torch.float32
+    H = t["q"].shape[1]
+    sums = {n: torch.zeros_like(t[n], dtype=torch.float64) for n in PARAMS}
+    worst = {}
+
+    def rel(a, b):
+        a, b = a.detach().double().cpu(), b.detach().double().cpu()
+        return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+    for h in range(H):
+        hs = slice(h, h + 1)
+        inp = {n: t[n][:, hs].double() for n in ("q", "k", "v", "y_pre", "z_pre")}
+        inp["pos_bias"] = t["pos_bias"][:, hs].double()
+        inp["scale_embed"] = t["scale_embed"].double()
+        inp["phase_base"] = t["phase_base"][:, hs].double()
+        inp["phase_gain"] = t["phase_gain"][:, hs].double()
+        ro, _, rg = dsqg_ref.dsqg_forward_backward(inp, offsets, js, t["dout"][:, hs].double(), query_start=1,
+                                                   round_se=False)
+        checks = [("out", out[:, hs], ro)] + [(n, grads[n][:, hs], rg[n])
+                                              for n in ("q", "k", "v", "y_pre", "z_pre")]
+        for n, got, ref in checks:
+            e = rel(got, ref)
+            worst[n] = max(worst.get(n, 0.0), e)
+            assert e < 1e-5, (n, h, e)
+        sums["pos_bias"][:, hs] += rg["pos_bias"]
+        sums["scale_embed"] += rg["scale_embed"]
+        sums["phase_base"][:, hs] += rg["phase_base"]
+        sums["phase_gain"][:, hs] += rg["phase_gain"]
+        note(f"head {h} of {H} checked")
+    for n in PARAMS:
+        worst[n] = rel(grads[n], sums[n])
+        assert worst[n] < 1e-5, (n, worst[n])
+    note("worst relative error (bar 1e-5): " + ", ".join(f"{n} {v:.2e}" for n, v in worst.items()))
+
+
 def test_bf16_gqa_ragged_many_tiles(pkg, device):
     """bf16 with GQA (H8 over 2 KV heads), a ragged N = 2047 (tail masks), query_start 3, plane shift 5, hot
     MOVT angles and 1,280 query tiles (more than either persistent grid)."""

@@ -126,3 +126,56 @@ def test_library_is_the_only_path(pkg):
             src = open(mod.__file__).read() if getattr(mod, "__file__", None) else ""
             assert "import oracle" not in src and "from oracle" not in src
     assert pkg.native_library_path().endswith("libdwarf_dsqg.so")
+
+
+def test_backward_sets_the_delta_stage_flag_itself(pkg, monkeypatch):
+    """A caller's schedule that carries DWARF_SCHED_DELTA_STAGE does not reach the serial stages (the dQ
+    launch would then skip the (delta, lse) pairs dK/dV reads and no delta launch would write them): the
+    flag is cleared and set only where the delta launch runs.  The C ABI is replaced by a recorder."""
+    dsqg = importlib.import_module("dwarf-v2_amd.dsqg")
+    L = pkg._lib
+    seen = []
+
+    class Recorder:
+        def dwarf_dsqg_bwd_workspace_bytes(self, args):
+            return 256
+
+        def __getattr__(self, name):
+            def launch(args, stream):
+                seen.append((name, args._obj.fwd.schedule))
+                return 0
+            return launch
+
+    monkeypatch.setattr(dsqg._lib, "load", lambda: Recorder())
+    monkeypatch.setattr(dsqg, "_stream", lambda device: 0)
+    a = _args(N=8, J=3, js=2)
+    a = {n: t.to(torch.bfloat16) if n in ("q", "k", "v") else t for n, t in a.items()}
+    off = torch.tensor([1, 2, 48], dtype=torch.int32)
+    out, lse = torch.zeros_like(a["q"]), torch.zeros(1, 2, 8)
+    for sched in (L.DWARF_SCHED_DELTA_STAGE, L.DWARF_SCHED_BAND | L.DWARF_SCHED_DELTA_STAGE):
+        seen.clear()
+        dsqg.dsqg_backward(torch.zeros_like(a["q"]), a["q"], a["k"], a["v"], a["pos_bias"], a["scale_embed"],
+                           a["phase_base"], a["phase_gain"], a["y_pre"], a["z_pre"], off, out, lse, 2, 1,
+                           schedule=sched, overlap=False)
+        assert [n for n, _ in seen] == ["dwarf_dsqg_bwd_dq", "dwarf_dsqg_bwd_params", "dwarf_dsqg_bwd_dkdv"]
+        assert all(s & L.DWARF_SCHED_DELTA_STAGE == 0 for _, s in seen), seen
+        assert all(s == sched & ~L.DWARF_SCHED_DELTA_STAGE for _, s in seen), seen
+        seen.clear()
+        dsqg.dsqg_backward(torch.zeros_like(a["q"]), a["q"], a["k"], a["v"], a["pos_bias"], a["scale_embed"],
+                           a["phase_base"], a["phase_gain"], a["y_pre"], a["z_pre"], off, out, lse, 2, 1,
+                           schedule=sched, overlap=True, one_call=True)
+        assert seen == [("dwarf_dsqg_bwd", sched)]
+
+
+def test_custom_ops_default_to_the_python_schedule(pkg):
+    """dwarf::dsqg_fwd / dsqg_bwd called without a schedule run the schedule dsqg_forward/backward and the
+    autograd Function run (DEFAULT_SCHEDULE), not the gather loops alone."""
+    import inspect
+
+    ops = importlib.import_module("dwarf-v2_amd.ops")
+    dsqg = importlib.import_module("dwarf-v2_amd.dsqg")
+    for fn in (ops.dsqg_fwd, ops.dsqg_bwd):
+        schema = fn._opoverload._schema
+        arg = [x for x in schema.arguments if x.name == "schedule"][0]
+        assert arg.default_value == dsqg.DEFAULT_SCHEDULE
+    assert inspect.signature(ops._dsqg_fwd_fake).parameters["schedule"].default == dsqg.DEFAULT_SCHEDULE

@@ -51,3 +51,31 @@ def test_noalloc_decode_matches_workspace_decode(pkg, device):
         got32 = pkg.q6.q6_decode_noalloc(*args, round_se=False)
         torch.cuda.synchronize()
         assert torch.equal(got32, ref32), (S, L, H, N)
+
+
+def test_noalloc_decode_allocates_nothing(pkg, device):
+    """With already-normalised inputs and ``out`` given, the call allocates nothing: the caching allocator's
+    count of allocations does not move across it, and the call records into a HIP graph under global
+    capture mode (where a device allocation would be refused).  Each of three replays, with new queries
+    copied in eagerly between them, equals the workspace decode of the same inputs bit for bit."""
+    args = list(_case(pkg, device, 5, 2, 8, 4, 600, list(pkg.ALL_OFFSETS), 17, 41, 2))
+    q = args[0].to(torch.bfloat16).contiguous()
+    args[0] = q
+    out = torch.empty(q.shape, device=device, dtype=torch.bfloat16)
+    pkg.q6.q6_decode_noalloc(*args, out=out)      # first call on the device looks up the array's address
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_stats(device)["allocation.all.allocated"]
+    pkg.q6.q6_decode_noalloc(*args, out=out)
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_stats(device)["allocation.all.allocated"] == before
+    assert torch.equal(out, pkg.q6.q6_decode(*args))
+    graph = torch.cuda.Graph()
+    with torch.cuda.graph(graph):
+        pkg.q6.q6_decode_noalloc(*args, out=out)
+    g = torch.Generator().manual_seed(7)
+    for rep in range(3):
+        q.copy_(torch.randn(q.shape, generator=g).to(torch.bfloat16).to(device))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, pkg.q6.q6_decode(*args)), rep
