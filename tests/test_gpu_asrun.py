@@ -41,12 +41,19 @@ def note(msg: str) -> None:
     print(f"[asrun] {msg}", file=sys.stderr, flush=True)
 
 
-def excess(got: torch.Tensor, ref: torch.Tensor, bf16: bool) -> float:
-    """Largest |got - ref| beyond the bar (<= 0 passes)."""
+MAX_ERR: dict = {}   # largest plain |got - ref| per result name over a test (the ulp term left out)
+
+
+def excess(got: torch.Tensor, ref: torch.Tensor, bf16: bool, name: str | None = None) -> float:
+    """Largest |got - ref| beyond the bar (<= 0 passes); with ``name``, also records the largest plain
+    |got - ref| in MAX_ERR."""
     g = got.detach().double().cpu()
     r = ref.detach().double().cpu()
+    err = (g - r).abs()
+    if name is not None:
+        MAX_ERR[name] = max(MAX_ERR.get(name, 0.0), float(err.max()))
     bar = BF16_ABS + (r.abs() * 2.0 ** -9 if bf16 else 0.0)
-    return float(((g - r).abs() - bar).max())
+    return float((err - bar).max())
 
 
 def run_gpu(pkg, t, offsets, js, shift, qs, device, mode=0):
@@ -62,6 +69,7 @@ def run_gpu(pkg, t, offsets, js, shift, qs, device, mode=0):
 def check_rows(pkg, t, offsets, js, shift, qs, device, head_chunk=None, mode=0):
     """GPU fwd+bwd on the whole batch, oracle per batch row (and head chunk): returns nothing, asserts."""
     out, grads = run_gpu(pkg, t, offsets, js, shift, qs, device, mode)
+    MAX_ERR.clear()
     cpu = {n: t[n].detach().cpu() for n in list(NAMES) + ["dout"]}
     B, H, N, _ = cpu["q"].shape
     Hkv = cpu["k"].shape[1]
@@ -82,13 +90,13 @@ def check_rows(pkg, t, offsets, js, shift, qs, device, head_chunk=None, mode=0):
             inp = {n: sl[n].float() for n in NAMES}
             ro, _, rg = dsqg_ref.dsqg_forward_backward(inp, offsets, js, sl["dout"].float(), plane_shift=shift,
                                                        query_start=qs, round_se=True, delta_from_bf16_out=True)
-            e = excess(out[b:b + 1, hs], ro, True)
+            e = excess(out[b:b + 1, hs], ro, True, "out")
             worst["out"] = max(worst.get("out", -1.0), e)
             assert e <= 0, ("out", b, h0, e)
             for n, got in (("q", grads["q"][b:b + 1, hs]), ("y_pre", grads["y_pre"][b:b + 1, hs]),
                            ("k", grads["k"][b:b + 1, ks]), ("v", grads["v"][b:b + 1, ks]),
                            ("z_pre", grads["z_pre"][b:b + 1, ks])):
-                e = excess(got, rg[n], n in BF16_OUT)
+                e = excess(got, rg[n], n in BF16_OUT, n)
                 worst[n] = max(worst.get(n, -1.0), e)
                 assert e <= 0, (n, b, h0, e)
             sums["pos_bias"][:, hs] += rg["pos_bias"].double()
@@ -97,10 +105,11 @@ def check_rows(pkg, t, offsets, js, shift, qs, device, head_chunk=None, mode=0):
             sums["phase_gain"][:, hs] += rg["phase_gain"].double()
         note(f"row {b} of {B} checked")
     for n in PARAMS:
-        e = excess(grads[n], sums[n], False)
+        e = excess(grads[n], sums[n], False, n)
         worst[n] = e
         assert e <= 0, (n, e)
     note("worst excess over the bar: " + ", ".join(f"{n} {v:+.2e}" for n, v in worst.items()))
+    note("largest |gpu - oracle| (bar 2e-2): " + ", ".join(f"{n} {v:.2e}" for n, v in MAX_ERR.items()))
 
 
 @pytest.mark.parametrize("mode", [0, 3])
@@ -198,14 +207,18 @@ def test_cfg3_q6_prefill_as_benched(pkg, device):
     offsets = t["offsets"].tolist()
     rng = np.random.default_rng(3)
     picks = [(0, 0), (19, 7)] + [(int(rng.integers(20)), int(rng.integers(8))) for _ in range(14)]
+    MAX_ERR.clear()
+    worst = -1.0
     for b, h in picks:
         kd, vd, _ = q6_ref.unpack_slots(cache[b:b + 1, h:h + 1].cpu().numpy())
         tables = {"pos_bias": t["pos_bias"][:, h:h + 1].cpu(), "scale_embed": t["scale_embed"].cpu(),
                   "phase_base": t["phase_base"][:, h:h + 1].cpu(), "phase_gain": t["phase_gain"][:, h:h + 1].cpu()}
         ref = _q6_oracle(t["q"][b:b + 1, h:h + 1].cpu(), torch.from_numpy(kd), torch.from_numpy(vd), tables,
                          offsets, js, qpn, kpn, 1)
-        e = excess(out[b:b + 1, h:h + 1], ref, True)
+        e = excess(out[b:b + 1, h:h + 1], ref, True, "out")
+        worst = max(worst, e)
         assert e <= 0, (b, h, e)
+    note(f"worst excess over the bar: out {worst:+.2e}; largest |gpu - oracle| {MAX_ERR['out']:.2e} (bar 2e-2)")
 
 
 def test_cfg5_q6_decode_as_benched(pkg, device):
@@ -220,6 +233,8 @@ def test_cfg5_q6_decode_as_benched(pkg, device):
     out = out.cpu()
     rng = np.random.default_rng(5)
     picks = [(0, 0), (255, 8)] + [(int(rng.integers(256)), int(rng.integers(9))) for _ in range(14)]
+    MAX_ERR.clear()
+    worst = -1.0
     for s, l in picks:
         tpos = int(w["pos"][s])
         kd, vd, _ = q6_ref.unpack_slots(w["caches"][l, s:s + 1, :, :tpos + 1].cpu().numpy())
@@ -228,7 +243,9 @@ def test_cfg5_q6_decode_as_benched(pkg, device):
         tables = {n: w[n][l].cpu() for n in PARAMS}
         ref = _q6_oracle(q, torch.from_numpy(kd), torch.from_numpy(vd), tables, w["offsets"], w["js"],
                          w["qpn"], w["kpn"], 0)
-        e = excess(out[s, l], ref[0, :, tpos], True)
+        e = excess(out[s, l], ref[0, :, tpos], True, "out")
+        worst = max(worst, e)
         assert e <= 0, (s, l, tpos, e)
+    note(f"worst excess over the bar: out {worst:+.2e}; largest |gpu - oracle| {MAX_ERR['out']:.2e} (bar 2e-2)")
     del w
     torch.cuda.empty_cache()

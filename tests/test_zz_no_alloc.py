@@ -69,7 +69,7 @@ def test_noalloc_decode_allocates_nothing(pkg, device):
     torch.cuda.synchronize()
     assert torch.cuda.memory_stats(device)["allocation.all.allocated"] == before
     assert torch.equal(out, pkg.q6.q6_decode(*args))
-    graph = torch.cuda.Graph()
+    graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         pkg.q6.q6_decode_noalloc(*args, out=out)
     g = torch.Generator().manual_seed(7)
