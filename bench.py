@@ -599,11 +599,15 @@ def main() -> int:
         extra["npci"] = npci_extra(pkg, device, args.steps, args.warmup)
         log("InterferencePacket pool: x [15,2048,512], three timescales")
         extra["packet"] = packet_extra(pkg, device, args.steps, args.warmup)
-    traffic = None
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs (profiles/traffic.json,
+    # stamped with the commit they were measured at); counters cannot run inside this timed process
+    traffic, traffic_commit = None, None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get(dominant)
+            tj = json.load(f)
+        traffic, traffic_commit = tj.get("overlapped", {}).get(dominant), tj.get("commit")
+        extra["roofline_serial"]["traffic"] = tj.get("serial", {}).get(dominant_s)
     line = {
         "metric": "DSQG fwd+bwd tokens/s (B15 T2048 bf16) + % HBM roofline; q6 decode tok/s",
         "value": B * N / (ms * 1e-3),
@@ -620,7 +624,7 @@ def main() -> int:
         "config": {"workload": "dsqg_fwd_bwd_training_microbatch", "batch": B, "heads": H, "seq_len": N,
                    "head_dim": 64, "offsets": 96, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": traffic,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": traffic, "traffic_commit": traffic_commit,
                      "schedule": "overlapped (the timed step): dQ and params on the launch stream, delta and "
                                  "dK/dV on a second stream; duration from events on the kernel's own stream"},
         "extra": extra,
