@@ -5,6 +5,9 @@ The directory name is not a Python identifier; import it with
 
 Public surface (reference names, Lanerra/dwarf-v2):
   dsqg_attention_v18_grouped, _DSQGV18GroupedFn      kernels/dsqg_attention_v22.py
+  dsqg_attention_with_probes, _DSQGProbedFn,
+  dsqg_block_forward (block module)                  the op and DSQGAttentionV19.forward with the
+                                                     block's y/z features inside the kernels
   ALL_OFFSETS, R_PLANES and the lattice helpers      kernels/dsqg_attention_v22.py
   causal_ema_scan, bounded_ema_factor,
   inverse_bounded_ema_factor                         kernels/causal_ema_scan.py
@@ -17,8 +20,10 @@ Public surface (reference names, Lanerra/dwarf-v2):
   q6: pack_kv, unpack_kv, q6_prefill, q6_decode      (no reference counterpart)
 """
 
-from . import _lib, lattice, npci, ops, packet, planner, probe, q6
-from .dsqg import _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_backward, dsqg_forward
+from . import _lib, block, lattice, npci, ops, packet, planner, probe, q6
+from .block import dsqg_block_forward
+from .dsqg import (_DSQGProbedFn, _DSQGV18GroupedFn, dsqg_attention_v18_grouped, dsqg_attention_with_probes,
+                   dsqg_backward, dsqg_forward)
 from .ema import bounded_ema_factor, causal_ema_scan, inverse_bounded_ema_factor
 from .npci import npci_rotate
 from .packet import _InterferencePacketFn, _InterferencePoolFn, interference_packet, interference_packet_forward, interference_pool
@@ -39,6 +44,7 @@ __all__ = [
     "ALL_OFFSETS",
     "GROUPED_MODE_IDS",
     "R_PLANES",
+    "_DSQGProbedFn",
     "_DSQGV18GroupedFn",
     "_InterferencePacketFn",
     "_InterferencePoolFn",
@@ -54,6 +60,8 @@ __all__ = [
     "build_offset_groups",
     "causal_ema_scan",
     "dsqg_attention_v18_grouped",
+    "dsqg_attention_with_probes",
+    "dsqg_block_forward",
     "dsqg_backward",
     "dsqg_forward",
     "interference_packet",

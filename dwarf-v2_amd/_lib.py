@@ -13,7 +13,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 
 LIB_NAME = "libdwarf_dsqg.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DWARF_OK = 0
 DWARF_ERR_INVALID_ARGUMENT = 1
@@ -85,6 +85,7 @@ class DsqgFwdArgs(ctypes.Structure):
         ("out", c_void_p), ("out_stride", _i64(4)),
         ("lse", c_void_p), ("lse_stride", _i64(3)),
         ("schedule", c_int32),
+        ("query_probes", c_void_p), ("key_probes", c_void_p), ("y_out", c_void_p),
     ]
 
 

@@ -135,7 +135,9 @@ int check_gather_span(const char* name, int64_t row_stride, int64_t elem, int N)
   return DWARF_OK;
 }
 
-int check_fwd(const dwarf_dsqg_fwd_args& a) {
+// forward: the arguments of dwarf_dsqg_fwd (y_pre is not read when query_probes is set; y_out is written);
+// otherwise those of a backward stage (y_pre holds the forward's y).
+int check_fwd(const dwarf_dsqg_fwd_args& a, bool forward) {
   if (a.B < 0) return fail(DWARF_ERR_INVALID_ARGUMENT, "B=%d", a.B);
   int rc = check_lattice(a.H, a.H_kv, a.N, a.head_dim, a.J, a.J_small, a.J_large, a.plane_shift, a.query_start);
   if (rc) return rc;
@@ -144,19 +146,27 @@ int check_fwd(const dwarf_dsqg_fwd_args& a) {
   if (a.schedule & ~kKnownSchedule)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "schedule=%d holds bits outside DWARF_SCHED_BAND | TWO_PASS | DELTA_STAGE",
                 a.schedule);
+  const bool probed = a.query_probes || a.key_probes;
+  if (probed && a.dtype != DWARF_BF16)
+    return fail(DWARF_ERR_UNSUPPORTED, "query_probes/key_probes (probe features in the kernels) are built for bf16 only");
+  if ((a.query_probes && !aligned16(a.query_probes)) || (a.key_probes && !aligned16(a.key_probes)))
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "query_probes/key_probes must be 16-byte aligned");
   if (a.B == 0 || a.N == 0) return DWARF_OK;   // no rows to read or write
+  const bool reads_y = !(forward && a.query_probes);
+  if (forward && a.query_probes && (!a.y_out || !aligned16(a.y_out)))
+    return fail(DWARF_ERR_INVALID_ARGUMENT, "y_out must be a 16-byte aligned [B,H,N,4] fp32 buffer when query_probes is set");
   if ((rc = check_rows("q", a.q, a.q_stride, 3, a.dtype))) return rc;
   if ((rc = check_rows("k", a.k, a.k_stride, 3, a.dtype))) return rc;
   if ((rc = check_rows("v", a.v, a.v_stride, 3, a.dtype))) return rc;
   if ((rc = check_rows("out", a.out, a.out_stride, 3, a.dtype))) return rc;
-  if ((rc = check_planes("y_pre", a.y_pre, a.y_stride))) return rc;
+  if (reads_y && (rc = check_planes("y_pre", a.y_pre, a.y_stride))) return rc;
   if ((rc = check_planes("z_pre", a.z_pre, a.z_stride))) return rc;
   if (!a.pos_bias || !a.scale_embed || !a.phase_base || !a.phase_gain || !a.offsets || !a.lse)
     return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter table, offsets or lse is NULL");
   if (a.dtype == DWARF_BF16) {
     if ((rc = check_gather_span("q", a.q_stride[2], 2, a.N))) return rc;
     if ((rc = check_gather_span("lse", a.lse_stride[2], 4, a.N))) return rc;
-    if ((rc = check_gather_span("y_pre", a.y_stride[2], 4, a.N))) return rc;
+    if (reads_y && (rc = check_gather_span("y_pre", a.y_stride[2], 4, a.N))) return rc;
     if ((rc = check_gather_span("k", a.k_stride[2], 2, a.N))) return rc;
     if ((rc = check_gather_span("v", a.v_stride[2], 2, a.N))) return rc;
     if ((rc = check_gather_span("z_pre", a.z_stride[2], 4, a.N))) return rc;
@@ -178,7 +188,7 @@ const char* dwarf_last_error(void) { return g_error; }
 
 int dwarf_dsqg_fwd(const dwarf_dsqg_fwd_args* args, dwarf_stream_t stream) {
   if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
-  int rc = check_fwd(*args);
+  int rc = check_fwd(*args, true);
   if (rc) return rc;
   if (args->B == 0 || args->N == 0) return ok();
   return hip_status(dwarf::launch_dsqg_fwd(*args, reinterpret_cast<hipStream_t>(stream)), "dwarf_dsqg_fwd");
@@ -193,7 +203,7 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
                      bool do_dkdv, const char* name) {
   if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
   const dwarf_dsqg_bwd_args& a = *args;
-  int rc = check_fwd(a.fwd);
+  int rc = check_fwd(a.fwd, false);
   if (rc) return rc;
   if (a.fwd.B == 0 || a.fwd.N == 0) {   // the parameter gradients are sums over nothing
     if (!do_params) return ok();
@@ -220,16 +230,20 @@ static int bwd_stage(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream, boo
   if (dt == DWARF_BF16 && (rc = check_gather_span("dout", a.dout_stride[2], 2, a.fwd.N))) return rc;
   if (do_dq) {
     if ((rc = check_contig_rows("dq", a.dq, a.dq_stride, dt))) return rc;
-    if (!a.dy_pre) return fail(DWARF_ERR_INVALID_ARGUMENT, "dy_pre is NULL");
-    if (!aligned16(a.dy_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dy_pre must be 16-byte aligned");
+    if (!a.fwd.query_probes) {   // with query_probes dy goes into dq instead
+      if (!a.dy_pre) return fail(DWARF_ERR_INVALID_ARGUMENT, "dy_pre is NULL");
+      if (!aligned16(a.dy_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dy_pre must be 16-byte aligned");
+    }
   }
   if (do_params && (!a.dpos_bias || !a.dscale_embed || !a.dphase_base || !a.dphase_gain))
     return fail(DWARF_ERR_INVALID_ARGUMENT, "a parameter gradient output is NULL");
   if (do_dkdv) {
     if ((rc = check_contig_rows("dk", a.dk, a.dk_stride, dt))) return rc;
     if ((rc = check_contig_rows("dv", a.dv, a.dv_stride, dt))) return rc;
-    if (!a.dz_pre) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre is NULL");
-    if (!aligned16(a.dz_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre must be 16-byte aligned");
+    if (!a.fwd.key_probes) {     // with key_probes dz goes into dk instead
+      if (!a.dz_pre) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre is NULL");
+      if (!aligned16(a.dz_pre)) return fail(DWARF_ERR_INVALID_ARGUMENT, "dz_pre must be 16-byte aligned");
+    }
   }
   const dwarf::BwdWorkspace ws = dwarf::bwd_workspace_layout(a);
   if (!a.workspace || a.workspace_bytes < ws.total)
@@ -259,7 +273,7 @@ int dwarf_dsqg_bwd_dkdv(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) 
 int dwarf_dsqg_bwd_delta(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream) {
   if (!args) return fail(DWARF_ERR_INVALID_ARGUMENT, "args is NULL");
   const dwarf_dsqg_bwd_args& a = *args;
-  int rc = check_fwd(a.fwd);
+  int rc = check_fwd(a.fwd, false);
   if (rc) return rc;
   if (a.fwd.dtype != DWARF_BF16)
     return fail(DWARF_ERR_UNSUPPORTED, "dwarf_dsqg_bwd_delta: bf16 only (the fp32 dQ launch forms delta itself)");

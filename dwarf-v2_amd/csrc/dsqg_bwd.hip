@@ -534,6 +534,9 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
 
   }
 
+  // with key_probes z came from the key probes: dz goes into dk through the probe features (the
+  // block's einsum backward, dsqg:3231-3254) instead of out to dz_pre
+  if (f.key_probes) fold_probe_grad(dk, k32, f.key_probes, g, zg, dz);
   if (!key_ok) return;
   uint4* k4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dk) + b * a.dk_stride[0] + hk * a.dk_stride[1] +
                                        mm * a.dk_stride[2] + 16 * g);
@@ -552,7 +555,7 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   x.x = pack_bf16x2(dv[8], dv[9]);   x.y = pack_bf16x2(dv[10], dv[11]);
   x.z = pack_bf16x2(dv[12], dv[13]); x.w = pack_bf16x2(dv[14], dv[15]);
   v4[1] = x;
-  a.dz_pre[(static_cast<int64_t>(bhk) * N + m) * kPlanes + g] = dz;
+  if (!f.key_probes) a.dz_pre[(static_cast<int64_t>(bhk) * N + m) * kPlanes + g] = dz;
 }
 
 hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {

@@ -1082,6 +1082,9 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
       }
       __builtin_amdgcn_wave_barrier();
     }
+    // with query_probes y was formed from q in the forward: dy goes into dq through the probe
+    // features (the block's einsum backward, dsqg:3231-3254) instead of out to dy_pre
+    if (f.query_probes) fold_probe_grad(dq, q32, f.query_probes, g, yg, dy);
     if (row_ok) {
       uint4* o4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dq) + b * a.dq_stride[0] + h * a.dq_stride[1] +
                                            nn * a.dq_stride[2] + 16 * g);
@@ -1092,7 +1095,7 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
       x1.z = pack_bf16x2(dq[12], dq[13]); x1.w = pack_bf16x2(dq[14], dq[15]);
       o4[0] = x0;
       o4[1] = x1;
-      a.dy_pre[(static_cast<int64_t>(bh) * N + n) * kPlanes + g] = dy;
+      if (!f.query_probes) a.dy_pre[(static_cast<int64_t>(bh) * N + n) * kPlanes + g] = dy;
     }
   }
 }

@@ -267,13 +267,15 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
     for (int ks = 0; ks < 2; ++ks)
       xa[ks] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(n0w + lr) * a.q_stride[2] + 32 * ks + 8 * lc);
   }
+  // with query_probes y is formed below from the q row (every row < N) and written to y_out
+  const bool probed = a.query_probes != nullptr;
   uint4 qx0 = {0u, 0u, 0u, 0u}, qx1 = {0u, 0u, 0u, 0u};
   float yg = 0.f;
-  if (live) {
+  if (probed ? row_ok : live) {
     const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * a.q_stride[2] + 16 * g);
     qx0 = q4[0];
     qx1 = q4[1];
-    yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
+    if (!probed) yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
   }
 
   stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kERowFwd);
@@ -321,6 +323,10 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
   const int cntp = (cnt + CJ - 1) / CJ * CJ;
 
   const uint32_t q32[8] = {qx0.x, qx0.y, qx0.z, qx0.w, qx1.x, qx1.y, qx1.z, qx1.w};
+  if (probed) {   // y of plane g (dsqg:3231-3254); the four lanes of each query take part
+    yg = probe_feature(q32, a.query_probes, g);
+    if (row_ok) a.y_out[(static_cast<int64_t>(b * a.H + h) * N + n) * kPlanes + g] = yg;
+  }
   // Per-lane byte offsets of row 0 shifted by the lane's query; a lane without
   // a live query uses n_eff = n0w - 2N, so n_eff - d < 0 for every listed d.
   const int n_eff = live ? n : n0w - 2 * N;
@@ -565,13 +571,15 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_win(const dwarf_dsqg_
     for (int ks = 0; ks < 2; ++ks)
       xa[ks] = *reinterpret_cast<const uint4*>(qbase + static_cast<int64_t>(n0w + lr) * a.q_stride[2] + 32 * ks + 8 * lc);
   }
+  // with query_probes y is formed below from the q row (every row < N) and written to y_out
+  const bool probed = a.query_probes != nullptr;
   uint4 qx0 = {0u, 0u, 0u, 0u}, qx1 = {0u, 0u, 0u, 0u};
   float yg = 0.f;
-  if (live) {
+  if (probed ? row_ok : live) {
     const uint4* q4 = reinterpret_cast<const uint4*>(qbase + nn * a.q_stride[2] + 16 * g);
     qx0 = q4[0];
     qx1 = q4[1];
-    yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
+    if (!probed) yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
   }
 
   stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kERowFwd);
@@ -621,6 +629,10 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_win(const dwarf_dsqg_
   const int JB = uniform(s_jn[0]);
 
   const uint32_t q32[8] = {qx0.x, qx0.y, qx0.z, qx0.w, qx1.x, qx1.y, qx1.z, qx1.w};
+  if (probed) {   // y of plane g (dsqg:3231-3254); the four lanes of each query take part
+    yg = probe_feature(q32, a.query_probes, g);
+    if (row_ok) a.y_out[(static_cast<int64_t>(b * a.H + h) * N + n) * kPlanes + g] = yg;
+  }
   // Per-lane byte offsets of row 0 shifted by the lane's query; a lane without
   // a live query uses n_eff = n0w - 2N, so n_eff - d < 0 for every listed d.
   const int n_eff = live ? n : n0w - 2 * N;

@@ -198,4 +198,62 @@ __device__ __forceinline__ float sum_over_queries16(float x) {
   return add_xor32(add_xor16(x));
 }
 
+// ---------------------------------------------------------------------------
+// Phase-probe features of a row held by a group of four lanes (lane g holds
+// dims [16g, 16g + 16) as 8 bf16 pairs), the DSQG block's y/z
+// (dsqg:3231-3254): f_r = s <x, p_r>, s = 1 / sqrt(|x|^2 + 1e-6 hd), with the
+// probes p [4][64] fp32 (rows already normalised) read from global memory.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float probe_row_scale(const uint32_t* x32) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = dot2bf(x32[i], x32[i], ss);
+  return rsqrtf(group_sum<4>(ss) + 1e-6f * 64);   // head_dim 64
+}
+
+// Feature f_g of this lane's plane g.
+__device__ __forceinline__ float probe_feature(const uint32_t* x32, const float* __restrict__ probes, int g) {
+  const float4* p4 = reinterpret_cast<const float4*>(probes) + 4 * g;   // row r, dims 16g + 4i: p4[16 r + i]
+  float f[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float x0 = bf16_lo(x32[2 * i]), x1 = bf16_hi(x32[2 * i]);
+    const float x2 = bf16_lo(x32[2 * i + 1]), x3 = bf16_hi(x32[2 * i + 1]);
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) {
+      const float4 p = p4[16 * r + i];
+      f[r] = fmaf(x0, p.x, f[r]);
+      f[r] = fmaf(x1, p.y, f[r]);
+      f[r] = fmaf(x2, p.z, f[r]);
+      f[r] = fmaf(x3, p.w, f[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kPlanes; ++r) f[r] = group_sum<4>(f[r]);
+  return pick4(g, f[0], f[1], f[2], f[3]) * probe_row_scale(x32);
+}
+
+// Adds the gradient reaching the row through its features to the lane's 16
+// dims of dx: dx += s sum_r df_r p_r - s^2 (sum_r df_r f_r) x, where lane g of
+// the group holds f_g and its gradient df_g.
+__device__ __forceinline__ void fold_probe_grad(float* dx, const uint32_t* x32, const float* __restrict__ probes,
+                                                int g, float fg, float dfg) {
+  const float s = probe_row_scale(x32);
+  const float c = group_sum<4>(dfg * fg) * s * s;
+  // df_r of every plane: quad_perm broadcasts of lane r of the group
+  const float d0 = s * dpp_f<0x00>(dfg), d1 = s * dpp_f<0x55>(dfg);
+  const float d2 = s * dpp_f<0xAA>(dfg), d3 = s * dpp_f<0xFF>(dfg);
+  const float4* p4 = reinterpret_cast<const float4*>(probes) + 4 * g;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 a = p4[i], b = p4[16 + i], e = p4[32 + i], h = p4[48 + i];
+    const float x[4] = {bf16_lo(x32[2 * i]), bf16_hi(x32[2 * i]), bf16_lo(x32[2 * i + 1]), bf16_hi(x32[2 * i + 1])};
+    const float pa[4] = {a.x, a.y, a.z, a.w}, pb[4] = {b.x, b.y, b.z, b.w};
+    const float pe[4] = {e.x, e.y, e.z, e.w}, ph[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      dx[4 * i + k] += fmaf(d0, pa[k], fmaf(d1, pb[k], fmaf(d2, pe[k], fmaf(d3, ph[k], -c * x[k]))));
+  }
+}
+
 }  // namespace dwarf

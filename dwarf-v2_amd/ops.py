@@ -1,6 +1,7 @@
 """torch.library registration of the HIP launches.
 
-``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::ema_fwd``,
+``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::dsqg_fwd_probed``,
+``dwarf::dsqg_bwd_probed``, ``dwarf::ema_fwd``,
 ``dwarf::ema_bwd``, ``dwarf::phase_probe_fwd``, ``dwarf::phase_probe_bwd``,
 ``dwarf::npci_fwd``, ``dwarf::npci_bwd``, ``dwarf::packet_pool_fwd``,
 ``dwarf::packet_pool_bwd``, ``dwarf::packet_fwd`` and ``dwarf::packet_bwd`` are
@@ -71,6 +72,52 @@ def _dsqg_bwd_fake(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain,
             q.new_empty(pos_bias.shape, dtype=f32), q.new_empty(scale_embed.shape, dtype=f32),
             q.new_empty(phase_base.shape, dtype=f32), q.new_empty(phase_gain.shape, dtype=f32),
             q.new_empty(y_pre.shape, dtype=f32), q.new_empty(z_pre.shape, dtype=f32))
+
+
+@torch.library.custom_op("dwarf::dsqg_fwd_probed", mutates_args=())
+def dsqg_fwd_probed(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, scale_embed: Tensor, phase_base: Tensor,
+                    phase_gain: Tensor, query_probes: Tensor, z_pre: Tensor, offsets: Tensor, j_small: int,
+                    j_large: int, plane_shift: int, query_start: int,
+                    schedule: int = _dsqg.DEFAULT_SCHEDULE) -> tuple[Tensor, Tensor, Tensor]:
+    """Forward launch forming y from q and normalised query probes; returns (out, lse, y [B,H,N,4] fp32)."""
+    t = _dsqg.normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, None, z_pre, offsets,
+                               j_small + j_large)
+    return _dsqg.dsqg_forward(*t, j_small, j_large, plane_shift, query_start, schedule=schedule,
+                              query_probes=_dsqg._planes(query_probes.float()))
+
+
+@dsqg_fwd_probed.register_fake
+def _dsqg_fwd_probed_fake(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, query_probes, z_pre, offsets,
+                          j_small, j_large, plane_shift, query_start, schedule=_dsqg.DEFAULT_SCHEDULE):
+    B, H, N, HD = q.shape
+    f32 = torch.float32
+    return q.new_empty((B, H, N, HD)), q.new_empty((B, H, N), dtype=f32), q.new_empty((B, H, N, 4), dtype=f32)
+
+
+@torch.library.custom_op("dwarf::dsqg_bwd_probed", mutates_args=())
+def dsqg_bwd_probed(dout: Tensor, q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor, scale_embed: Tensor,
+                    phase_base: Tensor, phase_gain: Tensor, query_probes: Tensor, key_probes: Tensor, y_pre: Tensor,
+                    z_pre: Tensor, offsets: Tensor, out: Tensor, lse: Tensor, j_small: int, j_large: int,
+                    plane_shift: int, query_start: int, schedule: int = _dsqg.DEFAULT_SCHEDULE
+                    ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Backward launches with dy and dz folded into dq and dk; returns (dq, dk, dv, dpos_bias, dscale_embed,
+    dphase_base, dphase_gain)."""
+    t = _dsqg.normalize_inputs(q, k, v, pos_bias, scale_embed, phase_base, phase_gain, y_pre, z_pre, offsets,
+                               j_small + j_large)
+    g = _dsqg.dsqg_backward(dout, *t, out, lse.contiguous(), j_small, j_large, plane_shift, query_start,
+                            schedule=schedule, query_probes=_dsqg._planes(query_probes.float()),
+                            key_probes=_dsqg._planes(key_probes.float()))
+    return g[:7]
+
+
+@dsqg_bwd_probed.register_fake
+def _dsqg_bwd_probed_fake(dout, q, k, v, pos_bias, scale_embed, phase_base, phase_gain, query_probes, key_probes,
+                          y_pre, z_pre, offsets, out, lse, j_small, j_large, plane_shift, query_start,
+                          schedule=_dsqg.DEFAULT_SCHEDULE):
+    f32 = torch.float32
+    return (q.new_empty(q.shape), q.new_empty(k.shape), q.new_empty(v.shape),
+            q.new_empty(pos_bias.shape, dtype=f32), q.new_empty(scale_embed.shape, dtype=f32),
+            q.new_empty(phase_base.shape, dtype=f32), q.new_empty(phase_gain.shape, dtype=f32))
 
 
 # ---- EMA -------------------------------------------------------------------------------------

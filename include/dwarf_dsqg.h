@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define DWARF_ABI_VERSION 8
+#define DWARF_ABI_VERSION 9
 #define DWARF_R_PLANES 4        /* MOVT planes per far offset: dsqg:69 */
 #define DWARF_Q6_GROUP 32       /* head-dim elements per q6 scale group */
 #define DWARF_Q6_SLOT_BYTES 128 /* one q6 K/V cache slot per (b, kv head, t) */
@@ -84,7 +84,34 @@ typedef struct {
   void* out;  int64_t out_stride[4];
   float* lse; int64_t lse_stride[3];
   int32_t schedule;       /* DWARF_SCHED_* bit flags: which schedule of the same mathematics runs */
+  /* Phase-probe features inside the kernels (bf16 only); NULL for the
+   * reference op's contract, where y_pre and z_pre are inputs and dy_pre and
+   * dz_pre outputs.  [4][hd] fp32, contiguous, 16-byte aligned, rows already
+   * normalised (the block's F.normalize of its probes, dsqg:3231-3232). */
+  const float* query_probes;
+  const float* key_probes;
+  float* y_out;           /* [B,H,N,4] fp32 contiguous: y written by the forward when query_probes is set */
 } dwarf_dsqg_fwd_args;
+
+/*
+ * The probe features inside the kernels replace the DSQG block's y/z einsum
+ * (DSQGAttentionV19.forward, dsqg:3231-3254: y = <q, p_r> / sqrt(|q|^2 + 1e-6
+ * hd), z likewise from k) and its backward:
+ *   - query_probes set: dwarf_dsqg_fwd forms y of every query row from q in
+ *     its prologue instead of reading y_pre (which may then be NULL) and
+ *     writes it to y_out (every row n < N).  The backward takes that y as
+ *     y_pre and adds dy's contribution to dq in the dQ launch's epilogue,
+ *     through the normalisation (dq += s sum_r dy_r p_r - s^2 (sum_r dy_r
+ *     y_r) q, s = 1 / sqrt(|q|^2 + 1e-6 hd)), instead of writing dy_pre
+ *     (which may then be NULL).
+ *   - key_probes set: z_pre holds the key features (for instance from
+ *     dwarf_phase_probe_fwd over k), and the dK/dV launch adds dz's
+ *     contribution to dk in its epilogue the same way instead of writing
+ *     dz_pre (which may then be NULL).  The forward does not read key_probes.
+ * The probe gradients are not formed (the trainer's probes are frozen,
+ * train:311); a caller that trains them uses y_pre/z_pre as the reference op
+ * does.
+ */
 
 /*
  * Schedules (dwarf_dsqg_fwd_args.schedule).  They compute the same function;
