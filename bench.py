@@ -418,6 +418,59 @@ def phase_probe_extra(pkg, device, steps, warmup):
                       "plus dprobes; timed from HIP-graph replays"}
 
 
+def probe_fusion_extra(pkg, device, steps, warmup):
+    """The DSQG block's y/z (row f1) at the training microbatch: fwd+bwd with autograd through q and k of
+    (a) the block's own route, y and z by an fp32 einsum over q and k (dsqg:3231-3254) and the op on them,
+    and (b) the op in its probe form (y in the forward kernel, z by the phase-probe kernel, dy and dz folded
+    into dq and dk).  Each step is timed by two events on the launch stream (which waits for the backward's
+    second stream); medians of `steps` steps."""
+    B, H, N = 15, 8, 2048
+    t, js, jl = synth(pkg, B, H, N, 0, device)
+    qp_raw, kp_raw = t["qp"].to(device), t["kp"].to(device)
+    off = t["offsets"]
+    tables = [t[n] for n in ("pos_bias", "scale_embed", "phase_base", "phase_gain")]
+    leaves = [t[n].detach().clone().requires_grad_(True) for n in ("q", "k", "v")]
+    dout = t["dout"]
+
+    def einsum_route():
+        q, k, v = leaves
+        qp = torch.nn.functional.normalize(qp_raw.float(), dim=-1)
+        kp = torch.nn.functional.normalize(kp_raw.float(), dim=-1)
+        qf, kf = q.float(), k.float()
+        y = (torch.einsum("bhnd,rd->bhnr", qf, qp) * torch.rsqrt(qf.square().sum(-1, keepdim=True) + 64e-6)).contiguous()
+        z = (torch.einsum("bhnd,rd->bhnr", kf, kp) * torch.rsqrt(kf.square().sum(-1, keepdim=True) + 64e-6)).contiguous()
+        out = pkg.dsqg_attention_v18_grouped(q, k, v, *tables, y, z, js + jl, js, jl, off, None, None, None, None,
+                                             None, 3, 0, False, 0, 0, 1)
+        out.backward(dout)
+
+    def probe_route():
+        q, k, v = leaves
+        out = pkg.dsqg_attention_with_probes(q, k, v, *tables, qp_raw, kp_raw, js + jl, js, jl, off, None, None,
+                                             None, None, None, 3, 0, False, 0, 0, 1)
+        out.backward(dout)
+
+    res = {}
+    for name, fn in (("einsum", einsum_route), ("probes_in_kernels", probe_route)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(max(steps, 10)):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        ts.sort()
+        res[f"ms_{name}"] = ts[len(ts) // 2]
+        for x in leaves:
+            x.grad = None
+    res["config"] = ("B15 H8 T2048 bf16 fwd+bwd with autograd through q and k; einsum = the block's fp32 einsum "
+                     "features then the reference-contract op; probes_in_kernels = dsqg_attention_with_probes")
+    return res
+
+
 def npci_extra(pkg, device, steps, warmup):
     """npci_rotate fwd and bwd (dx, ddelta, dtheta) on the training microbatch's keys: x a [B,N,H,hd] storage
     viewed as [B,H,N,hd], as the DSQG block hands it over, bf16 deltas."""
@@ -526,7 +579,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe", "npci", "packet"],
+    ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe", "npci", "packet",
+                                             "probe_fusion"],
                     help="run only this extra workload and print its JSON (for per-workload profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 10 times (scales HBM byte counters)")
@@ -553,7 +607,7 @@ def main() -> int:
     if args.extra_only:
         fn = {"q6_decode": q6_decode_extra, "q6_prefill": q6_prefill_extra,
               "long_context": long_context_extra, "phase_probe": phase_probe_extra,
-              "npci": npci_extra, "packet": packet_extra}[args.extra_only]
+              "npci": npci_extra, "packet": packet_extra, "probe_fusion": probe_fusion_extra}[args.extra_only]
         print(json.dumps({args.extra_only: fn(pkg, device, args.steps, args.warmup)}), flush=True)
         return 0
     B, H, N = 15, 8, 2048
@@ -595,6 +649,8 @@ def main() -> int:
         extra["long_context"] = long_context_extra(pkg, device, max(3, args.steps // 4), 2)
         log("phase-probe features: q of the training microbatch")
         extra["phase_probe"] = phase_probe_extra(pkg, device, args.steps, args.warmup)
+        log("block y/z: einsum route vs probe features inside the kernels")
+        extra["probe_fusion"] = probe_fusion_extra(pkg, device, args.steps, args.warmup)
         log("NPCI rotation: k of the training microbatch")
         extra["npci"] = npci_extra(pkg, device, args.steps, args.warmup)
         log("InterferencePacket pool: x [15,2048,512], three timescales")
