@@ -121,6 +121,7 @@ class EmaFwdArgs(ctypes.Structure):
         ("y", c_void_p), ("y_stride", _i64(3)),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
         ("reset", c_void_p), ("reset_stride", _i64(2)),
+        ("wait_limit", c_int32),
     ]
 
 
@@ -137,6 +138,7 @@ class EmaBwdArgs(ctypes.Structure):
         ("dalpha", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_size_t),
         ("reset", c_void_p), ("reset_stride", _i64(2)),
+        ("wait_limit", c_int32),
     ]
 
 

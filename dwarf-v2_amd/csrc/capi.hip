@@ -338,6 +338,7 @@ int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream) {
   const size_t need = dwarf::ema_fwd_workspace(a.B, a.N, a.D);
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  if (!aligned16(a.workspace)) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
   return hip_status(dwarf::launch_ema_fwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_ema_fwd");
 }
 
@@ -356,6 +357,7 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream) {
   const size_t need = dwarf::ema_bwd_workspace(a.B, a.N, a.D);
   if (!a.workspace || a.workspace_bytes < need)
     return fail(DWARF_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need, a.workspace_bytes);
+  if (!aligned16(a.workspace)) return fail(DWARF_ERR_WORKSPACE, "workspace must be 16-byte aligned");
   return hip_status(dwarf::launch_ema_bwd(a, reinterpret_cast<hipStream_t>(stream)), "dwarf_ema_bwd");
 }
 

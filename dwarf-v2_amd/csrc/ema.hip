@@ -236,8 +236,548 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
   for (int i = 0; i < VEC; ++i) dp[i] = da[i];
 }
 
+// ---------------------------------------------------------------------------
+// Single-pass scan with decoupled look-back (used where every [N][D] slab of
+// x, y, dy and dx spans less than 2 GiB, so rows take 32-bit buffer offsets).
+//
+// A tile is (b, block of 16 VEC channels, 4 SEG = 128 consecutive tokens),
+// one wave: lane (cg = lane & 15, ts = lane >> 4) holds channels
+// [16 VEC cb + VEC cg, +VEC) of tokens [s0, s0 + SEG), s0 = 4 SEG chunk +
+// SEG ts, loaded once into registers.  (64-token segments keep twice the rows
+// per lane and half the waves: 5 us slower at [4, 8192, 512]; 16-token
+// segments give more, shorter waits: 15 us slower.)  The wave
+//   1. scans each lane's segment from a zero state: its end L and its
+//      transfer factor A = decay^len (0 when a reset falls inside);
+//   2. composes the four segments of a channel in time order into the tile's
+//      (P, Q), state after the tile = P s + Q, and each lane's prefix;
+//   3. publishes Q as the tile's aggregate, tagged with its factor: tag 1
+//      for P = decay^(4 SEG), tag 3 for P = 0 (a reset inside, or a factor
+//      below fp32's range);
+//   4. forms the state C entering it from the aggregates of the tiles before
+//      it in a fixed order, C = P_p C + Q_p from the start of its run of
+//      kLbRun tiles, the run entered with the inclusive state the previous
+//      run's last tile publishes (tag 2); every input is published before
+//      its writer waits on anything, so the result is the same bits every run;
+//   5. rescans its segment from its incoming state and writes y.
+// A tile waits only on tiles of lower index (workgroup index), which the
+// hardware dispatches first; the only chain of waits is the runs' inclusive
+// states, and it ends at the first run.  (A counter handing out tile indices
+// in claim order measured 9 us slower at [4, 8192, 512]: one contended atomic
+// per tile.)  A value and its tag share one 64-bit word, written and read as
+// one agent-scope atomic (coherent across the XCDs' L2s without a fence);
+// `ema_lb_zero` clears the words before each scan.  A wait gives up after
+// wait_limit polls and poisons its channel with NaN rather than hang.
+// The backward runs the same scan in reverse time over dy for the adjoint
+// lambda, and in its rescan writes dx and each tile's dalpha partial.
+// ---------------------------------------------------------------------------
+constexpr int kLbGroups = 16;   // channel groups of a tile (lanes cg)
+constexpr int kLbSegs = 4;      // token segments of a tile (lanes ts)
+constexpr int kLbSeg = 32;                         // tokens per segment (the lane's registers)
+constexpr int kLbWaitLimit = 1 << 22;              // default polls before a wait gives up
+constexpr size_t kLbHead = 256;                    // bytes ahead of the words (unused, kept zero)
+constexpr int kLbRun = 32;                         // tiles per run (one inclusive state per run)
+constexpr int kLbBatch = 8;                        // aggregates loaded together by a carry walk
+
+struct LbGeom {
+  int B, N, D;
+  int CB;    // channel blocks of 16 VEC channels
+  int NCH;   // tiles along time per (b, channel block)
+  int S;     // (b, channel block) slices, B * CB
+  int per_channel;
+  float lo, hi;
+  const uint8_t* reset;
+  int64_t srb, srn;
+  unsigned long long* words;   // [NCH * S][16 VEC]: aggregates, (value bits, tag << 32)
+  unsigned long long* runs;    // [ceil(NCH / kLbRun) * S][16 VEC]: the runs' inclusive states
+  float* da_part;              // backward: [NCH][B][D] dalpha partials (row chunk * B + b)
+  int wait_limit;
+};
+
+__device__ __forceinline__ float lb_alpha(const float* alpha, const LbGeom& g, int d) {
+  const float a = alpha[g.per_channel ? d : 0];
+  return fminf(fmaxf(a, g.lo), g.hi);
+}
+
+__device__ __forceinline__ bool lb_reset(const LbGeom& g, int b, int t) {
+  return g.reset[b * g.srb + static_cast<int64_t>(t) * g.srn] != 0;
+}
+
+// Raw VEC channels of one token in registers, loaded and stored through
+// buffer resources (an out-of-range offset reads zeros / drops the store).
+template <typename T, int VEC>
+struct LbRaw {
+  static constexpr int kWords = (VEC * sizeof(T) + 3) / 4;
+  uint32_t w[kWords];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (VEC * sizeof(T) == 16) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+      w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+    } else if constexpr (VEC * sizeof(T) == 8) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+      w[0] = v[0]; w[1] = v[1];
+    } else if constexpr (VEC * sizeof(T) == 4) {
+      w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else {
+      w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void widen(float* v) const {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[i] = (i & 1) ? bf16_hi(w[i / 2]) : bf16_lo(w[i / 2]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[i] = __uint_as_float(w[i]);
+    }
+  }
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ void lb_store(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* v) {
+  if constexpr (sizeof(T) == 2 && VEC == 4) {
+    __builtin_amdgcn_raw_buffer_store_b64(
+        __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, make_uint2(pack_bf16x2(v[0], v[1]),
+                                                                                    pack_bf16x2(v[2], v[3]))),
+        r, off, 0, 0);
+  } else if constexpr (sizeof(T) == 4 && VEC == 4) {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned,
+                           make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                      __float_as_uint(v[3]))),
+        r, off, 0, 0);
+  } else if constexpr (sizeof(T) == 2) {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v[0]), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, off, 0, 0);
+  }
+}
+
+// One [N][D] slab of batch row b (the host bounds its span below 2 GiB).
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lb_rsrc(const T* base, int64_t sb, int64_t sn, int b, int N) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + b * sb), 0,
+                                           static_cast<int>(static_cast<int64_t>(N) * sn * sizeof(T)), 0x00020000);
+}
+
+__device__ __forceinline__ void lb_publish(unsigned long long* w, float v, unsigned tag) {
+  const unsigned long long x = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v);
+  __hip_atomic_store(w, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The published word, or 0 when the wait gives up.
+__device__ __forceinline__ unsigned long long lb_wait(const unsigned long long* w, int limit) {
+  for (int it = 0; it < limit; ++it) {
+    const unsigned long long x = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (x >> 32) return x;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return 0;
+}
+
+// The state entering the tile at scan-order index idx of its slice: the
+// previous run's inclusive state (0 in the first run), then the aggregates of
+// the run's tiles before it in order, C = P_p C + Q_p (P_p = full for tag 1,
+// 0 for tag 3).  Aggregates are loaded kLbBatch at a time.  NaN when a wait
+// gives up.
+__device__ __forceinline__ float lb_carry(const LbGeom& g, int slice, int ch, int ct, int idx, float full) {
+  const int run = idx / kLbRun, first = run * kLbRun;
+  float C = 0.f;
+  if (run > 0) {
+    const unsigned long long x = lb_wait(g.runs + (static_cast<int64_t>(run - 1) * g.S + slice) * ct + ch,
+                                         g.wait_limit);
+    if (!x) return __builtin_nanf("");
+    C = __uint_as_float(static_cast<uint32_t>(x));
+  }
+  for (int p0 = first; p0 < idx; p0 += kLbBatch) {
+    unsigned long long w[kLbBatch];
+#pragma unroll
+    for (int k = 0; k < kLbBatch; ++k) {   // a slot past idx - 1 reloads the last one (unused)
+      const int p = min(p0 + k, idx - 1);
+      w[k] = __hip_atomic_load(g.words + (static_cast<int64_t>(p) * g.S + slice) * ct + ch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int k = 0; k < kLbBatch; ++k) {
+      const int p = p0 + k;
+      if (p < idx) {
+        unsigned long long x = w[k];
+        if (!(x >> 32)) {
+          x = lb_wait(g.words + (static_cast<int64_t>(p) * g.S + slice) * ct + ch, g.wait_limit);
+          if (!x) return __builtin_nanf("");
+        }
+        C = fmaf((x >> 32) == 3u ? 0.f : full, C, __uint_as_float(static_cast<uint32_t>(x)));
+      }
+    }
+  }
+  return C;
+}
+
+// Steps 3-4 for the channel a lane owns: publish the aggregate, form the
+// incoming state, and publish the run's inclusive state from its last tile.
+__device__ __forceinline__ float lb_join(const LbGeom& g, int slice, int ch, int ct, int idx, float Po, float Qo,
+                                         float full) {
+  unsigned long long* mine = g.words + (static_cast<int64_t>(idx) * g.S + slice) * ct + ch;
+  lb_publish(mine, Qo, Po == 0.f ? 3u : 1u);
+  const float C = idx > 0 ? lb_carry(g, slice, ch, ct, idx, full) : 0.f;
+  if (idx % kLbRun == kLbRun - 1 && idx + 1 < g.NCH)
+    lb_publish(g.runs + (static_cast<int64_t>(idx / kLbRun) * g.S + slice) * ct + ch, fmaf(Po, C, Qo), 2u);
+  return C;
+}
+
+template <typename T, int VEC, bool RESET>
+__global__ __launch_bounds__(kWave) void ema_fwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
+                                                     T* __restrict__ y, int64_t syb, int64_t syn,
+                                                     const float* __restrict__ alpha, LbGeom g) {
+  constexpr int SEG = kLbSeg;
+  constexpr int CT = kLbGroups * VEC;   // channels (words) per tile
+  const int lane = threadIdx.x;
+  const int cg = lane & 15, ts = lane >> 4;
+  const int id = blockIdx.x;   // tiles of lower index are dispatched first
+  const int chunk = id / g.S, slice = id - chunk * g.S;
+  const int b = slice / g.CB, cb = slice - b * g.CB;
+  const int d0 = (cb * kLbGroups + cg) * VEC;
+  const bool dlive = d0 < g.D;
+  const int s0 = (chunk * kLbSegs + ts) * SEG;
+  const int len = max(0, min(SEG, g.N - s0));
+  float a[VEC], dec[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    a[i] = dlive ? lb_alpha(alpha, g, d0 + i) : 0.f;
+    dec[i] = 1.f - a[i];
+  }
+  const __amdgpu_buffer_rsrc_t rx = lb_rsrc(x, sxb, sxn, b, g.N);
+  const uint32_t rsx = static_cast<uint32_t>(sxn * sizeof(T)), cox = static_cast<uint32_t>(d0 * sizeof(T));
+  LbRaw<T, VEC> raw[SEG];
+#pragma unroll
+  for (int t = 0; t < SEG; ++t)
+    raw[t].load(rx, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsx + cox : kOutOfRange);
+
+  // 1. the segment from a zero state
+  float L[VEC], A[VEC];
+  bool cut = false;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) { L[i] = 0.f; A[i] = 1.f; }
+#pragma unroll
+  for (int t = 0; t < SEG; ++t) {
+    if (t < len) {
+      if constexpr (RESET) {
+        if (lb_reset(g, b, s0 + t)) {
+          cut = true;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) L[i] = 0.f;
+        }
+      }
+      float v[VEC];
+      raw[t].widen(v);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        L[i] = fmaf(a[i], v[i], dec[i] * L[i]);
+        A[i] *= dec[i];
+      }
+    }
+  }
+  if (cut) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) A[i] = 0.f;
+  }
+  // 2. the four segments of each channel in time order: the tile's (P, Q) and this lane's prefix
+  float P[VEC], Q[VEC], Pp[VEC], Qp[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) { P[i] = 1.f; Q[i] = 0.f; Pp[i] = 1.f; Qp[i] = 0.f; }
+#pragma unroll
+  for (int k = 0; k < kLbSegs; ++k) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float Ak = __shfl(A[i], cg + 16 * k), Lk = __shfl(L[i], cg + 16 * k);
+      Pp[i] = k == ts ? P[i] : Pp[i];
+      Qp[i] = k == ts ? Q[i] : Qp[i];
+      Q[i] = fmaf(Ak, Q[i], Lk);
+      P[i] *= Ak;
+    }
+  }
+  // 3-4. the channel this lane publishes (VEC 4: channel ts of the group; VEC 1: lanes ts = 0)
+  float full = 1.f;   // a full tile's factor, composed as a tile composes its segments
+  const int io = VEC == 4 ? ts : 0;
+  const bool owner = (VEC == 4 || ts == 0) && dlive && d0 + io < g.D;
+  const float dec_o = VEC == 4 ? pick4(io, dec[0], dec[VEC > 1 ? 1 : 0], dec[VEC > 2 ? 2 : 0], dec[VEC > 3 ? 3 : 0])
+                               : dec[0];
+  const float Po = VEC == 4 ? pick4(io, P[0], P[VEC > 1 ? 1 : 0], P[VEC > 2 ? 2 : 0], P[VEC > 3 ? 3 : 0]) : P[0];
+  const float Qo = VEC == 4 ? pick4(io, Q[0], Q[VEC > 1 ? 1 : 0], Q[VEC > 2 ? 2 : 0], Q[VEC > 3 ? 3 : 0]) : Q[0];
+  {
+    float seg = 1.f;
+    for (int t = 0; t < SEG; ++t) seg *= dec_o;
+#pragma unroll
+    for (int k = 0; k < kLbSegs; ++k) full *= seg;
+  }
+  const float C = owner ? lb_join(g, slice, cg * VEC + io, CT, chunk, Po, Qo, full) : 0.f;
+  // 5. incoming state of each channel of this lane's segment, then the rescan
+  float st[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const float Ci = __shfl(C, VEC == 4 ? cg + 16 * i : cg);
+    st[i] = fmaf(Pp[i], Ci, Qp[i]);
+  }
+  const __amdgpu_buffer_rsrc_t ry = lb_rsrc(y, syb, syn, b, g.N);
+  const uint32_t rsy = static_cast<uint32_t>(syn * sizeof(T)), coy = static_cast<uint32_t>(d0 * sizeof(T));
+#pragma unroll
+  for (int t = 0; t < SEG; ++t) {
+    if (t < len) {
+      if constexpr (RESET) {
+        if (lb_reset(g, b, s0 + t)) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) st[i] = 0.f;
+        }
+      }
+      float v[VEC];
+      raw[t].widen(v);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) st[i] = fmaf(a[i], v[i], dec[i] * st[i]);
+      lb_store<T, VEC>(ry, dlive ? static_cast<uint32_t>(s0 + t) * rsy + coy : kOutOfRange, st);
+    }
+  }
+}
+
+template <typename T, int VEC, bool RESET>
+__global__ __launch_bounds__(kWave) void ema_bwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
+                                                     const T* __restrict__ y, int64_t syb, int64_t syn,
+                                                     const T* __restrict__ dy, int64_t sgb, int64_t sgn,
+                                                     T* __restrict__ dx, int64_t sdb, int64_t sdn,
+                                                     const float* __restrict__ alpha, LbGeom g) {
+  constexpr int SEG = kLbSeg;
+  constexpr int CT = kLbGroups * VEC;
+  constexpr int R = 8;   // rows of x and y loaded per block of the rescan
+  const int lane = threadIdx.x;
+  const int cg = lane & 15, ts = lane >> 4;
+  const int id = blockIdx.x;   // tiles of lower index are dispatched first
+  const int order = id / g.S, slice = id - order * g.S;   // tiles in reverse time order
+  const int chunk = g.NCH - 1 - order;
+  const int b = slice / g.CB, cb = slice - b * g.CB;
+  const int d0 = (cb * kLbGroups + cg) * VEC;
+  const bool dlive = d0 < g.D;
+  const int s0 = (chunk * kLbSegs + ts) * SEG;
+  const int len = max(0, min(SEG, g.N - s0));
+  float a[VEC], dec[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    a[i] = dlive ? lb_alpha(alpha, g, d0 + i) : 0.f;
+    dec[i] = 1.f - a[i];
+  }
+  const __amdgpu_buffer_rsrc_t rg = lb_rsrc(dy, sgb, sgn, b, g.N);
+  const uint32_t rsg = static_cast<uint32_t>(sgn * sizeof(T)), cog = static_cast<uint32_t>(d0 * sizeof(T));
+  LbRaw<T, VEC> raw[SEG];
+#pragma unroll
+  for (int t = 0; t < SEG; ++t)
+    raw[t].load(rg, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsg + cog : kOutOfRange);
+
+  // 1. the segment in reverse time from a zero adjoint; a reset at token
+  // t + 1 cuts what flows from t + 1 back into t (ema:478-509)
+  float L[VEC], A[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) { L[i] = 0.f; A[i] = 1.f; }
+#pragma unroll
+  for (int t = SEG - 1; t >= 0; --t) {
+    if (t < len) {
+      if constexpr (RESET) {
+        if (t + 1 < len && lb_reset(g, b, s0 + t + 1)) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) L[i] = 0.f;
+        }
+      }
+      float v[VEC];
+      raw[t].widen(v);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        L[i] = fmaf(dec[i], L[i], v[i]);
+        A[i] *= dec[i];
+      }
+    }
+  }
+  if constexpr (RESET) {   // a reset at any of s0 + 1 .. s0 + len cuts the segment's carry
+    bool cut = false;
+    for (int t = s0 + 1; t <= s0 + len && t < g.N; ++t) cut = cut || lb_reset(g, b, t);
+    if (cut) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) A[i] = 0.f;
+    }
+  }
+  // 2. segments composed in reverse time order (3, 2, 1, 0)
+  float P[VEC], Q[VEC], Pp[VEC], Qp[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) { P[i] = 1.f; Q[i] = 0.f; Pp[i] = 1.f; Qp[i] = 0.f; }
+#pragma unroll
+  for (int k = kLbSegs - 1; k >= 0; --k) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float Ak = __shfl(A[i], cg + 16 * k), Lk = __shfl(L[i], cg + 16 * k);
+      Pp[i] = k == ts ? P[i] : Pp[i];
+      Qp[i] = k == ts ? Q[i] : Qp[i];
+      Q[i] = fmaf(Ak, Q[i], Lk);
+      P[i] *= Ak;
+    }
+  }
+  // 3-4. publish and walk back over the later tiles
+  const int io = VEC == 4 ? ts : 0;
+  const bool owner = (VEC == 4 || ts == 0) && dlive && d0 + io < g.D;
+  const float dec_o = VEC == 4 ? pick4(io, dec[0], dec[VEC > 1 ? 1 : 0], dec[VEC > 2 ? 2 : 0], dec[VEC > 3 ? 3 : 0])
+                               : dec[0];
+  const float Po = VEC == 4 ? pick4(io, P[0], P[VEC > 1 ? 1 : 0], P[VEC > 2 ? 2 : 0], P[VEC > 3 ? 3 : 0]) : P[0];
+  const float Qo = VEC == 4 ? pick4(io, Q[0], Q[VEC > 1 ? 1 : 0], Q[VEC > 2 ? 2 : 0], Q[VEC > 3 ? 3 : 0]) : Q[0];
+  float full = 1.f;
+  {
+    float seg = 1.f;
+    for (int t = 0; t < SEG; ++t) seg *= dec_o;
+#pragma unroll
+    for (int k = 0; k < kLbSegs; ++k) full *= seg;
+  }
+  // predecessors: scan-order indices order - 1, ..., 0, i.e. chunks chunk + 1, chunk + 2, ...
+  const float C = owner ? lb_join(g, slice, cg * VEC + io, CT, order, Po, Qo, full) : 0.f;
+  // 5. rescan: lambda from the incoming adjoint, dx = a lambda, dalpha terms
+  float st[VEC], da[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const float Ci = __shfl(C, VEC == 4 ? cg + 16 * i : cg);
+    st[i] = fmaf(Pp[i], Ci, Qp[i]);
+    da[i] = 0.f;
+  }
+  const __amdgpu_buffer_rsrc_t rx = lb_rsrc(x, sxb, sxn, b, g.N);
+  const __amdgpu_buffer_rsrc_t ry = lb_rsrc(y, syb, syn, b, g.N);
+  const __amdgpu_buffer_rsrc_t rd = lb_rsrc(dx, sdb, sdn, b, g.N);
+  const uint32_t rsx = static_cast<uint32_t>(sxn * sizeof(T)), cox = static_cast<uint32_t>(d0 * sizeof(T));
+  const uint32_t rsy = static_cast<uint32_t>(syn * sizeof(T)), coy = static_cast<uint32_t>(d0 * sizeof(T));
+  const uint32_t rsd = static_cast<uint32_t>(sdn * sizeof(T)), cod = static_cast<uint32_t>(d0 * sizeof(T));
+#pragma unroll
+  for (int tb = SEG - 1; tb >= 0; tb -= R) {
+    LbRaw<T, VEC> xr[R], yr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int t = tb - r;
+      const bool ok = t < len && dlive;
+      xr[r].load(rx, ok ? static_cast<uint32_t>(s0 + t) * rsx + cox : kOutOfRange);
+      // y[t - 1]; before token 0 the state is zero (the offset wraps out of range)
+      yr[r].load(ry, ok && s0 + t > 0 ? static_cast<uint32_t>(s0 + t - 1) * rsy + coy : kOutOfRange);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int t = tb - r;
+      if (t < len) {
+        float xv[VEC], yp[VEC], gv[VEC];
+        xr[r].widen(xv);
+        yr[r].widen(yp);
+        raw[t].widen(gv);
+        if constexpr (RESET) {
+          if (s0 + t + 1 < g.N && lb_reset(g, b, s0 + t + 1)) {   // cut from the future (or the carry)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) st[i] = 0.f;
+          }
+          if (lb_reset(g, b, s0 + t)) {   // y[t-1] does not feed token t (ema:445-448)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) yp[i] = 0.f;
+          }
+        }
+        float out[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          st[i] = fmaf(dec[i], st[i], gv[i]);
+          out[i] = a[i] * st[i];
+          da[i] = fmaf(st[i], xv[i] - yp[i], da[i]);
+        }
+        lb_store<T, VEC>(rd, dlive ? static_cast<uint32_t>(s0 + t) * rsd + cod : kOutOfRange, out);
+      }
+    }
+  }
+  // the tile's dalpha partial of each channel: its four segments in time order
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kLbSegs; ++k) s += __shfl(da[i], cg + 16 * k);
+    if (ts == 0 && dlive && d0 + i < g.D)
+      g.da_part[(static_cast<int64_t>(chunk) * g.B + b) * g.D + d0 + i] = s;
+  }
+}
+
+// Clears the look-back words of the next scan.
+__global__ __launch_bounds__(kEmaBlock) void ema_lb_zero(uint4* __restrict__ p, int64_t n16) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEmaBlock + threadIdx.x; i < n16;
+       i += static_cast<int64_t>(gridDim.x) * kEmaBlock)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Look-back plan: channel blocks, tiles along time, bytes of words.
+struct LbPlan {
+  int CB, NCH, S;
+  size_t words_bytes;   // aggregates and the runs' inclusive states
+};
+
+inline LbPlan lb_plan(int B, int N, int D, int vec, int seg) {
+  LbPlan p;
+  const int ct = kLbGroups * vec;
+  p.CB = (D + ct - 1) / ct;
+  p.NCH = (N + kLbSegs * seg - 1) / (kLbSegs * seg);
+  p.S = B * p.CB;
+  const int runs = (p.NCH + kLbRun - 1) / kLbRun;
+  p.words_bytes = static_cast<size_t>(p.NCH + runs) * p.S * ct * 8;
+  return p;
+}
+
+inline size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Workspace of the look-back scans: a zero head, the words and, backward,
+// the dalpha partials [NCH][B][D] and D channel sums.
+inline size_t lb_workspace(int B, int N, int D, bool backward) {
+  const LbPlan p = lb_plan(B, N, D, D % 4 == 0 ? 4 : 1, kLbSeg);
+  size_t n = kLbHead + round256(p.words_bytes);
+  if (backward) n += round256(static_cast<size_t>(p.NCH) * B * D * 4) + round256(static_cast<size_t>(D) * 4);
+  return n;
+}
+
+// Every [N][D] slab of these tensors within 32-bit buffer offsets.
+inline bool lb_fits(int N, int64_t sn, size_t elem) {
+  return static_cast<int64_t>(N) * sn * static_cast<int64_t>(elem) < (int64_t(1) << 31);
+}
+
+template <typename T, int VEC>
+LbGeom lb_geom(int B, int N, int D, int per_channel, float lo, float hi, const uint8_t* reset, const int64_t* rs,
+               void* ws, int wait_limit, bool backward, LbPlan* plan) {
+  const LbPlan p = lb_plan(B, N, D, VEC, kLbSeg);
+  LbGeom g;
+  g.B = B; g.N = N; g.D = D;
+  g.CB = p.CB; g.NCH = p.NCH; g.S = p.S;
+  g.per_channel = per_channel;
+  g.lo = lo; g.hi = hi;
+  g.reset = reset;
+  g.srb = reset ? rs[0] : 0;
+  g.srn = reset ? rs[1] : 0;
+  char* w = static_cast<char*>(ws);
+  g.words = reinterpret_cast<unsigned long long*>(w + kLbHead);
+  g.runs = g.words + static_cast<int64_t>(p.NCH) * p.S * kLbGroups * VEC;
+  g.da_part = backward ? reinterpret_cast<float*>(w + kLbHead + round256(p.words_bytes)) : nullptr;
+  g.wait_limit = wait_limit > 0 ? wait_limit : kLbWaitLimit;
+  *plan = p;
+  return g;
+}
+
+// The zeroing launch ahead of a scan: the words.
+inline void lb_zero(const LbGeom& g, const LbPlan& p, hipStream_t stream) {
+  const int64_t n16 = static_cast<int64_t>(p.words_bytes / 16);
+  const int blocks = static_cast<int>((n16 + kEmaBlock - 1) / kEmaBlock < 64 ? (n16 + kEmaBlock - 1) / kEmaBlock : 64);
+  hipLaunchKernelGGL(ema_lb_zero, dim3(blocks), dim3(kEmaBlock), 0, stream, reinterpret_cast<uint4*>(g.words), n16);
+}
+
 template <typename T, int VEC, bool RESET>
 hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
+  const T* x = static_cast<const T*>(a.x);
+  T* y = static_cast<T*>(a.y);
+  if (lb_fits(a.N, a.x_stride[1], sizeof(T)) && lb_fits(a.N, a.y_stride[1], sizeof(T))) {
+    LbPlan p;
+    const LbGeom g = lb_geom<T, VEC>(a.B, a.N, a.D, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
+                                     a.reset_stride, a.workspace, a.wait_limit, false, &p);
+    lb_zero(g, p, stream);
+    hipLaunchKernelGGL((ema_fwd_lb<T, VEC, RESET>), dim3(p.NCH * p.S), dim3(kWave), 0, stream, x, a.x_stride[0],
+                       a.x_stride[1], y, a.y_stride[0], a.y_stride[1], a.alpha, g);
+    return hipGetLastError();
+  }
+  // three-stage chunked scan (local, carry, apply) for larger slabs
   const size_t nf = ws_floats(a.B, a.N, a.D);
   const EmaGeom g = make_geom(a.B, a.N, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
                               a.reset_stride, a.workspace, 2 * nf);
@@ -245,8 +785,6 @@ hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
   float* carries = ends + nf;
   const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
-  const T* x = static_cast<const T*>(a.x);
-  T* y = static_cast<T*>(a.y);
   hipLaunchKernelGGL((ema_fwd_local<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
                      a.x_stride[1], a.alpha, ends, g);
   launch_carry<false, RESET>(ends, carries, a.alpha, g, a.B, a.D, stream);
@@ -255,8 +793,43 @@ hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// dalpha from per-row partials [rows][D] (rows = B * nc): per channel, or summed over the channels.
+inline void launch_dalpha(const float* da_part, const float* alpha, float* dalpha, float* chan, const EmaGeom& g,
+                          int per_channel, int D, hipStream_t stream) {
+  const int rb = (D + kDaChannels - 1) / kDaChannels;
+  if (per_channel) {
+    hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kWave * kCarryWaves), 0, stream, da_part, alpha, dalpha,
+                       g);
+  } else {
+    hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kWave * kCarryWaves), 0, stream, da_part, alpha, chan, g);
+    hipLaunchKernelGGL(ema_dalpha_scalar, dim3(1), dim3(kWave), 0, stream, chan, alpha, dalpha, g);
+  }
+}
+
 template <typename T, int VEC, bool RESET>
 hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
+  const T* x = static_cast<const T*>(a.x);
+  const T* y = static_cast<const T*>(a.y);
+  const T* dy = static_cast<const T*>(a.dy);
+  T* dx = static_cast<T*>(a.dx);
+  if (lb_fits(a.N, a.x_stride[1], sizeof(T)) && lb_fits(a.N, a.y_stride[1], sizeof(T)) &&
+      lb_fits(a.N, a.dy_stride[1], sizeof(T)) && lb_fits(a.N, a.dx_stride[1], sizeof(T))) {
+    LbPlan p;
+    const LbGeom g = lb_geom<T, VEC>(a.B, a.N, a.D, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
+                                     a.reset_stride, a.workspace, a.wait_limit, true, &p);
+    lb_zero(g, p, stream);
+    hipLaunchKernelGGL((ema_bwd_lb<T, VEC, RESET>), dim3(p.NCH * p.S), dim3(kWave), 0, stream, x, a.x_stride[0],
+                       a.x_stride[1], y, a.y_stride[0], a.y_stride[1], dy, a.dy_stride[0], a.dy_stride[1], dx,
+                       a.dx_stride[0], a.dx_stride[1], a.alpha, g);
+    if (a.dalpha) {
+      // the partials' rows are (chunk, b): the reduction's geometry with NC = NCH
+      EmaGeom eg = make_geom(a.B, p.NCH * kChunkT, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling, nullptr,
+                             nullptr, a.workspace, 0);
+      float* chan = g.da_part + round256(static_cast<size_t>(p.NCH) * a.B * a.D * 4) / 4;
+      launch_dalpha(g.da_part, a.alpha, a.dalpha, chan, eg, a.alpha_per_channel, a.D, stream);
+    }
+    return hipGetLastError();
+  }
   const size_t nf = ws_floats(a.B, a.N, a.D);
   const EmaGeom g = make_geom(a.B, a.N, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
                               a.reset_stride, a.workspace, 3 * nf);
@@ -265,35 +838,27 @@ hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
   float* da_part = carries + nf;
   const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
-  hipLaunchKernelGGL((ema_bwd_local<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream,
-                     static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1], a.alpha, starts, g);
+  hipLaunchKernelGGL((ema_bwd_local<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream, dy, a.dy_stride[0],
+                     a.dy_stride[1], a.alpha, starts, g);
   launch_carry<true, RESET>(starts, carries, a.alpha, g, a.B, a.D, stream);
-  hipLaunchKernelGGL((ema_bwd_apply<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream,
-                     static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<const T*>(a.y),
-                     a.y_stride[0], a.y_stride[1], static_cast<const T*>(a.dy), a.dy_stride[0], a.dy_stride[1],
-                     static_cast<T*>(a.dx), a.dx_stride[0], a.dx_stride[1], a.alpha, carries, da_part, g);
-  if (a.dalpha) {
-    const int rb = (a.D + kDaChannels - 1) / kDaChannels;
-    if (a.alpha_per_channel) {
-      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kWave * kCarryWaves), 0, stream, da_part, a.alpha,
-                         a.dalpha, g);
-    } else {
-      float* chan = starts;   // free after the apply stage; D <= B * NC * D floats
-      hipLaunchKernelGGL(ema_dalpha_channels, dim3(rb), dim3(kWave * kCarryWaves), 0, stream, da_part, a.alpha,
-                         chan, g);
-      hipLaunchKernelGGL(ema_dalpha_scalar, dim3(1), dim3(kWave), 0, stream, chan, a.alpha, a.dalpha, g);
-    }
-  }
+  hipLaunchKernelGGL((ema_bwd_apply<T, VEC, RESET>), dim3(blocks), dim3(kEmaBlock), 0, stream, x, a.x_stride[0],
+                     a.x_stride[1], y, a.y_stride[0], a.y_stride[1], dy, a.dy_stride[0], a.dy_stride[1], dx,
+                     a.dx_stride[0], a.dx_stride[1], a.alpha, carries, da_part, g);
+  if (a.dalpha) launch_dalpha(da_part, a.alpha, a.dalpha, starts, g, a.alpha_per_channel, a.D, stream);
   return hipGetLastError();
 }
 
 }  // namespace
 
 size_t ema_fwd_workspace(int B, int N, int D) {
-  return 2 * ws_floats(B, N, D) * sizeof(float) + ws_cut_bytes(B, N);
+  const size_t chunked = 2 * ws_floats(B, N, D) * sizeof(float) + ws_cut_bytes(B, N);
+  const size_t lb = lb_workspace(B, N, D, false);
+  return chunked > lb ? chunked : lb;
 }
 size_t ema_bwd_workspace(int B, int N, int D) {
-  return 3 * ws_floats(B, N, D) * sizeof(float) + ws_cut_bytes(B, N);
+  const size_t chunked = 3 * ws_floats(B, N, D) * sizeof(float) + ws_cut_bytes(B, N);
+  const size_t lb = lb_workspace(B, N, D, true);
+  return chunked > lb ? chunked : lb;
 }
 
 template <bool RESET>

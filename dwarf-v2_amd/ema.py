@@ -75,8 +75,9 @@ def _set_reset(a, reset: torch.Tensor | None) -> None:
 
 
 def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: float,
-                reset: torch.Tensor | None = None) -> torch.Tensor:
-    """Raw launch: y with x's dtype.  alpha fp32 on x's device, numel 1 or D; reset [B,N] bool or None."""
+                reset: torch.Tensor | None = None, *, wait_limit: int = 0) -> torch.Tensor:
+    """Raw launch: y with x's dtype.  alpha fp32 on x's device, numel 1 or D; reset [B,N] bool or None.
+    wait_limit: polls before a look-back wait gives up (its channel's tile then holds NaN); 0: the default."""
     lib = _lib.load()
     B, N, D = x.shape
     y = torch.empty((B, N, D), device=x.device, dtype=x.dtype)
@@ -88,6 +89,7 @@ def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: flo
     a.x, a.x_stride = x.data_ptr(), _lib.i64_array(x.stride())
     a.alpha = alpha.data_ptr()
     a.y, a.y_stride = y.data_ptr(), _lib.i64_array(y.stride())
+    a.wait_limit = int(wait_limit)
     _set_reset(a, reset)
     ws = torch.empty(max(int(lib.dwarf_ema_fwd_workspace_bytes(ctypes.byref(a))), 16), device=x.device,
                      dtype=torch.uint8)
@@ -96,8 +98,10 @@ def ema_forward(x: torch.Tensor, alpha: torch.Tensor, floor: float, ceiling: flo
     return y
 
 
-def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool, reset: torch.Tensor | None = None):
-    """Raw launch: (dx, dalpha or None); dalpha already clamp-projected; reset as in ema_forward."""
+def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool, reset: torch.Tensor | None = None, *,
+                 wait_limit: int = 0):
+    """Raw launch: (dx, dalpha or None); dalpha already clamp-projected; reset and wait_limit as in
+    ema_forward."""
     lib = _lib.load()
     B, N, D = x.shape
     dy = _btd(dy.to(x.dtype))
@@ -114,6 +118,7 @@ def ema_backward(x, y, dy, alpha, floor, ceiling, need_dalpha: bool, reset: torc
     a.alpha = alpha.data_ptr()
     a.dx, a.dx_stride = dx.data_ptr(), _lib.i64_array(dx.stride())
     a.dalpha = dalpha.data_ptr() if dalpha is not None else None
+    a.wait_limit = int(wait_limit)
     _set_reset(a, reset)
     ws = torch.empty(max(int(lib.dwarf_ema_bwd_workspace_bytes(ctypes.byref(a))), 16), device=x.device,
                      dtype=torch.uint8)

@@ -227,12 +227,20 @@ typedef struct {
   void* y; int64_t y_stride[3];
   void* workspace; size_t workspace_bytes;
   const uint8_t* reset; int64_t reset_stride[2];  /* [B,N] bool (1 byte), or NULL */
+  int32_t wait_limit;     /* polls before a look-back wait gives up (0: the default, 1 << 22) */
 } dwarf_ema_fwd_args;
 
 size_t dwarf_ema_fwd_workspace_bytes(const dwarf_ema_fwd_args* args);
 
 /* Replaces _CausalEMAFn.forward's three launches (ema:265-313) and, with
- * reset flags, _CausalEMAResetFn.forward's serial launch (ema:455-476). */
+ * reset flags, _CausalEMAResetFn.forward's serial launch (ema:455-476).
+ * Where each [N][D] slab of x and y spans less than 2 GiB the scan is one
+ * pass with decoupled look-back (a zeroing launch, then the scan): each
+ * 4-segment tile of tokens publishes its chunk state in the workspace and
+ * waits for those of the tiles before it, at most wait_limit polls per
+ * wait; a wait that gives up writes NaN for its channel's tile instead of
+ * hanging.  Larger slabs take a three-stage chunked scan.  Calls that share
+ * a workspace must not overlap. */
 int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream);
 
 /*
@@ -253,12 +261,15 @@ typedef struct {
   float* dalpha;
   void* workspace; size_t workspace_bytes;
   const uint8_t* reset; int64_t reset_stride[2];  /* the forward's reset flags, or NULL */
+  int32_t wait_limit;     /* as in dwarf_ema_fwd_args */
 } dwarf_ema_bwd_args;
 
 size_t dwarf_ema_bwd_workspace_bytes(const dwarf_ema_bwd_args* args);
 
 /* Replaces _CausalEMAFn.backward's three launches (ema:315-364) and, with
- * reset flags, _CausalEMAResetFn.backward's serial launch (ema:478-509). */
+ * reset flags, _CausalEMAResetFn.backward's serial launch (ema:478-509).
+ * The same scan in reverse time (look-back or three-stage), then the
+ * fixed-order dalpha reduction. */
 int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream);
 
 /* ------------------------------------------------------------------------ */

@@ -157,7 +157,8 @@ def run_reset(pkg, x, alpha, dy, reset, device):
 def reset_pattern(B, N, g, kind):
     r = torch.zeros(B, N, dtype=torch.bool)
     if kind == "chunk_edges":      # at chunk starts, chunk ends, the first and last token, back to back
-        for t in (0, 15, 16, 17, 31, 32, 33, 47, 48, N - 1):
+        # (the three-stage scan's 16-token chunks; the look-back scan's 32/64-token segments and 128/256-token tiles)
+        for t in (0, 15, 16, 17, 31, 32, 33, 47, 48, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 512, N - 1):
             if t < N:
                 r[:, t] = True
     else:
@@ -211,3 +212,65 @@ def test_empty_sequence(pkg, device, per_channel):
     y.float().sum().backward()
     torch.cuda.synchronize()
     assert x.grad.shape == (2, 0, 8) and torch.equal(a.grad.cpu(), torch.zeros(a.shape))
+
+
+@pytest.mark.parametrize("B,N,D,per_channel,kind", [(2, 10000, 20, True, None), (1, 9000, 7, False, None),
+                                                    (2, 9100, 12, True, "random"), (3, 4200, 64, False, "chunk_edges")])
+def test_lookback_runs_fp32(pkg, device, B, N, D, per_channel, kind):
+    """Sequences long enough for several runs of 32 look-back tiles (fp32 tiles hold 128 tokens: N = 10000 is
+    79 tiles, 3 runs), channel blocks cut by D (20, 12: one partial 64-channel block; 7: the one-channel
+    lanes), with and without resets: y, dx, dalpha within 1e-5 relative of the float64 oracle."""
+    g = torch.Generator().manual_seed(N + D + 7)
+    x = torch.randn(B, N, D, generator=g)
+    alpha = torch.rand(D if per_channel else 1, generator=g) * 0.2 + 0.01
+    dy = torch.randn(B, N, D, generator=g)
+    reset = None if kind is None else reset_pattern(B, N, g, kind)
+    if reset is None:
+        y, dx, da = run(pkg, x, alpha, dy, device)
+    else:
+        y, dx, da = run_reset(pkg, x, alpha, dy, reset, device)
+    ry = ema_ref.ema_scan(x.double(), alpha.double(), reset_mask=reset)
+    rdx, rda = ema_ref.ema_adjoint(x.double(), ry, dy.double(), alpha.double(), reset_mask=reset)
+    assert rel_err(y, ry) < 1e-5
+    assert rel_err(dx, rdx) < 1e-5
+    assert rel_err(da, rda) < 1e-5
+
+
+def test_lookback_is_deterministic(pkg, device):
+    """The look-back scan forms each tile's incoming state from the published aggregates in a fixed order,
+    so y, dx and dalpha are the same bits on every call, whatever order the tiles ran in (bf16, 3 runs)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 20000, 256, generator=g).to(torch.bfloat16).to(device)
+    alpha = (0.01 + 0.2 * torch.rand(256, generator=g)).to(device)
+    dy = torch.randn(2, 20000, 256, generator=g).to(torch.bfloat16).to(device)
+    ema = pkg.ema if hasattr(pkg, "ema") else __import__("importlib").import_module("dwarf-v2_amd.ema")
+    first = None
+    for _ in range(4):
+        y = ema.ema_forward(x, alpha, 1e-5, 0.5)
+        dx, da = ema.ema_backward(x, y, dy, alpha, 1e-5, 0.5, True)
+        torch.cuda.synchronize()
+        if first is None:
+            first = (y, dx, da)
+        else:
+            assert torch.equal(y, first[0]) and torch.equal(dx, first[1]) and torch.equal(da, first[2])
+
+
+def test_wait_limit_gives_up_without_hanging(pkg, device):
+    """A look-back wait is bounded by wait_limit polls.  Forced from the host to one poll, a tile whose
+    predecessors have not published yet gives up and writes NaN for that channel's tile instead of waiting;
+    the call still returns, and every value that is not NaN is the value of the unbounded call."""
+    import importlib
+
+    ema = importlib.import_module("dwarf-v2_amd.ema")
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(4, 16384, 512, generator=g).to(torch.bfloat16).to(device)
+    alpha = (0.01 + 0.2 * torch.rand(512, generator=g)).to(device)
+    dy = torch.randn(4, 16384, 512, generator=g).to(torch.bfloat16).to(device)
+    y_ref = ema.ema_forward(x, alpha, 1e-5, 0.5)
+    dx_ref, _ = ema.ema_backward(x, y_ref, dy, alpha, 1e-5, 0.5, True)
+    y = ema.ema_forward(x, alpha, 1e-5, 0.5, wait_limit=1)
+    dx, _ = ema.ema_backward(x, y_ref, dy, alpha, 1e-5, 0.5, True, wait_limit=1)
+    torch.cuda.synchronize()
+    for got, ref in ((y, y_ref), (dx, dx_ref)):
+        ok = torch.isnan(got) | (got == ref)
+        assert bool(ok.all())
