@@ -243,53 +243,64 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
 // A tile is (b, block of 16 VEC channels, 4 SEG = 128 consecutive tokens),
 // one wave: lane (cg = lane & 15, ts = lane >> 4) holds channels
 // [16 VEC cb + VEC cg, +VEC) of tokens [s0, s0 + SEG), s0 = 4 SEG chunk +
-// SEG ts, loaded once into registers.  (64-token segments keep twice the rows
+// SEG ts, loaded once into registers.  A workgroup takes kLbWaves tiles that
+// follow each other in scan order.  (64-token segments keep twice the rows
 // per lane and half the waves: 5 us slower at [4, 8192, 512]; 16-token
-// segments give more, shorter waits: 15 us slower.)  The wave
+// segments give more, shorter waits: 15 us slower.)  Each wave
 //   1. scans each lane's segment from a zero state: its end L and its
 //      transfer factor A = decay^len (0 when a reset falls inside);
 //   2. composes the four segments of a channel in time order into the tile's
 //      (P, Q), state after the tile = P s + Q, and each lane's prefix;
-//   3. publishes Q as the tile's aggregate, tagged with its factor: tag 1
-//      for P = decay^(4 SEG), tag 3 for P = 0 (a reset inside, or a factor
+// then the workgroup (lb_join)
+//   3. composes its tiles' maps in LDS into the workgroup's (P, Q) and
+//      publishes Q as its aggregate, tagged with its factor: tag 1 for a full
+//      workgroup's decay^(512), tag 3 for P = 0 (a reset inside, or a factor
 //      below fp32's range);
-//   4. forms the state C entering it from the aggregates of the tiles before
-//      it in a fixed order, C = P_p C + Q_p from the start of its run of
-//      kLbRun tiles, the run entered with the inclusive state the previous
-//      run's last tile publishes (tag 2); every input is published before
-//      its writer waits on anything, so the result is the same bits every run;
-//   5. rescans its segment from its incoming state and writes y.
-// A tile waits only on tiles of lower index (workgroup index), which the
-// hardware dispatches first; the only chain of waits is the runs' inclusive
-// states, and it ends at the first run.  (A counter handing out tile indices
-// in claim order measured 9 us slower at [4, 8192, 512]: one contended atomic
-// per tile.)  A value and its tag share one 64-bit word, written and read as
-// one agent-scope atomic (coherent across the XCDs' L2s without a fence);
-// `ema_lb_zero` clears the words before each scan.  A wait gives up after
-// wait_limit polls and poisons its channel with NaN rather than hang.
-// The backward runs the same scan in reverse time over dy for the adjoint
-// lambda, and in its rescan writes dx and each tile's dalpha partial.
+//   4. forms the state entering it from the aggregates of the workgroups
+//      before it in its run of kLbRun, composed in a fixed order and applied
+//      to the inclusive state the previous run's last workgroup publishes
+//      (tag 2); every input is published before its writer waits on anything,
+//      so the result is the same bits every run; each wave composes its own
+//      incoming state from that and the earlier tiles of its workgroup;
+// and each wave
+//   5. rescans its segments from their incoming states and writes y.
+// A workgroup waits only on workgroups of lower index, which the hardware
+// dispatches first; the only chain of waits is the runs' inclusive states,
+// and it ends at the first run.  Four tiles to a workgroup cut the look-back
+// walk fourfold (at [4, 8192, 512] one run of 16 workgroups per slice):
+// 18.2 / 30.4 us forward / backward against 23.2 / 32.4 with one tile to a
+// workgroup; two or eight tiles measured 20.3 / 32.2 and 18.2 / 31.3.  (A
+// counter handing out tile indices in claim order measured 9 us slower: one
+// contended atomic per tile.)  A value and its tag share one 64-bit word,
+// written and read as one agent-scope atomic (coherent across the XCDs' L2s
+// without a fence); `ema_lb_zero` clears the words before each scan.  A wait
+// gives up after wait_limit polls and poisons its channel with NaN rather
+// than hang.  The backward runs the same scan in reverse time over dy for
+// the adjoint lambda, and in its rescan writes dx and each workgroup's dalpha
+// partial.
 // ---------------------------------------------------------------------------
 constexpr int kLbGroups = 16;   // channel groups of a tile (lanes cg)
 constexpr int kLbSegs = 4;      // token segments of a tile (lanes ts)
 constexpr int kLbSeg = 32;                         // tokens per segment (the lane's registers)
 constexpr int kLbWaitLimit = 1 << 22;              // default polls before a wait gives up
 constexpr size_t kLbHead = 256;                    // bytes ahead of the words (unused, kept zero)
-constexpr int kLbRun = 32;                         // tiles per run (one inclusive state per run)
+constexpr int kLbWaves = 4;                        // tiles (one wave each) per workgroup, consecutive in scan order
+constexpr int kLbRun = 32;                         // workgroup tiles per run (one inclusive state per run)
 constexpr int kLbBatch = 8;                        // aggregates loaded together by a carry walk
 
 struct LbGeom {
   int B, N, D;
   int CB;    // channel blocks of 16 VEC channels
   int NCH;   // tiles along time per (b, channel block)
+  int NWG;   // workgroup tiles along time, ceil(NCH / kLbWaves)
   int S;     // (b, channel block) slices, B * CB
   int per_channel;
   float lo, hi;
   const uint8_t* reset;
   int64_t srb, srn;
-  unsigned long long* words;   // [NCH * S][16 VEC]: aggregates, (value bits, tag << 32)
-  unsigned long long* runs;    // [ceil(NCH / kLbRun) * S][16 VEC]: the runs' inclusive states
-  float* da_part;              // backward: [NCH][B][D] dalpha partials (row chunk * B + b)
+  unsigned long long* words;   // [NWG * S][16 VEC]: workgroup aggregates, (value bits, tag << 32)
+  unsigned long long* runs;    // [ceil(NWG / kLbRun) * S][16 VEC]: the runs' inclusive states
+  float* da_part;              // backward: [NWG][B][D] dalpha partials (row widx * B + b)
   int wait_limit;
 };
 
@@ -374,20 +385,15 @@ __device__ __forceinline__ unsigned long long lb_wait(const unsigned long long* 
   return 0;
 }
 
-// The state entering the tile at scan-order index idx of its slice: the
-// previous run's inclusive state (0 in the first run), then the aggregates of
-// the run's tiles before it in order, C = P_p C + Q_p (P_p = full for tag 1,
-// 0 for tag 3).  Aggregates are loaded kLbBatch at a time.  NaN when a wait
-// gives up.
+// The state entering the workgroup tile at scan-order index idx of its slice:
+// the aggregates of the run's tiles before it composed in order into
+// (Pa, Qa) (P_p = full for tag 1, 0 for tag 3), loaded kLbBatch at a time,
+// then applied to the previous run's inclusive state (none in the first run):
+// C = Pa C_run + Qa.  The run's state is waited on last, so the walk over the
+// aggregates overlaps the previous run's.  NaN when a wait gives up.
 __device__ __forceinline__ float lb_carry(const LbGeom& g, int slice, int ch, int ct, int idx, float full) {
   const int run = idx / kLbRun, first = run * kLbRun;
-  float C = 0.f;
-  if (run > 0) {
-    const unsigned long long x = lb_wait(g.runs + (static_cast<int64_t>(run - 1) * g.S + slice) * ct + ch,
-                                         g.wait_limit);
-    if (!x) return __builtin_nanf("");
-    C = __uint_as_float(static_cast<uint32_t>(x));
-  }
+  float Pa = 1.f, Qa = 0.f;
   for (int p0 = first; p0 < idx; p0 += kLbBatch) {
     unsigned long long w[kLbBatch];
 #pragma unroll
@@ -405,35 +411,74 @@ __device__ __forceinline__ float lb_carry(const LbGeom& g, int slice, int ch, in
           x = lb_wait(g.words + (static_cast<int64_t>(p) * g.S + slice) * ct + ch, g.wait_limit);
           if (!x) return __builtin_nanf("");
         }
-        C = fmaf((x >> 32) == 3u ? 0.f : full, C, __uint_as_float(static_cast<uint32_t>(x)));
+        const float Pp = (x >> 32) == 3u ? 0.f : full;
+        Qa = fmaf(Pp, Qa, __uint_as_float(static_cast<uint32_t>(x)));
+        Pa *= Pp;
       }
     }
   }
-  return C;
+  if (run == 0) return Qa;
+  const unsigned long long x = lb_wait(g.runs + (static_cast<int64_t>(run - 1) * g.S + slice) * ct + ch,
+                                       g.wait_limit);
+  if (!x) return __builtin_nanf("");
+  return fmaf(Pa, __uint_as_float(static_cast<uint32_t>(x)), Qa);
 }
 
-// Steps 3-4 for the channel a lane owns: publish the aggregate, form the
-// incoming state, and publish the run's inclusive state from its last tile.
-__device__ __forceinline__ float lb_join(const LbGeom& g, int slice, int ch, int ct, int idx, float Po, float Qo,
-                                         float full) {
-  unsigned long long* mine = g.words + (static_cast<int64_t>(idx) * g.S + slice) * ct + ch;
-  lb_publish(mine, Qo, Po == 0.f ? 3u : 1u);
-  const float C = idx > 0 ? lb_carry(g, slice, ch, ct, idx, full) : 0.f;
-  if (idx % kLbRun == kLbRun - 1 && idx + 1 < g.NCH)
-    lb_publish(g.runs + (static_cast<int64_t>(idx / kLbRun) * g.S + slice) * ct + ch, fmaf(Po, C, Qo), 2u);
+// LDS of a workgroup: each wave's tile maps (P, Q) per channel, and the state
+// entering the workgroup.
+struct LbShared {
+  float P[kLbWaves][kWave];
+  float Q[kLbWaves][kWave];
+  float C[kWave];
+};
+
+// Steps 3-4 for channel ch of wave w's tile (owner lanes only take part):
+// the tiles' maps meet in LDS; wave 0 composes them in scan order into the
+// workgroup's (P, Q), publishes Q tagged with its factor, forms the state
+// entering the workgroup from the earlier workgroups (lb_carry; full_wg is a
+// full workgroup's factor) and, in a run's last workgroup, publishes the run's
+// inclusive state; each wave then composes the state entering its own tile
+// from that and the earlier tiles of its workgroup, in order.  Every lane of
+// the workgroup reaches both barriers.
+__device__ __forceinline__ float lb_join(const LbGeom& g, LbShared& sh, int slice, int ch, bool owner, int ct,
+                                         int widx, int w, float Po, float Qo, float full_wg) {
+  if (owner) {
+    sh.P[w][ch] = Po;
+    sh.Q[w][ch] = Qo;
+  }
+  __syncthreads();
+  if (w == 0 && owner) {
+    float P = 1.f, Q = 0.f;
+#pragma unroll
+    for (int j = 0; j < kLbWaves; ++j) {
+      Q = fmaf(sh.P[j][ch], Q, sh.Q[j][ch]);
+      P *= sh.P[j][ch];
+    }
+    lb_publish(g.words + (static_cast<int64_t>(widx) * g.S + slice) * ct + ch, Q, P == 0.f ? 3u : 1u);
+    const float C = widx > 0 ? lb_carry(g, slice, ch, ct, widx, full_wg) : 0.f;
+    if (widx % kLbRun == kLbRun - 1 && widx + 1 < g.NWG)
+      lb_publish(g.runs + (static_cast<int64_t>(widx / kLbRun) * g.S + slice) * ct + ch, fmaf(P, C, Q), 2u);
+    sh.C[ch] = C;
+  }
+  __syncthreads();
+  if (!owner) return 0.f;
+  float C = sh.C[ch];
+  for (int j = 0; j < w; ++j) C = fmaf(sh.P[j][ch], C, sh.Q[j][ch]);
   return C;
 }
 
 template <typename T, int VEC, bool RESET>
-__global__ __launch_bounds__(kWave) void ema_fwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
+__global__ __launch_bounds__(kWave * kLbWaves) void ema_fwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
                                                      T* __restrict__ y, int64_t syb, int64_t syn,
                                                      const float* __restrict__ alpha, LbGeom g) {
   constexpr int SEG = kLbSeg;
   constexpr int CT = kLbGroups * VEC;   // channels (words) per tile
-  const int lane = threadIdx.x;
+  __shared__ LbShared sh;
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int cg = lane & 15, ts = lane >> 4;
-  const int id = blockIdx.x;   // tiles of lower index are dispatched first
-  const int chunk = id / g.S, slice = id - chunk * g.S;
+  const int id = blockIdx.x;   // workgroups of lower index are dispatched first
+  const int widx = id / g.S, slice = id - widx * g.S;
+  const int chunk = widx * kLbWaves + w;   // a chunk past the last holds no tokens
   const int b = slice / g.CB, cb = slice - b * g.CB;
   const int d0 = (cb * kLbGroups + cg) * VEC;
   const bool dlive = d0 < g.D;
@@ -509,7 +554,10 @@ __global__ __launch_bounds__(kWave) void ema_fwd_lb(const T* __restrict__ x, int
 #pragma unroll
     for (int k = 0; k < kLbSegs; ++k) full *= seg;
   }
-  const float C = owner ? lb_join(g, slice, cg * VEC + io, CT, chunk, Po, Qo, full) : 0.f;
+  float full_wg = 1.f;   // a full workgroup's factor, composed as wave 0 composes the tiles
+#pragma unroll
+  for (int j = 0; j < kLbWaves; ++j) full_wg *= full;
+  const float C = lb_join(g, sh, slice, cg * VEC + io, owner, CT, widx, w, Po, Qo, full_wg);
   // 5. incoming state of each channel of this lane's segment, then the rescan
   float st[VEC];
 #pragma unroll
@@ -538,7 +586,7 @@ __global__ __launch_bounds__(kWave) void ema_fwd_lb(const T* __restrict__ x, int
 }
 
 template <typename T, int VEC, bool RESET>
-__global__ __launch_bounds__(kWave) void ema_bwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
+__global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
                                                      const T* __restrict__ y, int64_t syb, int64_t syn,
                                                      const T* __restrict__ dy, int64_t sgb, int64_t sgn,
                                                      T* __restrict__ dx, int64_t sdb, int64_t sdn,
@@ -546,16 +594,17 @@ __global__ __launch_bounds__(kWave) void ema_bwd_lb(const T* __restrict__ x, int
   constexpr int SEG = kLbSeg;
   constexpr int CT = kLbGroups * VEC;
   constexpr int R = 8;   // rows of x and y loaded per block of the rescan
-  const int lane = threadIdx.x;
+  __shared__ LbShared sh;
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int cg = lane & 15, ts = lane >> 4;
-  const int id = blockIdx.x;   // tiles of lower index are dispatched first
-  const int order = id / g.S, slice = id - order * g.S;   // tiles in reverse time order
-  const int chunk = g.NCH - 1 - order;
+  const int id = blockIdx.x;   // workgroups of lower index are dispatched first
+  const int widx = id / g.S, slice = id - widx * g.S;   // workgroup tiles in reverse time order
+  const int chunk = g.NCH - 1 - (widx * kLbWaves + w);   // a chunk below 0 holds no tokens
   const int b = slice / g.CB, cb = slice - b * g.CB;
   const int d0 = (cb * kLbGroups + cg) * VEC;
   const bool dlive = d0 < g.D;
   const int s0 = (chunk * kLbSegs + ts) * SEG;
-  const int len = max(0, min(SEG, g.N - s0));
+  const int len = chunk < 0 ? 0 : max(0, min(SEG, g.N - s0));
   float a[VEC], dec[VEC];
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
@@ -629,8 +678,11 @@ __global__ __launch_bounds__(kWave) void ema_bwd_lb(const T* __restrict__ x, int
 #pragma unroll
     for (int k = 0; k < kLbSegs; ++k) full *= seg;
   }
-  // predecessors: scan-order indices order - 1, ..., 0, i.e. chunks chunk + 1, chunk + 2, ...
-  const float C = owner ? lb_join(g, slice, cg * VEC + io, CT, order, Po, Qo, full) : 0.f;
+  float full_wg = 1.f;   // a full workgroup's factor, composed as wave 0 composes the tiles
+#pragma unroll
+  for (int j = 0; j < kLbWaves; ++j) full_wg *= full;
+  // predecessors: workgroup tiles widx - 1, ..., 0, i.e. the chunks after this workgroup's
+  const float C = lb_join(g, sh, slice, cg * VEC + io, owner, CT, widx, w, Po, Qo, full_wg);
   // 5. rescan: lambda from the incoming adjoint, dx = a lambda, dalpha terms
   float st[VEC], da[VEC];
 #pragma unroll
@@ -685,14 +737,25 @@ __global__ __launch_bounds__(kWave) void ema_bwd_lb(const T* __restrict__ x, int
       }
     }
   }
-  // the tile's dalpha partial of each channel: its four segments in time order
+  // the workgroup's dalpha partial of each channel: each tile's four segments in time order, then the
+  // tiles in time order (waves kLbWaves - 1, ..., 0; a tile without tokens adds zero)
+  __shared__ float sda[kLbWaves][kWave];
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < kLbSegs; ++k) s += __shfl(da[i], cg + 16 * k);
-    if (ts == 0 && dlive && d0 + i < g.D)
-      g.da_part[(static_cast<int64_t>(chunk) * g.B + b) * g.D + d0 + i] = s;
+    if (ts == 0) sda[w][cg * VEC + i] = s;
+  }
+  __syncthreads();
+  if (w == 0 && ts == 0) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = kLbWaves - 1; j >= 0; --j) s += sda[j][cg * VEC + i];
+      if (dlive && d0 + i < g.D) g.da_part[(static_cast<int64_t>(widx) * g.B + b) * g.D + d0 + i] = s;
+    }
   }
 }
 
@@ -705,7 +768,7 @@ __global__ __launch_bounds__(kEmaBlock) void ema_lb_zero(uint4* __restrict__ p, 
 
 // Look-back plan: channel blocks, tiles along time, bytes of words.
 struct LbPlan {
-  int CB, NCH, S;
+  int CB, NCH, NWG, S;
   size_t words_bytes;   // aggregates and the runs' inclusive states
 };
 
@@ -714,20 +777,21 @@ inline LbPlan lb_plan(int B, int N, int D, int vec, int seg) {
   const int ct = kLbGroups * vec;
   p.CB = (D + ct - 1) / ct;
   p.NCH = (N + kLbSegs * seg - 1) / (kLbSegs * seg);
+  p.NWG = (p.NCH + kLbWaves - 1) / kLbWaves;
   p.S = B * p.CB;
-  const int runs = (p.NCH + kLbRun - 1) / kLbRun;
-  p.words_bytes = static_cast<size_t>(p.NCH + runs) * p.S * ct * 8;
+  const int runs = (p.NWG + kLbRun - 1) / kLbRun;
+  p.words_bytes = static_cast<size_t>(p.NWG + runs) * p.S * ct * 8;
   return p;
 }
 
 inline size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Workspace of the look-back scans: a zero head, the words and, backward,
-// the dalpha partials [NCH][B][D] and D channel sums.
+// the dalpha partials [NWG][B][D] and D channel sums.
 inline size_t lb_workspace(int B, int N, int D, bool backward) {
   const LbPlan p = lb_plan(B, N, D, D % 4 == 0 ? 4 : 1, kLbSeg);
   size_t n = kLbHead + round256(p.words_bytes);
-  if (backward) n += round256(static_cast<size_t>(p.NCH) * B * D * 4) + round256(static_cast<size_t>(D) * 4);
+  if (backward) n += round256(static_cast<size_t>(p.NWG) * B * D * 4) + round256(static_cast<size_t>(D) * 4);
   return n;
 }
 
@@ -742,7 +806,7 @@ LbGeom lb_geom(int B, int N, int D, int per_channel, float lo, float hi, const u
   const LbPlan p = lb_plan(B, N, D, VEC, kLbSeg);
   LbGeom g;
   g.B = B; g.N = N; g.D = D;
-  g.CB = p.CB; g.NCH = p.NCH; g.S = p.S;
+  g.CB = p.CB; g.NCH = p.NCH; g.NWG = p.NWG; g.S = p.S;
   g.per_channel = per_channel;
   g.lo = lo; g.hi = hi;
   g.reset = reset;
@@ -750,7 +814,7 @@ LbGeom lb_geom(int B, int N, int D, int per_channel, float lo, float hi, const u
   g.srn = reset ? rs[1] : 0;
   char* w = static_cast<char*>(ws);
   g.words = reinterpret_cast<unsigned long long*>(w + kLbHead);
-  g.runs = g.words + static_cast<int64_t>(p.NCH) * p.S * kLbGroups * VEC;
+  g.runs = g.words + static_cast<int64_t>(p.NWG) * p.S * kLbGroups * VEC;
   g.da_part = backward ? reinterpret_cast<float*>(w + kLbHead + round256(p.words_bytes)) : nullptr;
   g.wait_limit = wait_limit > 0 ? wait_limit : kLbWaitLimit;
   *plan = p;
@@ -773,7 +837,7 @@ hipError_t ema_fwd_typed(const dwarf_ema_fwd_args& a, hipStream_t stream) {
     const LbGeom g = lb_geom<T, VEC>(a.B, a.N, a.D, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
                                      a.reset_stride, a.workspace, a.wait_limit, false, &p);
     lb_zero(g, p, stream);
-    hipLaunchKernelGGL((ema_fwd_lb<T, VEC, RESET>), dim3(p.NCH * p.S), dim3(kWave), 0, stream, x, a.x_stride[0],
+    hipLaunchKernelGGL((ema_fwd_lb<T, VEC, RESET>), dim3(p.NWG * p.S), dim3(kWave * kLbWaves), 0, stream, x, a.x_stride[0],
                        a.x_stride[1], y, a.y_stride[0], a.y_stride[1], a.alpha, g);
     return hipGetLastError();
   }
@@ -818,14 +882,14 @@ hipError_t ema_bwd_typed(const dwarf_ema_bwd_args& a, hipStream_t stream) {
     const LbGeom g = lb_geom<T, VEC>(a.B, a.N, a.D, a.alpha_per_channel, a.floor_, a.ceiling, a.reset,
                                      a.reset_stride, a.workspace, a.wait_limit, true, &p);
     lb_zero(g, p, stream);
-    hipLaunchKernelGGL((ema_bwd_lb<T, VEC, RESET>), dim3(p.NCH * p.S), dim3(kWave), 0, stream, x, a.x_stride[0],
+    hipLaunchKernelGGL((ema_bwd_lb<T, VEC, RESET>), dim3(p.NWG * p.S), dim3(kWave * kLbWaves), 0, stream, x, a.x_stride[0],
                        a.x_stride[1], y, a.y_stride[0], a.y_stride[1], dy, a.dy_stride[0], a.dy_stride[1], dx,
                        a.dx_stride[0], a.dx_stride[1], a.alpha, g);
     if (a.dalpha) {
-      // the partials' rows are (chunk, b): the reduction's geometry with NC = NCH
-      EmaGeom eg = make_geom(a.B, p.NCH * kChunkT, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling, nullptr,
+      // the partials' rows are (workgroup tile, b): the reduction's geometry with NC = NWG
+      EmaGeom eg = make_geom(a.B, p.NWG * kChunkT, a.D, VEC, a.alpha_per_channel, a.floor_, a.ceiling, nullptr,
                              nullptr, a.workspace, 0);
-      float* chan = g.da_part + round256(static_cast<size_t>(p.NCH) * a.B * a.D * 4) / 4;
+      float* chan = g.da_part + round256(static_cast<size_t>(p.NWG) * a.B * a.D * 4) / 4;
       launch_dalpha(g.da_part, a.alpha, a.dalpha, chan, eg, a.alpha_per_channel, a.D, stream);
     }
     return hipGetLastError();

@@ -236,10 +236,10 @@ size_t dwarf_ema_fwd_workspace_bytes(const dwarf_ema_fwd_args* args);
  * reset flags, _CausalEMAResetFn.forward's serial launch (ema:455-476).
  * Where each [N][D] slab of x and y spans less than 2 GiB the scan is one
  * pass with decoupled look-back (a zeroing launch, then the scan): each
- * 4-segment tile of tokens publishes its chunk state in the workspace and
- * waits for those of the tiles before it, at most wait_limit polls per
- * wait; a wait that gives up writes NaN for its channel's tile instead of
- * hanging.  Larger slabs take a three-stage chunked scan.  Calls that share
+ * workgroup of four 128-token tiles publishes its chunk state in the
+ * workspace and waits for those of the workgroups before it, at most
+ * wait_limit polls per wait; a wait that gives up writes NaN for its
+ * channel's workgroup instead of hanging.  Larger slabs take a three-stage chunked scan.  Calls that share
  * a workspace must not overlap. */
 int dwarf_ema_fwd(const dwarf_ema_fwd_args* args, dwarf_stream_t stream);
 

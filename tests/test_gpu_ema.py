@@ -214,12 +214,13 @@ def test_empty_sequence(pkg, device, per_channel):
     assert x.grad.shape == (2, 0, 8) and torch.equal(a.grad.cpu(), torch.zeros(a.shape))
 
 
-@pytest.mark.parametrize("B,N,D,per_channel,kind", [(2, 10000, 20, True, None), (1, 9000, 7, False, None),
-                                                    (2, 9100, 12, True, "random"), (3, 4200, 64, False, "chunk_edges")])
+@pytest.mark.parametrize("B,N,D,per_channel,kind", [(2, 40000, 20, True, None), (1, 36000, 7, False, None),
+                                                    (2, 36100, 12, True, "random"), (3, 17000, 64, False, "chunk_edges")])
 def test_lookback_runs_fp32(pkg, device, B, N, D, per_channel, kind):
-    """Sequences long enough for several runs of 32 look-back tiles (fp32 tiles hold 128 tokens: N = 10000 is
-    79 tiles, 3 runs), channel blocks cut by D (20, 12: one partial 64-channel block; 7: the one-channel
-    lanes), with and without resets: y, dx, dalpha within 1e-5 relative of the float64 oracle."""
+    """Sequences long enough for several runs of 32 look-back workgroups (a workgroup takes four 128-token
+    tiles: N = 40000 is 313 tiles in 79 workgroups, 3 runs, the last workgroup with one tile and three
+    without tokens; 17000: 2 runs), channel blocks cut by D (20, 12: one partial 64-channel block; 7: the
+    one-channel lanes), with and without resets: y, dx, dalpha within 1e-5 relative of the float64 oracle."""
     g = torch.Generator().manual_seed(N + D + 7)
     x = torch.randn(B, N, D, generator=g)
     alpha = torch.rand(D if per_channel else 1, generator=g) * 0.2 + 0.01
@@ -238,11 +239,12 @@ def test_lookback_runs_fp32(pkg, device, B, N, D, per_channel, kind):
 
 def test_lookback_is_deterministic(pkg, device):
     """The look-back scan forms each tile's incoming state from the published aggregates in a fixed order,
-    so y, dx and dalpha are the same bits on every call, whatever order the tiles ran in (bf16, 3 runs)."""
+    so y, dx and dalpha are the same bits on every call, whatever order the workgroups ran in (bf16, 3 runs
+    of 32 workgroups)."""
     g = torch.Generator().manual_seed(5)
-    x = torch.randn(2, 20000, 256, generator=g).to(torch.bfloat16).to(device)
+    x = torch.randn(2, 40000, 256, generator=g).to(torch.bfloat16).to(device)
     alpha = (0.01 + 0.2 * torch.rand(256, generator=g)).to(device)
-    dy = torch.randn(2, 20000, 256, generator=g).to(torch.bfloat16).to(device)
+    dy = torch.randn(2, 40000, 256, generator=g).to(torch.bfloat16).to(device)
     ema = pkg.ema if hasattr(pkg, "ema") else __import__("importlib").import_module("dwarf-v2_amd.ema")
     first = None
     for _ in range(4):
@@ -256,8 +258,8 @@ def test_lookback_is_deterministic(pkg, device):
 
 
 def test_wait_limit_gives_up_without_hanging(pkg, device):
-    """A look-back wait is bounded by wait_limit polls.  Forced from the host to one poll, a tile whose
-    predecessors have not published yet gives up and writes NaN for that channel's tile instead of waiting;
+    """A look-back wait is bounded by wait_limit polls.  Forced from the host to one poll, a workgroup whose
+    predecessors have not published yet gives up and writes NaN for that channel's tiles instead of waiting;
     the call still returns, and every value that is not NaN is the value of the unbounded call."""
     import importlib
 
