@@ -583,7 +583,7 @@ hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace&
 // ---------------------------------------------------------------------------
 // Fixed-order reduction of the parameter-gradient partials.
 // ---------------------------------------------------------------------------
-constexpr int kRedRows = 16;  // rows summed per stage-1 group
+constexpr int kRedRows = 64;  // rows summed per stage-1 group (16 rows: the step 3-4 us longer at B15 H8 T2048)
 
 struct RedArray {
   const float* in;   // [nseg * rows][cols]
@@ -700,11 +700,12 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
     // accumulate dSE in their own slots (dPB partials per tile).
     w.dq_tpw = 0;
     w.dq_ntg = 0;
-    // beside a concurrent dK/dV launch (the delta stage) the dQ launch takes three workgroups per two CUs
-    // and leaves the rest to dK/dV, the longer of the two streams: at B15 H8 T2048 the step measured
-    // 0.556 ms with 384 workgroups against 0.572 with 512 (352: 0.578, 448: 0.565, 256: 0.626), at
-    // B4 H8 T8192 0.871 against 0.880
-    const int gather_max = (f.schedule & DWARF_SCHED_DELTA_STAGE) ? 256 * 3 / 2 : 256 * dq_gather_wgs_per_cu();
+    // beside a concurrent dK/dV launch (the delta stage) the dQ launch takes 400 workgroups (50 per XCD,
+    // about three per two CUs) and leaves the rest to dK/dV, so that the two streams end together: at
+    // B15 H8 T2048 the step measured 0.550-0.552 ms with 400 workgroups, 0.556 with 384 and 0.572 with 512
+    // (352: 0.578, 416: 0.557-0.561, 448: 0.565, 256: 0.626); at B4 H8 T8192 0.871-0.873 with 384 or 400
+    // against 0.880
+    const int gather_max = (f.schedule & DWARF_SCHED_DELTA_STAGE) ? 400 : 256 * dq_gather_wgs_per_cu();
     w.dq_gather_wgs = total_tiles < gather_max ? total_tiles : gather_max;
     const int dse_max = 256 * dq_dse_wgs_per_cu(f.J);
     w.dq_wgs = total_tiles < dse_max ? (total_tiles > 0 ? total_tiles : 1) : dse_max;

@@ -128,8 +128,9 @@ typedef struct {
  *     _fwd_v18_grouped dsqg:863-1044).
  *   DWARF_SCHED_DELTA_STAGE: the backward's (delta, lse) pairs come from
  *     dwarf_dsqg_bwd_delta (bf16): the dQ launch forms delta for itself but
- *     does not write the pairs, and runs three workgroups per two CUs so
- *     that a dK/dV launch on another stream can run beside it (the overlapped
+ *     does not write the pairs, and runs 400 persistent workgroups (about
+ *     three per two CUs) so that a dK/dV launch on another stream can run
+ *     beside it (the overlapped
  *     backward: delta then dK/dV on one stream, dQ then params on another).
  *     dwarf_dsqg_bwd, which runs every stage on one stream, then launches the
  *     delta stage first by itself.
