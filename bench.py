@@ -648,7 +648,7 @@ def main() -> int:
         log("q6 prefill: B20 H8 T2048")
         extra["q6_prefill"] = q6_prefill_extra(pkg, device, args.steps, args.warmup)
         log("long context: B4 T8192 DSQG fwd+bwd + EMA fwd+bwd")
-        extra["long_context"] = long_context_extra(pkg, device, max(3, args.steps // 4), 2)
+        extra["long_context"] = long_context_extra(pkg, device, args.steps, args.warmup)
         log("phase-probe features: q of the training microbatch")
         extra["phase_probe"] = phase_probe_extra(pkg, device, args.steps, args.warmup)
         log("block y/z: einsum route vs probe features inside the kernels")
