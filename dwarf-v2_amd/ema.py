@@ -7,8 +7,9 @@ y[t] = a x[t] + (1 - a) y[t-1] with fp32 state, a = clamp(ema_factor, floor,
 ceiling).  ``ema_factor`` may hold one value (the reference contract) or one
 value per channel of x (an extension used by the long-context benchmark).
 With ``reset_mask`` [B,N] the state is zeroed before the marked tokens, the
-reset-aware scan of ``_CausalEMAResetFn`` (ema:368-509), on the same chunked
-kernels.
+reset-aware scan of ``_CausalEMAResetFn`` (ema:368-509), on the same kernels:
+a single-pass scan with decoupled look-back (a three-stage chunked scan for
+slabs over 2 GiB).
 """
 
 from __future__ import annotations
