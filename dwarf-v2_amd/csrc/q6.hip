@@ -990,7 +990,8 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_win(const dwarf_dsqg_q6_
 }
 
 // ---------------------------------------------------------------------------
-// Decode.  One workgroup per (sequence, layer), one wave per head.
+// Decode.  One workgroup per (sequence, layer, group of kDecHeadsPerWg
+// heads), one wave per head.
 //
 // A slot's codes come in 12-byte chunks of 16 head dims (K at 12c, V at
 // 52 + 12c), so four lanes per gathered row -- lane c holding dims
@@ -1015,7 +1016,11 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_win(const dwarf_dsqg_q6_
 // reduce-scatter the 16 dims of a lane, then DPP row rotations).
 // ---------------------------------------------------------------------------
 constexpr int kDecRows = 16;      // rows per batch (one per 4-lane group)
-constexpr int kMaxDecHeads = 16;  // waves per workgroup
+constexpr int kMaxDecHeads = 16;  // heads the decode step takes
+// heads (waves) per decode workgroup: at cfg5 four per workgroup measured 43.0 / 47.9 / 53.1 us per step
+// (warm / advancing / cold) against 44.0 / 49.4 / 54.4 with all eight heads in one workgroup (28 resident
+// waves per CU instead of 24), two 43.2 / 48.2 / 53.6, one 43.4 / 48.1 / 53.0
+constexpr int kDecHeadsPerWg = 4;
 
 struct DecBatch {
   uint32_t k0, k1, k2, v0, v1, v2;
@@ -1162,16 +1167,22 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
   extern __shared__ float smem[];
   int2* s_list_all = reinterpret_cast<int2*>(smem);
 
-  const int sq = blockIdx.x / a.L;
-  const int ly = blockIdx.x - sq * a.L;
-  const int h = uniform(threadIdx.x / kWave);   // head = wave index
+  constexpr int HPW = kDecHeadsPerWg;
+  const int hgroups = (H + HPW - 1) / HPW;
+  const int hg = blockIdx.x % hgroups;
+  const int sl = blockIdx.x / hgroups;
+  const int sq = sl / a.L;
+  const int ly = sl - sq * a.L;
+  const int wv = uniform(threadIdx.x / kWave);
+  const int h = hg * HPW + wv;   // head = wave index within the group
+  if (h >= H) return;
   const int l = threadIdx.x % kWave;
   const int c = l & 3;        // 16-dim chunk
   const int rr = l >> 2;      // row of the batch
   const int hk = h / (H / a.H_kv);
   const int t = uniform(a.pos[sq]);
   const int Nc = a.Ncache;
-  int2* list = s_list_all + h * lay.list_len;
+  int2* list = s_list_all + wv * lay.list_len;
   // this (sequence, layer, head)'s row of the T table (q6_decode_table)
   const float* Th = T + (static_cast<int64_t>(ly * a.S + sq) * H + h) * lay.JE;
   // rows t - delta in [0, Nc); the sentinel (J, t + 1) gives row -1
@@ -1405,10 +1416,12 @@ hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, float* T, hipStr
   const int table_blocks = a.L * ((a.S * a.H + kTabRows - 1) / kTabRows);
   hipLaunchKernelGGL(q6_decode_table, dim3(table_blocks), dim3(kBlock), dec_table_lds(lay.JE, a.H, !a.se_round_bf16),
                      stream, a, T, lay.JE);
-  const int blocks = a.S * a.L;
-  const size_t lds = lay.bytes;
+  constexpr int HPW = kDecHeadsPerWg;
+  const int wpb = a.H < HPW ? a.H : HPW;
+  const int blocks = a.S * a.L * ((a.H + HPW - 1) / HPW);
+  const size_t lds = static_cast<size_t>(wpb) * lay.list_len * 8;
 #define DWARF_Q6D_CASE(S) \
-  case S: hipLaunchKernelGGL(q6_decode_q4<S>, dim3(blocks), dim3(kWave * a.H), lds, stream, a, T); break;
+  case S: hipLaunchKernelGGL(q6_decode_q4<S>, dim3(blocks), dim3(kWave * wpb), lds, stream, a, T); break;
   switch (a.plane_shift) {
     DWARF_Q6D_CASE(0) DWARF_Q6D_CASE(1) DWARF_Q6D_CASE(2) DWARF_Q6D_CASE(3) DWARF_Q6D_CASE(4)
     DWARF_Q6D_CASE(5) DWARF_Q6D_CASE(6) DWARF_Q6D_CASE(7) DWARF_Q6D_CASE(8) DWARF_Q6D_CASE(9)
