@@ -231,8 +231,8 @@ def test_decode_graph_replay_matches_eager(pkg, device):
 
 
 def test_decode_maximum_sizes(pkg, device):
-    """J = 256 offsets (17 near, 239 far) and H = 16 heads (a 1024-thread workgroup, H_kv = 4): the
-    decode step against the oracle on the dequantised cache."""
+    """J = 256 offsets (17 near, 239 far) and H = 16 heads (four workgroups of four heads per
+    (sequence, layer), H_kv = 4): the decode step against the oracle on the dequantised cache."""
     offsets = list(range(1, 18)) + list(range(48, 48 + 239))
     S, H, Hkv, N = 2, 16, 4, 320
     x = make_inputs(S, H, Hkv, N, offsets, 17, seed=81, dtype=torch.bfloat16, gain_std=6.0)
@@ -248,6 +248,32 @@ def test_decode_maximum_sizes(pkg, device):
     ref = _oracle_on_cache(x, cache.cpu().numpy(), offsets, 17, 0, qp, kp, 0)
     for s in range(S):
         assert max_abs(out[s, 0], ref[s, :, int(pos[s])]) < 2e-2, s
+
+
+@pytest.mark.parametrize("H,Hkv", [(3, 3), (6, 3)])
+def test_decode_head_groups(pkg, device, H, Hkv):
+    """A decode workgroup takes four heads: H = 3 is one workgroup of three waves; H = 6 (GQA, two query
+    heads per KV head) is two workgroups per (sequence, layer), the second with two heads and two waves
+    without one.  Every head against the oracle on the dequantised cache, at the full lattice."""
+    offsets = list(pkg.ALL_OFFSETS)
+    S, L, N = 3, 2, 700
+    layers = [make_inputs(S, H, Hkv, N, offsets, 17, seed=120 + 10 * H + l, dtype=torch.bfloat16, plane_shift=3,
+                          gain_std=6.0) for l in range(L)]
+    pos = torch.tensor([699, 97, 400], dtype=torch.int32)
+    qp, kp = orthogonal_probes(64, 3)
+    qp, kp = torch.nn.functional.normalize(qp, dim=-1), torch.nn.functional.normalize(kp, dim=-1)
+    caches = torch.stack([pkg.q6.pack_kv(x["k"].to(device), x["v"].to(device), kp.to(device)) for x in layers])
+    qdec = torch.stack([torch.stack([layers[l]["q"][s, :, int(pos[s])] for l in range(L)]) for s in range(S)])
+    tables = {n: torch.stack([x[n] for x in layers]).to(device) for n in ("pos_bias", "scale_embed", "phase_base",
+                                                                          "phase_gain")}
+    off = torch.tensor(offsets, dtype=torch.int32, device=device)
+    out = pkg.q6.q6_decode(qdec.to(device), pos.to(device), caches, tables["pos_bias"], tables["scale_embed"],
+                           tables["phase_base"], tables["phase_gain"], torch.stack([qp] * L).to(device), off,
+                           17, 79, 3).cpu()
+    for l in range(L):
+        ref = _oracle_on_cache(layers[l], caches[l].cpu().numpy(), offsets, 17, 3, qp, kp, 0)
+        for s in range(S):
+            assert max_abs(out[s, l], ref[s, :, int(pos[s])]) < 2e-2, (H, s, l)
 
 
 @pytest.mark.parametrize("widen", [True, False])
