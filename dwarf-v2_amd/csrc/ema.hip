@@ -279,201 +279,13 @@ __global__ __launch_bounds__(kEmaBlock) void ema_bwd_apply(const T* __restrict__
 // the adjoint lambda, and in its rescan writes dx and each workgroup's dalpha
 // partial.
 // ---------------------------------------------------------------------------
-constexpr int kLbGroups = 16;   // channel groups of a tile (lanes cg)
-constexpr int kLbSegs = 4;      // token segments of a tile (lanes ts)
-constexpr int kLbSeg = 32;                         // tokens per segment (the lane's registers)
-constexpr int kLbWaitLimit = 1 << 22;              // default polls before a wait gives up
-constexpr size_t kLbHead = 256;                    // bytes ahead of the words (unused, kept zero)
-constexpr int kLbWaves = 4;                        // tiles (one wave each) per workgroup, consecutive in scan order
-constexpr int kLbRun = 32;                         // workgroup tiles per run (one inclusive state per run)
-constexpr int kLbBatch = 8;                        // aggregates loaded together by a carry walk
-
-struct LbGeom {
-  int B, N, D;
-  int CB;    // channel blocks of 16 VEC channels
-  int NCH;   // tiles along time per (b, channel block)
-  int NWG;   // workgroup tiles along time, ceil(NCH / kLbWaves)
-  int S;     // (b, channel block) slices, B * CB
-  int per_channel;
-  float lo, hi;
-  const uint8_t* reset;
-  int64_t srb, srn;
-  unsigned long long* words;   // [NWG * S][16 VEC]: workgroup aggregates, (value bits, tag << 32)
-  unsigned long long* runs;    // [ceil(NWG / kLbRun) * S][16 VEC]: the runs' inclusive states
-  float* da_part;              // backward: [NWG][B][D] dalpha partials (row widx * B + b)
-  int wait_limit;
-};
-
-__device__ __forceinline__ float lb_alpha(const float* alpha, const LbGeom& g, int d) {
-  const float a = alpha[g.per_channel ? d : 0];
-  return fminf(fmaxf(a, g.lo), g.hi);
-}
-
-__device__ __forceinline__ bool lb_reset(const LbGeom& g, int b, int t) {
-  return g.reset[b * g.srb + static_cast<int64_t>(t) * g.srn] != 0;
-}
-
-// Raw VEC channels of one token in registers, loaded and stored through
-// buffer resources (an out-of-range offset reads zeros / drops the store).
-template <typename T, int VEC>
-struct LbRaw {
-  static constexpr int kWords = (VEC * sizeof(T) + 3) / 4;
-  uint32_t w[kWords];
-  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    if constexpr (VEC * sizeof(T) == 16) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-      w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
-    } else if constexpr (VEC * sizeof(T) == 8) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-      w[0] = v[0]; w[1] = v[1];
-    } else if constexpr (VEC * sizeof(T) == 4) {
-      w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-    } else {
-      w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-    }
-  }
-  __device__ __forceinline__ void widen(float* v) const {
-    if constexpr (sizeof(T) == 2) {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) v[i] = (i & 1) ? bf16_hi(w[i / 2]) : bf16_lo(w[i / 2]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) v[i] = __uint_as_float(w[i]);
-    }
-  }
-};
-
-template <typename T, int VEC>
-__device__ __forceinline__ void lb_store(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* v) {
-  if constexpr (sizeof(T) == 2 && VEC == 4) {
-    __builtin_amdgcn_raw_buffer_store_b64(
-        __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, make_uint2(pack_bf16x2(v[0], v[1]),
-                                                                                    pack_bf16x2(v[2], v[3]))),
-        r, off, 0, 0);
-  } else if constexpr (sizeof(T) == 4 && VEC == 4) {
-    __builtin_amdgcn_raw_buffer_store_b128(
-        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned,
-                           make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                                      __float_as_uint(v[3]))),
-        r, off, 0, 0);
-  } else if constexpr (sizeof(T) == 2) {
-    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v[0]), r, off, 0, 0);
-  } else {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, off, 0, 0);
-  }
-}
-
-// One [N][D] slab of batch row b (the host bounds its span below 2 GiB).
-template <typename T>
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t lb_rsrc(const T* base, int64_t sb, int64_t sn, int b, int N) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + b * sb), 0,
-                                           static_cast<int>(static_cast<int64_t>(N) * sn * sizeof(T)), 0x00020000);
-}
-
-__device__ __forceinline__ void lb_publish(unsigned long long* w, float v, unsigned tag) {
-  const unsigned long long x = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v);
-  __hip_atomic_store(w, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The published word, or 0 when the wait gives up.
-__device__ __forceinline__ unsigned long long lb_wait(const unsigned long long* w, int limit) {
-  for (int it = 0; it < limit; ++it) {
-    const unsigned long long x = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (x >> 32) return x;
-    __builtin_amdgcn_s_sleep(2);
-  }
-  return 0;
-}
-
-// The state entering the workgroup tile at scan-order index idx of its slice:
-// the aggregates of the run's tiles before it composed in order into
-// (Pa, Qa) (P_p = full for tag 1, 0 for tag 3), loaded kLbBatch at a time,
-// then applied to the previous run's inclusive state (none in the first run):
-// C = Pa C_run + Qa.  The run's state is waited on last, so the walk over the
-// aggregates overlaps the previous run's.  NaN when a wait gives up.
-__device__ __forceinline__ float lb_carry(const LbGeom& g, int slice, int ch, int ct, int idx, float full) {
-  const int run = idx / kLbRun, first = run * kLbRun;
-  float Pa = 1.f, Qa = 0.f;
-  for (int p0 = first; p0 < idx; p0 += kLbBatch) {
-    unsigned long long w[kLbBatch];
-#pragma unroll
-    for (int k = 0; k < kLbBatch; ++k) {   // a slot past idx - 1 reloads the last one (unused)
-      const int p = min(p0 + k, idx - 1);
-      w[k] = __hip_atomic_load(g.words + (static_cast<int64_t>(p) * g.S + slice) * ct + ch, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-#pragma unroll
-    for (int k = 0; k < kLbBatch; ++k) {
-      const int p = p0 + k;
-      if (p < idx) {
-        unsigned long long x = w[k];
-        if (!(x >> 32)) {
-          x = lb_wait(g.words + (static_cast<int64_t>(p) * g.S + slice) * ct + ch, g.wait_limit);
-          if (!x) return __builtin_nanf("");
-        }
-        const float Pp = (x >> 32) == 3u ? 0.f : full;
-        Qa = fmaf(Pp, Qa, __uint_as_float(static_cast<uint32_t>(x)));
-        Pa *= Pp;
-      }
-    }
-  }
-  if (run == 0) return Qa;
-  const unsigned long long x = lb_wait(g.runs + (static_cast<int64_t>(run - 1) * g.S + slice) * ct + ch,
-                                       g.wait_limit);
-  if (!x) return __builtin_nanf("");
-  return fmaf(Pa, __uint_as_float(static_cast<uint32_t>(x)), Qa);
-}
-
-// LDS of a workgroup: each wave's tile maps (P, Q) per channel, and the state
-// entering the workgroup.
-struct LbShared {
-  float P[kLbWaves][kWave];
-  float Q[kLbWaves][kWave];
-  float C[kWave];
-};
-
-// Steps 3-4 for channel ch of wave w's tile (owner lanes only take part):
-// the tiles' maps meet in LDS; wave 0 composes them in scan order into the
-// workgroup's (P, Q), publishes Q tagged with its factor, forms the state
-// entering the workgroup from the earlier workgroups (lb_carry; full_wg is a
-// full workgroup's factor) and, in a run's last workgroup, publishes the run's
-// inclusive state; each wave then composes the state entering its own tile
-// from that and the earlier tiles of its workgroup, in order.  Every lane of
-// the workgroup reaches both barriers.
-__device__ __forceinline__ float lb_join(const LbGeom& g, LbShared& sh, int slice, int ch, bool owner, int ct,
-                                         int widx, int w, float Po, float Qo, float full_wg) {
-  if (owner) {
-    sh.P[w][ch] = Po;
-    sh.Q[w][ch] = Qo;
-  }
-  __syncthreads();
-  if (w == 0 && owner) {
-    float P = 1.f, Q = 0.f;
-#pragma unroll
-    for (int j = 0; j < kLbWaves; ++j) {
-      Q = fmaf(sh.P[j][ch], Q, sh.Q[j][ch]);
-      P *= sh.P[j][ch];
-    }
-    lb_publish(g.words + (static_cast<int64_t>(widx) * g.S + slice) * ct + ch, Q, P == 0.f ? 3u : 1u);
-    const float C = widx > 0 ? lb_carry(g, slice, ch, ct, widx, full_wg) : 0.f;
-    if (widx % kLbRun == kLbRun - 1 && widx + 1 < g.NWG)
-      lb_publish(g.runs + (static_cast<int64_t>(widx / kLbRun) * g.S + slice) * ct + ch, fmaf(P, C, Q), 2u);
-    sh.C[ch] = C;
-  }
-  __syncthreads();
-  if (!owner) return 0.f;
-  float C = sh.C[ch];
-  for (int j = 0; j < w; ++j) C = fmaf(sh.P[j][ch], C, sh.Q[j][ch]);
-  return C;
-}
-
 template <typename T, int VEC, bool RESET>
 __global__ __launch_bounds__(kWave * kLbWaves) void ema_fwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
                                                      T* __restrict__ y, int64_t syb, int64_t syn,
                                                      const float* __restrict__ alpha, LbGeom g) {
   constexpr int SEG = kLbSeg;
   constexpr int CT = kLbGroups * VEC;   // channels (words) per tile
-  __shared__ LbShared sh;
+  __shared__ LbShared<1> sh;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int cg = lane & 15, ts = lane >> 4;
   const int id = blockIdx.x;   // workgroups of lower index are dispatched first
@@ -557,7 +369,8 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_fwd_lb(const T* __restri
   float full_wg = 1.f;   // a full workgroup's factor, composed as wave 0 composes the tiles
 #pragma unroll
   for (int j = 0; j < kLbWaves; ++j) full_wg *= full;
-  const float C = lb_join(g, sh, slice, cg * VEC + io, owner, CT, widx, w, Po, Qo, full_wg);
+  float C;
+  lb_join<1>(g, sh, slice, cg * VEC + io, owner, CT, widx, w, &Po, &Qo, &full_wg, &C);
   // 5. incoming state of each channel of this lane's segment, then the rescan
   float st[VEC];
 #pragma unroll
@@ -594,7 +407,7 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restri
   constexpr int SEG = kLbSeg;
   constexpr int CT = kLbGroups * VEC;
   constexpr int R = 8;   // rows of x and y loaded per block of the rescan
-  __shared__ LbShared sh;
+  __shared__ LbShared<1> sh;
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
   const int cg = lane & 15, ts = lane >> 4;
   const int id = blockIdx.x;   // workgroups of lower index are dispatched first
@@ -682,7 +495,8 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restri
 #pragma unroll
   for (int j = 0; j < kLbWaves; ++j) full_wg *= full;
   // predecessors: workgroup tiles widx - 1, ..., 0, i.e. the chunks after this workgroup's
-  const float C = lb_join(g, sh, slice, cg * VEC + io, owner, CT, widx, w, Po, Qo, full_wg);
+  float C;
+  lb_join<1>(g, sh, slice, cg * VEC + io, owner, CT, widx, w, &Po, &Qo, &full_wg, &C);
   // 5. rescan: lambda from the incoming adjoint, dx = a lambda, dalpha terms
   float st[VEC], da[VEC];
 #pragma unroll
@@ -759,31 +573,6 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restri
   }
 }
 
-// Clears the look-back words of the next scan.
-__global__ __launch_bounds__(kEmaBlock) void ema_lb_zero(uint4* __restrict__ p, int64_t n16) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEmaBlock + threadIdx.x; i < n16;
-       i += static_cast<int64_t>(gridDim.x) * kEmaBlock)
-    p[i] = make_uint4(0u, 0u, 0u, 0u);
-}
-
-// Look-back plan: channel blocks, tiles along time, bytes of words.
-struct LbPlan {
-  int CB, NCH, NWG, S;
-  size_t words_bytes;   // aggregates and the runs' inclusive states
-};
-
-inline LbPlan lb_plan(int B, int N, int D, int vec, int seg) {
-  LbPlan p;
-  const int ct = kLbGroups * vec;
-  p.CB = (D + ct - 1) / ct;
-  p.NCH = (N + kLbSegs * seg - 1) / (kLbSegs * seg);
-  p.NWG = (p.NCH + kLbWaves - 1) / kLbWaves;
-  p.S = B * p.CB;
-  const int runs = (p.NWG + kLbRun - 1) / kLbRun;
-  p.words_bytes = static_cast<size_t>(p.NWG + runs) * p.S * ct * 8;
-  return p;
-}
-
 inline size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Workspace of the look-back scans: a zero head, the words and, backward,
@@ -793,11 +582,6 @@ inline size_t lb_workspace(int B, int N, int D, bool backward) {
   size_t n = kLbHead + round256(p.words_bytes);
   if (backward) n += round256(static_cast<size_t>(p.NWG) * B * D * 4) + round256(static_cast<size_t>(D) * 4);
   return n;
-}
-
-// Every [N][D] slab of these tensors within 32-bit buffer offsets.
-inline bool lb_fits(int N, int64_t sn, size_t elem) {
-  return static_cast<int64_t>(N) * sn * static_cast<int64_t>(elem) < (int64_t(1) << 31);
 }
 
 template <typename T, int VEC>
@@ -814,18 +598,13 @@ LbGeom lb_geom(int B, int N, int D, int per_channel, float lo, float hi, const u
   g.srn = reset ? rs[1] : 0;
   char* w = static_cast<char*>(ws);
   g.words = reinterpret_cast<unsigned long long*>(w + kLbHead);
-  g.runs = g.words + static_cast<int64_t>(p.NWG) * p.S * kLbGroups * VEC;
+  g.runs = g.words + p.kw;
+  g.kw = p.kw;
+  g.kr = p.kr;
   g.da_part = backward ? reinterpret_cast<float*>(w + kLbHead + round256(p.words_bytes)) : nullptr;
   g.wait_limit = wait_limit > 0 ? wait_limit : kLbWaitLimit;
   *plan = p;
   return g;
-}
-
-// The zeroing launch ahead of a scan: the words.
-inline void lb_zero(const LbGeom& g, const LbPlan& p, hipStream_t stream) {
-  const int64_t n16 = static_cast<int64_t>(p.words_bytes / 16);
-  const int blocks = static_cast<int>((n16 + kEmaBlock - 1) / kEmaBlock < 64 ? (n16 + kEmaBlock - 1) / kEmaBlock : 64);
-  hipLaunchKernelGGL(ema_lb_zero, dim3(blocks), dim3(kEmaBlock), 0, stream, reinterpret_cast<uint4*>(g.words), n16);
 }
 
 template <typename T, int VEC, bool RESET>

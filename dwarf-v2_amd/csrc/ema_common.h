@@ -282,5 +282,271 @@ inline EmaGeom make_geom(int B, int N, int D, int vec, int per_channel, float lo
   return g;
 }
 
+
+// ---------------------------------------------------------------------------
+// Single-pass scans with decoupled look-back over [N][D] slabs (the causal EMA
+// in ema.hip, the InterferencePacket pool in packet.hip; ema.hip describes the
+// scheme).  A workgroup of kLbWaves waves takes that many consecutive
+// 128-token tiles of one (b, channel block); the helpers below publish and
+// walk the workgroups' packed (value, tag) words.
+// ---------------------------------------------------------------------------
+constexpr int kLbGroups = 16;   // channel groups of a tile (lanes cg)
+constexpr int kLbSegs = 4;      // token segments of a tile (lanes ts)
+constexpr int kLbSeg = 32;                         // tokens per segment (the lane's registers)
+constexpr int kLbWaitLimit = 1 << 22;              // default polls before a wait gives up
+constexpr size_t kLbHead = 256;                    // bytes ahead of the words (unused, kept zero)
+constexpr int kLbWaves = 4;                        // tiles (one wave each) per workgroup, consecutive in scan order
+constexpr int kLbRun = 32;                         // workgroup tiles per run (one inclusive state per run)
+constexpr int kLbBatch = 8;                        // aggregates loaded together by a carry walk
+
+struct LbGeom {
+  int B, N, D;
+  int CB;    // channel blocks of 16 VEC channels
+  int NCH;   // tiles along time per (b, channel block)
+  int NWG;   // workgroup tiles along time, ceil(NCH / kLbWaves)
+  int S;     // (b, channel block) slices, B * CB
+  int per_channel;
+  float lo, hi;
+  const uint8_t* reset;
+  int64_t srb, srn;
+  unsigned long long* words;   // [NWG * S][16 VEC]: workgroup aggregates, (value bits, tag << 32)
+  unsigned long long* runs;    // [ceil(NWG / kLbRun) * S][16 VEC]: the runs' inclusive states
+  int64_t kw, kr;              // words and runs of one scale (scale k at words + k kw, runs + k kr)
+  float* da_part;              // backward: [NWG][B][D] dalpha partials (row widx * B + b)
+  int wait_limit;
+};
+
+__device__ __forceinline__ float lb_alpha(const float* alpha, const LbGeom& g, int d) {
+  const float a = alpha[g.per_channel ? d : 0];
+  return fminf(fmaxf(a, g.lo), g.hi);
+}
+
+__device__ __forceinline__ bool lb_reset(const LbGeom& g, int b, int t) {
+  return g.reset[b * g.srb + static_cast<int64_t>(t) * g.srn] != 0;
+}
+
+// Raw VEC channels of one token in registers, loaded and stored through
+// buffer resources (an out-of-range offset reads zeros / drops the store).
+template <typename T, int VEC>
+struct LbRaw {
+  static constexpr int kWords = (VEC * sizeof(T) + 3) / 4;
+  uint32_t w[kWords];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (VEC * sizeof(T) == 16) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+      w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+    } else if constexpr (VEC * sizeof(T) == 8) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+      w[0] = v[0]; w[1] = v[1];
+    } else if constexpr (VEC * sizeof(T) == 4) {
+      w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else {
+      w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void widen(float* v) const {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[i] = (i & 1) ? bf16_hi(w[i / 2]) : bf16_lo(w[i / 2]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) v[i] = __uint_as_float(w[i]);
+    }
+  }
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ void lb_store(__amdgpu_buffer_rsrc_t r, uint32_t off, const float* v) {
+  if constexpr (sizeof(T) == 2 && VEC == 4) {
+    __builtin_amdgcn_raw_buffer_store_b64(
+        __builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, make_uint2(pack_bf16x2(v[0], v[1]),
+                                                                                    pack_bf16x2(v[2], v[3]))),
+        r, off, 0, 0);
+  } else if constexpr (sizeof(T) == 4 && VEC == 4) {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned,
+                           make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                      __float_as_uint(v[3]))),
+        r, off, 0, 0);
+  } else if constexpr (sizeof(T) == 2) {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v[0]), r, off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, off, 0, 0);
+  }
+}
+
+// One [N][D] slab of batch row b (the host bounds its span below 2 GiB).
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lb_rsrc(const T* base, int64_t sb, int64_t sn, int b, int N) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + b * sb), 0,
+                                           static_cast<int>(static_cast<int64_t>(N) * sn * sizeof(T)), 0x00020000);
+}
+
+__device__ __forceinline__ void lb_publish(unsigned long long* w, float v, unsigned tag) {
+  const unsigned long long x = (static_cast<unsigned long long>(tag) << 32) | __float_as_uint(v);
+  __hip_atomic_store(w, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The published word, or 0 when the wait gives up.
+__device__ __forceinline__ unsigned long long lb_wait(const unsigned long long* w, int limit) {
+  for (int it = 0; it < limit; ++it) {
+    const unsigned long long x = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (x >> 32) return x;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return 0;
+}
+
+// The state entering the workgroup tile at scan-order index idx of its slice:
+// the aggregates of the run's tiles before it composed in order into
+// (Pa, Qa) (P_p = full for tag 1, 0 for tag 3), loaded kLbBatch at a time,
+// then applied to the previous run's inclusive state (none in the first run):
+// C = Pa C_run + Qa.  The run's state is waited on last, so the walk over the
+// aggregates overlaps the previous run's.  NaN when a wait gives up.
+__device__ __forceinline__ float lb_carry(const LbGeom& g, const unsigned long long* words,
+                                         const unsigned long long* runs, int slice, int ch, int ct, int idx,
+                                         float full) {
+  const int run = idx / kLbRun, first = run * kLbRun;
+  float Pa = 1.f, Qa = 0.f;
+  for (int p0 = first; p0 < idx; p0 += kLbBatch) {
+    unsigned long long w[kLbBatch];
+#pragma unroll
+    for (int k = 0; k < kLbBatch; ++k) {   // a slot past idx - 1 reloads the last one (unused)
+      const int p = min(p0 + k, idx - 1);
+      w[k] = __hip_atomic_load(words + (static_cast<int64_t>(p) * g.S + slice) * ct + ch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int k = 0; k < kLbBatch; ++k) {
+      const int p = p0 + k;
+      if (p < idx) {
+        unsigned long long x = w[k];
+        if (!(x >> 32)) {
+          x = lb_wait(words + (static_cast<int64_t>(p) * g.S + slice) * ct + ch, g.wait_limit);
+          if (!x) return __builtin_nanf("");
+        }
+        const float Pp = (x >> 32) == 3u ? 0.f : full;
+        Qa = fmaf(Pp, Qa, __uint_as_float(static_cast<uint32_t>(x)));
+        Pa *= Pp;
+      }
+    }
+  }
+  if (run == 0) return Qa;
+  const unsigned long long x = lb_wait(runs + (static_cast<int64_t>(run - 1) * g.S + slice) * ct + ch,
+                                       g.wait_limit);
+  if (!x) return __builtin_nanf("");
+  return fmaf(Pa, __uint_as_float(static_cast<uint32_t>(x)), Qa);
+}
+
+// LDS of a workgroup: each wave's tile maps (P, Q) per channel and scale,
+// and the states entering the workgroup.
+template <int K>
+struct LbShared {
+  float P[K][kLbWaves][kWave];
+  float Q[K][kLbWaves][kWave];
+  float C[K][kWave];
+};
+
+// Steps 3-4 for channel ch of wave w's tile, for each of K scans of the same
+// tiles (owner lanes only take part): the tiles' maps meet in LDS; wave 0
+// composes them in scan order into the workgroup's (P, Q) of each scale and
+// publishes every scale's Q tagged with its factor before it waits on
+// anything, then forms the states entering the workgroup from the earlier
+// workgroups (lb_carry; full_wg is a full workgroup's factor per scale) and,
+// in a run's last workgroup, publishes the runs' inclusive states; each wave
+// then composes the states entering its own tile from those and the earlier
+// tiles of its workgroup, in order.  Every lane of the workgroup reaches both
+// barriers.
+template <int K>
+__device__ __forceinline__ void lb_join(const LbGeom& g, LbShared<K>& sh, int slice, int ch, bool owner, int ct,
+                                        int widx, int w, const float* Po, const float* Qo, const float* full_wg,
+                                        float* C) {
+  if (owner) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      sh.P[k][w][ch] = Po[k];
+      sh.Q[k][w][ch] = Qo[k];
+    }
+  }
+  __syncthreads();
+  if (w == 0 && owner) {
+    float P[K], Q[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      P[k] = 1.f;
+      Q[k] = 0.f;
+#pragma unroll
+      for (int j = 0; j < kLbWaves; ++j) {
+        Q[k] = fmaf(sh.P[k][j][ch], Q[k], sh.Q[k][j][ch]);
+        P[k] *= sh.P[k][j][ch];
+      }
+      lb_publish(g.words + k * g.kw + (static_cast<int64_t>(widx) * g.S + slice) * ct + ch, Q[k],
+                 P[k] == 0.f ? 3u : 1u);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float Ck = widx > 0 ? lb_carry(g, g.words + k * g.kw, g.runs + k * g.kr, slice, ch, ct, widx, full_wg[k])
+                                : 0.f;
+      if (widx % kLbRun == kLbRun - 1 && widx + 1 < g.NWG)
+        lb_publish(g.runs + k * g.kr + (static_cast<int64_t>(widx / kLbRun) * g.S + slice) * ct + ch,
+                   fmaf(P[k], Ck, Q[k]), 2u);
+      sh.C[k][ch] = Ck;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    float Ck = 0.f;
+    if (owner) {
+      Ck = sh.C[k][ch];
+      for (int j = 0; j < w; ++j) Ck = fmaf(sh.P[k][j][ch], Ck, sh.Q[k][j][ch]);
+    }
+    C[k] = Ck;
+  }
+}
+
+// Clears the look-back words of the next scan.
+__global__ __launch_bounds__(kEmaBlock) void ema_lb_zero(uint4* __restrict__ p, int64_t n16) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEmaBlock + threadIdx.x; i < n16;
+       i += static_cast<int64_t>(gridDim.x) * kEmaBlock)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Look-back plan: channel blocks, tiles along time, words of one scale and
+// bytes of the words of K scales (each scale's aggregates, then each scale's
+// runs' inclusive states).
+struct LbPlan {
+  int CB, NCH, NWG, S;
+  int64_t kw, kr;       // aggregate words and run words of one scale
+  size_t words_bytes;
+};
+
+inline LbPlan lb_plan(int B, int N, int D, int vec, int seg, int K = 1) {
+  LbPlan p;
+  const int ct = kLbGroups * vec;
+  p.CB = (D + ct - 1) / ct;
+  p.NCH = (N + kLbSegs * seg - 1) / (kLbSegs * seg);
+  p.NWG = (p.NCH + kLbWaves - 1) / kLbWaves;
+  p.S = B * p.CB;
+  const int runs = (p.NWG + kLbRun - 1) / kLbRun;
+  p.kw = static_cast<int64_t>(p.NWG) * p.S * ct;
+  p.kr = static_cast<int64_t>(runs) * p.S * ct;
+  p.words_bytes = static_cast<size_t>(K) * (p.kw + p.kr) * 8;
+  return p;
+}
+
+// Every [N][D] slab of these tensors within 32-bit buffer offsets.
+inline bool lb_fits(int N, int64_t sn, size_t elem) {
+  return static_cast<int64_t>(N) * sn * static_cast<int64_t>(elem) < (int64_t(1) << 31);
+}
+
+// The zeroing launch ahead of a scan: the words.
+inline void lb_zero(const LbGeom& g, const LbPlan& p, hipStream_t stream) {
+  const int64_t n16 = static_cast<int64_t>(p.words_bytes / 16);
+  const int blocks = static_cast<int>((n16 + kEmaBlock - 1) / kEmaBlock < 64 ? (n16 + kEmaBlock - 1) / kEmaBlock : 64);
+  hipLaunchKernelGGL(ema_lb_zero, dim3(blocks), dim3(kEmaBlock), 0, stream, reinterpret_cast<uint4*>(g.words), n16);
+}
+
+
 }  // namespace
 }  // namespace dwarf

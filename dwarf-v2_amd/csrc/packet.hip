@@ -5,8 +5,13 @@
 // with w_k = softmax(mix_logits)_k cast to T and every product and partial
 // sum rounded to T, as the reference's bf16 tensor arithmetic rounds them.
 // The reference runs K separate scans (each reading x and writing its scan)
-// and K products and K - 1 sums; here x is read twice and pooled written
-// once.
+// and K products and K - 1 sums; here the forward reads x once and writes
+// pooled once.
+//
+// The forward is one pass with the EMA's decoupled look-back (packet_fwd_lb)
+// wherever every [N][D] slab of x and pooled spans less than 2 GiB; the
+// three-stage forward below (x read twice) serves larger slabs, and the
+// backward's stages are as below.
 //
 // Stages, on the EMA's 16-token chunks (ema_common.h):
 //   forward:  local - the K chunk-end states with zero carry-in (reads x)
@@ -136,6 +141,154 @@ __global__ __launch_bounds__(kEmaBlock) void packet_fwd_apply(const T* __restric
         }
         stv<T, VEC>(po + static_cast<int64_t>(tb + r) * spn, out);
       }
+  }
+}
+
+// ---- forward in one pass (decoupled look-back, ema_common.h) -------------
+// The K scans of the pool in one pass over x with the EMA's look-back (its
+// tiles, run walk and bounded waits; ema.hip describes them): a wave takes
+// (b, 16 VEC channels, 128 tokens), lane (cg, ts) VEC channels of a 32-token
+// segment held in registers; the segment scans of every scale compose into
+// the tile's maps, and the workgroup's four tiles publish K aggregates per
+// channel.  The rescan writes, at every 16-token chunk start, the K incoming
+// states for the backward (state [B][NC][K][D], as the three-stage forward
+// does) and, with POOLED, the pool with the reference's rounding of each
+// scan, product and partial sum to T.  Every factor is one scalar per scale,
+// so a tile's factor P_k is the same for all its channels.
+template <typename T, int VEC, int K, bool POOLED>
+__global__ __launch_bounds__(kWave * kLbWaves) void packet_fwd_lb(const T* __restrict__ x, int64_t sxb, int64_t sxn,
+                                                                  T* __restrict__ pooled, int64_t spb, int64_t spn,
+                                                                  const float* __restrict__ alpha,
+                                                                  const float* __restrict__ weight,
+                                                                  float* __restrict__ state, LbGeom g, int NC) {
+  constexpr int SEG = kLbSeg;
+  constexpr int CT = kLbGroups * VEC;
+  __shared__ LbShared<K> sh;
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int cg = lane & 15, ts = lane >> 4;
+  const int id = blockIdx.x;   // workgroups of lower index are dispatched first
+  const int widx = id / g.S, slice = id - widx * g.S;
+  const int chunk = widx * kLbWaves + w;   // a chunk past the last holds no tokens
+  const int b = slice / g.CB, cb = slice - b * g.CB;
+  const int d0 = (cb * kLbGroups + cg) * VEC;
+  const bool dlive = d0 < g.D;
+  const int s0 = (chunk * kLbSegs + ts) * SEG;
+  const int len = max(0, min(SEG, g.N - s0));
+  float a[K], dec[K], wk[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    a[k] = fminf(fmaxf(alpha[k], g.lo), g.hi);
+    dec[k] = 1.f - a[k];
+    wk[k] = rnd<T>(weight[k]);
+  }
+  const __amdgpu_buffer_rsrc_t rx = lb_rsrc(x, sxb, sxn, b, g.N);
+  const uint32_t rsx = static_cast<uint32_t>(sxn * sizeof(T)), cox = static_cast<uint32_t>(d0 * sizeof(T));
+  LbRaw<T, VEC> raw[SEG];
+#pragma unroll
+  for (int t = 0; t < SEG; ++t)
+    raw[t].load(rx, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsx + cox : kOutOfRange);
+
+  // 1. the segment from a zero state, every scale
+  float L[K][VEC], A[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    A[k] = 1.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) L[k][i] = 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < SEG; ++t) {
+    if (t < len) {
+      float v[VEC];
+      raw[t].widen(v);
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) L[k][i] = fmaf(a[k], v[i], dec[k] * L[k][i]);
+        A[k] *= dec[k];
+      }
+    }
+  }
+  // 2. the four segments of each channel in time order: the tile's (P, Q) and this lane's prefix
+  float P[K], Q[K][VEC], Pp[K], Qp[K][VEC];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    P[k] = 1.f;
+    Pp[k] = 1.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) { Q[k][i] = 0.f; Qp[k][i] = 0.f; }
+  }
+#pragma unroll
+  for (int s = 0; s < kLbSegs; ++s) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float As = __shfl(A[k], cg + 16 * s);
+      Pp[k] = s == ts ? P[k] : Pp[k];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float Ls = __shfl(L[k][i], cg + 16 * s);
+        Qp[k][i] = s == ts ? Q[k][i] : Qp[k][i];
+        Q[k][i] = fmaf(As, Q[k][i], Ls);
+      }
+      P[k] *= As;
+    }
+  }
+  // 3-4. the channel this lane publishes (VEC 4: channel ts of the group; VEC 1: lanes ts = 0)
+  const int io = VEC == 4 ? ts : 0;
+  const bool owner = (VEC == 4 || ts == 0) && dlive && d0 + io < g.D;
+  float Qo[K], full_wg[K], C[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    Qo[k] = VEC == 4 ? pick4(io, Q[k][0], Q[k][VEC > 1 ? 1 : 0], Q[k][VEC > 2 ? 2 : 0], Q[k][VEC > 3 ? 3 : 0])
+                     : Q[k][0];
+    float seg = 1.f, full = 1.f;   // a full tile's factor, composed as a tile composes its segments
+    for (int t = 0; t < SEG; ++t) seg *= dec[k];
+#pragma unroll
+    for (int s = 0; s < kLbSegs; ++s) full *= seg;
+    full_wg[k] = 1.f;
+#pragma unroll
+    for (int j = 0; j < kLbWaves; ++j) full_wg[k] *= full;
+  }
+  lb_join<K>(g, sh, slice, cg * VEC + io, owner, CT, widx, w, P, Qo, full_wg, C);
+  // 5. incoming state of each channel of this lane's segment, then the rescan
+  float st[K][VEC];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) st[k][i] = fmaf(Pp[k], __shfl(C[k], VEC == 4 ? cg + 16 * i : cg), Qp[k][i]);
+  const __amdgpu_buffer_rsrc_t rp = lb_rsrc(pooled, spb, spn, b, g.N);
+  const uint32_t rsp = static_cast<uint32_t>(spn * sizeof(T)), cop = static_cast<uint32_t>(d0 * sizeof(T));
+#pragma unroll
+  for (int t = 0; t < SEG; ++t) {
+    if (t < len) {
+      if ((t % kChunkT) == 0 && dlive) {   // the states entering chunk (s0 + t) / 16
+        float* sr = state + ((static_cast<int64_t>(b) * NC + (s0 + t) / kChunkT) * K) * g.D + d0;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          if constexpr (VEC == 4) {
+            *reinterpret_cast<float4*>(sr + k * g.D) = make_float4(st[k][0], st[k][VEC > 1 ? 1 : 0],
+                                                                   st[k][VEC > 2 ? 2 : 0], st[k][VEC > 3 ? 3 : 0]);
+          } else {
+            sr[k * g.D] = st[k][0];
+          }
+        }
+      }
+      float v[VEC];
+      raw[t].widen(v);
+      float out[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          st[k][i] = fmaf(a[k], v[i], dec[k] * st[k][i]);
+          const float term = rnd<T>(wk[k] * rnd<T>(st[k][i]));
+          acc = k == 0 ? term : rnd<T>(acc + term);
+        }
+        out[i] = acc;
+      }
+      if constexpr (POOLED) lb_store<T, VEC>(rp, dlive ? static_cast<uint32_t>(s0 + t) * rsp + cop : kOutOfRange, out);
+    }
   }
 }
 
@@ -597,9 +750,36 @@ inline EmaGeom pk_carry_geom(int B, int N, int D, int K, float lo, float hi) {
   return g;
 }
 
+// The forward in one pass where every [N][D] slab of x and pooled spans less
+// than 2 GiB (32-bit buffer offsets): the words' zeroing launch, then
+// packet_fwd_lb (states, and with POOLED the pool).  False: the three-stage
+// forward runs instead.
+template <typename T, int VEC, int K, bool POOLED>
+bool pk_fwd_lookback(const dwarf_packet_pool_fwd_args& a, hipStream_t stream) {
+  if (!lb_fits(a.N, a.x_stride[1], sizeof(T)) || (POOLED && !lb_fits(a.N, a.pooled_stride[1], sizeof(T))))
+    return false;
+  const LbPlan p = lb_plan(a.B, a.N, a.D, VEC, kLbSeg, K);
+  LbGeom g{};
+  g.B = a.B; g.N = a.N; g.D = a.D;
+  g.CB = p.CB; g.NCH = p.NCH; g.NWG = p.NWG; g.S = p.S;
+  g.lo = a.floor_; g.hi = a.ceiling;
+  g.words = reinterpret_cast<unsigned long long*>(static_cast<char*>(a.workspace) + kLbHead);
+  g.runs = g.words + K * p.kw;
+  g.kw = p.kw;
+  g.kr = p.kr;
+  g.wait_limit = kLbWaitLimit;
+  lb_zero(g, p, stream);
+  hipLaunchKernelGGL((packet_fwd_lb<T, VEC, K, POOLED>), dim3(p.NWG * p.S), dim3(kWave * kLbWaves), 0, stream,
+                     static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<T*>(a.pooled),
+                     POOLED ? a.pooled_stride[0] : 0, POOLED ? a.pooled_stride[1] : 0, a.alpha, a.weight, a.state, g,
+                     pk_nc(a.N));
+  return true;
+}
+
 // The forward's local and carry stages: each chunk's incoming scan states in `state`.
 template <typename T, int VEC, int K>
 void pk_fwd_states(const dwarf_packet_pool_fwd_args& a, const EmaGeom& g, hipStream_t stream) {
+  if (pk_fwd_lookback<T, VEC, K, false>(a, stream)) return;
   float* ends = static_cast<float*>(a.workspace);
   const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
   const int blocks = static_cast<int>((lanes + kEmaBlock - 1) / kEmaBlock);
@@ -611,6 +791,7 @@ void pk_fwd_states(const dwarf_packet_pool_fwd_args& a, const EmaGeom& g, hipStr
 
 template <typename T, int VEC, int K>
 void pk_fwd_typed(const dwarf_packet_pool_fwd_args& a, hipStream_t stream) {
+  if (pk_fwd_lookback<T, VEC, K, true>(a, stream)) return;
   const EmaGeom g = pk_geom(a.B, a.N, a.D, VEC, a.floor_, a.ceiling);
   pk_fwd_states<T, VEC, K>(a, g, stream);
   const int64_t lanes = static_cast<int64_t>(a.B) * g.NC * g.DV;
@@ -725,7 +906,12 @@ void pkt_bwd_k(const dwarf_packet_bwd_args& p, hipStream_t s) {
 }  // namespace
 
 size_t packet_state_bytes(int B, int N, int D, int K) { return pk_state_floats(B, N, D, K) * sizeof(float); }
-size_t packet_fwd_workspace(int B, int N, int D, int K) { return pk_state_floats(B, N, D, K) * sizeof(float); }
+// The three-stage forward's chunk ends, or the look-back's words, whichever is larger.
+size_t packet_fwd_workspace(int B, int N, int D, int K) {
+  const size_t chunked = pk_state_floats(B, N, D, K) * sizeof(float);
+  const size_t lb = kLbHead + lb_plan(B, N, D, D % 4 == 0 ? 4 : 1, kLbSeg, K).words_bytes;
+  return chunked > lb ? chunked : lb;
+}
 size_t packet_bwd_workspace(int B, int N, int D, int K) { return pk_pool_bwd_ws(B, N, D, K); }
 // The pool's backward workspace, then dpooled [B,N,D] of the pool dtype.
 size_t interference_packet_bwd_workspace(int B, int N, int D, int K, int dtype) {

@@ -276,3 +276,30 @@ def test_wait_limit_gives_up_without_hanging(pkg, device):
     for got, ref in ((y, y_ref), (dx, dx_ref)):
         ok = torch.isnan(got) | (got == ref)
         assert bool(ok.all())
+
+
+def test_three_stage_scan_for_slabs_over_2gib(pkg, device):
+    """An x whose [N][row] slab spans more than 2 GiB (a [1, 300, 64] fp32 view of a wider buffer) is
+    beyond the look-back scan's 32-bit buffer offsets, so both directions take the three-stage chunked
+    scan: y, dx and dalpha within 1e-5 relative of the float64 oracle."""
+    import importlib
+
+    ema = importlib.import_module("dwarf-v2_amd.ema")
+    g = torch.Generator().manual_seed(33)
+    N, D = 300, 64
+    x = torch.randn(1, N, D, generator=g)
+    alpha = torch.rand(D, generator=g) * 0.2 + 0.01
+    dy = torch.randn(1, N, D, generator=g)
+    row = ((1 << 31) // (4 * N) + 8) // 4 * 4
+    big = torch.zeros(1, N, row, device=device, dtype=torch.float32)
+    xv = big[:, :, :D]
+    xv.copy_(x.to(device))
+    ad = alpha.to(device)
+    y = ema.ema_forward(xv, ad, 1e-5, 0.5)
+    dx, da = ema.ema_backward(xv, y, dy.to(device), ad, 1e-5, 0.5, True)
+    torch.cuda.synchronize()
+    ry, rdx, rda = oracle(x, alpha, dy)
+    assert rel_err(y.cpu(), ry) < 1e-5
+    assert rel_err(dx.cpu(), rdx) < 1e-5
+    assert rel_err(da.cpu(), rda) < 1e-5
+    del big

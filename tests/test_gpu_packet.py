@@ -76,7 +76,8 @@ def check(x, a, w, dp, got):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,N,D,K,strided", [(2, 37, 64, 3, False), (1, 9, 12, 2, False), (2, 50, 6, 4, False),
                                              (1, 64, 512, 1, True), (2, 1000, 96, 3, False),
-                                             (12, 150, 512, 3, False), (6, 100, 512, 3, False)])
+                                             (12, 150, 512, 3, False), (6, 100, 512, 3, False),
+                                             (1, 2100, 64, 3, True)])
 def test_matches_oracle(pkg, device, dtype, B, N, D, K, strided):
     x, a, w, dp = inputs(B, N, D, K, dtype, seed=N + D + K, strided=strided)
     check(x, a, w, dp, run(pkg, x, a, w, dp, device))
@@ -314,3 +315,36 @@ def test_packet_deterministic_compile_and_graph(pkg, device):
         torch.cuda.synchronize()
         assert all(torch.equal(u, v) for u, v in zip(outs, ref))
 
+
+
+def _wide_view(B, N, D, like):
+    """A [B, N, D] fp32 view of a wider device buffer whose [N][row] slab spans more than 2 GiB, holding
+    like's values: the kernels' 32-bit buffer offsets cannot reach it, so the forward takes its three-stage
+    path (local, carry, apply) instead of the look-back pass."""
+    row = ((1 << 31) // (4 * N) + 8) // 4 * 4
+    big = torch.zeros(B, N, row, device=like.device, dtype=torch.float32)
+    v = big[:, :, :D]
+    v.copy_(like)
+    return big, v
+
+
+def test_three_stage_forward_for_slabs_over_2gib(pkg, device):
+    """Slabs past 2 GiB take the three-stage forward: pooled, dx and the factor and weight gradients
+    within 1e-5 relative of the float64 oracle, and pooled and the chunk states (what the backward
+    reads) within 1e-6 relative of the look-back pass on the same values in a contiguous tensor."""
+    import importlib
+
+    packet = importlib.import_module("dwarf-v2_amd.packet")
+    B, N, D, K = 1, 300, 64, 3
+    x, a, w, dp = inputs(B, N, D, K, torch.float32, seed=31)
+    xd = x.to(device)
+    big, xv = _wide_view(B, N, D, xd)
+    pooled, state = packet.pool_forward(xv, a, w, 1e-5, 0.5)
+    dx, da, dw = packet.pool_backward(xv, a, w, state, dp.to(device), 1e-5, 0.5)
+    torch.cuda.synchronize()
+    check(x, a, w, dp, (pooled.cpu(), dx.cpu(), da.cpu(), dw.cpu()))
+    pooled_lb, state_lb = packet.pool_forward(xd, a, w, 1e-5, 0.5)
+    torch.cuda.synchronize()
+    assert rel_err(pooled.cpu(), pooled_lb.cpu()) < 1e-6
+    assert rel_err(state.cpu(), state_lb.cpu()) < 1e-6
+    del big
