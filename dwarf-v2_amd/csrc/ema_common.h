@@ -5,6 +5,8 @@
 // them holds its own copy.
 #pragma once
 
+#include <algorithm>
+
 #include "common.h"
 #include "gather.h"
 
@@ -310,7 +312,7 @@ struct LbGeom {
   const uint8_t* reset;
   int64_t srb, srn;
   unsigned long long* words;   // [NWG * S][16 VEC]: workgroup aggregates, (value bits, tag << 32)
-  unsigned long long* runs;    // [ceil(NWG / kLbRun) * S][16 VEC]: the runs' inclusive states
+  unsigned long long* runs;    // [(ceil(NWG / kLbRun) - 1) * S][16 VEC]: inclusive states of all runs but the last
   int64_t kw, kr;              // words and runs of one scale (scale k at words + k kw, runs + k kr)
   float* da_part;              // backward: [NWG][B][D] dalpha partials (row widx * B + b)
   int wait_limit;
@@ -528,9 +530,9 @@ inline LbPlan lb_plan(int B, int N, int D, int vec, int seg, int K = 1) {
   p.NCH = (N + kLbSegs * seg - 1) / (kLbSegs * seg);
   p.NWG = (p.NCH + kLbWaves - 1) / kLbWaves;
   p.S = B * p.CB;
-  const int runs = (p.NWG + kLbRun - 1) / kLbRun;
+  const int runs = (p.NWG + kLbRun - 1) / kLbRun;   // the last run publishes no inclusive state
   p.kw = static_cast<int64_t>(p.NWG) * p.S * ct;
-  p.kr = static_cast<int64_t>(runs) * p.S * ct;
+  p.kr = static_cast<int64_t>(std::max(runs - 1, 0)) * p.S * ct;
   p.words_bytes = static_cast<size_t>(K) * (p.kw + p.kr) * 8;
   return p;
 }
@@ -543,7 +545,7 @@ inline bool lb_fits(int N, int64_t sn, size_t elem) {
 // The zeroing launch ahead of a scan: the words.
 inline void lb_zero(const LbGeom& g, const LbPlan& p, hipStream_t stream) {
   const int64_t n16 = static_cast<int64_t>(p.words_bytes / 16);
-  const int blocks = static_cast<int>((n16 + kEmaBlock - 1) / kEmaBlock < 64 ? (n16 + kEmaBlock - 1) / kEmaBlock : 64);
+  const int blocks = static_cast<int>(std::min<int64_t>(std::max<int64_t>((n16 + kEmaBlock - 1) / kEmaBlock, 1), 1024));
   hipLaunchKernelGGL(ema_lb_zero, dim3(blocks), dim3(kEmaBlock), 0, stream, reinterpret_cast<uint4*>(g.words), n16);
 }
 

@@ -28,6 +28,8 @@
 //                     of T(dpooled scan_k) (dweight)
 //             reduce - the workgroup sums in a fixed order: dalpha with the
 //                      projected-clamp rule of ema:357-364, dweight in T.
+#include <algorithm>
+
 #include "ema_common.h"
 #include "dwarf_dsqg.h"
 
@@ -485,6 +487,265 @@ __global__ __launch_bounds__(kEmaBlock) void packet_bwd_apply(
   }
 }
 
+// Rounded scan values of VEC channels kept between the backward look-back's
+// forward recompute and its reverse pass: bf16 four to two registers.
+template <typename T, int VEC>
+struct LbKeep {
+  float v[VEC];
+  __device__ __forceinline__ void put(const float* y, float* s) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) s[i] = v[i] = rnd<T>(y[i]);
+  }
+  __device__ __forceinline__ float get(int i) const { return v[i]; }
+};
+template <>
+struct LbKeep<bf16, 4> {
+  uint32_t w[2];
+  __device__ __forceinline__ void put(const float* y, float* s) {
+    w[0] = pack_bf16x2(y[0], y[1]);
+    w[1] = pack_bf16x2(y[2], y[3]);
+    s[0] = bf16_lo(w[0]); s[1] = bf16_hi(w[0]); s[2] = bf16_lo(w[1]); s[3] = bf16_hi(w[1]);
+  }
+  __device__ __forceinline__ float get(int i) const { return (i & 1) ? bf16_hi(w[i / 2]) : bf16_lo(w[i / 2]); }
+};
+
+// The pool's backward in one pass with the decoupled look-back, in reverse
+// time (workgroup tile 0 holds the last tokens), where every [N][D] slab of
+// x, dpooled and dx spans less than 2 GiB.  Lane (cg, ts) holds VEC channels
+// of a 32-token segment:
+//   1. the adjoints of the K scans over the segment from zero, on
+//      dscan_k = T(dpooled w_k), and the segment's factor (1 - a_k)^len;
+//   2-4. the segments' and tiles' maps composed as in the forward, K
+//      aggregates per channel published and walked (lb_join), giving the
+//      adjoint entering each segment from the tokens after it;
+//   5. the segment again, KT tokens at a time from its end: the scans of
+//      the KT tokens recomputed forward from the state entering their
+//      16-token chunk (`state`, as the forward wrote it; a block that starts
+//      inside a chunk recomputes from the chunk's start), each rounded to T
+//      as the pool stored it and kept in registers, the dweight terms
+//      T(dpooled scan_k) summed on the way, then the adjoints run back over
+//      the block: dx = sum_k a_k lambda_k and the dalpha terms
+//      lambda_k (x[t] - scan_k[t-1]).
+// Each workgroup's dweight and dalpha sums (wave butterflies, then the waves
+// in order) go to one slot per (quantity, workgroup): part[q * slots + id].
+template <typename T, int VEC, int K, int KT>
+__global__ __launch_bounds__(kWave * kLbWaves) void packet_bwd_lb(
+    const T* __restrict__ x, int64_t sxb, int64_t sxn, const T* __restrict__ dp, int64_t sgb, int64_t sgn,
+    T* __restrict__ dx, int64_t sdb, int64_t sdn, const float* __restrict__ alpha, const float* __restrict__ weight,
+    const float* __restrict__ state, float* __restrict__ part, LbGeom g, int NC) {
+  constexpr int SEG = kLbSeg;
+  constexpr int CT = kLbGroups * VEC;
+  static_assert(kChunkT % KT == 0 && SEG % kChunkT == 0, "blocks tile the chunks");
+  __shared__ LbShared<K> sh;
+  __shared__ float s_p[kLbWaves][2 * K];
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+  const int cg = lane & 15, ts = lane >> 4;
+  const int id = blockIdx.x;   // workgroups of lower index are dispatched first
+  const int widx = id / g.S, slice = id - widx * g.S;
+  const int chunk = g.NCH - 1 - (widx * kLbWaves + w);   // a chunk below 0 holds no tokens
+  const int b = slice / g.CB, cb = slice - b * g.CB;
+  const int d0 = (cb * kLbGroups + cg) * VEC;
+  const bool dlive = d0 < g.D;
+  const int s0 = (chunk * kLbSegs + ts) * SEG;
+  const int len = chunk < 0 ? 0 : max(0, min(SEG, g.N - s0));
+  float a[K], dec[K], wk[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    a[k] = fminf(fmaxf(alpha[k], g.lo), g.hi);
+    dec[k] = 1.f - a[k];
+    wk[k] = rnd<T>(weight[k]);
+  }
+  const __amdgpu_buffer_rsrc_t rg = lb_rsrc(dp, sgb, sgn, b, g.N);
+  const uint32_t rsg = static_cast<uint32_t>(sgn * sizeof(T)), cog = static_cast<uint32_t>(d0 * sizeof(T));
+
+  // 1. the segment in reverse time from zero adjoints, every scale
+  float L[K][VEC], A[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    A[k] = 1.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) L[k][i] = 0.f;
+  }
+  {
+    LbRaw<T, VEC> raw[SEG];
+#pragma unroll
+    for (int t = 0; t < SEG; ++t)
+      raw[t].load(rg, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsg + cog : kOutOfRange);
+#pragma unroll
+    for (int t = SEG - 1; t >= 0; --t) {
+      if (t < len) {
+        float v[VEC];
+        raw[t].widen(v);
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) L[k][i] = fmaf(dec[k], L[k][i], rnd<T>(v[i] * wk[k]));
+          A[k] *= dec[k];
+        }
+      }
+    }
+  }
+  // 2. the segments composed in reverse time order (3, 2, 1, 0): the tile's (P, Q) and this lane's prefix
+  float P[K], Q[K][VEC], Pp[K], Qp[K][VEC];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    P[k] = 1.f;
+    Pp[k] = 1.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) { Q[k][i] = 0.f; Qp[k][i] = 0.f; }
+  }
+#pragma unroll
+  for (int s = kLbSegs - 1; s >= 0; --s) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float As = __shfl(A[k], cg + 16 * s);
+      Pp[k] = s == ts ? P[k] : Pp[k];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float Ls = __shfl(L[k][i], cg + 16 * s);
+        Qp[k][i] = s == ts ? Q[k][i] : Qp[k][i];
+        Q[k][i] = fmaf(As, Q[k][i], Ls);
+      }
+      P[k] *= As;
+    }
+  }
+  // 3-4. publish and walk back over the workgroups of later tokens
+  const int io = VEC == 4 ? ts : 0;
+  const bool owner = (VEC == 4 || ts == 0) && dlive && d0 + io < g.D;
+  float Qo[K], full_wg[K], C[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    Qo[k] = VEC == 4 ? pick4(io, Q[k][0], Q[k][VEC > 1 ? 1 : 0], Q[k][VEC > 2 ? 2 : 0], Q[k][VEC > 3 ? 3 : 0])
+                     : Q[k][0];
+    float seg = 1.f, full = 1.f;   // a full tile's factor, composed as a tile composes its segments
+    for (int t = 0; t < SEG; ++t) seg *= dec[k];
+#pragma unroll
+    for (int s = 0; s < kLbSegs; ++s) full *= seg;
+    full_wg[k] = 1.f;
+#pragma unroll
+    for (int j = 0; j < kLbWaves; ++j) full_wg[k] *= full;
+  }
+  lb_join<K>(g, sh, slice, cg * VEC + io, owner, CT, widx, w, P, Qo, full_wg, C);
+  // 5. the adjoints entering the segment from the tokens after it, then the blocks from the segment's end
+  float lam[K][VEC], da[K][VEC], dw[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    dw[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      lam[k][i] = fmaf(Pp[k], __shfl(C[k], VEC == 4 ? cg + 16 * i : cg), Qp[k][i]);
+      da[k][i] = 0.f;
+    }
+  }
+  const __amdgpu_buffer_rsrc_t rx = lb_rsrc(x, sxb, sxn, b, g.N);
+  const __amdgpu_buffer_rsrc_t rd = lb_rsrc(dx, sdb, sdn, b, g.N);
+  const uint32_t rsx = static_cast<uint32_t>(sxn * sizeof(T)), cox = static_cast<uint32_t>(d0 * sizeof(T));
+  const uint32_t rsd = static_cast<uint32_t>(sdn * sizeof(T)), cod = static_cast<uint32_t>(d0 * sizeof(T));
+#pragma unroll
+  for (int u0 = SEG - KT; u0 >= 0; u0 -= KT) {
+    if (u0 < len) {
+      const int c0 = u0 / kChunkT * kChunkT;   // the block's chunk starts at token s0 + c0
+      constexpr int R = kChunkT;               // rows c0 .. u0 + KT - 1 (at most one chunk)
+      LbRaw<T, VEC> xr[R], gr[KT];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int t = c0 + r;
+        if (t < u0 + KT)
+          xr[r].load(rx, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsx + cox : kOutOfRange);
+      }
+#pragma unroll
+      for (int r = 0; r < KT; ++r) {
+        const int t = u0 + r;
+        gr[r].load(rg, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsg + cog : kOutOfRange);
+      }
+      // the scans entering the chunk, as the forward kept them
+      float y[K][VEC], prev[K][VEC];
+      const int64_t srow = ((static_cast<int64_t>(b) * NC + (s0 + c0) / kChunkT) * K) * g.D + d0;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if constexpr (VEC == 4) {
+          const float4 v = dlive ? *reinterpret_cast<const float4*>(state + srow + k * g.D) : make_float4(0, 0, 0, 0);
+          y[k][0] = v.x; y[k][VEC > 1 ? 1 : 0] = v.y; y[k][VEC > 2 ? 2 : 0] = v.z; y[k][VEC > 3 ? 3 : 0] = v.w;
+        } else {
+          y[k][0] = dlive ? state[srow + k * g.D] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) prev[k][i] = s0 + c0 > 0 ? rnd<T>(y[k][i]) : 0.f;   // scan_k[t - 1] as stored
+      }
+      // forward over rows c0 .. u0 + KT - 1, keeping the block's rounded scans and summing its dweight terms
+      LbKeep<T, VEC> keep[KT][K];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int t = c0 + r;
+        if (t < u0 + KT && t < len) {
+          float xv[VEC];
+          xr[r].widen(xv);
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) y[k][i] = fmaf(a[k], xv[i], dec[k] * y[k][i]);
+            if (t >= u0) {
+              float sv[VEC], gv[VEC];
+              keep[t - u0 < 0 ? 0 : t - u0][k].put(y[k], sv);
+              gr[t - u0 < 0 ? 0 : t - u0].widen(gv);
+#pragma unroll
+              for (int i = 0; i < VEC; ++i) dw[k] += rnd<T>(gv[i] * sv[i]);
+            } else if (t == u0 - 1) {
+#pragma unroll
+              for (int i = 0; i < VEC; ++i) prev[k][i] = rnd<T>(y[k][i]);
+            }
+          }
+        }
+      }
+      // back over the block: the adjoints, dx and the dalpha terms
+#pragma unroll
+      for (int r = KT - 1; r >= 0; --r) {
+        const int t = u0 + r;
+        if (t < len) {
+          float xv[VEC], gv[VEC], out[VEC];
+          xr[t - c0].widen(xv);
+          gr[r].widen(gv);
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              lam[k][i] = fmaf(dec[k], lam[k][i], rnd<T>(gv[i] * wk[k]));
+              acc = fmaf(a[k], lam[k][i], acc);
+              const float sprev = r > 0 ? keep[r > 0 ? r - 1 : 0][k].get(i) : prev[k][i];
+              da[k][i] = fmaf(lam[k][i], xv[i] - sprev, da[k][i]);
+            }
+            out[i] = acc;
+          }
+          lb_store<T, VEC>(rd, dlive ? static_cast<uint32_t>(s0 + t) * rsd + cod : kOutOfRange, out);
+        }
+      }
+    }
+  }
+  // the workgroup's sums: dweight_k (q = k) and dalpha_k (q = K + k)
+#pragma unroll
+  for (int q = 0; q < 2 * K; ++q) {
+    float v;
+    if (q < K) {
+      v = dw[q];
+    } else {
+      v = da[q - K][0];
+#pragma unroll
+      for (int i = 1; i < VEC; ++i) v += da[q - K][i];
+    }
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o);
+    if (lane == 0) s_p[w][q] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * K) {
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < kLbWaves; ++j) t += s_p[j][threadIdx.x];
+    part[static_cast<int64_t>(threadIdx.x) * gridDim.x + id] = t;
+  }
+}
+
 // Row q of the per-workgroup partials, summed in a fixed order (thread i adds
 // slots i, i + 1024, ... in order, the wave by a fixed butterfly, the waves in
 // wave order): dweight_k = T(row k), as a sum-reduction in T returns it;
@@ -725,13 +986,40 @@ inline size_t pk_state_floats(int B, int N, int D, int K) {
   return static_cast<size_t>(B) * pk_nc(N) * D * K;
 }
 
-// The pool backward's workspace: starts and carries (K*D per chunk each),
-// then 2K slots per apply workgroup (a lane takes at least one (chunk,
-// channel) pair, so at most ceil(B*NC*D / 256) workgroups).
+inline size_t pk_round256(size_t n) { return (n + 255) / 256 * 256; }
+
+// The look-back backward's workspace: the head, the words of K scales, then
+// 2K slots per workgroup.
+inline size_t pk_lb_bwd_ws(int B, int N, int D, int K, int vec) {
+  const LbPlan p = lb_plan(B, N, D, vec, kLbSeg, K);
+  return kLbHead + pk_round256(p.words_bytes) + 2 * static_cast<size_t>(K) * p.NWG * p.S * sizeof(float);
+}
+
+// The pool backward's workspace: the three-stage backward's starts and
+// carries (K*D per chunk each) and 2K slots per apply workgroup (a lane
+// takes at least one (chunk, channel) pair, so at most ceil(B*NC*D / 256)
+// workgroups), or the look-back's (four channels or one per lane), whichever
+// is largest.
 inline size_t pk_pool_bwd_ws(int B, int N, int D, int K) {
   const size_t pairs = static_cast<size_t>(B) * pk_nc(N) * D;
-  return (2 * pk_state_floats(B, N, D, K) + 2 * static_cast<size_t>(K) * ((pairs + kEmaBlock - 1) / kEmaBlock)) *
-         sizeof(float);
+  size_t n = (2 * pk_state_floats(B, N, D, K) + 2 * static_cast<size_t>(K) * ((pairs + kEmaBlock - 1) / kEmaBlock)) *
+             sizeof(float);
+  n = std::max(n, pk_lb_bwd_ws(B, N, D, K, 1));
+  return std::max(n, pk_lb_bwd_ws(B, N, D, K, 4));
+}
+
+// The look-back geometry of a pool scan (K scales' words after the head of ws).
+inline LbGeom pk_lb_geom(int B, int N, int D, int K, float lo, float hi, void* ws, const LbPlan& p) {
+  LbGeom g{};
+  g.B = B; g.N = N; g.D = D;
+  g.CB = p.CB; g.NCH = p.NCH; g.NWG = p.NWG; g.S = p.S;
+  g.lo = lo; g.hi = hi;
+  g.words = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + kLbHead);
+  g.runs = g.words + K * p.kw;
+  g.kw = p.kw;
+  g.kr = p.kr;
+  g.wait_limit = kLbWaitLimit;
+  return g;
 }
 
 // The geometry of the x-shaped stages (D channels, VEC per lane).
@@ -759,15 +1047,7 @@ bool pk_fwd_lookback(const dwarf_packet_pool_fwd_args& a, hipStream_t stream) {
   if (!lb_fits(a.N, a.x_stride[1], sizeof(T)) || (POOLED && !lb_fits(a.N, a.pooled_stride[1], sizeof(T))))
     return false;
   const LbPlan p = lb_plan(a.B, a.N, a.D, VEC, kLbSeg, K);
-  LbGeom g{};
-  g.B = a.B; g.N = a.N; g.D = a.D;
-  g.CB = p.CB; g.NCH = p.NCH; g.NWG = p.NWG; g.S = p.S;
-  g.lo = a.floor_; g.hi = a.ceiling;
-  g.words = reinterpret_cast<unsigned long long*>(static_cast<char*>(a.workspace) + kLbHead);
-  g.runs = g.words + K * p.kw;
-  g.kw = p.kw;
-  g.kr = p.kr;
-  g.wait_limit = kLbWaitLimit;
+  const LbGeom g = pk_lb_geom(a.B, a.N, a.D, K, a.floor_, a.ceiling, a.workspace, p);
   lb_zero(g, p, stream);
   hipLaunchKernelGGL((packet_fwd_lb<T, VEC, K, POOLED>), dim3(p.NWG * p.S), dim3(kWave * kLbWaves), 0, stream,
                      static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<T*>(a.pooled),
@@ -817,8 +1097,41 @@ void pkt_fwd_typed(const dwarf_packet_fwd_args& p, hipStream_t stream) {
                      a.alpha, a.weight, a.state, g);
 }
 
+// The backward in one pass where every [N][D] slab of x, dpooled and dx spans
+// less than 2 GiB: the words' zeroing launch, packet_bwd_lb, then the
+// parameter sums over its workgroups' slots.  False: the three-stage
+// backward runs instead.
+template <typename T, int VEC, int K, int KT>
+bool pk_bwd_lookback(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
+  const dwarf_packet_pool_fwd_args& f = a.fwd;
+  if (!lb_fits(f.N, f.x_stride[1], sizeof(T)) || !lb_fits(f.N, a.dpooled_stride[1], sizeof(T)) ||
+      !lb_fits(f.N, a.dx_stride[1], sizeof(T)))
+    return false;
+  const LbPlan p = lb_plan(f.B, f.N, f.D, VEC, kLbSeg, K);
+  const LbGeom g = pk_lb_geom(f.B, f.N, f.D, K, f.floor_, f.ceiling, a.workspace, p);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kLbHead + pk_round256(p.words_bytes));
+  const int slots = p.NWG * p.S;
+  lb_zero(g, p, stream);
+  hipLaunchKernelGGL((packet_bwd_lb<T, VEC, K, KT>), dim3(slots), dim3(kWave * kLbWaves), 0, stream,
+                     static_cast<const T*>(f.x), f.x_stride[0], f.x_stride[1], static_cast<const T*>(a.dpooled),
+                     a.dpooled_stride[0], a.dpooled_stride[1], static_cast<T*>(a.dx), a.dx_stride[0], a.dx_stride[1],
+                     f.alpha, f.weight, f.state, part, g, pk_nc(f.N));
+  if (a.dalpha || a.dweight) {
+    const EmaGeom ga = pk_geom(f.B, f.N, f.D, 1, f.floor_, f.ceiling);
+    hipLaunchKernelGGL((packet_param_reduce<T>), dim3(2 * K), dim3(kPkRedThreads), 0, stream, part,
+                       static_cast<int64_t>(slots), K, f.alpha, a.dweight, a.dalpha, ga);
+  }
+  return true;
+}
+
+// Rows a lane keeps per block of the look-back backward's reverse pass (bf16,
+// four channels per lane; one channel per lane keeps a whole chunk).
+constexpr int kPkLbKeep = 8;
+
 template <typename T, int VEC, int VA, int K>
 void pk_bwd_typed(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
+  constexpr int LBV = sizeof(T) == 2 && VEC == 4 ? 4 : 1;
+  if (pk_bwd_lookback<T, LBV, K, LBV == 4 ? kPkLbKeep : kChunkT>(a, stream)) return;
   const dwarf_packet_pool_fwd_args& f = a.fwd;
   const size_t nf = pk_state_floats(f.B, f.N, f.D, K);
   float* starts = static_cast<float*>(a.workspace);

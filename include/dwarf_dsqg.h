@@ -286,7 +286,10 @@ int dwarf_ema_bwd(const dwarf_ema_bwd_args* args, dwarf_stream_t stream);
  * arithmetic rounds them (train:262-267 with K = 3 timescales).  `state`
  * (dwarf_packet_pool_state_bytes, fp32) receives each 16-token chunk's
  * incoming scan states; the backward reads it.  Workspaces are 16-byte
- * aligned.
+ * aligned.  Where every [N][D] slab of the operands spans less than 2 GiB,
+ * forward and backward each run as one pass with the EMA's decoupled
+ * look-back (a wait that gives up after 2^22 polls poisons its channels
+ * with NaN instead of hanging); larger slabs take the three-stage scans.
  */
 #define DWARF_PACKET_MAX_SCALES 4
 

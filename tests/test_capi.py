@@ -145,8 +145,13 @@ def test_validation_errors_without_gpu(pkg, lib):
     kb = L.PacketPoolBwdArgs()
     kb.fwd = k
     assert lib.dwarf_packet_pool_bwd(ctypes.byref(kb), None) == L.DWARF_ERR_INVALID_ARGUMENT
-    # starts and carries [B][N/16][K*D] fp32, then 2K slots per apply workgroup (one here)
-    assert lib.dwarf_packet_pool_bwd_workspace_bytes(ctypes.byref(kb)) == (2 * 1 * 2 * 3 * 8 + 2 * 3) * 4
+    # the larger of the three-stage backward's (starts and carries [B][N/16][K*D] fp32, then 2K slots per
+    # apply workgroup, one here: 408 bytes) and the look-back's: a 256-byte head, the words of K scales
+    # (one workgroup tile's aggregates, 16 VEC channels; VEC 4 is the larger; a single run keeps no run
+    # states), then 2K slots per workgroup
+    three_stage = (2 * 1 * 2 * 3 * 8 + 2 * 3) * 4
+    lookback = 256 + 3 * 64 * 8 + 2 * 3 * 4
+    assert lib.dwarf_packet_pool_bwd_workspace_bytes(ctypes.byref(kb)) == max(three_stage, lookback)
     pf = L.PacketFwdArgs()
     pf.pool = k
     pf.pool.floor_, pf.pool.ceiling = 1e-5, 0.5
@@ -160,7 +165,7 @@ def test_validation_errors_without_gpu(pkg, lib):
     pbk.fwd = pf
     pbk.fwd.pool.D = 8
     # the pool's backward workspace (256-byte aligned), then dpooled [B,N,D] bf16
-    assert lib.dwarf_packet_bwd_workspace_bytes(ctypes.byref(pbk)) == 512 + 1 * 32 * 8 * 2   # 408 -> 512
+    assert lib.dwarf_packet_bwd_workspace_bytes(ctypes.byref(pbk)) == 2048 + 1 * 32 * 8 * 2   # 1816 -> 2048
     assert lib.dwarf_packet_bwd(ctypes.byref(pbk), None) == L.DWARF_ERR_INVALID_ARGUMENT  # x is NULL
 
 

@@ -8,7 +8,8 @@ against the oracle's bf16 rounding of each term, the factor gradients within
 1e-3 and the weight gradients (returned in bf16 precision) within 1e-2
 relative.  Cases: K = 1..4, D with and without 4-channel vectors, N below one
 16-token chunk, not a multiple of 16, and long enough for the carry stage to
-join many chunks, B*K*D wide enough for the 64- and 32-channel carry runs, a
+join many chunks and for the look-back scans to span two runs of workgroup
+tiles (17,000 tokens), B*K*D wide enough for the 64- and 32-channel carry runs, a
 strided x view, a factor outside [floor, ceiling];
 determinism and torch.compile; and ``interference_packet_forward`` against
 the same module composed of separate ``causal_ema_scan`` calls.
@@ -77,7 +78,7 @@ def check(x, a, w, dp, got):
 @pytest.mark.parametrize("B,N,D,K,strided", [(2, 37, 64, 3, False), (1, 9, 12, 2, False), (2, 50, 6, 4, False),
                                              (1, 64, 512, 1, True), (2, 1000, 96, 3, False),
                                              (12, 150, 512, 3, False), (6, 100, 512, 3, False),
-                                             (1, 2100, 64, 3, True)])
+                                             (1, 2100, 64, 3, True), (1, 17000, 64, 3, False)])
 def test_matches_oracle(pkg, device, dtype, B, N, D, K, strided):
     x, a, w, dp = inputs(B, N, D, K, dtype, seed=N + D + K, strided=strided)
     check(x, a, w, dp, run(pkg, x, a, w, dp, device))
@@ -91,6 +92,11 @@ def test_factor_outside_bounds_uses_projected_derivative(pkg, device):
 
 
 def test_deterministic_and_compile(pkg, device):
+    # 17,000 tokens: 34 workgroup tiles of the look-back scans per channel block, in two runs
+    xl, al, wl, dpl = inputs(2, 17000, 128, 3, torch.bfloat16, seed=10)
+    r1 = run(pkg, xl, al, wl, dpl, device)
+    r2 = run(pkg, xl, al, wl, dpl, device)
+    assert all(torch.equal(u, v) for u, v in zip(r1, r2))
     x, a, w, dp = inputs(2, 300, 64, 3, torch.bfloat16, seed=9)
     r1 = run(pkg, x, a, w, dp, device)
     r2 = run(pkg, x, a, w, dp, device)
