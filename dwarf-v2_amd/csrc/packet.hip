@@ -38,6 +38,12 @@ namespace {
 
 constexpr int kMaxScales = 4;
 constexpr int kPkRedThreads = 1024;
+// Rows a lane keeps per block of the look-back backward's reverse pass (bf16,
+// four channels per lane; one channel per lane keeps a whole chunk).
+constexpr int kPkLbKeep = 8;
+// Tokens per lane segment of the look-back backward (16-token segments, twice
+// the waves, measured 2 us slower at [15, 2048, 512]).
+constexpr int kPkLbSeg = kLbSeg;
 
 // The value a T tensor holds for v.
 template <typename T>
@@ -528,12 +534,11 @@ struct LbKeep<bf16, 4> {
 //      lambda_k (x[t] - scan_k[t-1]).
 // Each workgroup's dweight and dalpha sums (wave butterflies, then the waves
 // in order) go to one slot per (quantity, workgroup): part[q * slots + id].
-template <typename T, int VEC, int K, int KT>
+template <typename T, int VEC, int K, int KT, int SEG>
 __global__ __launch_bounds__(kWave * kLbWaves) void packet_bwd_lb(
     const T* __restrict__ x, int64_t sxb, int64_t sxn, const T* __restrict__ dp, int64_t sgb, int64_t sgn,
     T* __restrict__ dx, int64_t sdb, int64_t sdn, const float* __restrict__ alpha, const float* __restrict__ weight,
     const float* __restrict__ state, float* __restrict__ part, LbGeom g, int NC) {
-  constexpr int SEG = kLbSeg;
   constexpr int CT = kLbGroups * VEC;
   static_assert(kChunkT % KT == 0 && SEG % kChunkT == 0, "blocks tile the chunks");
   __shared__ LbShared<K> sh;
@@ -990,8 +995,8 @@ inline size_t pk_round256(size_t n) { return (n + 255) / 256 * 256; }
 
 // The look-back backward's workspace: the head, the words of K scales, then
 // 2K slots per workgroup.
-inline size_t pk_lb_bwd_ws(int B, int N, int D, int K, int vec) {
-  const LbPlan p = lb_plan(B, N, D, vec, kLbSeg, K);
+inline size_t pk_lb_bwd_ws(int B, int N, int D, int K, int vec, int seg) {
+  const LbPlan p = lb_plan(B, N, D, vec, seg, K);
   return kLbHead + pk_round256(p.words_bytes) + 2 * static_cast<size_t>(K) * p.NWG * p.S * sizeof(float);
 }
 
@@ -1004,8 +1009,8 @@ inline size_t pk_pool_bwd_ws(int B, int N, int D, int K) {
   const size_t pairs = static_cast<size_t>(B) * pk_nc(N) * D;
   size_t n = (2 * pk_state_floats(B, N, D, K) + 2 * static_cast<size_t>(K) * ((pairs + kEmaBlock - 1) / kEmaBlock)) *
              sizeof(float);
-  n = std::max(n, pk_lb_bwd_ws(B, N, D, K, 1));
-  return std::max(n, pk_lb_bwd_ws(B, N, D, K, 4));
+  n = std::max(n, pk_lb_bwd_ws(B, N, D, K, 1, kPkLbSeg));
+  return std::max(n, pk_lb_bwd_ws(B, N, D, K, 4, kPkLbSeg));
 }
 
 // The look-back geometry of a pool scan (K scales' words after the head of ws).
@@ -1101,18 +1106,18 @@ void pkt_fwd_typed(const dwarf_packet_fwd_args& p, hipStream_t stream) {
 // less than 2 GiB: the words' zeroing launch, packet_bwd_lb, then the
 // parameter sums over its workgroups' slots.  False: the three-stage
 // backward runs instead.
-template <typename T, int VEC, int K, int KT>
+template <typename T, int VEC, int K, int KT, int SEG>
 bool pk_bwd_lookback(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
   const dwarf_packet_pool_fwd_args& f = a.fwd;
   if (!lb_fits(f.N, f.x_stride[1], sizeof(T)) || !lb_fits(f.N, a.dpooled_stride[1], sizeof(T)) ||
       !lb_fits(f.N, a.dx_stride[1], sizeof(T)))
     return false;
-  const LbPlan p = lb_plan(f.B, f.N, f.D, VEC, kLbSeg, K);
+  const LbPlan p = lb_plan(f.B, f.N, f.D, VEC, SEG, K);
   const LbGeom g = pk_lb_geom(f.B, f.N, f.D, K, f.floor_, f.ceiling, a.workspace, p);
   float* part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kLbHead + pk_round256(p.words_bytes));
   const int slots = p.NWG * p.S;
   lb_zero(g, p, stream);
-  hipLaunchKernelGGL((packet_bwd_lb<T, VEC, K, KT>), dim3(slots), dim3(kWave * kLbWaves), 0, stream,
+  hipLaunchKernelGGL((packet_bwd_lb<T, VEC, K, KT, SEG>), dim3(slots), dim3(kWave * kLbWaves), 0, stream,
                      static_cast<const T*>(f.x), f.x_stride[0], f.x_stride[1], static_cast<const T*>(a.dpooled),
                      a.dpooled_stride[0], a.dpooled_stride[1], static_cast<T*>(a.dx), a.dx_stride[0], a.dx_stride[1],
                      f.alpha, f.weight, f.state, part, g, pk_nc(f.N));
@@ -1124,14 +1129,11 @@ bool pk_bwd_lookback(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
   return true;
 }
 
-// Rows a lane keeps per block of the look-back backward's reverse pass (bf16,
-// four channels per lane; one channel per lane keeps a whole chunk).
-constexpr int kPkLbKeep = 8;
 
 template <typename T, int VEC, int VA, int K>
 void pk_bwd_typed(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
   constexpr int LBV = sizeof(T) == 2 && VEC == 4 ? 4 : 1;
-  if (pk_bwd_lookback<T, LBV, K, LBV == 4 ? kPkLbKeep : kChunkT>(a, stream)) return;
+  if (pk_bwd_lookback<T, LBV, K, LBV == 4 ? kPkLbKeep : kChunkT, kPkLbSeg>(a, stream)) return;
   const dwarf_packet_pool_fwd_args& f = a.fwd;
   const size_t nf = pk_state_floats(f.B, f.N, f.D, K);
   float* starts = static_cast<float*>(a.workspace);
