@@ -78,7 +78,8 @@ def check(x, a, w, dp, got):
 @pytest.mark.parametrize("B,N,D,K,strided", [(2, 37, 64, 3, False), (1, 9, 12, 2, False), (2, 50, 6, 4, False),
                                              (1, 64, 512, 1, True), (2, 1000, 96, 3, False),
                                              (12, 150, 512, 3, False), (6, 100, 512, 3, False),
-                                             (1, 2100, 64, 3, True), (1, 17000, 64, 3, False)])
+                                             (1, 2100, 64, 3, True), (1, 17000, 64, 3, False),
+                                             (2, 700, 128, 4, False)])
 def test_matches_oracle(pkg, device, dtype, B, N, D, K, strided):
     x, a, w, dp = inputs(B, N, D, K, dtype, seed=N + D + K, strided=strided)
     check(x, a, w, dp, run(pkg, x, a, w, dp, device))
