@@ -53,6 +53,47 @@ __device__ __forceinline__ float rnd<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ float rnd<bf16>(float v) { return round_bf16(v); }
 
+// rnd<T> of VEC values in place, bf16 two to a conversion (v_cvt_pk_bf16_f32
+// rounds both halves to nearest even, as the single conversion does).
+template <typename T, int VEC>
+__device__ __forceinline__ void rnd_vec(float* v) {
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int i = 0; i + 1 < VEC; i += 2) {
+      const uint32_t w = pack_bf16x2(v[i], v[i + 1]);
+      v[i] = bf16_lo(w);
+      v[i + 1] = bf16_hi(w);
+    }
+    if constexpr (VEC & 1) v[VEC - 1] = round_bf16(v[VEC - 1]);
+  }
+}
+
+// One token of the pool for VEC channels: each scan advanced over x, then
+// pooled = T(...T(T(w_0 T(scan_0)) + T(w_1 T(scan_1)))...), every value's
+// operations in the reference's order.
+template <typename T, int VEC, int K>
+__device__ __forceinline__ void pool_token(const float* xv, const float* a, const float* dec, const float* wk,
+                                           float (&st)[K][VEC], float* out) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    float term[VEC];
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) term[i] = st[k][i] = fmaf(a[k], xv[i], dec[k] * st[k][i]);
+    rnd_vec<T, VEC>(term);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) term[i] *= wk[k];
+    rnd_vec<T, VEC>(term);
+    if (k == 0) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) out[i] = term[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) out[i] += term[i];
+      rnd_vec<T, VEC>(out);
+    }
+  }
+}
+
 // Factor k clamped to [lo, hi] (one scalar EMA factor per scale, ema:274-277).
 __device__ __forceinline__ float pk_alpha(const float* alpha, int k, const EmaGeom& g) {
   return fminf(fmaxf(alpha[k], g.lo), g.hi);
@@ -284,17 +325,7 @@ __global__ __launch_bounds__(kWave * kLbWaves) void packet_fwd_lb(const T* __res
       float v[VEC];
       raw[t].widen(v);
       float out[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        float acc = 0.f;
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          st[k][i] = fmaf(a[k], v[i], dec[k] * st[k][i]);
-          const float term = rnd<T>(wk[k] * rnd<T>(st[k][i]));
-          acc = k == 0 ? term : rnd<T>(acc + term);
-        }
-        out[i] = acc;
-      }
+      pool_token<T, VEC, K>(v, a, dec, wk, st, out);
       if constexpr (POOLED) lb_store<T, VEC>(rp, dlive ? static_cast<uint32_t>(s0 + t) * rsp + cop : kOutOfRange, out);
     }
   }
@@ -583,8 +614,12 @@ __global__ __launch_bounds__(kWave * kLbWaves) void packet_bwd_lb(
         raw[t].widen(v);
 #pragma unroll
         for (int k = 0; k < K; ++k) {
+          float gk[VEC];
 #pragma unroll
-          for (int i = 0; i < VEC; ++i) L[k][i] = fmaf(dec[k], L[k][i], rnd<T>(v[i] * wk[k]));
+          for (int i = 0; i < VEC; ++i) gk[i] = v[i] * wk[k];
+          rnd_vec<T, VEC>(gk);
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) L[k][i] = fmaf(dec[k], L[k][i], gk[i]);
           A[k] *= dec[k];
         }
       }
@@ -677,7 +712,7 @@ __global__ __launch_bounds__(kWave * kLbWaves) void packet_bwd_lb(
 #pragma unroll
         for (int i = 0; i < VEC; ++i) prev[k][i] = s0 + c0 > 0 ? rnd<T>(y[k][i]) : 0.f;   // scan_k[t - 1] as stored
       }
-      // forward over rows c0 .. u0 + KT - 1, keeping the block's rounded scans and summing its dweight terms
+      // forward over rows c0 .. u0 + KT - 1, keeping the block's rounded scans
       LbKeep<T, VEC> keep[KT][K];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -690,11 +725,8 @@ __global__ __launch_bounds__(kWave * kLbWaves) void packet_bwd_lb(
 #pragma unroll
             for (int i = 0; i < VEC; ++i) y[k][i] = fmaf(a[k], xv[i], dec[k] * y[k][i]);
             if (t >= u0) {
-              float sv[VEC], gv[VEC];
+              float sv[VEC];
               keep[t - u0 < 0 ? 0 : t - u0][k].put(y[k], sv);
-              gr[t - u0 < 0 ? 0 : t - u0].widen(gv);
-#pragma unroll
-              for (int i = 0; i < VEC; ++i) dw[k] += rnd<T>(gv[i] * sv[i]);
             } else if (t == u0 - 1) {
 #pragma unroll
               for (int i = 0; i < VEC; ++i) prev[k][i] = rnd<T>(y[k][i]);
@@ -702,20 +734,33 @@ __global__ __launch_bounds__(kWave * kLbWaves) void packet_bwd_lb(
           }
         }
       }
-      // back over the block: the adjoints, dx and the dalpha terms
+      // back over the block: the dweight terms, the adjoints, dx and the dalpha terms
 #pragma unroll
       for (int r = KT - 1; r >= 0; --r) {
         const int t = u0 + r;
         if (t < len) {
-          float xv[VEC], gv[VEC], out[VEC];
+          float xv[VEC], gv[VEC], out[VEC], gk[K][VEC];
           xr[t - c0].widen(xv);
           gr[r].widen(gv);
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            float pr[VEC];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              gk[k][i] = gv[i] * wk[k];
+              pr[i] = gv[i] * keep[r][k].get(i);
+            }
+            rnd_vec<T, VEC>(gk[k]);
+            rnd_vec<T, VEC>(pr);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) dw[k] += pr[i];
+          }
 #pragma unroll
           for (int i = 0; i < VEC; ++i) {
             float acc = 0.f;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
-              lam[k][i] = fmaf(dec[k], lam[k][i], rnd<T>(gv[i] * wk[k]));
+              lam[k][i] = fmaf(dec[k], lam[k][i], gk[k][i]);
               acc = fmaf(a[k], lam[k][i], acc);
               const float sprev = r > 0 ? keep[r > 0 ? r - 1 : 0][k].get(i) : prev[k][i];
               da[k][i] = fmaf(lam[k][i], xv[i] - sprev, da[k][i]);
@@ -845,11 +890,12 @@ __global__ __launch_bounds__(kPkRowMaxThreads) void packet_fwd_rows(
 #pragma unroll
     for (int i = 0; i < VEC; ++i) u[t][i] = 0.f;
   if (live) {
-    float a[K], wk[K], st[K][VEC];
+    float a[K], dec[K], wk[K], st[K][VEC];
     const float* cr = state + (static_cast<int64_t>(b) * g.NC + c) * (K * g.D) + d0;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       a[k] = pk_alpha(alpha, k, g);
+      dec[k] = 1.f - a[k];
       wk[k] = rnd<T>(weight[k]);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) st[k][i] = cr[k * g.D + i];
@@ -863,17 +909,7 @@ __global__ __launch_bounds__(kPkRowMaxThreads) void packet_fwd_rows(
 #pragma unroll
     for (int t = 0; t < kChunkT; ++t)
       if (t < len) {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          float acc = 0.f;
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            st[k][i] = fmaf(a[k], xv[t][i], (1.f - a[k]) * st[k][i]);
-            const float term = rnd<T>(wk[k] * rnd<T>(st[k][i]));
-            acc = k == 0 ? term : rnd<T>(acc + term);
-          }
-          u[t][i] = acc;
-        }
+        pool_token<T, VEC, K>(xv[t], a, dec, wk, st, u[t]);
         stv<T, VEC>(po + static_cast<int64_t>(t) * spn, u[t]);
       }
   }
@@ -1135,7 +1171,9 @@ bool pk_bwd_lookback(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
 
 template <typename T, int VEC, int VA, int K>
 void pk_bwd_typed(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
-  constexpr int LBV = sizeof(T) == 2 && VEC == 4 ? 4 : 1;
+  // four channels per lane for bf16 up to three scales (four scales there overflow the registers into
+  // scratch memory), else one
+  constexpr int LBV = sizeof(T) == 2 && VEC == 4 && K <= 3 ? 4 : 1;
   if (pk_bwd_lookback<T, LBV, K, LBV == 4 ? kPkLbKeep : kChunkT, kPkLbSeg>(a, stream)) return;
   const dwarf_packet_pool_fwd_args& f = a.fwd;
   const size_t nf = pk_state_floats(f.B, f.N, f.D, K);
