@@ -832,10 +832,11 @@ __global__ __launch_bounds__(kPkRedThreads) void packet_param_reduce(const float
 // Per token, with u the stored pooled values and s = sigmoid(gate logit):
 //   ms = mean_d u^2,   r = rsqrt(ms + 1e-6),   conf = tanh(sqrt(ms) / 0.25)
 //   packet = G(((u r) conf) s)                 (G: the packet's dtype)
-// packet_fwd_rows is the pool's apply stage laid out by rows: one workgroup
-// per (batch row, 16-token chunk) with its lanes over all D channels (VEC
-// each), so after the chunk's scans are rescanned and pooled is stored, the
-// 16 tokens' ms are one two-level LDS sum (fixed order) away.
+// packet_fwd_rows takes one workgroup per (batch row, 16-token chunk) with
+// its lanes over all D channels (VEC each): it reads the chunk's pooled rows
+// as the look-back forward stored them (or, with RESCAN, rescans the chunk
+// from its incoming states as the pool's apply stage and stores pooled), so
+// the 16 tokens' ms are one two-level LDS sum (fixed order) away.
 constexpr int kPkRowMaxThreads = 1024;
 constexpr float kPkEps = 1e-6f;
 constexpr float kPkConfScale = 0.25f;
@@ -868,7 +869,7 @@ __device__ __forceinline__ void pk_rows_sum(float* s_red, float* s_mid, float* s
   __syncthreads();
 }
 
-template <typename T, typename G, int VEC, int K>
+template <typename T, typename G, int VEC, int K, bool RESCAN>
 __global__ __launch_bounds__(kPkRowMaxThreads) void packet_fwd_rows(
     const T* __restrict__ x, int64_t sxb, int64_t sxn, T* __restrict__ pooled, int64_t spb, int64_t spn,
     const G* __restrict__ gate, int64_t sgb, int64_t sgn, G* __restrict__ packet, int64_t sqb, int64_t sqn,
@@ -889,7 +890,13 @@ __global__ __launch_bounds__(kPkRowMaxThreads) void packet_fwd_rows(
   for (int t = 0; t < kChunkT; ++t)
 #pragma unroll
     for (int i = 0; i < VEC; ++i) u[t][i] = 0.f;
-  if (live) {
+  if (live && !RESCAN) {   // pooled as the look-back forward stored it
+    const T* po = pooled + b * spb + static_cast<int64_t>(t0) * spn + d0;
+#pragma unroll
+    for (int t = 0; t < kChunkT; ++t)
+      if (t < len) ldv<T, VEC>(po + static_cast<int64_t>(t) * spn, u[t]);
+  }
+  if (live && RESCAN) {
     float a[K], dec[K], wk[K], st[K][VEC];
     const float* cr = state + (static_cast<int64_t>(b) * g.NC + c) * (K * g.D) + d0;
 #pragma unroll
@@ -1127,14 +1134,19 @@ void pk_fwd_typed(const dwarf_packet_pool_fwd_args& a, hipStream_t stream) {
 
 inline int pk_row_threads(int DV) { return (DV + kWave - 1) / kWave * kWave; }
 
+// The packet's forward: the pool by the look-back pass (pooled and the chunk
+// states), then packet_fwd_rows on the stored pooled; for slabs over 2 GiB
+// the three-stage chunk states, then packet_fwd_rows rescanning each chunk.
 template <typename T, typename G, int VEC, int K>
 void pkt_fwd_typed(const dwarf_packet_fwd_args& p, hipStream_t stream) {
   const dwarf_packet_pool_fwd_args& a = p.pool;
   const EmaGeom g = pk_geom(a.B, a.N, a.D, VEC, a.floor_, a.ceiling);
-  pk_fwd_states<T, VEC, K>(a, g, stream);
+  const bool pooled_done = pk_fwd_lookback<T, VEC, K, true>(a, stream);
+  if (!pooled_done) pk_fwd_states<T, VEC, K>(a, g, stream);
   const int nt = pk_row_threads(g.DV);
   const size_t lds = static_cast<size_t>(kChunkT * nt + nt + 16) * sizeof(float);
-  hipLaunchKernelGGL((packet_fwd_rows<T, G, VEC, K>), dim3(a.B * g.NC), dim3(nt), lds, stream,
+  auto rows = pooled_done ? packet_fwd_rows<T, G, VEC, K, false> : packet_fwd_rows<T, G, VEC, K, true>;
+  hipLaunchKernelGGL(rows, dim3(a.B * g.NC), dim3(nt), lds, stream,
                      static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<T*>(a.pooled),
                      a.pooled_stride[0], a.pooled_stride[1], static_cast<const G*>(p.gate), p.gate_stride[0],
                      p.gate_stride[1], static_cast<G*>(p.packet), p.packet_stride[0], p.packet_stride[1], p.ms,
