@@ -355,3 +355,27 @@ def test_three_stage_forward_for_slabs_over_2gib(pkg, device):
     assert rel_err(pooled.cpu(), pooled_lb.cpu()) < 1e-6
     assert rel_err(state.cpu(), state_lb.cpu()) < 1e-6
     del big
+
+
+def test_packet_three_stage_for_slabs_over_2gib(pkg, device):
+    """x past 2 GiB per slab: the packet's forward takes the three-stage chunk states and the row kernel
+    that rescans each chunk, its backward the three-stage pool backward. The packet and every gradient
+    against the oracle at the fp32 bars, and the packet, pooled and ms within 1e-6 relative of the
+    look-back forward on the same values in a contiguous tensor."""
+    packet_mod = pkg.packet
+    B, N, D, K = 1, 300, 64, 3
+    x, a, w, gate, dpk = packet_inputs(B, N, D, K, torch.float32, torch.float32, seed=41)
+    xd, ad, wd, gd = x.to(device), a.to(device), w.to(device), gate.to(device)
+    big, xv = _wide_view(B, N, D, xd)
+    pk, pooled, state, ms = packet_mod.packet_forward(xv, ad, wd, gd, 1e-5, 0.5)
+    dx, da, dw, dg = packet_mod.packet_backward(xv, ad, wd, gd, pooled, state, ms, dpk.to(device), 1e-5, 0.5)
+    pk_lb, pooled_lb, _, ms_lb = packet_mod.packet_forward(xd, ad, wd, gd, 1e-5, 0.5)
+    torch.cuda.synchronize()
+    pk, pooled, ms, dx, da, dw, dg = (t.cpu() for t in (pk, pooled, ms, dx, da, dw, dg))
+    rpk, rdx, rda, rdw, rdg = packet_oracle(x, a, w, gate, pooled, dpk)
+    assert rel_err(pooled, ema_ref.interference_pool(x.double(), a.double(), w.double())) < 1e-5
+    for got, ref in ((pk, rpk), (dg, rdg), (dx, rdx), (da, rda), (dw, rdw)):
+        assert rel_err(got, ref) < 1e-5
+    for got, ref in ((pk, pk_lb), (pooled, pooled_lb), (ms, ms_lb)):
+        assert rel_err(got, ref.cpu()) < 1e-6
+    del big
