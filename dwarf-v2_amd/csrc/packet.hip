@@ -846,15 +846,17 @@ constexpr float kPkConfScale = 0.25f;
 // rounded division.  e^-z = inf gives 0 and e^-z = 0 gives 1.
 __device__ __forceinline__ float pk_sigmoid(float z) { return __builtin_amdgcn_rcpf(1.f + __expf(-z)); }
 
-// Sum of row r of s_red ([16][nt]) in a fixed order: level 1 adds 16 entries
-// per (row, quarter-block), level 2 adds the nt / 16 partials of each row.
-// Every thread of the block calls it; returns the 16 sums in s_out.
+// Sum of row r of s_red ([16][nt + 1]: rows padded by one word, so the
+// sixteen rows a wave's level-1 reads span sit in different banks) in a
+// fixed order: level 1 adds 16 entries per (row, quarter-block), level 2
+// adds the nt / 16 partials of each row.  Every thread of the block calls
+// it; returns the 16 sums in s_out.
 __device__ __forceinline__ void pk_rows_sum(float* s_red, float* s_mid, float* s_out) {
   const int nt = blockDim.x, q = nt / 16;
   __syncthreads();
   {
     const int r = threadIdx.x & 15, part = threadIdx.x >> 4;
-    const float* src = s_red + r * nt + part * 16;
+    const float* src = s_red + r * (nt + 1) + part * 16;
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) sum += src[e];
@@ -876,8 +878,8 @@ __global__ __launch_bounds__(kPkRowMaxThreads) void packet_fwd_rows(
     float* __restrict__ ms, const float* __restrict__ alpha, const float* __restrict__ weight,
     const float* __restrict__ state, EmaGeom g) {
   extern __shared__ float s_pk[];
-  float* s_red = s_pk;                          // [16][nt]
-  float* s_mid = s_red + kChunkT * blockDim.x;  // [16][nt / 16]
+  float* s_red = s_pk;                                // [16][nt + 1]
+  float* s_mid = s_red + kChunkT * (blockDim.x + 1);  // [16][nt / 16]
   float* s_ms = s_mid + blockDim.x;             // [16]
   const int c = blockIdx.x % g.NC, b = blockIdx.x / g.NC;
   const int dv = threadIdx.x;
@@ -925,7 +927,7 @@ __global__ __launch_bounds__(kPkRowMaxThreads) void packet_fwd_rows(
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < VEC; ++i) sq = fmaf(u[t][i], u[t][i], sq);
-    s_red[t * blockDim.x + threadIdx.x] = sq;
+    s_red[t * (blockDim.x + 1) + threadIdx.x] = sq;
   }
   pk_rows_sum(s_red, s_mid, s_ms);
   const float inv_d = 1.f / static_cast<float>(g.D);
@@ -1144,7 +1146,7 @@ void pkt_fwd_typed(const dwarf_packet_fwd_args& p, hipStream_t stream) {
   const bool pooled_done = pk_fwd_lookback<T, VEC, K, true>(a, stream);
   if (!pooled_done) pk_fwd_states<T, VEC, K>(a, g, stream);
   const int nt = pk_row_threads(g.DV);
-  const size_t lds = static_cast<size_t>(kChunkT * nt + nt + 16) * sizeof(float);
+  const size_t lds = static_cast<size_t>(kChunkT * (nt + 1) + nt + 16) * sizeof(float);
   auto rows = pooled_done ? packet_fwd_rows<T, G, VEC, K, false> : packet_fwd_rows<T, G, VEC, K, true>;
   hipLaunchKernelGGL(rows, dim3(a.B * g.NC), dim3(nt), lds, stream,
                      static_cast<const T*>(a.x), a.x_stride[0], a.x_stride[1], static_cast<T*>(a.pooled),
