@@ -8,12 +8,11 @@
 // and K products and K - 1 sums; here the forward reads x once and writes
 // pooled once.
 //
-// The forward is one pass with the EMA's decoupled look-back (packet_fwd_lb)
-// wherever every [N][D] slab of x and pooled spans less than 2 GiB; the
-// three-stage forward below (x read twice) serves larger slabs, and the
-// backward's stages are as below.
-//
-// Stages, on the EMA's 16-token chunks (ema_common.h):
+// Forward and backward are each one pass with the EMA's decoupled look-back
+// (packet_fwd_lb, packet_bwd_lb; the backward's parameter sums then take one
+// reduction launch) wherever every [N][D] slab of the operands spans less
+// than 2 GiB.  Larger slabs take three stages on the EMA's 16-token chunks
+// (ema_common.h), the forward then reading x twice:
 //   forward:  local - the K chunk-end states with zero carry-in (reads x)
 //             carry - the EMA carry stage over K*D scale-major channels,
 //                     writing each chunk's incoming states to `state`
