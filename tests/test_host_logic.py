@@ -179,3 +179,16 @@ def test_custom_ops_default_to_the_python_schedule(pkg):
         arg = [x for x in schema.arguments if x.name == "schedule"][0]
         assert arg.default_value == dsqg.DEFAULT_SCHEDULE
     assert inspect.signature(ops._dsqg_fwd_fake).parameters["schedule"].default == dsqg.DEFAULT_SCHEDULE
+
+
+def test_integration_guide_names_exist(pkg):
+    """Every ``amd.<name>`` the drop-in guide tells a maintainer to bind exists in the package, so the
+    rebinding it shows runs as written."""
+    import os
+    import re
+
+    guide = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "INTEGRATION.md")).read()
+    names = sorted(set(re.findall(r"\bamd\.([A-Za-z_][A-Za-z0-9_]*)", guide)))
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(pkg, n)]
+    assert not missing, missing
