@@ -309,6 +309,9 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_fwd_lb(const T* __restri
   for (int t = 0; t < SEG; ++t)
     raw[t].load(rx, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsx + cox : kOutOfRange);
 
+  uint64_t rb = 0;   // reset flags of tokens s0 .. s0 + SEG
+  if constexpr (RESET) rb = lb_reset_bits(g, b, s0);
+
   // 1. the segment from a zero state
   float L[VEC], A[VEC];
   bool cut = false;
@@ -318,7 +321,7 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_fwd_lb(const T* __restri
   for (int t = 0; t < SEG; ++t) {
     if (t < len) {
       if constexpr (RESET) {
-        if (lb_reset(g, b, s0 + t)) {
+        if (lb_bit(rb, t)) {
           cut = true;
 #pragma unroll
           for (int i = 0; i < VEC; ++i) L[i] = 0.f;
@@ -384,7 +387,7 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_fwd_lb(const T* __restri
   for (int t = 0; t < SEG; ++t) {
     if (t < len) {
       if constexpr (RESET) {
-        if (lb_reset(g, b, s0 + t)) {
+        if (lb_bit(rb, t)) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) st[i] = 0.f;
         }
@@ -431,6 +434,9 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restri
   for (int t = 0; t < SEG; ++t)
     raw[t].load(rg, t < len && dlive ? static_cast<uint32_t>(s0 + t) * rsg + cog : kOutOfRange);
 
+  uint64_t rb = 0;   // reset flags of tokens s0 .. s0 + SEG
+  if constexpr (RESET) rb = lb_reset_bits(g, b, s0);
+
   // 1. the segment in reverse time from a zero adjoint; a reset at token
   // t + 1 cuts what flows from t + 1 back into t (ema:478-509)
   float L[VEC], A[VEC];
@@ -440,7 +446,7 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restri
   for (int t = SEG - 1; t >= 0; --t) {
     if (t < len) {
       if constexpr (RESET) {
-        if (t + 1 < len && lb_reset(g, b, s0 + t + 1)) {
+        if (t + 1 < len && lb_bit(rb, t + 1)) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) L[i] = 0.f;
         }
@@ -454,9 +460,8 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restri
       }
     }
   }
-  if constexpr (RESET) {   // a reset at any of s0 + 1 .. s0 + len cuts the segment's carry
-    bool cut = false;
-    for (int t = s0 + 1; t <= s0 + len && t < g.N; ++t) cut = cut || lb_reset(g, b, t);
+  if constexpr (RESET) {   // a reset at any of s0 + 1 .. s0 + len cuts the segment's carry (bits past N are 0)
+    const bool cut = len > 0 && ((rb >> 1) & ((uint64_t(1) << len) - 1)) != 0;
     if (cut) {
 #pragma unroll
       for (int i = 0; i < VEC; ++i) A[i] = 0.f;
@@ -531,11 +536,11 @@ __global__ __launch_bounds__(kWave * kLbWaves) void ema_bwd_lb(const T* __restri
         yr[r].widen(yp);
         raw[t].widen(gv);
         if constexpr (RESET) {
-          if (s0 + t + 1 < g.N && lb_reset(g, b, s0 + t + 1)) {   // cut from the future (or the carry)
+          if (lb_bit(rb, t + 1)) {   // cut from the future (or the carry; 0 past N)
 #pragma unroll
             for (int i = 0; i < VEC; ++i) st[i] = 0.f;
           }
-          if (lb_reset(g, b, s0 + t)) {   // y[t-1] does not feed token t (ema:445-448)
+          if (lb_bit(rb, t)) {   // y[t-1] does not feed token t (ema:445-448)
 #pragma unroll
             for (int i = 0; i < VEC; ++i) yp[i] = 0.f;
           }

@@ -323,9 +323,27 @@ __device__ __forceinline__ float lb_alpha(const float* alpha, const LbGeom& g, i
   return fminf(fmaxf(a, g.lo), g.hi);
 }
 
-__device__ __forceinline__ bool lb_reset(const LbGeom& g, int b, int t) {
-  return g.reset[b * g.srb + static_cast<int64_t>(t) * g.srn] != 0;
+// The reset flags of tokens s0 .. s0 + kLbSeg of batch row b as bits 0 ..
+// kLbSeg (a token outside [0, N) reads 0), for lane (cg = lane & 15,
+// ts = lane >> 4) of a tile whose segment ts starts at s0: the segment's 16
+// lanes read two flags each and two wave ballots hand every lane its 32,
+// and each lane reads the flag of the token after its segment.  The scans
+// then test bits instead of loading a flag at each use.  Every lane of the
+// wave calls it.
+__device__ __forceinline__ uint64_t lb_reset_bits(const LbGeom& g, int b, int s0) {
+  static_assert(kLbSeg == 32 && kLbGroups == 16 && kLbSegs * kLbGroups == kWave, "16 lanes per 32-token segment");
+  const int lane = threadIdx.x & (kWave - 1), cg = lane & 15, ts = lane >> 4;
+  const uint8_t* p = g.reset + b * g.srb;
+  auto flag = [&](int tt) {
+    const uint8_t f = p[static_cast<int64_t>(min(max(tt, 0), g.N - 1)) * g.srn];   // an address inside the row
+    return tt >= 0 && tt < g.N && f != 0;
+  };
+  const uint64_t lo = __ballot(flag(s0 + cg)), hi = __ballot(flag(s0 + 16 + cg));
+  const bool nx = flag(s0 + kLbSeg);
+  return ((lo >> (16 * ts)) & 0xffffu) | (((hi >> (16 * ts)) & 0xffffu) << 16) | (static_cast<uint64_t>(nx) << 32);
 }
+
+__device__ __forceinline__ bool lb_bit(uint64_t m, int t) { return (m >> t) & 1u; }
 
 // Raw VEC channels of one token in registers, loaded and stored through
 // buffer resources (an out-of-range offset reads zeros / drops the store).
