@@ -37,9 +37,11 @@ namespace {
 
 constexpr int kMaxScales = 4;
 constexpr int kPkRedThreads = 1024;
-// Rows a lane keeps per block of the look-back backward's reverse pass (bf16,
-// four channels per lane; one channel per lane keeps a whole chunk).
-constexpr int kPkLbKeep = 8;
+// Rows a lane keeps per block of the look-back backward's reverse pass with
+// four channels per lane (bf16 8, fp32 4: its kept scans take a register
+// each); one channel per lane keeps a whole chunk.
+template <typename T>
+constexpr int pk_lb_keep() { return sizeof(T) == 2 ? 8 : 4; }
 // Tokens per lane segment of the look-back backward (16-token segments, twice
 // the waves, measured 2 us slower at [15, 2048, 512]).
 constexpr int kPkLbSeg = kLbSeg;
@@ -1184,10 +1186,10 @@ bool pk_bwd_lookback(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
 
 template <typename T, int VEC, int VA, int K>
 void pk_bwd_typed(const dwarf_packet_pool_bwd_args& a, hipStream_t stream) {
-  // four channels per lane for bf16 up to three scales (four scales there overflow the registers into
-  // scratch memory), else one
-  constexpr int LBV = sizeof(T) == 2 && VEC == 4 && K <= 3 ? 4 : 1;
-  if (pk_bwd_lookback<T, LBV, K, LBV == 4 ? kPkLbKeep : kChunkT, kPkLbSeg>(a, stream)) return;
+  // four channels per lane up to three scales (four scales there overflow the registers into scratch
+  // memory), else one
+  constexpr int LBV = VEC == 4 && K <= 3 ? 4 : 1;
+  if (pk_bwd_lookback<T, LBV, K, LBV == 4 ? pk_lb_keep<T>() : kChunkT, kPkLbSeg>(a, stream)) return;
   const dwarf_packet_pool_fwd_args& f = a.fwd;
   const size_t nf = pk_state_floats(f.B, f.N, f.D, K);
   float* starts = static_cast<float*>(a.workspace);
