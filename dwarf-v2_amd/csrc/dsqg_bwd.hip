@@ -212,7 +212,7 @@ struct KvChunk {
 template <int SHIFT, int CJ, int MINWG>
 __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
                                                                    const float* __restrict__ delta_ws, int tiles,
-                                                                   int total) {
+                                                                   int total, int nsplit, float* __restrict__ kvp) {
   constexpr float kC = 0.125f * kLog2e;
   constexpr float kScale = 0.125f;
   static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
@@ -233,10 +233,13 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   float2* s_dl = reinterpret_cast<float2*>(sm + lay.off_dl);
 
   const int work = xcd_remap(blockIdx.x, total);
-  const int bhk = work / tiles;
-  const int tile = work - bhk * tiles;
+  const int unit = work / tiles;   // (b, kv head, subset of its query heads)
+  const int tile = work - unit * tiles;
+  const int bhk = unit / nsplit;
+  const int split = unit - bhk * nsplit;
   const int b = bhk / f.H_kv;
   const int hk = bhk - b * f.H_kv;
+  const int hh0 = split * (group / nsplit), hh1 = hh0 + group / nsplit;   // the workgroup's query heads
 
   // this lane's key row (K, V slices and z) is requested first, so its latency
   // overlaps the table staging
@@ -318,7 +321,7 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   const int qb_lane = m_eff * qs_b + 32 * g, db_lane = m_eff * ds_b + 32 * g;
   const int yb_lane = m_eff * ys_b + 4 * g;
 
-  for (int hh = 0; hh < group; ++hh) {
+  for (int hh = hh0; hh < hh1; ++hh) {
     const int h = hk * group + hh;
     const int bh = b * f.H + h;
     const __amdgpu_buffer_rsrc_t rq =
@@ -534,6 +537,20 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
 
   }
 
+  if (kvp) {   // a subset of the query heads: its partial sums, which dsqg_bwd_dkdv_combine adds up
+    if (!key_ok) return;
+    const int64_t rows = static_cast<int64_t>(f.B) * f.H_kv * N;
+    const int64_t row = static_cast<int64_t>(bhk) * N + m;
+    float4* pk = reinterpret_cast<float4*>(kvp + (split * rows + row) * kHeadDim + 16 * g);
+    float4* pv = reinterpret_cast<float4*>(kvp + ((nsplit + split) * rows + row) * kHeadDim + 16 * g);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pk[i] = make_float4(dk[4 * i], dk[4 * i + 1], dk[4 * i + 2], dk[4 * i + 3]);
+      pv[i] = make_float4(dv[4 * i], dv[4 * i + 1], dv[4 * i + 2], dv[4 * i + 3]);
+    }
+    kvp[2 * nsplit * rows * kHeadDim + (split * rows + row) * kPlanes + g] = dz;
+    return;
+  }
   // with key_probes z came from the key probes: dz goes into dk through the probe features (the
   // block's einsum backward, dsqg:3231-3254) instead of out to dz_pre
   if (f.key_probes) fold_probe_grad(dk, k32, f.key_probes, g, zg, dz);
@@ -558,17 +575,97 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   if (!f.key_probes) a.dz_pre[(static_cast<int64_t>(bhk) * N + m) * kPlanes + g] = dz;
 }
 
+// Sums the query-head subsets' partial dK, dV and dZ of each key in subset order, folds dZ into dK
+// through the key probes when z came from them, and writes the bf16 gradients. Four lanes per key,
+// lane g holding dims 16g .. 16g + 15 and plane g, as in dsqg_bwd_dkdv_bf16_k4.
+__global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_combine(const dwarf_dsqg_bwd_args a,
+                                                                const float* __restrict__ kvp, int nsplit) {
+  const dwarf_dsqg_fwd_args& f = a.fwd;
+  const int N = f.N;
+  const int64_t rows = static_cast<int64_t>(f.B) * f.H_kv * N;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t row = t >> 2;
+  const int g = static_cast<int>(t & 3);
+  if (row >= rows) return;   // rows * 4 threads: a key's four lanes leave together
+  const int bhk = static_cast<int>(row / N);
+  const int64_t mm = row - static_cast<int64_t>(bhk) * N;
+  const int b = bhk / f.H_kv, hk = bhk - b * f.H_kv;
+  float dk[16], dv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) { dk[i] = 0.f; dv[i] = 0.f; }
+  float dz = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float4* pk = reinterpret_cast<const float4*>(kvp + (s * rows + row) * kHeadDim + 16 * g);
+    const float4* pv = reinterpret_cast<const float4*>(kvp + ((nsplit + s) * rows + row) * kHeadDim + 16 * g);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 x = pk[i], y = pv[i];
+      dk[4 * i] += x.x; dk[4 * i + 1] += x.y; dk[4 * i + 2] += x.z; dk[4 * i + 3] += x.w;
+      dv[4 * i] += y.x; dv[4 * i + 1] += y.y; dv[4 * i + 2] += y.z; dv[4 * i + 3] += y.w;
+    }
+    dz += kvp[2 * nsplit * rows * kHeadDim + (s * rows + row) * kPlanes + g];
+  }
+  if (f.key_probes) {
+    const bf16* kb = reinterpret_cast<const bf16*>(f.k) + b * f.k_stride[0] + hk * f.k_stride[1];
+    const uint4* k4 = reinterpret_cast<const uint4*>(kb + mm * f.k_stride[2] + 16 * g);
+    const uint4 kx0 = k4[0], kx1 = k4[1];
+    const uint32_t k32[8] = {kx0.x, kx0.y, kx0.z, kx0.w, kx1.x, kx1.y, kx1.z, kx1.w};
+    const float zg = f.z_pre[b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2] + g];
+    fold_probe_grad(dk, k32, f.key_probes, g, zg, dz);
+  }
+  uint4* k4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dk) + b * a.dk_stride[0] + hk * a.dk_stride[1] +
+                                       mm * a.dk_stride[2] + 16 * g);
+  uint4* v4 = reinterpret_cast<uint4*>(reinterpret_cast<bf16*>(a.dv) + b * a.dv_stride[0] + hk * a.dv_stride[1] +
+                                       mm * a.dv_stride[2] + 16 * g);
+  uint4 x;
+  x.x = pack_bf16x2(dk[0], dk[1]);   x.y = pack_bf16x2(dk[2], dk[3]);
+  x.z = pack_bf16x2(dk[4], dk[5]);   x.w = pack_bf16x2(dk[6], dk[7]);
+  k4[0] = x;
+  x.x = pack_bf16x2(dk[8], dk[9]);   x.y = pack_bf16x2(dk[10], dk[11]);
+  x.z = pack_bf16x2(dk[12], dk[13]); x.w = pack_bf16x2(dk[14], dk[15]);
+  k4[1] = x;
+  x.x = pack_bf16x2(dv[0], dv[1]);   x.y = pack_bf16x2(dv[2], dv[3]);
+  x.z = pack_bf16x2(dv[4], dv[5]);   x.w = pack_bf16x2(dv[6], dv[7]);
+  v4[0] = x;
+  x.x = pack_bf16x2(dv[8], dv[9]);   x.y = pack_bf16x2(dv[10], dv[11]);
+  x.z = pack_bf16x2(dv[12], dv[13]); x.w = pack_bf16x2(dv[14], dv[15]);
+  v4[1] = x;
+  if (!f.key_probes) a.dz_pre[row * kPlanes + g] = dz;
+}
+
+// Grouped-query heads: a KV head's workgroups walk all of its query heads, so the grid has 1 / group
+// of the MHA grid's workgroups. A grid that does not fill the resident slots once (256 CUs x kMinWgKv)
+// gets its query heads split into subsets, one workgroup per (key tile, KV head, subset): the smallest
+// divisor of the group size giving two rounds of the slots. The subsets' fp32 partials are summed by
+// dsqg_bwd_dkdv_combine. A grid of one to two rounds keeps whole groups: at B15 N2048 H8 over 2 KV
+// heads (960 workgroups) the partials' traffic cost what the split gained (dK/dV 277 us whole,
+// 281 us in 2 subsets, 299 us in 4); over 1 KV head (480) 4 subsets take it from 394 to 284 us.
+constexpr int kKvResidentWgs = 256 * kMinWgKv;
+
+int dkdv_split(const dwarf_dsqg_fwd_args& f) {
+  const int group = f.H_kv > 0 ? f.H / f.H_kv : 1;
+  const int64_t wgs = static_cast<int64_t>((f.N + kKPB - 1) / kKPB) * f.B * f.H_kv;
+  if (wgs >= kKvResidentWgs) return 1;
+  int s = 1;
+  while (s < group && wgs * s < 2 * kKvResidentWgs) {
+    do ++s; while (group % s);
+  }
+  return s;
+}
+
 hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
   const float* delta = reinterpret_cast<const float*>(static_cast<char*>(a.workspace) + ws.delta_off);
   const int tiles = (f.N + kKPB - 1) / kKPB;
-  const int total = tiles * f.B * f.H_kv;
+  const int ns = ws.kv_split;
+  float* kvp = ns > 1 ? reinterpret_cast<float*>(static_cast<char*>(a.workspace) + ws.kv_part_off) : nullptr;
+  const int total = tiles * f.B * f.H_kv * ns;
   if (total == 0) return hipSuccess;
   const size_t lds = kv_layout(f.J, f.J_large, f.H / f.H_kv, kChunkKv).bytes;
 #define DWARF_KV4_CASE(S) \
   case S:                                                                                                     \
     hipLaunchKernelGGL((dsqg_bwd_dkdv_bf16_k4<S, kChunkKv, kMinWgKv>), dim3(total), dim3(kBlock), lds, stream, a, \
-                       delta, tiles, total);                                                                  \
+                       delta, tiles, total, ns, kvp);                                                         \
     break;
   switch (f.plane_shift) {
     DWARF_KV4_CASE(0) DWARF_KV4_CASE(1) DWARF_KV4_CASE(2) DWARF_KV4_CASE(3) DWARF_KV4_CASE(4)
@@ -577,6 +674,11 @@ hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace&
     default: return hipErrorInvalidValue;
   }
 #undef DWARF_KV4_CASE
+  if (ns > 1) {
+    const int64_t threads = static_cast<int64_t>(f.B) * f.H_kv * f.N * kPlanes;
+    hipLaunchKernelGGL(dsqg_bwd_dkdv_combine, dim3(static_cast<unsigned>((threads + kBlock - 1) / kBlock)),
+                       dim3(kBlock), 0, stream, a, kvp, ns);
+  }
   return hipGetLastError();
 }
 
@@ -747,6 +849,12 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
                  static_cast<size_t>(f.H) * w.red_groups_pb * f.J +
                  static_cast<size_t>(f.H) * w.red_groups_ph * JL * 8) * sizeof(float);
   off += align256(w.red_bytes);
+  w.kv_split = f.dtype == DWARF_BF16 ? dkdv_split(f) : 1;
+  w.kv_part_off = off;
+  w.kv_part_bytes = w.kv_split > 1 ? static_cast<size_t>(w.kv_split) * f.B * f.H_kv * f.N *
+                                         (2 * kHeadDim + kPlanes) * sizeof(float)
+                                   : 0;
+  off += align256(w.kv_part_bytes);
   w.total = off;
   return w;
 }
