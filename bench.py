@@ -546,6 +546,24 @@ def packet_extra(pkg, device, steps, warmup):
                       "packet; timed from HIP-graph replays"}
 
 
+def gqa_extra(pkg, device, steps, warmup):
+    """The training microbatch with grouped K/V heads: H8 over 2 and over 1 KV heads (the query side, tables and
+    dO as benched; K, V and z the first H_kv heads of the benched ones)."""
+    B, H, N = 15, 8, 2048
+    t, js, jl = synth(pkg, B, H, N, 0, device)
+    res = {}
+    for hkv in (2, 1):
+        u = dict(t)
+        for n in ("k", "v", "z_pre"):
+            u[n] = t[n][:, :hkv].contiguous()
+        ms, per, _ = time_dsqg_step(pkg, u, js, jl, steps, warmup)
+        res[f"hkv{hkv}"] = {"tokens_per_s": B * N / (ms * 1e-3), "ms_per_step": ms, "per_launch_ms_serial": per}
+        del u
+    res["config"] = ("B=15 H=8 T=2048 bf16 DSQG fwd+bwd with H_kv 2 and 1 (GQA groups of 4 and 8); "
+                     "step on the overlapped schedule, per-launch times on the serial one")
+    return res
+
+
 def long_context_extra(pkg, device, steps, warmup):
     B, H, N = 4, 8, 8192
     t, js, jl = synth(pkg, B, H, N, 4, device)
@@ -582,7 +600,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--extra-only", choices=["q6_decode", "q6_prefill", "long_context", "phase_probe", "npci", "packet",
-                                             "probe_fusion"],
+                                             "probe_fusion", "gqa"],
                     help="run only this extra workload and print its JSON (for per-workload profiles)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 10 times (scales HBM byte counters)")
@@ -609,7 +627,8 @@ def main() -> int:
     if args.extra_only:
         fn = {"q6_decode": q6_decode_extra, "q6_prefill": q6_prefill_extra,
               "long_context": long_context_extra, "phase_probe": phase_probe_extra,
-              "npci": npci_extra, "packet": packet_extra, "probe_fusion": probe_fusion_extra}[args.extra_only]
+              "npci": npci_extra, "packet": packet_extra, "probe_fusion": probe_fusion_extra,
+              "gqa": gqa_extra}[args.extra_only]
         print(json.dumps({args.extra_only: fn(pkg, device, args.steps, args.warmup)}), flush=True)
         return 0
     B, H, N = 15, 8, 2048
@@ -657,6 +676,8 @@ def main() -> int:
         extra["npci"] = npci_extra(pkg, device, args.steps, args.warmup)
         log("InterferencePacket pool: x [15,2048,512], three timescales")
         extra["packet"] = packet_extra(pkg, device, args.steps, args.warmup)
+        log("training microbatch with grouped K/V heads: H8 over 2 and 1")
+        extra["gqa"] = gqa_extra(pkg, device, args.steps, args.warmup)
     # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE runs (profiles/traffic.json,
     # stamped with the commit they were measured at); counters cannot run inside this timed process
     traffic, traffic_commit = None, None
