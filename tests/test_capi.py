@@ -203,6 +203,26 @@ def test_backward_limits_without_gpu(pkg, lib):
     assert b"LDS" in lib.dwarf_last_error()
 
 
+def test_gqa_head_split_workspace_without_gpu(pkg, lib):
+    """bf16 dK/dV with grouped heads on a grid that fills no round of the 768 resident slots splits the query
+    heads into subsets and keeps their fp32 partials (dK and dV 64 floats each, dZ 4, per key and subset) in
+    the workspace: B1 H8 over one KV head at N 2048 (32 key tiles) takes all 8 subsets; B15 over 2 KV heads
+    (960 key tiles) and fp32 none, so those sizes equal the MHA layout's."""
+    L = pkg._lib
+
+    def need(B, H, H_kv, N, dtype):
+        b = L.DsqgBwdArgs()
+        b.fwd = _fake_fwd(L, B, H, H_kv, N, 96, 17)
+        b.fwd.dtype = dtype
+        b.dout, b.dout_stride = 0x10000, L.i64_array((H * N * 64, N * 64, 64, 1))
+        return lib.dwarf_dsqg_bwd_workspace_bytes(ctypes.byref(b))
+
+    assert need(1, 8, 1, 2048, L.DWARF_BF16) - need(1, 8, 8, 2048, L.DWARF_BF16) == 8 * 2048 * (2 * 64 + 4) * 4
+    assert need(2, 8, 1, 2048, L.DWARF_BF16) - need(2, 8, 8, 2048, L.DWARF_BF16) == 8 * 2 * 2048 * (2 * 64 + 4) * 4
+    assert need(15, 8, 2, 2048, L.DWARF_BF16) == need(15, 8, 8, 2048, L.DWARF_BF16)
+    assert need(1, 8, 1, 2048, L.DWARF_F32) == need(1, 8, 8, 2048, L.DWARF_F32)
+
+
 def test_prefill_gather_span_without_gpu(pkg, lib):
     """The q6 prefill gathers cache rows with 32-bit offsets: (2N + 128) x 128 B must stay below 2 GiB."""
     L = pkg._lib
