@@ -209,108 +209,6 @@ struct KvChunk {
   int j[CJ];
 };
 
-// The dK/dV workgroup's tables: E in bf16 (rows of kERowKv), log2(e) pb_j of the group's heads, the
-// offsets, the group's MOVT (base, gain) pairs and the near band's slot table.  Every global load of the
-// first round is in flight before the first LDS store (a load under a condition is waited for at its
-// join, one round trip each), entries past a table reading zeros through buffer loads; the slot table
-// is then built by wave 0 from the offsets its lanes loaded, with what build_band_slots computes.
-// Entries past the first round (J > 127, a GQA group's tables) take element loops, and table layouts
-// beyond 32-bit offsets the element loops throughout.  Returns false (nothing staged) for those.
-__device__ __forceinline__ bool kv_stage_tables(const dwarf_dsqg_fwd_args& f, const KvLayout& lay, int hk,
-                                                uint16_t* sE, float* s_pb2, int* s_off, float2* s_ph, int* s_jn) {
-  const int J = f.J, JE = lay.JE, JL = f.J_large, group = lay.group;
-  const int64_t pbs0 = f.pb_stride[0], pbs1 = f.pb_stride[1];
-  const int64_t bs0 = f.pbase_stride[0], bs1 = f.pbase_stride[1], gs0 = f.pgain_stride[0], gs1 = f.pgain_stride[1];
-  const int64_t se0 = f.se_stride[0];
-  constexpr int64_t kSpan = int64_t(1) << 31;
-  const int64_t pb_span = ((J - 1) * pbs0 + (group - 1) * pbs1 + 1) * 4;
-  const int64_t b_span = JL > 0 ? ((JL - 1) * bs0 + (group - 1) * bs1 + kPlanes) * 4 : 0;
-  const int64_t g_span = JL > 0 ? ((JL - 1) * gs0 + (group - 1) * gs1 + kPlanes) * 4 : 0;
-  if (!(f.se_stride[1] == 1 && (se0 & 3) == 0 && se0 <= (int64_t(1) << 20) &&
-        (reinterpret_cast<uintptr_t>(f.scale_embed) & 15) == 0 && pbs0 >= 0 && pbs1 >= 0 && pb_span < kSpan &&
-        bs0 >= 0 && bs1 >= 0 && b_span < kSpan && gs0 >= 0 && gs1 >= 0 && g_span < kSpan))
-    return false;
-  const int tid = threadIdx.x;
-  const int ne = JE * 16, npb = group * JE, nph = group * JL * kPlanes;
-  const int rb = static_cast<int>(se0) * 4;   // E row bytes
-  const __amdgpu_buffer_rsrc_t rse = rows_rsrc(f.scale_embed, rb, J, 256);
-  const __amdgpu_buffer_rsrc_t rpb = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(f.pos_bias + hk * group * pbs1), 0, static_cast<int>(pb_span), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rof = __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(f.offsets), 0, J * 4, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rbs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(f.phase_base + hk * group * bs1), 0, static_cast<int>(b_span), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rgn = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(f.phase_gain + hk * group * gs1), 0, static_cast<int>(g_span), 0x00020000);
-  auto pb_off = [&](int t) {   // byte offset of entry t = hh * JE + j, or out of range for j >= J
-    const int hh = t / JE, j = t - hh * JE;
-    return t < npb && j < J ? static_cast<uint32_t>((j * pbs0 + hh * pbs1) * 4) : kOutOfRange;
-  };
-  auto ph_off = [&](int t, int64_t s0, int64_t s1) {   // entry t = (hh * JL + i) * kPlanes + r
-    if (t >= nph) return kOutOfRange;                  // (also every entry when JL = 0)
-    const int hh = t / (JL * kPlanes), rest = t - hh * JL * kPlanes;
-    const int i = rest / kPlanes, r = rest - i * kPlanes;
-    return static_cast<uint32_t>((i * s0 + hh * s1 + r) * 4);
-  };
-  auto ph_slot = [&](int t) {
-    const int hh = t / (JL * kPlanes);
-    return hh * lay.JL4 * kPlanes + (t - hh * JL * kPlanes);
-  };
-  // first round: every load, then every store
-  uint4 ex[kSeBatch];
-#pragma unroll
-  for (int u = 0; u < kSeBatch; ++u) {
-    const int i = tid + u * kBlock;
-    ex[u] = buf_load16(rse, i < ne ? static_cast<uint32_t>((i >> 4) * rb + 16 * (i & 15)) : kOutOfRange);
-  }
-  const float pbv = buf_load_f32(rpb, pb_off(tid));
-  const int ofv = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rof, tid < JE ? 4 * tid : kOutOfRange, 0, 0));
-  float phb[2], phg[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    phb[u] = buf_load_f32(rbs, ph_off(tid + u * kBlock, bs0, bs1));
-    phg[u] = buf_load_f32(rgn, ph_off(tid + u * kBlock, gs0, gs1));
-  }
-  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-#pragma unroll
-  for (int u = 0; u < kSeBatch; ++u) {
-    const int i = tid + u * kBlock;
-    if (i < ne) {
-      const bf16x4_t h = {static_cast<__bf16>(__uint_as_float(ex[u].x)), static_cast<__bf16>(__uint_as_float(ex[u].y)),
-                          static_cast<__bf16>(__uint_as_float(ex[u].z)), static_cast<__bf16>(__uint_as_float(ex[u].w))};
-      *reinterpret_cast<bf16x4_t*>(sE + (i >> 4) * kERowKv + 4 * (i & 15)) = h;
-    }
-  }
-  if (tid < npb) s_pb2[tid] = kLog2e * pbv;
-  if (tid < JE) s_off[tid] = ofv;
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-    if (tid + u * kBlock < nph) s_ph[ph_slot(tid + u * kBlock)] = make_float2(phb[u], phg[u]);
-  // near band slots (build_band_slots): offsets j < JB ascending in [1, kBandMaxKv], JB <= kBandMaxKv
-  if (tid < kWave) {
-    const int prev = __shfl_up(ofv, 1);
-    const bool ok = (f.schedule & DWARF_SCHED_BAND) != 0 && tid < f.J_small && tid < kBandMaxKv && ofv >= 1 &&
-                    ofv <= kBandMaxKv && (tid == 0 || ofv > prev);
-    const uint64_t m = __ballot(ok);
-    const int jb = static_cast<int>(__builtin_ctzll(~m));
-    static_assert(kJnSize == kWave && kBandMaxKv < kWave, "one slot-table entry per lane of wave 0");
-    s_jn[tid] = tid == 0 ? jb : -1;
-    if (tid < jb) s_jn[kJnBias + ofv] = tid;   // after the lane's -1: the wave's stores land in order
-  }
-  // what the first round did not cover
-  for (int i = tid + kSeBatch * kBlock; i < ne; i += kBlock) {
-    const uint4 x = buf_load16(rse, static_cast<uint32_t>((i >> 4) * rb + 16 * (i & 15)));
-    const bf16x4_t h = {static_cast<__bf16>(__uint_as_float(x.x)), static_cast<__bf16>(__uint_as_float(x.y)),
-                        static_cast<__bf16>(__uint_as_float(x.z)), static_cast<__bf16>(__uint_as_float(x.w))};
-    *reinterpret_cast<bf16x4_t*>(sE + (i >> 4) * kERowKv + 4 * (i & 15)) = h;
-  }
-  for (int t = tid + kBlock; t < npb; t += kBlock) s_pb2[t] = kLog2e * buf_load_f32(rpb, pb_off(t));
-  for (int j = tid + kBlock; j < JE; j += kBlock)
-    s_off[j] = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rof, 4 * j, 0, 0));
-  for (int t = tid + 2 * kBlock; t < nph; t += kBlock)
-    s_ph[ph_slot(t)] = make_float2(buf_load_f32(rbs, ph_off(t, bs0, bs1)), buf_load_f32(rgn, ph_off(t, gs0, gs1)));
-  return true;
-}
-
 template <int SHIFT, int CJ, int MINWG>
 __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
                                                                    const float* __restrict__ delta_ws, int tiles,
@@ -367,25 +265,10 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
     zg = f.z_pre[b * f.z_stride[0] + hk * f.z_stride[1] + mm * f.z_stride[2] + g];
   }
 
-  if (!kv_stage_tables(f, lay, hk, sE, s_pb2, s_off, s_ph, s_jn)) {   // uniform
-    stage_se_bf16(f.scale_embed, f.se_stride, J, lay.JE, sE, kERowKv);
-    for (int t = threadIdx.x; t < group * lay.JE; t += kBlock) {
-      const int hh = t / lay.JE, j = t - hh * lay.JE;
-      const int h = hk * group + hh;
-      s_pb2[t] = j < J ? kLog2e * f.pos_bias[j * f.pb_stride[0] + h * f.pb_stride[1]] : 0.f;
-    }
-    for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
-    for (int t = threadIdx.x; t < group * JL * kPlanes; t += kBlock) {
-      const int hh = t / (JL * kPlanes), rest = t - hh * JL * kPlanes;
-      const int i = rest / kPlanes, r = rest - i * kPlanes;
-      const int h = hk * group + hh;
-      s_ph[hh * lay.JL4 * kPlanes + rest] =
-          make_float2(f.phase_base[i * f.pbase_stride[0] + h * f.pbase_stride[1] + r],
-                      f.phase_gain[i * f.pgain_stride[0] + h * f.pgain_stride[1] + r]);
-    }
-    if (threadIdx.x == 0)
-      build_band_slots(s_jn, f.offsets, J_small, kBandMaxKv, kBandMaxKv, (f.schedule & DWARF_SCHED_BAND) != 0);
-  }
+  stage_tables<true, true, true, true, true>(
+      f, lay.JE, hk * group, group,
+      TableStage{sE, kERowKv, s_pb2, kLog2e, s_off, s_ph, lay.JL4 * kPlanes, s_jn, kBandMaxKv, kBandMaxKv,
+                 (f.schedule & DWARF_SCHED_BAND) != 0});
   __syncthreads();
   const int JB = s_jn[0];
   const bool wave_live = m0w < N;   // waves past the end still reach every barrier

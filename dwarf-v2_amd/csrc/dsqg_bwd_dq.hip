@@ -638,11 +638,9 @@ __global__ __launch_bounds__(kBlock, kGatherWgsPerCu) void dsqg_bwd_dq_bf16_g4(
   int* s_jn = reinterpret_cast<int*>(sm + lay.off_jn);       // [0]: JB; [kJnBias + d]: band slot of delta d, or -1
   char* s_win = sm + lay.off_st;                              // K window [96][128 B] (aliases the dQe staging)
 
-  stage_se_bf16(f.scale_embed, f.se_stride, J, lay.JE, sE, kERowT);
-  for (int j = threadIdx.x; j < lay.JE; j += kBlock) s_off[j] = j < J ? f.offsets[j] : 0;
-  __syncthreads();
-  if (threadIdx.x == 0)
-    build_band_slots(s_jn, s_off, J_small, kBandMax, kBandSlots, (f.schedule & DWARF_SCHED_BAND) != 0);
+  stage_tables<true, false, true, false, true>(
+      f, lay.JE, 0, 1, TableStage{sE, kERowT, nullptr, 0.f, s_off, nullptr, 0, s_jn, kBandMax, kBandSlots,
+                                  (f.schedule & DWARF_SCHED_BAND) != 0});
   __syncthreads();   // s_jn is read in every tile's prologue
 
   const int lane = threadIdx.x;

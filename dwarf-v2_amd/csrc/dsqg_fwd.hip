@@ -278,16 +278,8 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_q4(const dwarf_dsqg_f
     if (!probed) yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
   }
 
-  stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kERowFwd);
-  for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
-    s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
-    s_off[j] = j < J ? a.offsets[j] : 0;
-  }
-  for (int t = threadIdx.x; t < a.J_large * kPlanes; t += kBlock) {
-    const int i = t / kPlanes, r = t - i * kPlanes;
-    s_ph[t] = make_float2(a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r],
-                          a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r]);
-  }
+  stage_tables<true, true, true, true, false>(
+      a, lay.JE, h, 1, TableStage{sE, kERowFwd, s_pb, 1.0f, s_off, s_ph, 0, nullptr, 0, 0, false});
   __syncthreads();
 
   // s_qe[query][j] = log2(e) * (<q, e_j> / 8 + pb_j) for the wave's 16 queries:
@@ -582,19 +574,10 @@ __global__ __launch_bounds__(kBlock, 2) void dsqg_fwd_bf16_win(const dwarf_dsqg_
     if (!probed) yg = a.y_pre[b * a.y_stride[0] + h * a.y_stride[1] + nn * a.y_stride[2] + g];
   }
 
-  stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kERowFwd);
-  for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
-    s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
-    s_off[j] = j < J ? a.offsets[j] : 0;
-  }
-  for (int t = threadIdx.x; t < a.J_large * kPlanes; t += kBlock) {
-    const int i = t / kPlanes, r = t - i * kPlanes;
-    s_ph[t] = make_float2(a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r],
-                          a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r]);
-  }
+  stage_tables<true, true, true, true, true>(
+      a, lay.JE, h, 1, TableStage{sE, kERowFwd, s_pb, 1.0f, s_off, s_ph, 0, s_jn, kFwdWinBack, lay.JBh, true});
   __syncthreads();
 
-  if (threadIdx.x == 0) build_band_slots(s_jn, s_off, J_small, kFwdWinBack, lay.JBh, true);
   // q.E tables, log2(e) * (<q, e_j> / 8 + pb_j) for the wave's 16 queries:
   // products into registers, a barrier (every wave is done reading sE), then
   // the near columns into s_near and the far columns over sE.

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.h"
+#include "dsqg_internal.h"
 
 namespace dwarf {
 
@@ -125,6 +126,148 @@ __device__ __forceinline__ void stage_se_bf16(const float* se, const int64_t* se
   }
 }
 
+
+// Destinations of the per-workgroup tables staged by stage_tables.
+struct TableStage {
+  uint16_t* sE;      // E rows in bf16, rows of e_row elements (rows J..JE-1 zero)
+  int e_row;
+  float* s_pb;       // pb_scale * pos_bias[j][h0 + hh] at hh * JE + j (0 for j >= J)
+  float pb_scale;
+  int* s_off;        // the offsets (0 for j >= J), JE entries
+  float2* s_ph;      // (phase_base, phase_gain)[i][h0 + hh][r] at hh * ph_head + i * kPlanes + r
+  int ph_head;
+  int* s_jn;         // the near band's slot table (build_band_slots)
+  int band_delta, band_slots;
+  bool band;
+};
+
+// Stages the tables a gather workgroup reads (Args: the DSQG or q6 prefill arguments, which name them
+// alike), for heads h0 .. h0 + nh - 1, with every global load of the
+// first round in flight before the first LDS store.  A load under a condition is waited for at its join
+// (one round trip each), so entries past a table read zeros through buffer loads instead; the band slot
+// table (JN) is built by wave 0 from the offsets its lanes loaded, with what build_band_slots computes.
+// Entries past the first round (J > 127, or the tables of several heads) take element loops; table
+// layouts beyond 32-bit offsets take element loops throughout, with the slot table built by thread 0
+// from memory.  The caller's barrier completes the staging.  band_delta <= kJnSize - 1 - kJnBias.
+static_assert(kJnSize == kWave, "stage_tables builds the slot table one entry per lane of wave 0");
+
+template <bool E, bool PB, bool OFF, bool PH, bool JN, typename Args>
+__device__ __forceinline__ void stage_tables(const Args& f, int JE, int h0, int nh, const TableStage& d) {
+  const int J = f.J, JL = f.J_large;
+  const int64_t pbs0 = f.pb_stride[0], pbs1 = f.pb_stride[1];
+  const int64_t bs0 = f.pbase_stride[0], bs1 = f.pbase_stride[1], gs0 = f.pgain_stride[0], gs1 = f.pgain_stride[1];
+  const int64_t se0 = f.se_stride[0];
+  constexpr int64_t kSpan = int64_t(1) << 31;
+  const int64_t pb_span = ((J - 1) * pbs0 + (nh - 1) * pbs1 + 1) * 4;
+  const int64_t b_span = JL > 0 ? ((JL - 1) * bs0 + (nh - 1) * bs1 + kPlanes) * 4 : 0;
+  const int64_t g_span = JL > 0 ? ((JL - 1) * gs0 + (nh - 1) * gs1 + kPlanes) * 4 : 0;
+  const bool fast =
+      (!E || (f.se_stride[1] == 1 && (se0 & 3) == 0 && se0 <= (int64_t(1) << 20) &&
+              (reinterpret_cast<uintptr_t>(f.scale_embed) & 15) == 0)) &&
+      (!PB || (pbs0 >= 0 && pbs1 >= 0 && pb_span < kSpan)) &&
+      (!PH || (bs0 >= 0 && bs1 >= 0 && b_span < kSpan && gs0 >= 0 && gs1 >= 0 && g_span < kSpan));
+  const int tid = threadIdx.x, nt = static_cast<int>(blockDim.x);
+  const int ne = JE * 16, npb = nh * JE, nph = nh * JL * kPlanes;
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  auto put_e = [&](int i, uint4 x) {
+    const bf16x4_t h = {static_cast<__bf16>(__uint_as_float(x.x)), static_cast<__bf16>(__uint_as_float(x.y)),
+                        static_cast<__bf16>(__uint_as_float(x.z)), static_cast<__bf16>(__uint_as_float(x.w))};
+    *reinterpret_cast<bf16x4_t*>(d.sE + (i >> 4) * d.e_row + 4 * (i & 15)) = h;
+  };
+  auto ph_slot = [&](int t) {   // entry t = (hh * JL + i) * kPlanes + r, t < nph
+    const int hh = t / (JL * kPlanes);
+    return hh * d.ph_head + (t - hh * JL * kPlanes);
+  };
+  if (!fast) {
+    if (E) stage_se_bf16(f.scale_embed, f.se_stride, J, JE, d.sE, d.e_row);
+    if (PB)
+      for (int t = tid; t < npb; t += nt) {
+        const int hh = t / JE, j = t - hh * JE;
+        d.s_pb[t] = j < J ? d.pb_scale * f.pos_bias[j * pbs0 + (h0 + hh) * pbs1] : 0.f;
+      }
+    if (OFF)
+      for (int j = tid; j < JE; j += nt) d.s_off[j] = j < J ? f.offsets[j] : 0;
+    if (PH)
+      for (int t = tid; t < nph; t += nt) {
+        const int hh = t / (JL * kPlanes), rest = t - hh * JL * kPlanes;
+        const int i = rest / kPlanes, r = rest - i * kPlanes;
+        d.s_ph[ph_slot(t)] = make_float2(f.phase_base[i * bs0 + (h0 + hh) * bs1 + r],
+                                         f.phase_gain[i * gs0 + (h0 + hh) * gs1 + r]);
+      }
+    if (JN && tid == 0) build_band_slots(d.s_jn, f.offsets, f.J_small, d.band_delta, d.band_slots, d.band);
+    return;
+  }
+  const int rb = static_cast<int>(se0) * 4;   // E row bytes
+  const __amdgpu_buffer_rsrc_t rse = rows_rsrc(f.scale_embed, rb, J, 256);
+  const __amdgpu_buffer_rsrc_t rpb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(f.pos_bias + h0 * pbs1), 0, static_cast<int>(PB ? pb_span : 0), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rof = __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(f.offsets), 0, J * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rbs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(f.phase_base + h0 * bs1), 0, static_cast<int>(PH ? b_span : 0), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rgn = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(f.phase_gain + h0 * gs1), 0, static_cast<int>(PH ? g_span : 0), 0x00020000);
+  auto e_off = [&](int i) { return i < ne ? static_cast<uint32_t>((i >> 4) * rb + 16 * (i & 15)) : kOutOfRange; };
+  auto pb_off = [&](int t) {   // entry t = hh * JE + j
+    const int hh = t / JE, j = t - hh * JE;
+    return t < npb && j < J ? static_cast<uint32_t>((j * pbs0 + hh * pbs1) * 4) : kOutOfRange;
+  };
+  auto ph_off = [&](int t, int64_t s0, int64_t s1) {
+    if (t >= nph) return kOutOfRange;   // (every entry when JL = 0)
+    const int hh = t / (JL * kPlanes), rest = t - hh * JL * kPlanes;
+    const int i = rest / kPlanes, r = rest - i * kPlanes;
+    return static_cast<uint32_t>((i * s0 + hh * s1 + r) * 4);
+  };
+  // first round: every load, then every store
+  uint4 ex[E ? kSeBatch : 1];
+  if (E) {
+#pragma unroll
+    for (int u = 0; u < kSeBatch; ++u) ex[u] = buf_load16(rse, e_off(tid + u * nt));
+  }
+  const float pbv = PB ? buf_load_f32(rpb, pb_off(tid)) : 0.f;
+  const int ofv = OFF || JN ? static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(
+                                  rof, tid < JE ? static_cast<uint32_t>(4 * tid) : kOutOfRange, 0, 0))
+                            : 0;
+  float phb[2] = {0.f, 0.f}, phg[2] = {0.f, 0.f};
+  if (PH) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      phb[u] = buf_load_f32(rbs, ph_off(tid + u * nt, bs0, bs1));
+      phg[u] = buf_load_f32(rgn, ph_off(tid + u * nt, gs0, gs1));
+    }
+  }
+  if (E) {
+#pragma unroll
+    for (int u = 0; u < kSeBatch; ++u)
+      if (tid + u * nt < ne) put_e(tid + u * nt, ex[u]);
+  }
+  if (PB && tid < npb) d.s_pb[tid] = d.pb_scale * pbv;
+  if (OFF && tid < JE) d.s_off[tid] = ofv;
+  if (PH) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (tid + u * nt < nph) d.s_ph[ph_slot(tid + u * nt)] = make_float2(phb[u], phg[u]);
+  }
+  if (JN && tid < kWave) {   // build_band_slots from the lanes' offsets j = lane
+    const int prev = __shfl_up(ofv, 1);
+    const bool ok = d.band && tid < f.J_small && tid < d.band_slots && ofv >= 1 && ofv <= d.band_delta &&
+                    (tid == 0 || ofv > prev);
+    const uint64_t m = __ballot(ok);
+    const int jb = static_cast<int>(__builtin_ctzll(~m));
+    d.s_jn[tid] = tid == 0 ? jb : -1;
+    if (tid < jb) d.s_jn[kJnBias + ofv] = tid;   // after the lane's -1: a wave's LDS stores land in order
+  }
+  // what the first round did not cover
+  if (E)
+    for (int i = tid + kSeBatch * nt; i < ne; i += nt) put_e(i, buf_load16(rse, e_off(i)));
+  if (PB)
+    for (int t = tid + nt; t < npb; t += nt) d.s_pb[t] = d.pb_scale * buf_load_f32(rpb, pb_off(t));
+  if (OFF)
+    for (int j = tid + nt; j < JE; j += nt)
+      d.s_off[j] = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rof, static_cast<uint32_t>(4 * j), 0, 0));
+  if (PH)
+    for (int t = tid + 2 * nt; t < nph; t += nt)
+      d.s_ph[ph_slot(t)] = make_float2(buf_load_f32(rbs, ph_off(t, bs0, bs1)), buf_load_f32(rgn, ph_off(t, gs0, gs1)));
+}
 
 // Appends to `list` (wave-private LDS) the (index, offset) pairs of the
 // offsets that give some position in [lo, hi] a partner position inside

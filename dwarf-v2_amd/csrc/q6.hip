@@ -376,17 +376,11 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_q4(const dwarf_dsqg_q6_p
     qx1 = q4[1];
   }
 
-  stage_se_bf16(a.scale_embed, a.se_stride, J, lay.JE, sE, kPfERow);
-  for (int j = threadIdx.x; j < lay.JE; j += kBlock) {
-    s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
-    s_off[j] = j < J ? a.offsets[j] : 0;
-  }
-  for (int t = threadIdx.x; t < a.J_large * kPlanes; t += kBlock) {
-    const int i = t / kPlanes, r = t - i * kPlanes;
-    s_ph[t] = make_float2(a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r],
-                          a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r]);
-  }
-  for (int i = threadIdx.x; i < kPlanes * kHeadDim; i += kBlock) s_qp[i] = a.query_probes[i];
+  static_assert(kPlanes * kHeadDim == kBlock, "one query-probe entry per thread");
+  const float qpv = a.query_probes[threadIdx.x];   // in flight with the tables' loads
+  stage_tables<true, true, true, true, false>(
+      a, lay.JE, h, 1, TableStage{sE, kPfERow, s_pb, 1.0f, s_off, s_ph, 0, nullptr, 0, 0, false});
+  s_qp[threadIdx.x] = qpv;
   __syncthreads();
 
   // s_qe[query][j] = log2(e) * (<q, e_j> / 8 + pb_j): products into registers,
@@ -706,20 +700,12 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_win(const dwarf_dsqg_q6_
     qx1 = q4[1];
   }
 
-  stage_se_bf16(a.scale_embed, a.se_stride, J, JE, sE, kPfERow);
-  for (int j = threadIdx.x; j < JE; j += kBlock) {
-    s_pb[j] = j < J ? a.pos_bias[j * a.pb_stride[0] + h * a.pb_stride[1]] : 0.f;
-    s_off[j] = j < J ? a.offsets[j] : 0;
-  }
-  for (int t = threadIdx.x; t < a.J_large * kPlanes; t += kBlock) {
-    const int i = t / kPlanes, r = t - i * kPlanes;
-    s_ph[t] = make_float2(a.phase_base[i * a.pbase_stride[0] + h * a.pbase_stride[1] + r],
-                          a.phase_gain[i * a.pgain_stride[0] + h * a.pgain_stride[1] + r]);
-  }
-  for (int i = threadIdx.x; i < kPlanes * kHeadDim; i += kBlock) s_qp[i] = a.query_probes[i];
+  const float qpv = a.query_probes[threadIdx.x];   // in flight with the tables' loads
+  stage_tables<true, true, true, true, true>(
+      a, JE, h, 1, TableStage{sE, kPfERow, s_pb, 1.0f, s_off, s_ph, 0, s_jn, kPfWinBack, JBh, true});
+  s_qp[threadIdx.x] = qpv;
   __syncthreads();
 
-  if (threadIdx.x == 0) build_band_slots(s_jn, s_off, J_small, kPfWinBack, JBh, true);
   // q.E tables: products into registers, a barrier (every wave is done
   // reading sE), then the near columns into s_near and the far ones over sE
   {
