@@ -298,6 +298,32 @@ __device__ __forceinline__ int build_offset_list(int2* list, const int* s_off, i
   return cnt;
 }
 
+// build_offset_list with the offsets already in registers: lane l holds offset j = 64 c + l in offv[c]
+// (0 for j >= J), loaded with the kernel's other prologue loads, so the list waits on no memory.
+template <int CJ, int NC>
+__device__ __forceinline__ int build_offset_list_regs(int2* list, const int* offv, int J, int lo, int hi, int N,
+                                                      int dir, int2 pad) {
+  const int l = threadIdx.x % kWave;
+  int cnt = 0;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int j = kWave * c + l;
+    const int d = offv[c];
+    const int sd = dir * d;
+    const bool need = j < J && sd <= hi && sd >= lo - (N - 1);
+    const uint64_t mask = __ballot(need);
+    const int pos = cnt + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+    if (need) list[pos] = make_int2(j, d);
+    cnt += __popcll(mask);
+  }
+  cnt = uniform(cnt);
+  const int cntp = (cnt + CJ - 1) / CJ * CJ;
+  for (int t = cnt + l; t < cntp + 2 * CJ; t += kWave) list[t] = pad;
+  __builtin_amdgcn_wave_barrier();
+  return cnt;
+}
+
 // x + x of lane ^ 16 (v_permlane16_swap on copies of x: rows 0/2 receive
 // rows 1/3 and the reverse) and x + x of lane ^ 32 (v_permlane32_swap, the
 // two halves).  Both stay in the VALU, without an LDS round trip.

@@ -1003,6 +1003,7 @@ __global__ __launch_bounds__(kBlock, 2) void q6_prefill_win(const dwarf_dsqg_q6_
 // ---------------------------------------------------------------------------
 constexpr int kDecRows = 16;      // rows per batch (one per 4-lane group)
 constexpr int kMaxDecHeads = 16;  // heads the decode step takes
+constexpr int kMaxDecOffsets = 256;   // offsets the decode step takes
 // heads (waves) per decode workgroup: at cfg5 four per workgroup measured 43.0 / 47.9 / 53.1 us per step
 // (warm / advancing / cold) against 44.0 / 49.4 / 54.4 with all eight heads in one workgroup (28 resident
 // waves per CU instead of 24), two 43.2 / 48.2 / 53.6, one 43.4 / 48.1 / 53.0
@@ -1166,13 +1167,41 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
   const int c = l & 3;        // 16-dim chunk
   const int rr = l >> 2;      // row of the batch
   const int hk = h / (H / a.H_kv);
+  // The prologue's independent loads go out together: the position, the offsets (lane l holds offset
+  // 64 c + l; zeros past J), this head's query slice and the query probes; the offset list is then
+  // built from registers.
   const int t = uniform(a.pos[sq]);
+  constexpr int kOffChunks = (kMaxDecOffsets + kWave - 1) / kWave;
+  int offv[kOffChunks];
+  {
+    const __amdgpu_buffer_rsrc_t rof =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(a.offsets), 0, J * 4, 0x00020000);
+#pragma unroll
+    for (int ci = 0; ci < kOffChunks; ++ci)
+      offv[ci] = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rof, static_cast<uint32_t>(4 * (kWave * ci + l)), 0, 0));
+  }
+  const bf16* qrows = reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1];
+  const bf16* qh = qrows + h * a.q_stride[2];
+  uint32_t q32[8];
+  {
+    const uint4* q4 = reinterpret_cast<const uint4*>(qh + 16 * c);
+    const uint4 x0 = q4[0], x1 = q4[1];
+    q32[0] = x0.x; q32[1] = x0.y; q32[2] = x0.z; q32[3] = x0.w;
+    q32[4] = x1.x; q32[5] = x1.y; q32[6] = x1.z; q32[7] = x1.w;
+  }
+  const float qd = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(qh)[l]) << 16);
+  float qpl[kPlanes];
+  {
+    const float* qp = a.query_probes + ly * a.qprobe_layer_stride;
+#pragma unroll
+    for (int r = 0; r < kPlanes; ++r) qpl[r] = qp[r * kHeadDim + l];
+  }
   const int Nc = a.Ncache;
   int2* list = s_list_all + wv * lay.list_len;
   // this (sequence, layer, head)'s row of the T table (q6_decode_table)
   const float* Th = T + (static_cast<int64_t>(ly * a.S + sq) * H + h) * lay.JE;
   // rows t - delta in [0, Nc); the sentinel (J, t + 1) gives row -1
-  const int cnt = build_offset_list<kDecRows>(list, a.offsets, J, t, t, Nc, 1, make_int2(J, t + 1));
+  const int cnt = build_offset_list_regs<kDecRows, kOffChunks>(list, offv, J, t, t, Nc, 1, make_int2(J, t + 1));
   const int cntp = (cnt + kDecRows - 1) / kDecRows * kDecRows;
 
   const uint8_t* cb = a.cache + ly * a.cache_stride[0] + sq * a.cache_stride[1] + hk * a.cache_stride[2];
@@ -1212,29 +1241,18 @@ __global__ __launch_bounds__(kWave * kMaxDecHeads) void q6_decode_q4(const dwarf
   DecBatch b0, b1;
   if (cnt > 0) fetch(0, b0);
 
-  const bf16* qrows = reinterpret_cast<const bf16*>(a.q) + sq * a.q_stride[0] + ly * a.q_stride[1];
   // this head's query: lane c's 16 dims as bf16 pairs, their sum, and y of
   // plane c = <q, probe_c> / sqrt(|q|^2 + 1e-6 hd) (dsqg:3231-3249)
-  const bf16* qh = qrows + h * a.q_stride[2];
-  uint32_t q32[8];
-  {
-    const uint4* q4 = reinterpret_cast<const uint4*>(qh + 16 * c);
-    const uint4 x0 = q4[0], x1 = q4[1];
-    q32[0] = x0.x; q32[1] = x0.y; q32[2] = x0.z; q32[3] = x0.w;
-    q32[4] = x1.x; q32[5] = x1.y; q32[6] = x1.z; q32[7] = x1.w;
-  }
   float qbias = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) qbias = dot2bf(q32[i], 0x3f803f80u, qbias);   // (1, 1) in bf16
   qbias *= -160.f;
   float yg;
   {
-    const float qd = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(qh)[l]) << 16);
-    const float* qp = a.query_probes + ly * a.qprobe_layer_stride;
     const float ss = wave_allsum(qd * qd);
     float yp[kPlanes];
 #pragma unroll
-    for (int r = 0; r < kPlanes; ++r) yp[r] = wave_allsum(qd * qp[r * kHeadDim + l]);
+    for (int r = 0; r < kPlanes; ++r) yp[r] = wave_allsum(qd * qpl[r]);
     yg = pick4(c, yp[0], yp[1], yp[2], yp[3]) * rsqrtf(ss + 1e-6f * kHeadDim);
   }
 
@@ -1418,7 +1436,7 @@ hipError_t launch_q6_decode(const dwarf_dsqg_q6_decode_args& a, float* T, hipStr
   return hipGetLastError();
 }
 
-int q6_max_decode_offsets() { return 256; }
+int q6_max_decode_offsets() { return kMaxDecOffsets; }
 int q6_max_decode_heads() { return kMaxDecHeads; }
 
 }  // namespace dwarf
