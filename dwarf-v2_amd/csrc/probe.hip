@@ -139,13 +139,8 @@ __global__ __launch_bounds__(kBlock, kPrWgsPerCu) void phase_probe_fwd_kernel(
       if (st.rw.live) load_raw(x + st.rw.b * sx0 + st.rw.h * sx1 + static_cast<int64_t>(st.rw.n) * sx2 + kPrDims * g, st.x);
     }
   };
-  PrStep<T> nxt;
-  int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPrRows;
-  fetch(r0, nxt);
-  for (; r0 < gm.rows; r0 += stride) {
-    const PrStep<T> cur = nxt;
-    if (r0 + stride < gm.rows) fetch(r0 + stride, nxt);
-    if (!cur.ok) continue;
+  auto process = [&](const PrStep<T>& cur) {
+    if (!cur.ok) return;
     float y = 0.f;
     if (cur.rw.live) {
       float xv[kPrDims];
@@ -155,6 +150,18 @@ __global__ __launch_bounds__(kBlock, kPrWgsPerCu) void phase_probe_fwd_kernel(
       y = pick4(g, raw[0], raw[1], raw[2], raw[3]) * rsqrtf(ss + eps);
     }
     out[cur.rw.b * so0 + cur.rw.h * so1 + static_cast<int64_t>(cur.rw.n) * so2 + g * so3] = y;
+  };
+  // two step buffers in turn, the next step's loads in flight while one is consumed (a copy of a
+  // prefetch buffer into a current one would wait for its loads at every step)
+  PrStep<T> s0, s1;
+  int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPrRows;
+  if (r0 < gm.rows) fetch(r0, s0);
+  for (; r0 < gm.rows; r0 += 2 * stride) {
+    if (r0 + stride < gm.rows) fetch(r0 + stride, s1);
+    process(s0);
+    if (r0 + stride >= gm.rows) break;
+    if (r0 + 2 * stride < gm.rows) fetch(r0 + 2 * stride, s0);
+    process(s1);
   }
 }
 
@@ -188,13 +195,8 @@ __global__ __launch_bounds__(kBlock, pr_bwd_wgs_per_cu(DPROBES)) void phase_prob
       }
     }
   };
-  PrStep<T> nxt;
-  int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPrRows;
-  fetch(r0, nxt);
-  for (; r0 < gm.rows; r0 += stride) {
-    const PrStep<T> cur = nxt;
-    if (r0 + stride < gm.rows) fetch(r0 + stride, nxt);
-    if (!cur.ok) continue;
+  auto process = [&](const PrStep<T>& cur) {
+    if (!cur.ok) return;
     const PrRow& rw = cur.rw;
     float dxv[kPrDims];
 #pragma unroll
@@ -233,6 +235,17 @@ __global__ __launch_bounds__(kBlock, pr_bwd_wgs_per_cu(DPROBES)) void phase_prob
       }
     }
     store16<T>(dx + rw.b * sd0 + rw.h * sd1 + static_cast<int64_t>(rw.n) * sd2 + kPrDims * g, dxv);
+  };
+  // two step buffers in turn (as in the forward)
+  PrStep<T> s0, s1;
+  int64_t r0 = static_cast<int64_t>(blockIdx.x) * kPrRows;
+  if (r0 < gm.rows) fetch(r0, s0);
+  for (; r0 < gm.rows; r0 += 2 * stride) {
+    if (r0 + stride < gm.rows) fetch(r0 + stride, s1);
+    process(s0);
+    if (r0 + stride >= gm.rows) break;
+    if (r0 + 2 * stride < gm.rows) fetch(r0 + 2 * stride, s0);
+    process(s1);
   }
   if constexpr (DPROBES) {
     // Sum over the wave's 16 rows (lanes sharing g), reduce-scattered: after
