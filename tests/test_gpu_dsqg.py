@@ -411,3 +411,28 @@ def test_bf16_gqa_head_subsets_match_expanded_heads(pkg, device):
         bar = 2.0 ** -8 * (per_head.abs().sum(1) + a.abs()) + 1e-6
         assert bool(((a - b).abs() <= bar).all()), (n, float((a - b).abs().max()))
     assert rel_err(g1["z_pre"][:, 0], gh["z_pre"].double().sum(1)) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lattice_without_far_offsets(pkg, device, dtype):
+    """Every offset small (J_large = 0: no MOVT rotation, so the [1, H, 4] phase tables, y and z do not enter
+    the output), a ragged N, query_start 2: their gradients exactly zero (the oracle's autograd gives none),
+    the output and the q, k, v, pos_bias and scale_embed gradients against the oracle (fp32 1e-5 relative,
+    bf16 2e-2 max-abs; bf16 serves the five offsets on the band)."""
+    offsets = [1, 2, 3, 5, 8]
+    x = make_inputs(2, 4, 2, 301, offsets, 5, seed=61, dtype=dtype, plane_shift=1)
+    dout = torch.randn(2, 4, 301, 64, generator=torch.Generator().manual_seed(62)).to(dtype)
+    out, grads = gpu_fwd_bwd(pkg, x, offsets, 5, 1, 2, dout, device)
+    ro, _, rg = oracle_fwd_bwd(x, offsets, 5, 1, 2, dout.float(), round_se=dtype == torch.bfloat16)
+    unused = ("phase_base", "phase_gain", "y_pre", "z_pre")
+    for n in unused:
+        assert rg[n] is None and torch.equal(grads[n].cpu(), torch.zeros_like(grads[n].cpu())), n
+    used = [n for n in NAMES if n not in unused]
+    if dtype == torch.float32:
+        assert rel_err(out, ro) < FP32_REL
+        for n in used:
+            assert rel_err(grads[n], rg[n]) < FP32_REL, (n, rel_err(grads[n], rg[n]))
+    else:
+        assert max_abs(out, ro) < BF16_ABS
+        for n in used:
+            assert max_abs(grads[n], rg[n]) < BF16_ABS, (n, max_abs(grads[n], rg[n]))
