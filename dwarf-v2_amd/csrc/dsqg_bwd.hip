@@ -212,7 +212,8 @@ struct KvChunk {
 template <int SHIFT, int CJ, int MINWG>
 __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwarf_dsqg_bwd_args a,
                                                                    const float* __restrict__ delta_ws, int tiles,
-                                                                   int total, int nsplit, float* __restrict__ kvp) {
+                                                                   int total, int whole, int nsplit,
+                                                                   float* __restrict__ kvp) {
   constexpr float kC = 0.125f * kLog2e;
   constexpr float kScale = 0.125f;
   static_assert(SHIFT + 1 < kHeadDim / kPlanes, "MOVT pair must stay inside one lane's slice");
@@ -232,14 +233,24 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
   char* s_dw = s_qw + kWinRowsKv * 128;                  // dO rows, same layout
   float2* s_dl = reinterpret_cast<float2*>(sm + lay.off_dl);
 
-  const int work = xcd_remap(blockIdx.x, total);
-  const int unit = work / tiles;   // (b, kv head, subset of its query heads)
-  const int tile = work - unit * tiles;
-  const int bhk = unit / nsplit;
-  const int split = unit - bhk * nsplit;
+  // Work units are (b, kv head, key tile).  The first `whole` workgroups take units 0 .. whole - 1 with all
+  // of the group's query heads; the others take the remaining units in subsets of group / nsplit query
+  // heads, the subsets of a unit side by side, and leave fp32 partials for dsqg_bwd_dkdv_combine.
+  const bool part = static_cast<int>(blockIdx.x) >= whole;   // uniform
+  int unit, split = 0, ns = 1;
+  if (!part) {
+    unit = xcd_remap(blockIdx.x, whole);
+  } else {
+    const int t = xcd_remap(blockIdx.x - whole, total - whole);
+    unit = whole + t / nsplit;
+    split = t - (unit - whole) * nsplit;
+    ns = nsplit;
+  }
+  const int bhk = unit / tiles;
+  const int tile = unit - bhk * tiles;
   const int b = bhk / f.H_kv;
   const int hk = bhk - b * f.H_kv;
-  const int hh0 = split * (group / nsplit), hh1 = hh0 + group / nsplit;   // the workgroup's query heads
+  const int hh0 = split * (group / ns), hh1 = hh0 + group / ns;   // the workgroup's query heads
 
   // this lane's key row (K, V slices and z) is requested first, so its latency
   // overlaps the table staging
@@ -524,10 +535,11 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
 
   }
 
-  if (kvp) {   // a subset of the query heads: its partial sums, which dsqg_bwd_dkdv_combine adds up
+  if (part) {   // a subset of the query heads: its partial sums, which dsqg_bwd_dkdv_combine adds up
     if (!key_ok) return;
-    const int64_t rows = static_cast<int64_t>(f.B) * f.H_kv * N;
-    const int64_t row = static_cast<int64_t>(bhk) * N + m;
+    // rows of the split units, kKPB per unit: [split][unit - whole][key in tile]
+    const int64_t rows = static_cast<int64_t>(total - whole) / nsplit * kKPB;
+    const int64_t row = static_cast<int64_t>(unit - whole) * kKPB + (m - tile * kKPB);
     float4* pk = reinterpret_cast<float4*>(kvp + (split * rows + row) * kHeadDim + 16 * g);
     float4* pv = reinterpret_cast<float4*>(kvp + ((nsplit + split) * rows + row) * kHeadDim + 16 * g);
 #pragma unroll
@@ -566,16 +578,19 @@ __global__ __launch_bounds__(kBlock, MINWG) void dsqg_bwd_dkdv_bf16_k4(const dwa
 // through the key probes when z came from them, and writes the bf16 gradients. Four lanes per key,
 // lane g holding dims 16g .. 16g + 15 and plane g, as in dsqg_bwd_dkdv_bf16_k4.
 __global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_combine(const dwarf_dsqg_bwd_args a,
-                                                                const float* __restrict__ kvp, int nsplit) {
+                                                                const float* __restrict__ kvp, int tiles,
+                                                                int whole, int split_units, int nsplit) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
   const int N = f.N;
-  const int64_t rows = static_cast<int64_t>(f.B) * f.H_kv * N;
+  const int64_t rows = static_cast<int64_t>(split_units) * kKPB;   // the split units' key rows
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
   const int64_t row = t >> 2;
   const int g = static_cast<int>(t & 3);
   if (row >= rows) return;   // rows * 4 threads: a key's four lanes leave together
-  const int bhk = static_cast<int>(row / N);
-  const int64_t mm = row - static_cast<int64_t>(bhk) * N;
+  const int unit = whole + static_cast<int>(row / kKPB);
+  const int bhk = unit / tiles, tile = unit - bhk * tiles;
+  const int64_t mm = static_cast<int64_t>(tile) * kKPB + (row - static_cast<int64_t>(unit - whole) * kKPB);
+  if (mm >= N) return;   // past the end of the last tile: a key's four lanes leave together
   const int b = bhk / f.H_kv, hk = bhk - b * f.H_kv;
   float dk[16], dv[16];
 #pragma unroll
@@ -617,42 +632,54 @@ __global__ __launch_bounds__(kBlock) void dsqg_bwd_dkdv_combine(const dwarf_dsqg
   x.x = pack_bf16x2(dv[8], dv[9]);   x.y = pack_bf16x2(dv[10], dv[11]);
   x.z = pack_bf16x2(dv[12], dv[13]); x.w = pack_bf16x2(dv[14], dv[15]);
   v4[1] = x;
-  if (!f.key_probes) a.dz_pre[row * kPlanes + g] = dz;
+  if (!f.key_probes) a.dz_pre[(static_cast<int64_t>(bhk) * N + mm) * kPlanes + g] = dz;
 }
 
 // Grouped-query heads: a KV head's workgroups walk all of its query heads, so the grid has 1 / group
-// of the MHA grid's workgroups. A grid that does not fill the resident slots once (256 CUs x kMinWgKv)
-// gets its query heads split into subsets, one workgroup per (key tile, KV head, subset): the smallest
-// divisor of the group size giving two rounds of the slots. The subsets' fp32 partials are summed by
-// dsqg_bwd_dkdv_combine. A grid of one to two rounds keeps whole groups: at B15 N2048 H8 over 2 KV
-// heads (960 workgroups) the partials' traffic cost what the split gained (dK/dV 277 us whole,
-// 281 us in 2 subsets, 299 us in 4); over 1 KV head (480) 4 subsets take it from 394 to 284 us.
+// of the MHA grid's workgroups, each group-times as long.  Units (key tile, KV head) past what the
+// resident slots (256 CUs x kMinWgKv) take in a whole round are split into subsets of the query heads,
+// one workgroup per subset, the smallest divisor of the group size whose subsets fill a round (two rounds
+// for a grid that fills none): the last round then runs shorter workgroups instead of a few whole-group
+// ones alone on the chip.  The subsets' fp32 partials are summed by dsqg_bwd_dkdv_combine.  A grid of
+// two or more rounds keeps whole groups.
 constexpr int kKvResidentWgs = 256 * kMinWgKv;
 
-int dkdv_split(const dwarf_dsqg_fwd_args& f) {
+KvSplit dkdv_split(const dwarf_dsqg_fwd_args& f) {
   const int group = f.H_kv > 0 ? f.H / f.H_kv : 1;
-  const int64_t wgs = static_cast<int64_t>((f.N + kKPB - 1) / kKPB) * f.B * f.H_kv;
-  if (wgs >= kKvResidentWgs) return 1;
+  const int64_t units = static_cast<int64_t>((f.N + kKPB - 1) / kKPB) * f.B * f.H_kv;
+  KvSplit k{static_cast<int>(units), 1};
+  if (group == 1 || units >= 2 * kKvResidentWgs) return k;
+  int64_t target = kKvResidentWgs;
+  if (units < kKvResidentWgs) {
+    k.whole = 0;
+    target = 2 * kKvResidentWgs;
+  } else {
+    k.whole = kKvResidentWgs;
+  }
+  const int64_t rest = units - k.whole;
   int s = 1;
-  while (s < group && wgs * s < 2 * kKvResidentWgs) {
+  while (s < group && rest * s < target) {
     do ++s; while (group % s);
   }
-  return s;
+  k.nsplit = s;
+  if (s == 1) k.whole = static_cast<int>(units);
+  return k;
 }
 
 hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace& ws, hipStream_t stream) {
   const dwarf_dsqg_fwd_args& f = a.fwd;
   const float* delta = reinterpret_cast<const float*>(static_cast<char*>(a.workspace) + ws.delta_off);
   const int tiles = (f.N + kKPB - 1) / kKPB;
-  const int ns = ws.kv_split;
+  const int units = tiles * f.B * f.H_kv;
+  const int ns = ws.kv_split, whole = ws.kv_whole;
   float* kvp = ns > 1 ? reinterpret_cast<float*>(static_cast<char*>(a.workspace) + ws.kv_part_off) : nullptr;
-  const int total = tiles * f.B * f.H_kv * ns;
+  const int total = whole + (units - whole) * ns;
   if (total == 0) return hipSuccess;
   const size_t lds = kv_layout(f.J, f.J_large, f.H / f.H_kv, kChunkKv).bytes;
 #define DWARF_KV4_CASE(S) \
   case S:                                                                                                     \
     hipLaunchKernelGGL((dsqg_bwd_dkdv_bf16_k4<S, kChunkKv, kMinWgKv>), dim3(total), dim3(kBlock), lds, stream, a, \
-                       delta, tiles, total, ns, kvp);                                                         \
+                       delta, tiles, total, whole, ns, kvp);                                                  \
     break;
   switch (f.plane_shift) {
     DWARF_KV4_CASE(0) DWARF_KV4_CASE(1) DWARF_KV4_CASE(2) DWARF_KV4_CASE(3) DWARF_KV4_CASE(4)
@@ -662,9 +689,9 @@ hipError_t launch_dkdv_bf16_k4(const dwarf_dsqg_bwd_args& a, const BwdWorkspace&
   }
 #undef DWARF_KV4_CASE
   if (ns > 1) {
-    const int64_t threads = static_cast<int64_t>(f.B) * f.H_kv * f.N * kPlanes;
+    const int64_t threads = static_cast<int64_t>(units - whole) * kKPB * kPlanes;
     hipLaunchKernelGGL(dsqg_bwd_dkdv_combine, dim3(static_cast<unsigned>((threads + kBlock - 1) / kBlock)),
-                       dim3(kBlock), 0, stream, a, kvp, ns);
+                       dim3(kBlock), 0, stream, a, kvp, tiles, whole, units - whole, ns);
   }
   return hipGetLastError();
 }
@@ -836,11 +863,14 @@ BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a) {
                  static_cast<size_t>(f.H) * w.red_groups_pb * f.J +
                  static_cast<size_t>(f.H) * w.red_groups_ph * JL * 8) * sizeof(float);
   off += align256(w.red_bytes);
-  w.kv_split = f.dtype == DWARF_BF16 ? dkdv_split(f) : 1;
+  const int kv_units = (f.N + kKPB - 1) / kKPB * f.B * f.H_kv;
+  const KvSplit ks = f.dtype == DWARF_BF16 ? dkdv_split(f) : KvSplit{kv_units, 1};
+  w.kv_split = ks.nsplit;
+  w.kv_whole = ks.whole;
   w.kv_part_off = off;
-  w.kv_part_bytes = w.kv_split > 1 ? static_cast<size_t>(w.kv_split) * f.B * f.H_kv * f.N *
-                                         (2 * kHeadDim + kPlanes) * sizeof(float)
-                                   : 0;
+  w.kv_part_bytes = ks.nsplit > 1 ? static_cast<size_t>(ks.nsplit) * (kv_units - ks.whole) * kKPB *
+                                        (2 * kHeadDim + kPlanes) * sizeof(float)
+                                  : 0;
   off += align256(w.kv_part_bytes);
   w.total = off;
   return w;

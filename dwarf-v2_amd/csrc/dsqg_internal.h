@@ -44,8 +44,8 @@ struct BwdWorkspace {
   size_t part_ph_off, part_ph_bytes;    // [H][ph_rows][J_L][8] fp32
   size_t ds_off, ds_bytes;              // bf16 launch: dS [B*H][J][N] fp32
   size_t red_off, red_bytes;            // stage-1 sums of the reduction
-  size_t kv_part_off, kv_part_bytes;    // bf16, kv_split > 1: [kv_split][B*H_kv*N] partial dK and dV (64 fp32
-                                        // each), then dZ (4 fp32), of each subset of a KV head's query heads
+  size_t kv_part_off, kv_part_bytes;    // bf16, kv_split > 1: [kv_split][split units x 64 keys] partial dK and
+                                        // dV (64 fp32 each), then dZ (4 fp32), of each subset of the query heads
   size_t total;
   int dq_tiles;   // query tiles per (b, h)
   int dq_tpw;     // tiles per workgroup (fp32 launch)
@@ -54,9 +54,14 @@ struct BwdWorkspace {
   int dq_gather_wgs;   // bf16: persistent workgroups of the dQ gather launch
   int pb_rows, ph_rows;   // dPB / dPhase partial rows per head
   int red_groups_se, red_groups_pb, red_groups_ph;  // stage-1 row groups per segment
-  int kv_split;   // bf16: workgroups sharing one (key tile, KV head), each over a subset of its query heads
+  int kv_split;   // bf16: workgroups sharing one split (key tile, KV head), each over a subset of its query heads
+  int kv_whole;   // bf16: (key tile, KV head) units taken whole, before the split ones
 };
 BwdWorkspace bwd_workspace_layout(const dwarf_dsqg_bwd_args& a);
+struct KvSplit {
+  int whole;    // (key tile, KV head) units a workgroup takes with the whole query-head group
+  int nsplit;   // subsets of the query heads for each of the other units (1: none)
+};
 // do_dq: delta + dQ/dY + the parameter-gradient inputs in the workspace (bf16:
 // the dS matrix and dPhase partials; fp32: all partials); do_params: the
 // parameter gradients from those (bf16: the dSE/dPB launch, then the fixed-

@@ -191,10 +191,11 @@ int dwarf_dsqg_bwd(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
  * as fixed-order reductions: dpos_bias, dscale_embed, dphase_base and
  * dphase_gain.  dwarf_dsqg_bwd_dkdv replaces _bwd_dkdv_v18_grouped
  * (dsqg:2456-2544): it reads delta and writes dk, dv and dz_pre; in bf16
- * with grouped heads on a grid of fewer than 768 key-tile workgroups it
- * also keeps per-subset fp32 partials in a workspace region of its own
- * (no other stage touches it), summed in fixed order.  Fields a stage does
- * not write may be NULL.
+ * with grouped heads on a grid of fewer than 1536 (key tile, KV head) units
+ * it splits the query heads of the units past the first 768 (of every
+ * unit below 768) into subsets and keeps their fp32 partials in a
+ * workspace region of its own (no other stage touches it), summed in fixed
+ * order.  Fields a stage does not write may be NULL.
  */
 int dwarf_dsqg_bwd_dq(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);
 int dwarf_dsqg_bwd_params(const dwarf_dsqg_bwd_args* args, dwarf_stream_t stream);

@@ -204,10 +204,12 @@ def test_backward_limits_without_gpu(pkg, lib):
 
 
 def test_gqa_head_split_workspace_without_gpu(pkg, lib):
-    """bf16 dK/dV with grouped heads on a grid that fills no round of the 768 resident slots splits the query
-    heads into subsets and keeps their fp32 partials (dK and dV 64 floats each, dZ 4, per key and subset) in
-    the workspace: B1 H8 over one KV head at N 2048 (32 key tiles) takes all 8 subsets; B15 over 2 KV heads
-    (960 key tiles) and fp32 none, so those sizes equal the MHA layout's."""
+    """bf16 dK/dV with grouped heads splits the query heads of the (key tile, KV head) units past the 768 that
+    one round of resident workgroups takes whole, and keeps their fp32 partials (dK and dV 64 floats each, dZ
+    4, per key of the unit's 64 and subset) in the workspace: B1 H8 over one KV head at N 2048 (32 units, no
+    whole round) takes all 8 subsets of every unit; B15 over 2 KV heads (960 units) splits the last 192 in 4;
+    B15 over one KV head at N 8192 (1,920 units, two rounds) and fp32 split none, so those sizes equal the MHA
+    layout's."""
     L = pkg._lib
 
     def need(B, H, H_kv, N, dtype):
@@ -219,7 +221,8 @@ def test_gqa_head_split_workspace_without_gpu(pkg, lib):
 
     assert need(1, 8, 1, 2048, L.DWARF_BF16) - need(1, 8, 8, 2048, L.DWARF_BF16) == 8 * 2048 * (2 * 64 + 4) * 4
     assert need(2, 8, 1, 2048, L.DWARF_BF16) - need(2, 8, 8, 2048, L.DWARF_BF16) == 8 * 2 * 2048 * (2 * 64 + 4) * 4
-    assert need(15, 8, 2, 2048, L.DWARF_BF16) == need(15, 8, 8, 2048, L.DWARF_BF16)
+    assert need(15, 8, 2, 2048, L.DWARF_BF16) - need(15, 8, 8, 2048, L.DWARF_BF16) == 4 * 192 * 64 * (2 * 64 + 4) * 4
+    assert need(15, 8, 1, 8192, L.DWARF_BF16) == need(15, 8, 8, 8192, L.DWARF_BF16)
     assert need(1, 8, 1, 2048, L.DWARF_F32) == need(1, 8, 8, 2048, L.DWARF_F32)
 
 

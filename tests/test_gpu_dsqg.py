@@ -388,29 +388,33 @@ def test_overlapped_backward_repeated_at_training_shape(pkg, device):
             assert torch.equal(a, b), (it, i)
 
 
-def test_bf16_gqa_head_subsets_match_expanded_heads(pkg, device):
-    """B12 H8 over one KV head, N 2048: 384 key-tile workgroups fill no round of the resident slots, so the dK/dV
-    launch splits the 8 query heads into 4 subsets of 2 and sums their fp32 partials in a second kernel.  Against
-    the same inputs with K, V and z repeated per head (MHA, one workgroup per head, no split): dQ, dY and the
-    table gradients equal bit for bit; dK and dV within a bf16 ulp of each side (the split's bf16 rounding of the
-    sum, plus the eight per-head bf16 roundings summed); dZ within 1e-5 relative (fp32 sums in another order)."""
+@pytest.mark.parametrize("B,Hkv", [(12, 1), (15, 2)])
+def test_bf16_gqa_head_subsets_match_expanded_heads(pkg, device, B, Hkv):
+    """N 2048, H8.  Over one KV head at B12 the 384 key-tile units fill no round of the 768 resident slots, so
+    the dK/dV launch splits every unit's 8 query heads into 4 subsets of 2; over two KV heads at B15 the first
+    768 of 960 units run whole and the last 192 in 4 subsets of one head.  The subsets' fp32 partials are summed
+    in a second kernel.  Against the same inputs with K, V and z repeated per head (MHA, one workgroup per head,
+    no split): dQ, dY and the table gradients equal bit for bit; dK and dV within a bf16 ulp of each side (the
+    bf16 rounding of the group's sum, plus the per-head bf16 roundings summed); dZ within 1e-5 relative (fp32
+    sums in another order)."""
     offsets = lattice(pkg)
-    B, H, N = 12, 8, 2048
-    x = make_inputs(B, H, 1, N, offsets, 17, seed=91, dtype=torch.bfloat16, plane_shift=3, gain_std=4.0)
+    H, N = 8, 2048
+    x = make_inputs(B, H, Hkv, N, offsets, 17, seed=91, dtype=torch.bfloat16, plane_shift=3, gain_std=4.0)
     dout = torch.randn(B, H, N, 64, generator=torch.Generator().manual_seed(92)).to(torch.bfloat16)
     _, g1 = gpu_fwd_bwd(pkg, x, offsets, 17, 3, 1, dout, device)
     xm = dict(x)
-    for n in ("k", "v", "z_pre"):
-        xm[n] = x[n].expand(B, H, *x[n].shape[2:]).contiguous()
+    for n in ("k", "v", "z_pre"):   # query head h reads KV head h // (H / Hkv)
+        xm[n] = x[n].repeat_interleave(H // Hkv, dim=1).contiguous()
     _, gh = gpu_fwd_bwd(pkg, xm, offsets, 17, 3, 1, dout, device)
     for n in ("q", "y_pre", "pos_bias", "scale_embed", "phase_base", "phase_gain"):
         assert torch.equal(g1[n], gh[n]), n
+    G = H // Hkv
     for n in ("k", "v"):
-        per_head = gh[n].double().cpu()
-        a, b = g1[n].double().cpu()[:, 0], per_head.sum(1)
-        bar = 2.0 ** -8 * (per_head.abs().sum(1) + a.abs()) + 1e-6
+        per_head = gh[n].double().cpu().reshape(B, Hkv, G, N, 64)
+        a, b = g1[n].double().cpu(), per_head.sum(2)
+        bar = 2.0 ** -8 * (per_head.abs().sum(2) + a.abs()) + 1e-6
         assert bool(((a - b).abs() <= bar).all()), (n, float((a - b).abs().max()))
-    assert rel_err(g1["z_pre"][:, 0], gh["z_pre"].double().sum(1)) < 1e-5
+    assert rel_err(g1["z_pre"], gh["z_pre"].double().reshape(B, Hkv, G, N, 4).sum(2)) < 1e-5
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
